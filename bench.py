@@ -1,0 +1,411 @@
+"""Benchmark of the gfx950 small/irregular-shape GEMM path (one JSON line).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2]
+                    [--detail FILE] [--no-cpu]
+
+A step is one pass of the hot path over one batch of synthetic input.  The
+default workload is BASELINE config C2 (the configuration the metric is
+quoted on): fp32 C = A B + C for M in {2,3,5,7} x N in {1009,4099,11003},
+K = 2048, alpha = beta = 1, A, B ~ N(0, 0.02), C ~ U[-1, 1).  One step runs
+all twelve shapes once.  Other workloads (c1, c3, c4, c5) are selectable for
+per-config measurements; `--workload all` writes one line per workload to
+--detail and prints the default line.
+
+`value` is the algorithmic bytes of a step (sA*M*K + sB*K*N + sC*M*N*(1 +
+[beta != 0]), each operand counted once) divided by the wall time of the
+timed steps, measured with HIP events on the stream the kernels run on.
+Operands are resident in HBM before timing starts; every buffer of a step is
+touched once per step and a step's working set exceeds the 256 MB Infinity
+Cache (extra copies are rotated when it would not), so nothing is served from
+the cache between two launches of the same shape.
+
+`roofline` is for the kernel with the largest share of the step time:
+achieved = its algorithmic bytes (or flops) per launch / its mean launch
+time (HIP events around each launch).  `traffic` is filled from
+profiles/<kernel>_<workload>_traffic.json when a rocprofv3 --pmc summary has
+been committed for it.
+
+`cpu_baseline` times the oracle's restatement of the reference's CPU path
+(oracle/liboracle.so) on the host, on every shape of the workload once per
+run (2 warmup runs, 5 timed runs, median -- the reference's
+dnnopt::benchmark method).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+HBM_PEAK_GBS = 8000.0
+PEAKS_TFLOPS = {"f32": 157.3, "bf16": 2500.0, "s8": 5000.0}
+METRIC = "GB/s (% HBM peak) at M=1-7; TFLOPS (% MFMA peak) tall-skinny"
+SEED = 42
+
+
+def _binding():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("dnnopt_hip", os.path.join(ROOT, "dnn-opt_amd", "python",
+                                                                             "dnnopt_hip.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+# ---------------------------------------------------------------- workloads
+class Case:
+    def __init__(self, name, kind, M, N, K, alpha=1.0, beta=0.0, ta=0, init=None, dtype="f32"):
+        self.name, self.kind = name, kind
+        self.M, self.N, self.K = M, N, K
+        self.alpha, self.beta, self.ta = alpha, beta, ta
+        self.init = init or {}
+        self.dtype = dtype
+
+    def sizes(self):
+        sa, sb = {"f32": (4, 4), "bf16": (2, 2), "f2b": (4, 4), "s8": (1, 1), "s8s": (1, 1)}[self.kind]
+        sc = 4
+        extra = 4 * self.N if self.kind == "s8s" else 0
+        return sa, sb, sc, extra
+
+    def bytes_alg(self):
+        sa, sb, sc, extra = self.sizes()
+        M, N, K = self.M, self.N, self.K
+        return sa * M * K + sb * K * N + sc * M * N * (1 + (1 if self.beta != 0.0 else 0)) + extra
+
+    def flops_alg(self):
+        return 2.0 * self.M * self.N * self.K
+
+
+def workload(name):
+    if name == "c1":
+        return ("C1: fp32 M=1 N=4096 K=4096, alpha=1 beta=0, A,B ~ U[-1,1)",
+                [Case("c1", "f32", 1, 4096, 4096, init={"A": ("u", -1, 1), "B": ("u", -1, 1)})])
+    if name == "c2":
+        cs = []
+        for M in (2, 3, 5, 7):
+            for N in (1009, 4099, 11003):
+                cs.append(Case(f"c2_m{M}_n{N}", "f32", M, N, 2048, 1.0, 1.0,
+                               init={"A": ("n", 0, 0.02), "B": ("n", 0, 0.02), "C": ("u", -1, 1)}))
+        return ("C2: fp32 M in {2,3,5,7} x N in {1009,4099,11003} x K=2048, alpha=1 beta=1, "
+                "A,B ~ N(0,0.02), C ~ U[-1,1), row-major", cs)
+    if name == "c3":
+        u = {"A": ("u", -1, 1), "B": ("u", -1, 1)}
+        return ("C3: fp32 tall-skinny 65536x{16,64}x256 and 64x64x262144 (A stored KxM), beta=0", [
+            Case("c3_n16", "f32", 65536, 16, 256, init=u), Case("c3_n64", "f32", 65536, 64, 256, init=u),
+            Case("c3_splitk_tn", "f32", 64, 64, 262144, ta=1, init=u)])
+    if name == "c4":
+        return ("C4: bf16 storage, fp32 accumulate/output, M in {1,4,32,256} x N=11008 x K=4096, "
+                "weights ~ N(0,0.02), activations ~ N(0,1)", [
+                    Case(f"c4_m{M}", "bf16", M, 11008, 4096, init={"A": ("n", 0, 1), "B": ("n", 0, 0.02)},
+                         dtype="bf16") for M in (1, 4, 32, 256)])
+    if name == "c5":
+        cs = []
+        for M in (1, 8, 128):
+            for N in (4096, 4093):
+                cs.append(Case(f"c5_m{M}_n{N}", "s8", M, N, 4096, init={"A": ("i",), "B": ("i",)}, dtype="s8"))
+        cs.append(Case("c5_m128_n4093_scale", "s8s", 128, 4093, 4096, init={"A": ("i",), "B": ("i",)}, dtype="s8"))
+        return ("C5: int8 s8 x s8 -> s32 (B as N x K), M in {1,8,128} x N in {4096,4093} x K=4096; "
+                "+ per-column fp32 scale", cs)
+    raise SystemExit(f"unknown workload {name}")
+
+
+# ---------------------------------------------------------------- GPU side
+class Buffers:
+    def __init__(self, torch, lib, case, copies, dev):
+        self.case = case
+        M, N, K = case.M, case.N, case.K
+        tA = {"f32": torch.float32, "f2b": torch.float32, "bf16": torch.int16, "s8": torch.int8,
+              "s8s": torch.int8}[case.kind]
+        dt_code = {torch.float32: 0, torch.int16: 1, torch.int8: 2}[tA]
+        a_elems = M * K
+        b_elems = K * N
+        self.A, self.B, self.C, self.S = [], [], [], []
+        for r in range(copies):
+            A = torch.empty(a_elems, dtype=tA, device=dev)
+            B = torch.empty(b_elems, dtype=tA, device=dev)
+            cdt = torch.int32 if case.kind == "s8" else torch.float32
+            C = torch.empty(M * N, dtype=cdt, device=dev)
+            for t, key, tid in ((A, "A", 1), (B, "B", 2)):
+                spec = case.init.get(key, ("u", -1, 1))
+                if spec[0] == "i":
+                    lib.fill(t, t.numel(), 2, 2, SEED + r, tid, -127, 127)
+                else:
+                    lib.fill(t, t.numel(), dt_code, 0 if spec[0] == "u" else 1, SEED + r, tid, spec[1], spec[2])
+            if case.kind != "s8":
+                spec = case.init.get("C", ("u", -1, 1))
+                lib.fill(C, C.numel(), 0, 0, SEED + r, 3, spec[1], spec[2])
+            self.A.append(A)
+            self.B.append(B)
+            self.C.append(C)
+            if case.kind == "s8s":
+                S = torch.empty(N, dtype=torch.float32, device=dev)
+                lib.fill(S, N, 0, 0, SEED + r, 4, 0.001, 0.01)
+                self.S.append(S)
+
+    def launch(self, lib, r, stream):
+        c = self.case
+        M, N, K = c.M, c.N, c.K
+        A, B, C = self.A[r], self.B[r], self.C[r]
+        if c.kind == "f32":
+            lda = M if c.ta else K
+            lib.sgemm(M, N, K, c.alpha, A, lda, B, N, c.beta, C, N, transA=c.ta, stream=stream)
+        elif c.kind == "bf16":
+            lib.gemm_bf16(M, N, K, c.alpha, A, K, B, N, c.beta, C, N, stream=stream)
+        elif c.kind == "f2b":
+            lib.gemm_bf16_f32in(M, N, K, c.alpha, A, K, B, N, c.beta, C, N, stream=stream)
+        elif c.kind == "s8":
+            lib.gemm_s8s8s32(M, N, K, A, K, B, K, C, N, stream=stream)
+        else:
+            lib.gemm_s8s8f32_colscale(M, N, K, A, K, B, K, self.S[r], C, N, stream=stream)
+
+
+def kernel_key(lib, case):
+    """Kernel template instance as rocprof names it (family<params>)."""
+    if case.kind in ("f32",):
+        p = lib.plan_sgemm(case.M, case.N, case.K, transA=case.ta)
+    elif case.kind in ("bf16", "f2b"):
+        p = lib.plan_bf16(case.M, case.N, case.K, fp32_inputs=int(case.kind == "f2b"))
+    else:
+        p = lib.plan_s8(case.M, case.N, case.K, with_scale=int(case.kind == "s8s"))
+    if p["name"] == "dnnopt_skinny":
+        mode = {"f32": 0, "bf16": 1, "f2b": 2}[case.kind]
+        return f"dnnopt_skinny<{case.M}, {p['block'] // 64}, {mode}>", p
+    return f"{p['name']}[{p['rows']}x{p['cols']}]", p
+
+
+def run_gpu(args, wl_name):
+    import torch
+
+    b = _binding()
+    lib = b.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    desc, cases = workload(wl_name)
+    step_bytes = sum(c.bytes_alg() for c in cases)
+    # Rotate copies so one pass of every buffer exceeds 2x the 256 MB cache.
+    copies = max(1, -(-(600 << 20) // step_bytes))
+    bufs = [Buffers(torch, lib, c, copies, dev) for c in cases]
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    sp = s.cuda_stream
+    keys = [kernel_key(lib, c) for c in cases]
+
+    for w in range(args.warmup):
+        for bf in bufs:
+            bf.launch(lib, w % copies, sp)
+    torch.cuda.synchronize()
+
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in cases]
+          for _ in range(args.steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(s)
+    for st in range(args.steps):
+        r = (args.warmup + st) % copies
+        for i, bf in enumerate(bufs):
+            ev[st][i][0].record(s)
+            bf.launch(lib, r, sp)
+            ev[st][i][1].record(s)
+    t1.record(s)
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    ms_per_step = total_ms / args.steps
+
+    per_case = []
+    for i, c in enumerate(cases):
+        d = [ev[st][i][0].elapsed_time(ev[st][i][1]) for st in range(args.steps)]
+        med = statistics.median(d)
+        per_case.append({
+            "case": c.name, "M": c.M, "N": c.N, "K": c.K, "kernel": keys[i][0], "plan": keys[i][1],
+            "us_median": med * 1e3, "us_mean": sum(d) / len(d) * 1e3,
+            "GBps": c.bytes_alg() / (med * 1e-3) / 1e9, "TFLOPs": c.flops_alg() / (med * 1e-3) / 1e12,
+        })
+    # dominant kernel instance: largest share of the per-launch time
+    groups = {}
+    for i, c in enumerate(cases):
+        k = keys[i][0]
+        g = groups.setdefault(k, {"ms": 0.0, "bytes": 0.0, "flops": 0.0, "launches": 0, "dtype": c.dtype,
+                                  "cases": []})
+        for st in range(args.steps):
+            g["ms"] += ev[st][i][0].elapsed_time(ev[st][i][1])
+            g["bytes"] += c.bytes_alg()
+            g["flops"] += c.flops_alg()
+            g["launches"] += 1
+        g["cases"].append(c.name)
+    dom_key, dom = max(groups.items(), key=lambda kv: kv[1]["ms"])
+    mean_s = dom["ms"] / dom["launches"] * 1e-3
+    bytes_per = dom["bytes"] / dom["launches"]
+    flops_per = dom["flops"] / dom["launches"]
+    # bound: HBM unless the shape's arithmetic intensity exceeds the ridge
+    ai = flops_per / bytes_per
+    peak_t = PEAKS_TFLOPS.get(dom["dtype"], 157.3)
+    ridge = peak_t * 1e12 / (HBM_PEAK_GBS * 1e9)
+    if ai > ridge:
+        achieved = flops_per / mean_s / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": peak_t, "unit": "TFLOP/s",
+                "frac": round(achieved / peak_t, 4)}
+    else:
+        achieved = bytes_per / mean_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4)}
+    roof["kernel"] = dom_key
+    roof["launch_us"] = round(mean_s * 1e6, 3)
+    roof["bytes_per_launch"] = int(bytes_per)
+    roof["traffic"] = read_traffic(dom_key, wl_name)
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    return {
+        "desc": desc, "value": value, "ms_per_step": ms_per_step, "step_bytes": step_bytes,
+        "step_flops": sum(c.flops_alg() for c in cases), "copies": copies, "roofline": roof,
+        "per_case": per_case, "cases": cases,
+    }
+
+
+def read_traffic(kernel, wl):
+    safe = kernel.replace("<", "_").replace(">", "").replace(", ", "_").replace("[", "_").replace("]", "")
+    path = os.path.join(ROOT, "profiles", f"{safe}_{wl}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline(cases, budget_s=20.0):
+    """Time the oracle's restatement of the reference CPU path on the host."""
+    import ctypes
+
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _util as u
+
+    orc = u.load_oracle()
+    nthreads = os.cpu_count() or 1
+    os.environ.setdefault("OMP_NUM_THREADS", str(nthreads))
+    prepared = []
+    for c in cases:
+        M, N, K = c.M, c.N, c.K
+        if c.kind == "f32" and c.M <= 8:
+            A = (u.normal if c.init["A"][0] == "n" else u.uniform)(orc, M * K, 1, *c.init["A"][1:])
+            B = (u.normal if c.init["B"][0] == "n" else u.uniform)(orc, K * N, 2, *c.init["B"][1:])
+            C = u.uniform(orc, M * N, 3)
+
+            def run(A=A, B=B, C=C, c=c):
+                cc = C.copy()
+                rc = orc.orc_gemm_f32_smallm(c.M, c.N, c.K, c.alpha, u.ptr(A), c.K, u.ptr(B), c.N, c.beta,
+                                             u.ptr(cc), c.N, nthreads)
+                if rc != 0:
+                    raise RuntimeError("shape outside the restated small-M path")
+        elif c.kind in ("s8", "s8s"):
+            A, B = u.ints8(orc, M * K, 1), u.ints8(orc, N * K, 2)
+            C = np.empty(M * N, np.int32)
+
+            def run(A=A, B=B, C=C, c=c):
+                orc.orc_gemm_s8s8s32(c.M, c.N, c.K, u.ptr(A), c.K, u.ptr(B), c.K, u.ptr(C), c.N)
+        elif c.kind == "bf16" and c.M <= 8:
+            A = u.bf16_bits(orc, u.normal(orc, M * K, 1))
+            B = u.bf16_bits(orc, u.normal(orc, K * N, 2, 0, 0.02))
+            C = np.zeros(M * N, np.float32)
+
+            def run(A=A, B=B, C=C, c=c):
+                orc.orc_gemm_bf16(c.M, c.N, c.K, 1.0, u.ptr(A), c.K, u.ptr(B), c.N, 0.0, u.ptr(C), c.N)
+        else:
+            continue
+        prepared.append((c, run))
+    if not prepared:
+        return None
+    # bounded sample: scale repetitions to the budget
+    t = time.perf_counter()
+    for _, run in prepared:
+        run()
+    one = time.perf_counter() - t
+    runs = []
+    total_bytes = sum(c.bytes_alg() for c, _ in prepared)
+    reps = 5 if one * 7 < budget_s else max(1, int(budget_s / max(one, 1e-9)) - 2)
+    for _ in range(min(2, reps)):
+        for _, run in prepared:
+            run()
+    for _ in range(reps):
+        t = time.perf_counter()
+        for _, run in prepared:
+            run()
+        runs.append(time.perf_counter() - t)
+    med = statistics.median(runs)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    del ctypes
+    threaded = any(c.kind == "f32" and c.M in (5, 7) and c.N * c.K > 4 * 1024 * 1024 for c, _ in prepared)
+    return {
+        "value": round(total_bytes / med / 1e9, 3), "unit": "GB/s",
+        "cores": nthreads if threaded else 1, "kind": "port",
+        "sample": (f"every shape of the workload once ({len(prepared)} GEMMs, {total_bytes / 1e6:.0f} MB "
+                   f"algorithmic), median of {reps} runs after warmup; oracle restatement of the reference CPU "
+                   f"path (GEMV / wide driver single-threaded, adaptive tiles on {nthreads} OpenMP threads); "
+                   f"host CPU: {cpu_model}"),
+    }
+
+
+# ---------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "all"])
+    ap.add_argument("--detail", default=os.path.join(ROOT, "gpurun_out", "bench_detail.jsonl"))
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is described in DESIGN.md, not run).", file=sys.stderr)
+        sys.exit(2)
+
+    names = ["c1", "c2", "c3", "c4", "c5"] if args.workload == "all" else [args.workload]
+    main_name = "c2" if args.workload == "all" else args.workload
+    results = {}
+    for wl in names:
+        r = run_gpu(args, wl)
+        results[wl] = r
+        print(f"[bench] {wl}: {r['value']:.1f} GB/s per step, {r['ms_per_step'] * 1e3:.1f} us/step, "
+              f"dominant {r['roofline']['kernel']} frac {r['roofline']['frac']}", file=sys.stderr, flush=True)
+    r = results[main_name]
+    cpu = None if args.no_cpu else cpu_baseline(r["cases"])
+    line = {
+        "metric": METRIC, "value": round(r["value"], 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(r["ms_per_step"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": {"c4": "bf16", "c5": "s8"}.get(main_name, "f32"),
+        "data": "synthetic: SplitMix64 seed 42 (device generator), distributions of BASELINE.json",
+        "config": {"workload": r["desc"], "shapes": len(r["cases"]), "bytes_per_step": r["step_bytes"],
+                   "hbm_frac": round(r["value"] / HBM_PEAK_GBS, 4), "buffer_copies": r["copies"],
+                   "parallelism": "1 GPU"},
+        "roofline": {k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
+        "roofline_kernel": {k: r["roofline"][k] for k in ("kernel", "launch_us", "bytes_per_launch")},
+        "cpu_baseline": cpu,
+    }
+    if args.detail:
+        os.makedirs(os.path.dirname(args.detail), exist_ok=True)
+        with open(args.detail, "a") as f:
+            for wl, rr in results.items():
+                f.write(json.dumps({"workload": wl, "desc": rr["desc"], "GBps_step": rr["value"],
+                                    "ms_per_step": rr["ms_per_step"], "roofline": rr["roofline"],
+                                    "per_case": rr["per_case"]}) + "\n")
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

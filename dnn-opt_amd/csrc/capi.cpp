@@ -1,0 +1,272 @@
+// capi.cpp -- the extern "C" boundary declared in include/dnnopt_hip.h.
+//
+// Each entry point validates its arguments, asks the dispatcher for a launch,
+// takes the stream's workspace when the launch needs one, and enqueues the
+// kernel.  Nothing here falls back to the host: a failure is a status code.
+#include <hip/hip_runtime.h>
+
+#include "dnnopt_hip.h"
+#include "host.h"
+
+using namespace dnnopt_hip;
+
+namespace {
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+int finish_launch(hipError_t e) {
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return to_status(e);
+    }
+    return DNNOPT_OK;
+}
+
+int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B, int ldb, float* C, int ldc,
+               int M, int N, int K, float alpha, float beta, hipStream_t s) {
+    SkinnyArgs a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.a_sm = a_sm;
+    a.a_sk = a_sk;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.splits = (int)L.grid.y;
+    a.ncols_pad = (int)L.grid.x * skinny_tile_cols(L.mode);
+    if (a.splits > 1) {
+        void* part = nullptr;
+        unsigned* tickets = nullptr;
+        int st = get_workspace(s, L.part_bytes, &part, &tickets);
+        if (st != DNNOPT_OK) return st;
+        a.part = static_cast<float*>(part);
+        a.tickets = tickets;
+    }
+    return finish_launch(launch_skinny(L.mode, L.mr, L.nw, L.grid, a, s));
+}
+
+int run_tile(const Launch& L, int ta, int tb, const void* A, int lda, const void* B, int ldb, float* C, int ldc,
+             int M, int N, int K, float alpha, float beta, hipStream_t s) {
+    TileArgs a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.transA = ta;
+    a.transB = tb;
+    a.splits = (int)L.grid.z;
+    a.defer_reduce = L.defer_reduce;
+    if (a.splits > 1) {
+        void* part = nullptr;
+        unsigned* tickets = nullptr;
+        int st = get_workspace(s, L.part_bytes, &part, &tickets);
+        if (st != DNNOPT_OK) return st;
+        a.part = static_cast<float*>(part);
+        a.tickets = tickets;
+    }
+    int st = finish_launch(launch_tile(L.mode, L.cfg, ta, tb, L.grid, a, s));
+    if (st != DNNOPT_OK || !L.defer_reduce) return st;
+    return finish_launch(launch_splitk_reduce(a.part, a.splits, (int)L.grid.x, (int)L.grid.y, L.bm, L.bn, M, N,
+                                              alpha, beta, C, ldc, s));
+}
+
+bool dims_ok(int M, int N, int K) { return M > 0 && N > 0 && K > 0; }
+
+}  // namespace
+
+extern "C" {
+
+int dnnopt_hip_abi_version(void) { return 1; }
+
+int dnnopt_hip_device_count(void) { return visible_devices(); }
+
+const char* dnnopt_hip_status_string(int status) {
+    switch (status) {
+        case DNNOPT_OK: return "ok";
+        case DNNOPT_ERR_INVALID_ARG: return "invalid argument";
+        case DNNOPT_ERR_NO_DEVICE: return "no HIP device visible";
+        case DNNOPT_ERR_HIP: return "HIP runtime error";
+        case DNNOPT_ERR_UNSUPPORTED: return "unsupported shape or option";
+        case DNNOPT_ERR_OUT_OF_MEMORY: return "device memory allocation failed";
+        default: return "unknown status";
+    }
+}
+
+int dnnopt_hip_plan_sgemm(int transA, int transB, int M, int N, int K, dnnopt_plan* out) {
+    if (!out || (transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return DNNOPT_ERR_INVALID_ARG;
+    if (!dims_ok(M, N, K)) return DNNOPT_ERR_INVALID_ARG;
+    Launch L;
+    int st = plan_sgemm(transA, transB, M, N, K, transA ? M : K, transB ? K : N, &L);
+    if (st == DNNOPT_OK) *out = L.pub;
+    return st;
+}
+
+int dnnopt_hip_plan_gemm_bf16(int fp32_inputs, int M, int N, int K, dnnopt_plan* out) {
+    if (!out || !dims_ok(M, N, K)) return DNNOPT_ERR_INVALID_ARG;
+    Launch L;
+    int st = plan_bf16(fp32_inputs ? 1 : 0, M, N, K, K, N, &L);
+    if (st == DNNOPT_OK) *out = L.pub;
+    return st;
+}
+
+int dnnopt_hip_plan_gemm_s8(int with_scale, int M, int N, int K, dnnopt_plan* out) {
+    if (!out || !dims_ok(M, N, K)) return DNNOPT_ERR_INVALID_ARG;
+    Launch L;
+    int st = plan_s8(with_scale ? 1 : 0, M, N, K, &L);
+    if (st == DNNOPT_OK) *out = L.pub;
+    return st;
+}
+
+int dnnopt_hip_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
+                     const float* B, int ldb, float beta, float* C, int ldc, void* stream) {
+    if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return DNNOPT_ERR_INVALID_ARG;
+    if (!dims_ok(M, N, K)) return DNNOPT_OK;
+    if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
+    if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    Launch L;
+    int st = plan_sgemm(transA, transB, M, N, K, lda, ldb, &L);
+    if (st != DNNOPT_OK) return st;
+    hipStream_t s = as_stream(stream);
+    if (L.family == DNNOPT_K_SKINNY_F32)
+        return run_skinny(L, A, transA ? 1 : lda, transA ? lda : 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+    return run_tile(L, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+}
+
+int dnnopt_hip_sgemm_naive(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                           float beta, float* C, int ldc, void* stream) {
+    if (!dims_ok(M, N, K)) return DNNOPT_OK;
+    if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
+    if (lda < K || ldb < N || ldc < N) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    if ((long long)(M + 3) / 4 > 65535) return DNNOPT_ERR_UNSUPPORTED;
+    return finish_launch(launch_naive_f32(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, as_stream(stream)));
+}
+
+static int gemm_bf16_common(int fp32_inputs, int M, int N, int K, float alpha, const void* A, int lda,
+                            const void* B, int ldb, float beta, float* C, int ldc, void* stream) {
+    if (!dims_ok(M, N, K)) return DNNOPT_OK;
+    if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
+    if (lda < K || ldb < N || ldc < N) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    Launch L;
+    int st = plan_bf16(fp32_inputs, M, N, K, lda, ldb, &L);
+    if (st != DNNOPT_OK) return st;
+    hipStream_t s = as_stream(stream);
+    if (L.family == DNNOPT_K_SKINNY_BF16 || L.family == DNNOPT_K_SKINNY_F2B)
+        return run_skinny(L, A, lda, 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+    return run_tile(L, 0, 0, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+}
+
+int dnnopt_hip_gemm_bf16(int M, int N, int K, float alpha, const uint16_t* A, int lda, const uint16_t* B, int ldb,
+                         float beta, float* C, int ldc, void* stream) {
+    return gemm_bf16_common(0, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream);
+}
+
+int dnnopt_hip_gemm_bf16_f32in(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                               float beta, float* C, int ldc, void* stream) {
+    return gemm_bf16_common(1, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream);
+}
+
+static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda, const int8_t* B, int ldb,
+                          const float* scale, void* C, int ldc, void* stream) {
+    if (!dims_ok(M, N, K)) return DNNOPT_OK;
+    if (!A || !B || !C || (epi && !scale)) return DNNOPT_ERR_INVALID_ARG;
+    if (lda < K || ldb < K || ldc < N) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    Launch L;
+    int st = plan_s8(epi, M, N, K, &L);
+    if (st != DNNOPT_OK) return st;
+    if ((long long)L.bm * lda + K >= 0x7FFFFFFFll || (long long)L.bn * ldb + K >= 0x7FFFFFFFll)
+        return DNNOPT_ERR_UNSUPPORTED;
+    hipStream_t s = as_stream(stream);
+    S8Args a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.scale = scale;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.splits = (int)L.grid.z;
+    if (a.splits > 1) {
+        void* part = nullptr;
+        unsigned* tickets = nullptr;
+        st = get_workspace(s, L.part_bytes, &part, &tickets);
+        if (st != DNNOPT_OK) return st;
+        a.part = static_cast<int32_t*>(part);
+        a.tickets = tickets;
+    }
+    return finish_launch(launch_mfma_s8(L.cfg, epi, L.grid, a, s));
+}
+
+int dnnopt_hip_gemm_s8s8s32(int M, int N, int K, const int8_t* A, int lda, const int8_t* B, int ldb, int32_t* C,
+                            int ldc, void* stream) {
+    return gemm_s8_common(0, M, N, K, A, lda, B, ldb, nullptr, C, ldc, stream);
+}
+
+int dnnopt_hip_gemm_s8s8f32_colscale(int M, int N, int K, const int8_t* A, int lda, const int8_t* B, int ldb,
+                                     const float* col_scale, float* C, int ldc, void* stream) {
+    return gemm_s8_common(1, M, N, K, A, lda, B, ldb, col_scale, C, ldc, stream);
+}
+
+int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                             float beta, float* C, int ldc, void* stream) {
+    if (!dims_ok(M, N, K)) return DNNOPT_OK;
+    if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
+    if (lda < K || ldb < N || ldc < N) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    hipStream_t s = as_stream(stream);
+    // Staging (slot 1): [int32 acc M*N][qA M*K][qB N*K][2 absmax words].
+    const size_t acc_bytes = (size_t)M * N * 4;
+    const size_t qa_bytes = ((size_t)M * K + 255) & ~(size_t)255;
+    const size_t qb_bytes = ((size_t)N * K + 255) & ~(size_t)255;
+    void* stage = nullptr;
+    unsigned* unused = nullptr;
+    int st = get_workspace(s, acc_bytes + qa_bytes + qb_bytes + 256, &stage, &unused, 1);
+    if (st != DNNOPT_OK) return st;
+    char* base = static_cast<char*>(stage);
+    int32_t* acc = reinterpret_cast<int32_t*>(base);
+    int8_t* qa = reinterpret_cast<int8_t*>(base + acc_bytes);
+    int8_t* qb = reinterpret_cast<int8_t*>(base + acc_bytes + qa_bytes);
+    unsigned* amax = reinterpret_cast<unsigned*>(base + acc_bytes + qa_bytes + qb_bytes);
+    st = finish_launch(launch_quant_prepare(A, lda, B, ldb, M, N, K, amax, qa, qb, s));
+    if (st != DNNOPT_OK) return st;
+    st = gemm_s8_common(0, M, N, K, qa, K, qb, K, nullptr, acc, N, stream);
+    if (st != DNNOPT_OK) return st;
+    return finish_launch(launch_dequant(acc, M, N, amax, alpha, beta, C, ldc, s));
+}
+
+int dnnopt_hip_saxpy(int N, float alpha, const float* X, int incX, float* Y, int incY, void* stream) {
+    if (N <= 0 || alpha == 0.0f) return DNNOPT_OK;
+    if (!X || !Y || incX <= 0 || incY <= 0) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    return finish_launch(launch_saxpy(N, alpha, X, incX, Y, incY, as_stream(stream)));
+}
+
+int dnnopt_hip_fill(void* dst, size_t n, int dtype, int dist, uint64_t seed, uint32_t tensor_id, double p0,
+                    double p1, void* stream) {
+    if (n == 0) return DNNOPT_OK;
+    if (!dst || dtype < 0 || dtype > 2 || dist < 0 || dist > 2) return DNNOPT_ERR_INVALID_ARG;
+    if ((dtype == 2) != (dist == 2)) return DNNOPT_ERR_INVALID_ARG;
+    if (dtype == 2 && (p0 < -128 || p1 > 127 || p0 > p1)) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    return finish_launch(launch_fill(dst, n, dtype, dist, seed, tensor_id, p0, p1, as_stream(stream)));
+}
+
+}  // extern "C"

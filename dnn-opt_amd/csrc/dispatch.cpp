@@ -1,0 +1,199 @@
+// dispatch.cpp -- shape dispatcher for the gfx950 GEMM path.
+//
+// Replaces the reference's routing (src/gemm/gemm.cpp:175-455), which is
+// tuned for Neoverse caches: tiny/GEMV kernels, the small-M wide driver below
+// M=8, adaptive register tiles, and a packed BLIS driver with cache-derived
+// blocking (src/gemm/gemm_config.h:43-145) and OpenMP decomposition.
+//
+// On MI355X the questions are different: a launch must put enough bytes in
+// flight to cover HBM latency on every compute unit, and the shapes of this
+// path are almost all HBM-bound.  The rules:
+//   * M <= 8 (fp32, bf16): the skinny kernel streams B once.  Work is split
+//     over column tiles, over the waves of a workgroup and, when there are too
+//     few column tiles to occupy the chip, over k across workgroups (split-k
+//     with a ticketed, ordered reduction) -- about eight waves per CU.
+//   * M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for N <= 16,
+//     64 x 64 otherwise); split-k when the tile count cannot occupy the CUs,
+//     with a separate reduce kernel once the split count is large.
+//   * int8 (B as N x K): MFMA tiles of 16 rows for M <= 16, 128 x 64 for
+//     large M, split-k as above.
+// Tunables (environment, read once, for sweeps):
+//   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
+//   DNNOPT_MAX_SPLITS (default 256).
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cstdio>
+
+#include "host.h"
+
+namespace dnnopt_hip {
+
+namespace {
+
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    if (!v || !*v) return dflt;
+    int x = atoi(v);
+    return x > 0 ? x : dflt;
+}
+
+int waves_per_cu() {
+    static int v = env_int("DNNOPT_WAVES_PER_CU", 8);
+    return v;
+}
+int skinny_nw() {
+    static int v = [] {
+        int x = env_int("DNNOPT_SKINNY_NW", 8);
+        return (x == 4 || x == 8 || x == 16) ? x : 8;
+    }();
+    return v;
+}
+int max_splits() {
+    static int v = env_int("DNNOPT_MAX_SPLITS", 256);
+    return v;
+}
+
+// Splits beyond this are reduced by a separate kernel rather than by the
+// last-arriving workgroup.
+constexpr int kTicketSplitLimit = 16;
+
+long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
+
+void fill_pub(Launch* L, int kernel, const char* name, int rows, int cols, int splits, int block) {
+    L->pub.kernel = kernel;
+    L->pub.rows = rows;
+    L->pub.cols = cols;
+    L->pub.splits = splits;
+    L->pub.grid_x = (int)L->grid.x;
+    L->pub.grid_y = (int)L->grid.y;
+    L->pub.grid_z = (int)L->grid.z;
+    L->pub.block = block;
+    L->pub.workspace_bytes = L->part_bytes + (L->tickets ? (size_t)kMaxTickets * sizeof(unsigned) : 0);
+    snprintf(L->pub.name, sizeof L->pub.name, "%s", name);
+    L->family = kernel;
+}
+
+}  // namespace
+
+int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
+    if (M < 1 || M > 8) return DNNOPT_ERR_UNSUPPORTED;
+    *L = Launch{};
+    const int tw = skinny_tile_cols(mode);
+    const int es = skinny_elem_bytes(mode);
+    const int nw = skinny_nw();
+    const long long tiles = ceil_div(N, tw);
+    const long long target_waves = (long long)num_cus() * waves_per_cu();
+    long long s = ceil_div(target_waves, tiles * nw);
+    // Each wave should own at least one unrolled step of rows.
+    const long long smax = std::max<long long>(1, K / ((long long)nw * kSkinnyUnroll));
+    s = std::max<long long>(1, std::min<long long>({s, smax, (long long)kTicketSplitLimit * 2}));
+    // Keep per-workgroup buffer offsets inside 31 bits.
+    while (s < K && ceil_div(K, s) * (long long)ldb * es + (long long)tw * es >= 0x7FFFFFFFll) s *= 2;
+    if (ceil_div(K, s) * (long long)ldb * es + (long long)tw * es >= 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
+    if (s > 1 && tiles > kMaxTickets) s = 1;
+    L->mode = mode;
+    L->mr = M;
+    L->nw = nw;
+    L->grid = dim3((unsigned)tiles, (unsigned)s, 1);
+    L->part_bytes = s > 1 ? (size_t)s * M * tiles * tw * sizeof(float) : 0;
+    L->tickets = s > 1 ? (int)tiles : 0;
+    const int kernel = mode == kSkinnyF32 ? DNNOPT_K_SKINNY_F32
+                       : mode == kSkinnyBF16 ? DNNOPT_K_SKINNY_BF16
+                                             : DNNOPT_K_SKINNY_F2B;
+    fill_pub(L, kernel, "dnnopt_skinny", M, tw, (int)s, nw * 64);
+    return DNNOPT_OK;
+}
+
+int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L) {
+    *L = Launch{};
+    int cfg;
+    if (mode == kTileF32 && N <= 16) {
+        cfg = 0;
+    } else if (mode == kTileF32 && N <= 64 && M >= 4096) {
+        cfg = 1;
+    } else if (M >= 128 && N >= 128) {
+        cfg = 4;
+    } else {
+        cfg = 2;
+    }
+    const TileConfig c = tile_config(cfg);
+    const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
+    const int kb = mode == kTileF32 ? 64 : 128;
+    const long long tn = ceil_div(N, bn), tm = ceil_div(M, bm), tiles = tn * tm;
+    const long long nblk = ceil_div(K, kb);
+    const int waves_per_wg = c.wm * c.wn * c.kw;
+    const long long target_wgs = (long long)num_cus() * waves_per_cu() / waves_per_wg;
+    long long s = 1;
+    if (tiles < target_wgs) {
+        s = ceil_div(target_wgs, tiles);
+        s = std::min<long long>({s, std::max<long long>(1, nblk / (2 * c.kw)), (long long)max_splits()});
+        s = std::max<long long>(1, s);
+    }
+    // Per-workgroup buffer offsets must fit in 31 bits: an operand read along
+    // its rows spans one tile of rows, one read along k spans the k-range of
+    // one workgroup.  More splits shorten that range.
+    const long long es = mode == kTileBF16 ? 2 : 4;
+    auto span_ok = [&](long long splits) {
+        const long long kext = ceil_div(nblk, splits) * kb;
+        const long long a = transA ? kext * lda : (long long)bm * lda;
+        const long long b = transB ? (long long)bn * ldb : kext * ldb;
+        return (a + kext + bm) * es < 0x7FFFFFFFll && (b + kext + bn) * es < 0x7FFFFFFFll;
+    };
+    while (!span_ok(s) && s < nblk) s *= 2;
+    if (s > nblk) s = nblk;
+    if (!span_ok(s)) return DNNOPT_ERR_UNSUPPORTED;
+    if (tm > 65535 || s > 65535) return DNNOPT_ERR_UNSUPPORTED;
+    L->mode = mode;
+    L->cfg = cfg;
+    L->bm = bm;
+    L->bn = bn;
+    L->grid = dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
+    L->defer_reduce = (s > kTicketSplitLimit || (s > 1 && tiles > kMaxTickets)) ? 1 : 0;
+    L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(float) : 0;
+    L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
+    const int kernel = mode == kTileF32 ? DNNOPT_K_TILE_F32 : DNNOPT_K_TILE_BF16;
+    fill_pub(L, kernel, mode == kTileF32 ? "dnnopt_tile_f32" : "dnnopt_tile_bf16", bm, bn, (int)s,
+             waves_per_wg * 64);
+    return DNNOPT_OK;
+}
+
+int plan_s8(int epi, int M, int N, int K, Launch* L) {
+    *L = Launch{};
+    const int cfg = M <= 16 ? 1 : (M >= 128 ? 3 : 2);
+    const S8Config c = s8_config(cfg);
+    const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
+    const long long tn = ceil_div(N, bn), tm = ceil_div(M, bm), tiles = tn * tm;
+    const long long nblk = ceil_div(K, 256);
+    const int waves_per_wg = c.wm * c.wn * c.kw;
+    const long long target_wgs = (long long)num_cus() * waves_per_cu() / waves_per_wg;
+    long long s = 1;
+    if (tiles < target_wgs) {
+        s = ceil_div(target_wgs, tiles);
+        s = std::min<long long>({s, std::max<long long>(1, nblk / c.kw), (long long)kTicketSplitLimit});
+        s = std::max<long long>(1, s);
+    }
+    if (s > 1 && tiles > kMaxTickets) s = 1;
+    L->mode = epi;
+    L->cfg = cfg;
+    L->bm = bm;
+    L->bn = bn;
+    L->grid = dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
+    L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(int32_t) : 0;
+    L->tickets = s > 1 ? (int)tiles : 0;
+    fill_pub(L, DNNOPT_K_MFMA_S8, "dnnopt_mfma_s8", bm, bn, (int)s, waves_per_wg * 64);
+    return DNNOPT_OK;
+}
+
+int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L) {
+    if (M <= 8 && !transB) return plan_skinny(kSkinnyF32, M, N, K, ldb, L);
+    return plan_tile(kTileF32, transA, transB, M, N, K, lda, ldb, L);
+}
+
+int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L) {
+    if (M <= 8) return plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L);
+    return plan_tile(fp32_inputs ? kTileF2B : kTileBF16, 0, 0, M, N, K, lda, ldb, L);
+}
+
+}  // namespace dnnopt_hip

@@ -1,0 +1,49 @@
+// host.h -- internal host-side interfaces: device state, workspace, dispatch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+#include "dnnopt_hip.h"
+#include "kernels.h"
+
+namespace dnnopt_hip {
+
+// ---------------------------------------------------------------- runtime
+// Compute units of the current device, or 256 (MI355X) when no device is
+// visible, so that plans can be computed and tested without a GPU.
+int num_cus();
+int visible_devices();
+int to_status(hipError_t e);
+
+// Per-(device, stream, slot) scratch: `tickets` (kMaxTickets counters, zero
+// between launches) followed by `part_bytes` of partial-sum space.  Launches
+// on one stream are ordered, so they can share it; the buffer only grows.
+// Slot 0 serves the GEMM kernels, slot 1 the int8 quantization staging.
+constexpr int kMaxTickets = 16384;
+int get_workspace(hipStream_t s, size_t part_bytes, void** part, unsigned** tickets, int slot = 0);
+
+// ---------------------------------------------------------------- dispatch
+struct Launch {
+    dnnopt_plan pub;
+    int family = DNNOPT_K_NONE;
+    int mode = 0;        // SkinnyMode / TileMode / int8 epilogue
+    int mr = 0, nw = 0;  // skinny
+    int cfg = 0;         // tile / int8 configuration index
+    int bm = 0, bn = 0;  // tile shape
+    dim3 grid;
+    size_t part_bytes = 0;
+    int tickets = 0;
+    int defer_reduce = 0;
+};
+
+int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L);
+int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L);
+int plan_s8(int epi, int M, int N, int K, Launch* L);
+
+// Route an fp32 GEMM to a kernel family (skinny or tile).
+int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L);
+// Route a bf16 GEMM (fp32_inputs: operands are fp32 and rounded in registers).
+int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L);
+
+}  // namespace dnnopt_hip

@@ -1,0 +1,130 @@
+// k_misc.hip -- scalar-reference GEMM, saxpy and synthetic-input kernels (gfx950).
+#include "device_common.h"
+#include "kernels.h"
+#include "synth.h"
+
+using namespace dnnopt_dev;
+
+namespace dnnopt_hip {
+
+// One thread per output, k ascending, product and sum rounded separately
+// (no fused multiply-add), then alpha*acc + beta*C with C always read: the
+// reference's scalar loop (src/gemm/gemm.cpp:88-100) as compiled for a target
+// without FMA contraction.  Used for GemmAlgo::kNaive.
+__global__ __launch_bounds__(256) void dnnopt_naive_f32(int M, int N, int K, float alpha, const float* A,
+                                                       int lda, const float* B, int ldb, float beta, float* C,
+                                                       int ldc) {
+    const int j = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int i = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (i >= M || j >= N) return;
+    const float* a = A + (size_t)i * lda;
+    float acc = 0.0f;
+    for (int k = 0; k < K; ++k) acc = __fadd_rn(acc, __fmul_rn(a[k], B[(size_t)k * ldb + j]));
+    float* c = C + (size_t)i * ldc + j;
+    *c = __fadd_rn(__fmul_rn(alpha, acc), __fmul_rn(beta, *c));
+}
+
+// Y[i*incy] = fma(alpha, X[i*incx], Y[i*incy])  (src/blas/cblas_saxpy.cpp:17-49
+// computes the same fused update on its NEON path).
+__global__ __launch_bounds__(256) void dnnopt_saxpy(int n, float alpha, const float* x, int incx, float* y,
+                                                   int incy) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < (size_t)n; i += stride) {
+        float* yp = y + i * (size_t)incy;
+        *yp = __builtin_fmaf(alpha, x[i * (size_t)incx], *yp);
+    }
+}
+
+#pragma clang fp contract(off)
+__global__ __launch_bounds__(256) void dnnopt_fill(void* dst, size_t n, int dtype, int dist, uint64_t key,
+                                                  double p0, double p1) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        if (dtype == 2) {
+            static_cast<int8_t*>(dst)[i] = dnnopt_synth::int_value(key, i, (int)p0, (int)p1);
+            continue;
+        }
+        const float v = dist == 1 ? dnnopt_synth::normal_value(key, i, p0, p1)
+                                  : dnnopt_synth::uniform_value(key, i, p0, p1);
+        if (dtype == 0) {
+            static_cast<float*>(dst)[i] = v;
+        } else {
+            static_cast<uint16_t*>(dst)[i] = f32_to_bf16_bits(v);
+        }
+    }
+}
+#pragma clang fp contract(on)
+
+hipError_t launch_naive_f32(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                            float beta, float* C, int ldc, hipStream_t s) {
+    dim3 grid((N + 63) / 64, (M + 3) / 4);
+    hipLaunchKernelGGL(dnnopt_naive_f32, grid, dim3(256), 0, s, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+    return hipGetLastError();
+}
+
+hipError_t launch_saxpy(int n, float alpha, const float* x, int incx, float* y, int incy, hipStream_t s) {
+    int blocks = (n + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(dnnopt_saxpy, dim3(blocks), dim3(256), 0, s, n, alpha, x, incx, y, incy);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill(void* dst, size_t n, int dtype, int dist, uint64_t seed, uint32_t tensor_id, double p0,
+                       double p1, hipStream_t s) {
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(dnnopt_fill, dim3((unsigned)blocks), dim3(256), 0, s, dst, n, dtype, dist,
+                       dnnopt_synth::tensor_key(seed, tensor_id), p0, p1);
+    return hipGetLastError();
+}
+
+}  // namespace dnnopt_hip
+
+namespace dnnopt_hip {
+
+// Reduce k-split partial tiles written as [split][tile][BM*BN] (tile =
+// tile_m * tiles_n + tile_n) into C with the reference epilogue.  Each output
+// is summed by Q threads over interleaved ranges of splits, then the Q
+// partial sums are added in ascending split-range order through LDS, so the
+// order is fixed and the result reproducible.  Used when there are too many
+// k-splits for the last-arriving workgroup to reduce alone.
+__global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restrict__ part, int splits,
+                                                           int tiles_n, int tiles, int bm, int bn, int M, int N,
+                                                           float alpha, float beta, float* C, int ldc) {
+    constexpr int Q = 8, OUTS = 256 / Q;
+    __shared__ float red[Q][OUTS];
+    const int o = threadIdx.x % OUTS, q = threadIdx.x / OUTS;
+    const long long idx = (long long)blockIdx.x * OUTS + o;
+    const bool valid = idx < (long long)M * N;
+    const int m = valid ? (int)(idx / N) : 0, n = valid ? (int)(idx % N) : 0;
+    const int tile_id = (m / bm) * tiles_n + n / bn;
+    const size_t local = (size_t)(m % bm) * bn + (n % bn);
+    const size_t stride = (size_t)tiles * bm * bn;
+    const int s_lo = (int)((long long)splits * q / Q), s_hi = (int)((long long)splits * (q + 1) / Q);
+    float s = 0.0f;
+    if (valid && s_lo < s_hi) {
+        const float* src = part + (size_t)tile_id * bm * bn + local;
+        s = src[(size_t)s_lo * stride];
+        for (int sp = s_lo + 1; sp < s_hi; ++sp) s += src[(size_t)sp * stride];
+    }
+    red[q][o] = s;
+    __syncthreads();
+    if (q != 0 || !valid) return;
+    float t = red[0][o];
+    for (int qq = 1; qq < Q; ++qq)
+        if ((long long)splits * qq / Q < (long long)splits * (qq + 1) / Q) t += red[qq][o];
+    float* c = C + (size_t)m * ldc + n;
+    *c = epilogue(t, alpha, beta, c);
+}
+
+hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
+                                int N, float alpha, float beta, float* C, int ldc, hipStream_t s) {
+    const long long outs = (long long)M * N;
+    const unsigned blocks = (unsigned)((outs + 31) / 32);
+    hipLaunchKernelGGL(dnnopt_splitk_reduce, dim3(blocks), dim3(256), 0, s, part, splits, tiles_n,
+                       tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc);
+    return hipGetLastError();
+}
+
+}  // namespace dnnopt_hip

@@ -1,0 +1,406 @@
+// k_tile.hip -- fp32 and bf16 MFMA tile kernels for M > 8 (gfx950).
+//
+// Replaces the reference's packed BLIS path for these shapes
+// (src/gemm/gemm_driver_generic.cpp:27-248 with the fp32 8x12/8x16 and bf16
+// BFMMLA 8x8 micro-kernels, src/gemm/gemm_driver_bf16.cpp:134-218) and the
+// materialized transposes of cblas_sgemm (src/blas/cblas_sgemm.cpp:80-98):
+// transposed operands are read in place.
+//
+// Matrix-core operand packing (16 x 16 output tile, wave64):
+//   fp32  v_mfma_f32_16x16x4_f32 : lane l gives 1 value,  k = 4*(l/16) + c
+//   bf16  v_mfma_f32_16x16x32_bf16: lane l gives 8 values, k = 8*(l/16) + e
+// with row (A) or column (B) = l % 16.  A loop step covers 64 k (fp32: four
+// groups j of 16 k, each four MFMAs c) or 128 k (bf16: four groups of 32 k).
+// The k assigned to a (lane, register) slot is the same for A and B, so each
+// k meets its partner once.  Output register i of lane l holds row
+// 4*(l/16) + i, column l % 16 of the tile.
+//
+// Accumulation is fp32.  Waves that split k inside a workgroup are combined
+// in ascending k order through LDS, k-split workgroups in ascending split
+// order by the last workgroup to arrive; the result is bit-reproducible.
+//
+// Tails: operand rows/columns outside M/N and k outside K read as zero
+// (out-of-range buffer offsets, and masking inside a partially valid 128-bit
+// chunk), so garbage past an edge never reaches an accumulator.
+#include "device_common.h"
+#include "kernels.h"
+
+using namespace dnnopt_dev;
+
+namespace dnnopt_hip {
+
+namespace {
+
+__device__ __forceinline__ uint32_t clamp_rec(size_t bytes) {
+    return bytes > 0x7FFFFFFFull ? 0x7FFFFFFFu : (uint32_t)bytes;
+}
+
+// Keep the first `valid` 32-bit lanes of v (0..4).
+__device__ __forceinline__ u32x4 keep_dwords(u32x4 v, int valid) {
+    u32x4 r;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) r[d] = d < valid ? v[d] : 0u;
+    return r;
+}
+
+// Keep the first `valid` 16-bit halves of v (0..8).
+__device__ __forceinline__ u32x4 keep_halves(u32x4 v, int valid) {
+    u32x4 r;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const int keep = valid - 2 * d;
+        r[d] = keep >= 2 ? v[d] : (keep == 1 ? (v[d] & 0xFFFFu) : 0u);
+    }
+    return r;
+}
+
+template <int MT, int NT, int WM, int WN, int KW>
+struct TileShape {
+    static constexpr int BM = WM * MT * 16;
+    static constexpr int BN = WN * NT * 16;
+    static constexpr int SUB = MT * NT * 4;
+    static constexpr int RED = (KW > 1 ? (KW - 1) : 1) * WM * WN * SUB * 64;
+};
+
+// Combine k-split waves (LDS) and k-split workgroups (ticket), then apply the
+// epilogue.  Shared by the fp32 and bf16 kernels.
+template <int MT, int NT, int WM, int WN, int KW>
+__device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][NT], float* red,
+                                            int* last_flag, int w, int lane) {
+    using S = TileShape<MT, NT, WM, WN, KW>;
+    const int r = lane & 15, g = lane >> 4;
+    const int wn = w % WN, wm = (w / WN) % WM, wk = w / (WN * WM);
+    if constexpr (KW > 1) {
+        const int slot = wm * WN + wn;
+        if (wk > 0) {
+            float* dst = &red[(((wk - 1) * WM * WN + slot) * S::SUB) * 64];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dst[((mt * NT + nt) * 4 + i) * 64 + lane] = acc[mt][nt][i];
+        }
+        __syncthreads();
+        if (wk == 0) {
+#pragma unroll
+            for (int q = 1; q < KW; ++q) {
+                const float* src = &red[(((q - 1) * WM * WN + slot) * S::SUB) * 64];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[mt][nt][i] += src[((mt * NT + nt) * 4 + i) * 64 + lane];
+            }
+        }
+    }
+
+    const int tile_n = blockIdx.x, tile_m = blockIdx.y, split = blockIdx.z;
+    const int tiles = gridDim.x * gridDim.y;
+    const int tile_id = tile_m * gridDim.x + tile_n;
+    if (p.splits > 1) {
+        if (wk == 0) {
+            float* mine = p.part + ((size_t)split * tiles + tile_id) * (S::BM * S::BN);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int ml = (wm * MT + mt) * 16 + 4 * g + i;
+                        const int nl = (wn * NT + nt) * 16 + r;
+                        mine[ml * S::BN + nl] = acc[mt][nt][i];
+                    }
+        }
+        if (p.defer_reduce) return;
+        if (!split_ticket(&p.tickets[tile_id], (unsigned)p.splits, last_flag)) return;
+        if (wk != 0) return;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int ml = (wm * MT + mt) * 16 + 4 * g + i;
+                    const int nl = (wn * NT + nt) * 16 + r;
+                    const float* src = p.part + (size_t)tile_id * (S::BM * S::BN) + ml * S::BN + nl;
+                    const size_t stride = (size_t)tiles * (S::BM * S::BN);
+                    float s = src[0];
+                    for (int sp = 1; sp < p.splits; ++sp) s += src[sp * stride];
+                    acc[mt][nt][i] = s;
+                }
+    } else if (wk != 0) {
+        return;
+    }
+
+    const int m0 = tile_m * S::BM, n0 = tile_n * S::BN;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m0 + (wm * MT + mt) * 16 + 4 * g + i;
+                const int n = n0 + (wn * NT + nt) * 16 + r;
+                if (m < p.M && n < p.N) {
+                    float* c = p.C + (size_t)m * p.ldc + n;
+                    *c = epilogue(acc[mt][nt][i], p.alpha, p.beta, c);
+                }
+            }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- fp32
+template <int MT, int NT, int WM, int WN, int KW, int TA, int TB>
+__global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_f32(TileArgs p) {
+    using S = TileShape<MT, NT, WM, WN, KW>;
+    constexpr int KB = 64;
+    __shared__ float red[S::RED];
+    __shared__ int last_flag;
+
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+    const int w = wave_id();
+    const int wn = w % WN, wm = (w / WN) % WM, wk = w / (WN * WM);
+    const int m0 = blockIdx.y * S::BM, n0 = blockIdx.x * S::BN;
+
+    const int nblk = (p.K + KB - 1) / KB;
+    const long long chunks = (long long)p.splits * KW;
+    const long long cw = (long long)blockIdx.z * KW + wk;
+    const int b_lo = (int)(((long long)nblk * cw) / chunks);
+    const int b_hi = (int)(((long long)nblk * (cw + 1)) / chunks);
+    const int ks = (int)(((long long)nblk * ((long long)blockIdx.z * KW)) / chunks) * KB;
+
+    const float* A = static_cast<const float*>(p.A);
+    const float* B = static_cast<const float*>(p.B);
+    // Descriptors start at (m0 or n0, ks) of each operand.
+    const float* abase = TA ? A + (size_t)ks * p.lda + m0 : A + (size_t)m0 * p.lda + ks;
+    const size_t arem = TA ? (size_t)(p.K - 1 - ks) * p.lda + (p.M - m0) : (size_t)(p.M - 1 - m0) * p.lda + (p.K - ks);
+    const float* bbase = TB ? B + (size_t)n0 * p.ldb + ks : B + (size_t)ks * p.ldb + n0;
+    const size_t brem = TB ? (size_t)(p.N - 1 - n0) * p.ldb + (p.K - ks) : (size_t)(p.K - 1 - ks) * p.ldb + (p.N - n0);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(abase, clamp_rec(arem * 4));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase, clamp_rec(brem * 4));
+
+    int mloc[MT], nloc[NT];
+    bool mval[MT], nval[NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        mloc[mt] = (wm * MT + mt) * 16 + r;
+        mval[mt] = m0 + mloc[mt] < p.M;
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        nloc[nt] = (wn * NT + nt) * 16 + r;
+        nval[nt] = n0 + nloc[nt] < p.N;
+    }
+
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int blk = b_lo; blk < b_hi; ++blk) {
+        const int kl0 = blk * KB - ks;  // k of this block relative to ks
+        u32x4 a[MT][4], b[NT][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int kq = kl0 + 16 * j + 4 * g;  // first k of this lane's quad (relative)
+            const int kvalid = p.K - (ks + kq);   // how many of the 4 k are < K
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                if constexpr (TA == 0) {
+                    const uint32_t off = (mval[mt] && kvalid > 0) ? ((uint32_t)mloc[mt] * p.lda + kq) * 4u : kOobOffset;
+                    a[mt][j] = buf_load_x4(ra, off);
+                    if (kvalid < 4) a[mt][j] = keep_dwords(a[mt][j], kvalid);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const uint32_t off = (mval[mt] && c < kvalid) ? ((uint32_t)(kq + c) * p.lda + mloc[mt]) * 4u : kOobOffset;
+                        a[mt][j][c] = buf_load_x1(ra, off);
+                    }
+                }
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                if constexpr (TB == 1) {
+                    const uint32_t off = (nval[nt] && kvalid > 0) ? ((uint32_t)nloc[nt] * p.ldb + kq) * 4u : kOobOffset;
+                    b[nt][j] = buf_load_x4(rb, off);
+                    if (kvalid < 4) b[nt][j] = keep_dwords(b[nt][j], kvalid);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const uint32_t off = (nval[nt] && c < kvalid) ? ((uint32_t)(kq + c) * p.ldb + nloc[nt]) * 4u : kOobOffset;
+                        b[nt][j][c] = buf_load_x1(rb, off);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(as_f32(a[mt][j][c]), as_f32(b[nt][j][c]),
+                                                                          acc[mt][nt], 0, 0, 0);
+    }
+
+    tile_finish<MT, NT, WM, WN, KW>(p, acc, red, &last_flag, w, lane);
+}
+
+// ---------------------------------------------------------------- bf16
+// MODE kTileBF16: A, B hold bf16 bit patterns.  MODE kTileF2B: A, B are fp32
+// and are rounded to bf16 (nearest even, reference formula) on load.
+template <int MT, int NT, int WM, int WN, int KW, int MODE>
+__global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) {
+    using S = TileShape<MT, NT, WM, WN, KW>;
+    constexpr int KB = 128;
+    constexpr int ES = MODE == kTileBF16 ? 2 : 4;
+    __shared__ float red[S::RED];
+    __shared__ int last_flag;
+
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+    const int w = wave_id();
+    const int wn = w % WN, wm = (w / WN) % WM, wk = w / (WN * WM);
+    const int m0 = blockIdx.y * S::BM, n0 = blockIdx.x * S::BN;
+
+    const int nblk = (p.K + KB - 1) / KB;
+    const long long chunks = (long long)p.splits * KW;
+    const long long cw = (long long)blockIdx.z * KW + wk;
+    const int b_lo = (int)(((long long)nblk * cw) / chunks);
+    const int b_hi = (int)(((long long)nblk * (cw + 1)) / chunks);
+    const int ks = (int)(((long long)nblk * ((long long)blockIdx.z * KW)) / chunks) * KB;
+
+    const char* A = static_cast<const char*>(p.A);
+    const char* B = static_cast<const char*>(p.B);
+    const char* abase = A + ((size_t)m0 * p.lda + ks) * ES;
+    const size_t arem = (size_t)(p.M - 1 - m0) * p.lda + (p.K - ks);
+    const char* bbase = B + ((size_t)ks * p.ldb + n0) * ES;
+    const size_t brem = (size_t)(p.K - 1 - ks) * p.ldb + (p.N - n0);
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(abase, clamp_rec(arem * ES));
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase, clamp_rec(brem * ES));
+
+    int mloc[MT], nloc[NT];
+    bool mval[MT], nval[NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        mloc[mt] = (wm * MT + mt) * 16 + r;
+        mval[mt] = m0 + mloc[mt] < p.M;
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        nloc[nt] = (wn * NT + nt) * 16 + r;
+        nval[nt] = n0 + nloc[nt] < p.N;
+    }
+
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int blk = b_lo; blk < b_hi; ++blk) {
+        const int kl0 = blk * KB - ks;
+        u32x4 a[MT][4], b[NT][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ko = kl0 + 32 * j + 8 * g;  // first of this lane's 8 k (relative)
+            const int kvalid = p.K - (ks + ko);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                if constexpr (MODE == kTileBF16) {
+                    const uint32_t off = (mval[mt] && kvalid > 0) ? ((uint32_t)mloc[mt] * p.lda + ko) * 2u : kOobOffset;
+                    a[mt][j] = buf_load_x4(ra, off);
+                    if (kvalid < 8) a[mt][j] = keep_halves(a[mt][j], kvalid);
+                } else {
+                    const uint32_t off = (mval[mt] && kvalid > 0) ? ((uint32_t)mloc[mt] * p.lda + ko) * 4u : kOobOffset;
+                    u32x4 lo = buf_load_x4(ra, off);
+                    u32x4 hi = buf_load_x4(ra, (mval[mt] && kvalid > 4) ? off + 16u : kOobOffset);
+                    if (kvalid < 4) lo = keep_dwords(lo, kvalid);
+                    if (kvalid < 8) hi = keep_dwords(hi, kvalid - 4);
+#pragma unroll
+                    for (int d = 0; d < 2; ++d) {
+                        a[mt][j][d] = (uint32_t)f32_to_bf16_bits(as_f32(lo[2 * d])) |
+                                      ((uint32_t)f32_to_bf16_bits(as_f32(lo[2 * d + 1])) << 16);
+                        a[mt][j][d + 2] = (uint32_t)f32_to_bf16_bits(as_f32(hi[2 * d])) |
+                                          ((uint32_t)f32_to_bf16_bits(as_f32(hi[2 * d + 1])) << 16);
+                    }
+                }
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                uint32_t h[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t off = (nval[nt] && e < kvalid) ? ((uint32_t)(ko + e) * p.ldb + nloc[nt]) * ES : kOobOffset;
+                    if constexpr (MODE == kTileBF16) {
+                        h[e] = buf_load_u16(rb, off);
+                    } else {
+                        h[e] = f32_to_bf16_bits(as_f32(buf_load_x1(rb, off)));
+                    }
+                }
+#pragma unroll
+                for (int d = 0; d < 4; ++d) b[nt][j][d] = h[2 * d] | (h[2 * d + 1] << 16);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[mt][j]),
+                                                                         __builtin_bit_cast(bf16x8, b[nt][j]),
+                                                                         acc[mt][nt], 0, 0, 0);
+    }
+
+    tile_finish<MT, NT, WM, WN, KW>(p, acc, red, &last_flag, w, lane);
+}
+
+// ---------------------------------------------------------------- launch table
+// {MT, NT, WM, WN, KW}
+static const TileConfig kTileConfigs[] = {
+    {1, 1, 4, 1, 1},  // 0: 64 x 16   tall-skinny, narrow N
+    {1, 4, 4, 1, 1},  // 1: 64 x 64   tall-skinny, N = 64
+    {2, 2, 2, 2, 1},  // 2: 64 x 64   general / split-k
+    {2, 2, 2, 2, 2},  // 3: 64 x 64   k split over 2 waves
+    {2, 4, 2, 2, 1},  // 4: 64 x 128
+};
+
+int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
+TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
+
+#define DNNOPT_TILE_CASE(IDX, MT, NT, WM, WN, KW)                                                        \
+    case IDX:                                                                                            \
+        if (mode == kTileF32) {                                                                          \
+            if (!ta && !tb) hipLaunchKernelGGL((dnnopt_tile_f32<MT, NT, WM, WN, KW, 0, 0>), grid, blk, 0, s, a); \
+            else if (ta && !tb) hipLaunchKernelGGL((dnnopt_tile_f32<MT, NT, WM, WN, KW, 1, 0>), grid, blk, 0, s, a); \
+            else if (!ta && tb) hipLaunchKernelGGL((dnnopt_tile_f32<MT, NT, WM, WN, KW, 0, 1>), grid, blk, 0, s, a); \
+            else hipLaunchKernelGGL((dnnopt_tile_f32<MT, NT, WM, WN, KW, 1, 1>), grid, blk, 0, s, a);    \
+        } else if (mode == kTileBF16) {                                                                  \
+            hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileBF16>), grid, blk, 0, s, a);    \
+        } else {                                                                                         \
+            hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileF2B>), grid, blk, 0, s, a);     \
+        }                                                                                                \
+        break;
+
+hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, dim3 grid, const TileArgs& a, hipStream_t s) {
+    if (mode != kTileF32 && (ta || tb)) return hipErrorInvalidValue;
+    const TileConfig c = kTileConfigs[cfg_idx];
+    const dim3 blk(c.wm * c.wn * c.kw * 64);
+    switch (cfg_idx) {
+        DNNOPT_TILE_CASE(0, 1, 1, 4, 1, 1)
+        DNNOPT_TILE_CASE(1, 1, 4, 4, 1, 1)
+        DNNOPT_TILE_CASE(2, 2, 2, 2, 2, 1)
+        DNNOPT_TILE_CASE(3, 2, 2, 2, 2, 2)
+        DNNOPT_TILE_CASE(4, 2, 4, 2, 2, 1)
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace dnnopt_hip

@@ -1,0 +1,122 @@
+// kernels.h -- argument blocks and launch wrappers of the gfx950 kernels.
+//
+// Host code (dispatch.cpp, capi.cpp) fills these structs and calls the
+// launch_* wrappers; each wrapper maps its configuration onto one template
+// instantiation and enqueues it on the given stream.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dnnopt_hip {
+
+// ---------------------------------------------------------------- skinny
+// M <= 8 rows against a row-major K x N operand B that is streamed once.
+// Workgroup (x, y) = (column tile, k-split); its NW waves split the k-range
+// of the workgroup and are reduced through LDS; split groups are reduced by
+// the last workgroup to arrive (ticket) in split order.
+enum SkinnyMode {
+    kSkinnyF32 = 0,   // A, B fp32
+    kSkinnyBF16 = 1,  // A, B bf16 storage
+    kSkinnyF2B = 2,   // A, B fp32 rounded to bf16 in registers
+};
+
+struct SkinnyArgs {
+    const void* A;
+    const void* B;
+    float* C;
+    float* part;        // [splits][M][ncols_pad] partial sums (splits > 1)
+    unsigned* tickets;  // one per column tile (splits > 1)
+    int a_sm, a_sk;     // element strides of A over m and over k (lda,1 or 1,lda)
+    int ldb, ldc;
+    int M, N, K;
+    float alpha, beta;
+    int splits;
+    int ncols_pad;
+};
+
+constexpr int kSkinnyUnroll = 8;
+inline int skinny_tile_cols(int mode) { return mode == kSkinnyBF16 ? 512 : 256; }
+inline int skinny_elem_bytes(int mode) { return mode == kSkinnyBF16 ? 2 : 4; }
+
+hipError_t launch_skinny(int mode, int mr, int nw, dim3 grid, const SkinnyArgs& a,
+                         hipStream_t s);
+
+// ---------------------------------------------------------------- int8 MFMA
+// Exact s8 x s8 -> s32 with B stored N x K.  Each wave owns MT x NT tiles of
+// 16 x 16 outputs (v_mfma_i32_16x16x64_i8); a workgroup is WM x WN x KW waves
+// (KW waves split k and are reduced through LDS); grid.z splits k across
+// workgroups with a ticket reduction.
+struct S8Args {
+    const int8_t* A;
+    const int8_t* B;
+    void* C;             // int32_t* (EPI 0) or float* (EPI 1)
+    const float* scale;  // per-column scale (EPI 1)
+    int32_t* part;       // [splits][tiles][BM*BN]
+    unsigned* tickets;   // one per output tile
+    int lda, ldb, ldc;
+    int M, N, K;
+    int splits;
+};
+
+struct S8Config {
+    int mt, nt, wm, wn, kw;
+};
+// Index into the table of built int8 configurations.
+int s8_config_count();
+S8Config s8_config(int idx);
+hipError_t launch_mfma_s8(int cfg_idx, int epi, dim3 grid, const S8Args& a, hipStream_t s);
+
+// ---------------------------------------------------------------- fp32 / bf16 tiles
+// Row-major C (M x N) = alpha * op(A) op(B) + beta * C with MFMA tiles.
+// Operand element type per mode: fp32 (v_mfma_f32_16x16x4_f32), bf16 storage
+// or fp32 rounded to bf16 (v_mfma_f32_16x16x32_bf16).
+enum TileMode {
+    kTileF32 = 0,
+    kTileBF16 = 1,
+    kTileF2B = 2,
+};
+
+struct TileArgs {
+    const void* A;
+    const void* B;
+    float* C;
+    float* part;        // [splits][tiles][BM*BN]
+    unsigned* tickets;  // one per output tile
+    int lda, ldb, ldc;
+    int M, N, K;
+    float alpha, beta;
+    int transA, transB;
+    int splits;
+    int defer_reduce;   // splits > 1: 1 = only store partials (a reduce kernel follows)
+};
+
+struct TileConfig {
+    int mt, nt, wm, wn, kw;
+};
+int tile_config_count();
+TileConfig tile_config(int idx);
+hipError_t launch_tile(int mode, int cfg_idx, int transA, int transB, dim3 grid,
+                       const TileArgs& a, hipStream_t s);
+
+// ---------------------------------------------------------------- small kernels
+hipError_t launch_naive_f32(int M, int N, int K, float alpha, const float* A, int lda,
+                            const float* B, int ldb, float beta, float* C, int ldc,
+                            hipStream_t s);
+hipError_t launch_saxpy(int n, float alpha, const float* x, int incx, float* y, int incy,
+                        hipStream_t s);
+hipError_t launch_fill(void* dst, size_t n, int dtype, int dist, uint64_t seed,
+                       uint32_t tensor_id, double p0, double p1, hipStream_t s);
+// fp32-API int8: zero the two absmax words, reduce max|A| and max|B|, quantize
+// A (M x K) and B (K x N, written transposed as N x K), then after the int8
+// GEMM dequantize the int32 accumulators into C.
+hipError_t launch_quant_prepare(const float* A, int lda, const float* B, int ldb, int M, int N, int K,
+                                unsigned* amax, int8_t* qA, int8_t* qB, hipStream_t s);
+hipError_t launch_dequant(const int32_t* acc, int M, int N, const unsigned* amax, float alpha,
+                          float beta, float* C, int ldc, hipStream_t s);
+// Reduce partial tiles [splits][tiles_m*tiles_n][bm*bn] into C (epilogue applied).
+hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm,
+                                int bn, int M, int N, float alpha, float beta, float* C, int ldc,
+                                hipStream_t s);
+
+}  // namespace dnnopt_hip

@@ -1,0 +1,170 @@
+#ifndef DNNOPT_HIP_H
+#define DNNOPT_HIP_H
+/*
+ * dnnopt_hip.h -- C-ABI boundary of the gfx950 small/irregular-shape GEMM path.
+ *
+ * These are the entry points a foreign-function binding (ctypes, cgo, JNI,
+ * a oneDNN hook) calls.  Every function takes plain pointers and sizes and
+ * returns a status code; nothing in a signature is a HIP or PyTorch type.
+ *
+ * Conventions shared by every GEMM entry point:
+ *   - row-major storage, ld* = row stride in elements;
+ *   - A, B, C (and col_scale) are DEVICE pointers; the work is enqueued on
+ *     `stream` (a hipStream_t passed as void*, NULL = the null stream) and
+ *     the call returns without waiting;
+ *   - M <= 0, N <= 0 or K <= 0 is a successful no-op that does not touch C
+ *     (reference: src/gemm/gemm.cpp:180);
+ *   - beta == 0 never reads C;
+ *   - a non-zero status means nothing was enqueued and C is untouched;
+ *   - results are deterministic: the same call on the same inputs gives the
+ *     same bits every time (fixed reduction order, no floating atomics).
+ *
+ * The synchronous host-pointer API of the reference (dnnopt::gemm_* in
+ * dnnopt/gemm/gemm.h, cblas_sgemm in dnnopt/blas/cblas.h) is implemented on
+ * top of these functions in the same shared library.
+ */
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define DNNOPT_OK                0
+#define DNNOPT_ERR_INVALID_ARG   1  /* bad size, stride, flag or NULL pointer */
+#define DNNOPT_ERR_NO_DEVICE     2  /* no HIP device visible                  */
+#define DNNOPT_ERR_HIP           3  /* a HIP runtime call failed               */
+#define DNNOPT_ERR_UNSUPPORTED   4  /* shape/option outside what is built      */
+#define DNNOPT_ERR_OUT_OF_MEMORY 5  /* workspace or staging allocation failed  */
+
+/* operand transpose flags for dnnopt_hip_sgemm */
+#define DNNOPT_OP_N 0
+#define DNNOPT_OP_T 1
+
+/* ---- GEMM entry points (device pointers, stream-ordered) --------------- */
+
+/* fp32: C = alpha * op(A) * op(B) + beta * C.  op(A) is M x K, op(B) is K x N.
+ * With transA, A is stored K x M (lda >= M); with transB, B is stored N x K
+ * (ldb >= K).  Epilogue as the reference kernels: beta == 0 gives
+ * alpha*acc, otherwise fma(alpha, acc, beta*C).
+ * Replaces dnnopt::gemm_fp32 (src/gemm/gemm.cpp:168-377) and the transposed
+ * cases of cblas_sgemm (src/blas/cblas_sgemm.cpp:67-99), which the
+ * reference materializes as temporaries. */
+int dnnopt_hip_sgemm(int transA, int transB, int M, int N, int K,
+                     float alpha, const float* A, int lda,
+                     const float* B, int ldb,
+                     float beta, float* C, int ldc, void* stream);
+
+/* fp32 scalar reference: one output per thread, k ascending, separate
+ * multiply and add roundings, then alpha*acc + beta*C -- bit-identical to
+ * the reference's naive loop.  Serves GemmAlgo::kNaive
+ * (src/gemm/gemm.cpp:88-100, 182-185). */
+int dnnopt_hip_sgemm_naive(int M, int N, int K,
+                           float alpha, const float* A, int lda,
+                           const float* B, int ldb,
+                           float beta, float* C, int ldc, void* stream);
+
+/* bf16 storage (raw bf16 bit patterns), fp32 accumulation, fp32 C.
+ * Replaces dnnopt::gemm_bf16_bf16bf16f32 (src/gemm/gemm_driver_bf16.cpp:134). */
+int dnnopt_hip_gemm_bf16(int M, int N, int K,
+                         float alpha, const uint16_t* A, int lda,
+                         const uint16_t* B, int ldb,
+                         float beta, float* C, int ldc, void* stream);
+
+/* fp32 storage, both operands rounded to bf16 (nearest even) in registers,
+ * fp32 accumulation.  Replaces dnnopt::gemm_bf16 (src/gemm/gemm.cpp:379-416). */
+int dnnopt_hip_gemm_bf16_f32in(int M, int N, int K,
+                               float alpha, const float* A, int lda,
+                               const float* B, int ldb,
+                               float beta, float* C, int ldc, void* stream);
+
+/* Exact int8 x int8 -> int32, C overwritten.  B is N x K (K contiguous).
+ * Replaces dnnopt::gemm_int8_int8int8int32
+ * (src/gemm/gemm_int8_native.cpp:189-248). */
+int dnnopt_hip_gemm_s8s8s32(int M, int N, int K,
+                            const int8_t* A, int lda,
+                            const int8_t* B, int ldb,
+                            int32_t* C, int ldc, void* stream);
+
+/* Same contraction with a per-column dequantization epilogue:
+ * C[i][j] = (float)acc[i][j] * col_scale[j] (one rounding for the int->float
+ * conversion, one for the multiply).  The reference has no per-column scale;
+ * its caller applies a per-tensor scale the same way
+ * (src/conv/conv3d.cpp:511-514). */
+int dnnopt_hip_gemm_s8s8f32_colscale(int M, int N, int K,
+                                     const int8_t* A, int lda,
+                                     const int8_t* B, int ldb,
+                                     const float* col_scale,
+                                     float* C, int ldc, void* stream);
+
+/* fp32 storage, dynamic symmetric per-tensor int8 quantization (scale =
+ * max|X|/127, or 1 for an all-zero operand; round to nearest even; clamp to
+ * [-128, 127]), exact int32 contraction, then
+ * C = alpha*sA*sB*acc (beta == 0) or fma(alpha*sA*sB, acc, beta*C).
+ * Replaces dnnopt::gemm_int8 (src/gemm/gemm.cpp:418-455 with the packed-path
+ * quantization of src/gemm/gemm_driver_generic.cpp:49-67). */
+int dnnopt_hip_gemm_int8_f32(int M, int N, int K,
+                             float alpha, const float* A, int lda,
+                             const float* B, int ldb,
+                             float beta, float* C, int ldc, void* stream);
+
+/* Y = alpha * X + Y (strided).  Replaces cblas_saxpy
+ * (src/blas/cblas_saxpy.cpp:13-51): N <= 0 or alpha == 0 is a no-op. */
+int dnnopt_hip_saxpy(int N, float alpha, const float* X, int incX,
+                     float* Y, int incY, void* stream);
+
+/* ---- planning (host only; needs no device) ----------------------------- */
+
+/* Kernel families chosen by the dispatcher. */
+#define DNNOPT_K_NONE        0
+#define DNNOPT_K_SKINNY_F32  1  /* M <= 8, fp32 B streamed once             */
+#define DNNOPT_K_SKINNY_BF16 2  /* M <= 8, bf16 B streamed once             */
+#define DNNOPT_K_SKINNY_F2B  3  /* M <= 8, fp32 B rounded to bf16 in regs   */
+#define DNNOPT_K_MFMA_S8     4  /* int8 MFMA tiles, B as N x K              */
+#define DNNOPT_K_TILE_F32    5  /* fp32 MFMA tiles (tall-skinny, split-K)   */
+#define DNNOPT_K_TILE_BF16   6  /* bf16 MFMA tiles                          */
+#define DNNOPT_K_NAIVE_F32   7  /* scalar reference kernel                  */
+
+typedef struct dnnopt_plan {
+    int kernel;             /* DNNOPT_K_* */
+    int rows;               /* M rows handled per workgroup tile          */
+    int cols;               /* N columns handled per workgroup tile       */
+    int splits;             /* split-K factor (1 = none)                  */
+    int grid_x, grid_y, grid_z;
+    int block;              /* threads per workgroup                      */
+    size_t workspace_bytes; /* device scratch needed (partials+tickets)   */
+    char name[64];          /* kernel symbol prefix, as rocprof lists it  */
+} dnnopt_plan;
+
+int dnnopt_hip_plan_sgemm(int transA, int transB, int M, int N, int K,
+                          dnnopt_plan* out);
+int dnnopt_hip_plan_gemm_bf16(int fp32_inputs, int M, int N, int K,
+                              dnnopt_plan* out);
+int dnnopt_hip_plan_gemm_s8(int with_scale, int M, int N, int K,
+                            dnnopt_plan* out);
+
+/* ---- synthetic inputs on the device ------------------------------------
+ * Counter-based SplitMix64: element i of tensor `tensor_id` under `seed`
+ * is a pure function of (seed, tensor_id, i), so any slice can be
+ * regenerated on the host.
+ *   dtype: 0 = fp32, 1 = bf16 (fp32 value rounded to nearest even), 2 = int8
+ *   dist : 0 = uniform [p0, p1), 1 = normal(mean p0, sigma p1),
+ *          2 = uniform integers in [p0, p1] (int8 only)                   */
+int dnnopt_hip_fill(void* dst, size_t n, int dtype, int dist,
+                    uint64_t seed, uint32_t tensor_id,
+                    double p0, double p1, void* stream);
+
+/* ---- status and device queries ---------------------------------------- */
+const char* dnnopt_hip_status_string(int status);
+int dnnopt_hip_last_status(void);     /* last failure of the C++/cblas API on
+                                         this thread, DNNOPT_OK if none      */
+int dnnopt_hip_device_count(void);    /* 0 when no device is visible        */
+int dnnopt_hip_abi_version(void);     /* bumped on any signature change     */
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DNNOPT_HIP_H */

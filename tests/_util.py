@@ -1,0 +1,179 @@
+"""Shared helpers of the test suite: library/oracle loading, synthetic inputs,
+tolerances.
+
+Tolerances (stated once, used everywhere):
+
+* fp32 and bf16 kernels accumulate in fp32.  For any summation order the
+  forward error of a K-term sum is at most gamma_K * sum|a_k b_k| with
+  gamma_K ~= K * 2^-24; the epilogue adds at most two more roundings.  A
+  result passes when, element-wise,
+      |C - C_exact| <= (2K + 4) * 2^-24 * (|alpha| * S + |beta * C0|)
+  with S = |A| @ |B| computed in fp64 and C_exact the fp64 product (on the
+  bf16-rounded operands for bf16).  This is tighter than the 1e-5 * K scaled
+  bound the path is specified with (2 * 2^-24 = 1.2e-7 < 1e-5).
+* bf16 against the unrounded fp32 inputs: |C - C_exact| <= 1e-2 * (|alpha| S
+  + |beta C0|)  (bf16 rounding of both operands costs at most 2^-7 relative
+  per product).
+* int8: bit-exact.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import importlib.util
+import os
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libref.so")
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+U = 2.0 ** -24
+
+_bind = None
+
+
+def binding():
+    global _bind
+    if _bind is None:
+        path = os.path.join(ROOT, "dnn-opt_amd", "python", "dnnopt_hip.py")
+        spec = importlib.util.spec_from_file_location("dnnopt_hip", path)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _bind = mod
+    return _bind
+
+
+def load_lib():
+    return binding().load()
+
+
+P = ctypes.c_void_p
+I = ctypes.c_int
+F = ctypes.c_float
+
+ORACLE_ABI = {
+    "orc_mix64": (ctypes.c_uint64, [ctypes.c_uint64]),
+    "orc_splitmix64": (None, [ctypes.c_uint64, P, ctypes.c_size_t]),
+    "orc_tensor_key": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint32]),
+    "orc_fill_uniform_f32": (None, [P, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_double,
+                                    ctypes.c_double]),
+    "orc_fill_normal_f32": (None, [P, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_double,
+                                   ctypes.c_double]),
+    "orc_fill_int8": (None, [P, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_uint32, I, I]),
+    "orc_bf16_rne": (ctypes.c_uint16, [F]),
+    "orc_bf16_to_f32": (F, [ctypes.c_uint16]),
+    "orc_round_bf16": (None, [P, P, ctypes.c_size_t]),
+    "orc_gemm_naive_f32": (None, [I, I, I, F, P, I, P, I, F, P, I]),
+    "orc_gemv_1xn_f32": (None, [I, I, F, P, P, I, F, P]),
+    "orc_smallm_wide_f32": (None, [I, I, I, F, P, I, P, I, F, P, I]),
+    "orc_adaptive_f32": (None, [I, I, I, F, P, I, P, I, F, P, I, I, I, I]),
+    "orc_gemm_f32_smallm": (I, [I, I, I, F, P, I, P, I, F, P, I, I]),
+    "orc_gemm_s8s8s32": (None, [I, I, I, P, I, P, I, P, I]),
+    "orc_gemm_s8_colscale": (None, [I, I, I, P, I, P, I, P, P, I]),
+    "orc_gemm_bf16": (None, [I, I, I, F, P, I, P, I, F, P, I]),
+    "orc_gemm_int8_dynq": (None, [I, I, I, F, P, I, P, I, F, P, I]),
+    "orc_cblas_sgemm": (None, [I, I, I, I, I, I, F, P, I, P, I, F, P, I]),
+    "orc_saxpy": (None, [I, F, P, I, P, I, I]),
+    "orc_max_threads": (I, []),
+}
+
+REF_ABI = {
+    "ref_bf16_round": (ctypes.c_uint16, [F]),
+    "ref_bf16_widen": (F, [ctypes.c_uint16]),
+    "ref_gemm_naive_f32": (None, [I, I, I, F, P, I, P, I, F, P, I]),
+    "ref_gemm_s8s8s32": (None, [I, I, I, P, I, P, I, P, I]),
+    "ref_saxpy": (None, [I, F, P, I, P, I]),
+}
+
+
+def _bind_table(so, table):
+    for name, (res, args) in table.items():
+        fn = getattr(so, name)
+        fn.restype = res
+        fn.argtypes = args
+    return so
+
+
+def load_oracle():
+    if not os.path.exists(ORACLE_SO):
+        raise FileNotFoundError(f"{ORACLE_SO} missing: run __graft_entry__.build()")
+    return _bind_table(ctypes.CDLL(ORACLE_SO), ORACLE_ABI)
+
+
+def load_ref():
+    if not os.path.exists(REF_SO):
+        return None
+    # Lazy binding: the AArch64-only paths of the reference stay unresolved
+    # and are never called.
+    return _bind_table(ctypes.CDLL(REF_SO, mode=os.RTLD_LAZY), REF_ABI)
+
+
+def ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ---------------------------------------------------------------- inputs
+SEED = 42
+TID_A, TID_B, TID_C, TID_SCALE = 1, 2, 3, 4
+
+
+def uniform(orc, n, tid, lo=-1.0, hi=1.0, seed=SEED):
+    out = np.empty(n, np.float32)
+    orc.orc_fill_uniform_f32(ptr(out), n, seed, tid, lo, hi)
+    return out
+
+
+def normal(orc, n, tid, mu=0.0, sigma=1.0, seed=SEED):
+    out = np.empty(n, np.float32)
+    orc.orc_fill_normal_f32(ptr(out), n, seed, tid, mu, sigma)
+    return out
+
+
+def ints8(orc, n, tid, lo=-127, hi=127, seed=SEED):
+    out = np.empty(n, np.int8)
+    orc.orc_fill_int8(ptr(out), n, seed, tid, lo, hi)
+    return out
+
+
+def bf16_bits(orc, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    orc.orc_round_bf16(ptr(x), ptr(out), x.size)
+    return out
+
+
+def bf16_value(bits: np.ndarray) -> np.ndarray:
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+# ---------------------------------------------------------------- reference maths
+def exact(A, B, alpha=1.0, beta=0.0, C0=None):
+    """fp64 alpha*A@B + beta*C0 and the error scale |alpha| |A|@|B| + |beta C0|."""
+    A64, B64 = A.astype(np.float64), B.astype(np.float64)
+    prod = A64 @ B64
+    scale = abs(alpha) * (np.abs(A64) @ np.abs(B64))
+    val = alpha * prod
+    if beta != 0.0 and C0 is not None:
+        val = val + beta * C0.astype(np.float64)
+        scale = scale + abs(beta) * np.abs(C0.astype(np.float64))
+    return val, scale
+
+
+def fp32_tol(K, scale):
+    return (2 * K + 4) * U * scale + 1e-30
+
+
+def assert_fp32_close(got, want, scale, K, what=""):
+    got = np.asarray(got, np.float64)
+    tol = fp32_tol(K, scale)
+    err = np.abs(got - want)
+    bad = ~(err <= tol)
+    if bad.any():
+        idx = np.unravel_index(np.argmax(np.where(bad, err / np.maximum(tol, 1e-300), 0)), err.shape)
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {err.size} outside (2K+4)u*scale; worst at {idx}: "
+            f"got {got[idx]!r} want {want[idx]!r} tol {tol[idx]!r}"
+        )
+    return float((err / np.maximum(scale, 1e-300)).max())

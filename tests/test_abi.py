@@ -1,0 +1,167 @@
+"""C-ABI library checks that need no GPU: it loads, it exports every symbol the
+headers declare, the dispatcher's plans are sane, and argument/no-device
+errors come back as status codes with C untouched."""
+
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import _util as u
+
+INCLUDE = os.path.join(u.ROOT, "include")
+
+
+def _c_functions(header):
+    text = open(header).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    names = re.findall(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\([^;{)]*(?:\([^)]*\)[^;{)]*)*\)\s*;", text)
+    skip = {"if", "for", "while", "return", "sizeof", "switch"}
+    return sorted({n for n in names if n not in skip})
+
+
+def _exports(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True)
+    return {line.split()[-1] for line in out.stdout.splitlines() if line.strip()}
+
+
+def test_library_loads(lib):
+    assert lib.so.dnnopt_hip_abi_version() == 1
+
+
+def test_every_c_declaration_is_exported(lib):
+    exported = _exports(lib.path)
+    declared = _c_functions(os.path.join(INCLUDE, "dnnopt_hip.h")) + _c_functions(
+        os.path.join(INCLUDE, "dnnopt", "blas", "cblas.h"))
+    assert declared, "header parse found nothing"
+    missing = [n for n in declared if n not in exported]
+    assert not missing, missing
+    b = u.binding()
+    assert set(declared) == set(b.C_ABI) | set(b.BLAS_ABI)
+
+
+def test_every_cxx_declaration_is_exported(lib):
+    exported = _exports(lib.path)
+    b = u.binding()
+    for key, (sym, _, _) in b.CXX_ABI.items():
+        assert sym in exported, key
+    # every dnnopt:: function of the C++ headers has a binding entry
+    for hdr in ("gemm/gemm.h", "aligned_alloc.h"):
+        names = set(re.findall(r"^\s*(?:void\*?|int)\s+(\w+)\s*\(", open(os.path.join(INCLUDE, "dnnopt", hdr)).read(),
+                               re.M))
+        for n in names - {"operator"}:
+            assert any(k == n or k.startswith(n + "_") for k in b.CXX_ABI), n
+    # nothing internal leaks out of the library
+    leaked = [s for s in exported if "dnnopt_hip" in s and s.startswith("_Z")]
+    assert not leaked, leaked
+
+
+def test_status_strings(lib):
+    b = u.binding()
+    for st in range(6):
+        assert lib.so.dnnopt_hip_status_string(st)
+    assert lib.so.dnnopt_hip_status_string(b.ERR_NO_DEVICE) == b"no HIP device visible"
+
+
+# ---------------------------------------------------------------- dispatcher
+def test_plans_for_the_configs(lib):
+    b = u.binding()
+    p = lib.plan_sgemm(1, 4096, 4096)
+    assert p["kernel"] == b.K_SKINNY_F32 and p["rows"] == 1 and p["splits"] >= 1
+    # enough waves for a 256-CU part
+    assert p["grid_x"] * p["grid_y"] * p["block"] // 64 >= 1024
+    for M in (2, 3, 5, 7):
+        for N in (1009, 4099, 11003):
+            p = lib.plan_sgemm(M, N, 2048)
+            assert p["kernel"] == b.K_SKINNY_F32 and p["rows"] == M
+            assert p["grid_x"] == -(-N // 256)
+    assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TILE_F32
+    p = lib.plan_sgemm(64, 64, 262144, transA=1)
+    assert p["kernel"] == b.K_TILE_F32 and p["splits"] > 16
+    for M in (1, 4):
+        assert lib.plan_bf16(M, 11008, 4096)["kernel"] == b.K_SKINNY_BF16
+        assert lib.plan_bf16(M, 11008, 4096, fp32_inputs=1)["kernel"] == b.K_SKINNY_F2B
+    for M in (32, 256):
+        assert lib.plan_bf16(M, 11008, 4096)["kernel"] == b.K_TILE_BF16
+    for M in (1, 8, 128):
+        for N in (4096, 4093):
+            p = lib.plan_s8(M, N, 4096)
+            assert p["kernel"] == b.K_MFMA_S8 and p["rows"] >= min(M, 16)
+
+
+def test_plan_split_never_exceeds_k(lib):
+    for K in (1, 7, 64, 65, 1000):
+        for M in (1, 7):
+            p = lib.plan_sgemm(M, 4096, K)
+            assert p["splits"] <= max(1, K)
+        p = lib.plan_sgemm(64, 64, K)
+        assert p["splits"] <= max(1, -(-K // 64))
+
+
+def test_plan_rejects_bad_args(lib):
+    b = u.binding()
+    with pytest.raises(b.DnnoptError):
+        lib.plan_sgemm(0, 4, 4)
+    with pytest.raises(b.DnnoptError):
+        lib.plan_sgemm(4, 4, 4, transA=2)
+
+
+# ---------------------------------------------------------------- no-device behaviour
+no_device = pytest.mark.skipif(u.load_lib().device_count() > 0, reason="a device is visible")
+
+
+@no_device
+def test_c_abi_without_device(lib):
+    b = u.binding()
+    A = np.ones(16, np.float32)
+    C = np.full(16, 7.0, np.float32)
+    st = lib.so.dnnopt_hip_sgemm(0, 0, 4, 4, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 4, 0.0, C.ctypes.data, 4,
+                                 None)
+    assert st == b.ERR_NO_DEVICE
+    assert (C == 7.0).all()
+    # empty problems succeed without touching anything
+    assert lib.so.dnnopt_hip_sgemm(0, 0, 0, 4, 4, 1.0, None, 4, None, 4, 0.0, None, 4, None) == b.OK
+    assert lib.so.dnnopt_hip_gemm_s8s8s32(4, 4, 0, None, 4, None, 4, None, 4, None) == b.OK
+    # invalid arguments are reported before the device is needed
+    assert lib.so.dnnopt_hip_sgemm(0, 0, 4, 4, 4, 1.0, A.ctypes.data, 3, A.ctypes.data, 4, 0.0, C.ctypes.data, 4,
+                                   None) == b.ERR_INVALID_ARG
+    assert lib.so.dnnopt_hip_sgemm(3, 0, 4, 4, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 4, 0.0, C.ctypes.data, 4,
+                                   None) == b.ERR_INVALID_ARG
+    assert lib.so.dnnopt_hip_fill(C.ctypes.data, 16, 2, 0, 1, 1, 0.0, 1.0, None) == b.ERR_INVALID_ARG
+
+
+@no_device
+def test_cxx_and_cblas_api_without_device(lib):
+    b = u.binding()
+    A = np.ones(16, np.float32)
+    C = np.full(16, 7.0, np.float32)
+    lib.cxx["gemm_fp32"](4, 4, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 4, 0.0, C.ctypes.data, 4)
+    assert lib.last_status() == b.ERR_NO_DEVICE and (C == 7.0).all()
+    lib.cxx["gemm_fp32"](0, 4, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 4, 0.0, C.ctypes.data, 4)
+    assert lib.last_status() == b.OK
+    lib.so.cblas_sgemm(102, 112, 111, 4, 4, 4, 1.0, A.ctypes.data, 4, A.ctypes.data, 4, 0.0, C.ctypes.data, 4)
+    assert lib.last_status() == b.ERR_NO_DEVICE and (C == 7.0).all()
+    # alpha == 0 and beta == 1 returns before anything (cblas_sgemm.cpp:115)
+    lib.so.cblas_sgemm(101, 111, 111, 4, 4, 4, 0.0, A.ctypes.data, 4, A.ctypes.data, 4, 1.0, C.ctypes.data, 4)
+    assert (C == 7.0).all()
+
+
+def test_thread_setters_round_trip(lib):
+    lib.so.openblas_set_num_threads(6)
+    assert lib.so.openblas_get_num_threads() == 6
+    lib.cxx["gemm_set_num_threads"](3)
+    assert lib.cxx["gemm_get_num_threads"]() == 3
+    lib.so.blas_set_num_threads(0)
+    assert lib.so.openblas_get_num_threads() == 0
+
+
+def test_aligned_alloc(lib):
+    p = lib.cxx["aligned_malloc"](1000, 64)
+    assert p and p % 64 == 0
+    lib.cxx["aligned_free"](p)
+    q = lib.cxx["aligned_malloc_huge"](5 << 20, 64)
+    assert q and q % 64 == 0
+    lib.cxx["aligned_free_huge"](q, 5 << 20)

@@ -1,0 +1,331 @@
+"""Parity of the gfx950 kernels with the CPU oracle, through the C-ABI.
+
+Inputs come from the seeded SplitMix64 generator (tests/_util.py); device
+memory is plain torch tensors.  Tolerances are those stated in _util.py:
+fp32/bf16 element-wise (2K+4) * 2^-24 * (|alpha| |A||B| + |beta C0|) against
+the fp64 product (bf16: of the bf16-rounded operands), int8 bit-exact.
+"""
+
+import numpy as np
+import pytest
+
+import _util as u
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def dev_copy(x, device):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(device)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ---------------------------------------------------------------- fp32 skinny (M <= 8)
+SKINNY = [(M, N, K) for M in (1, 2, 3, 4, 5, 6, 7, 8) for (N, K) in ((1, 1), (3, 7), (257, 64), (1009, 300))]
+SKINNY += [(1, 4096, 4096), (2, 255, 2048), (5, 4099, 129), (8, 513, 1000), (7, 256, 8), (3, 11003, 33)]
+
+
+@pytest.mark.parametrize("M,N,K", SKINNY)
+def test_sgemm_skinny(lib, orc, dev, M, N, K):
+    A = u.normal(orc, M * K, 1, 0, 0.02).reshape(M, K)
+    B = u.normal(orc, K * N, 2, 0, 0.02).reshape(K, N)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    dA, dB = dev_copy(A, dev), dev_copy(B, dev)
+    for alpha, beta in ((1.0, 1.0), (1.0, 0.0), (-0.75, 0.5)):
+        dC = dev_copy(C0 if beta != 0.0 else np.full_like(C0, np.nan), dev)
+        lib.sgemm(M, N, K, alpha, dA, K, dB, N, beta, dC, N, stream=stream())
+        got = host(dC)
+        want, scale = u.exact(A, B, alpha, beta, C0)
+        u.assert_fp32_close(got, want, scale, K, f"skinny {M}x{N}x{K} a={alpha} b={beta}")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096)] + [(M, N, 2048) for M in (2, 3, 5, 7) for N in (1009, 4099, 11003)])
+def test_sgemm_configs_c1_c2(lib, orc, dev, M, N, K):
+    """Full BASELINE shapes: C1 (beta 0, C pre-filled NaN) and C2 (beta 1),
+    against fp64 and against the order-faithful oracle of the reference path."""
+    if M == 1:
+        A, B = u.uniform(orc, K, 1).reshape(1, K), u.uniform(orc, K * N, 2).reshape(K, N)
+        C0, beta = np.full((1, N), np.nan, np.float32), 0.0
+    else:
+        A, B = u.normal(orc, M * K, 1, 0, 0.02).reshape(M, K), u.normal(orc, K * N, 2, 0, 0.02).reshape(K, N)
+        C0, beta = u.uniform(orc, M * N, 3).reshape(M, N), 1.0
+    dC = dev_copy(C0, dev)
+    lib.sgemm(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, beta, dC, N, stream=stream())
+    got = host(dC)
+    want, scale = u.exact(A, B, 1.0, beta, C0 if beta else None)
+    u.assert_fp32_close(got, want, scale, K, f"C1/C2 {M}x{N}x{K}")
+    Co = C0.copy()
+    assert orc.orc_gemm_f32_smallm(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, beta, u.ptr(Co), N, 4) == 0
+    d = np.abs(got.astype(np.float64) - Co)
+    assert (d <= 2 * u.fp32_tol(K, scale)).all(), "far from the reference-path oracle"
+
+
+def test_sgemm_deterministic(lib, orc, dev):
+    M, N, K = 7, 4099, 2048
+    A, B = u.normal(orc, M * K, 1, 0, 0.02), u.normal(orc, K * N, 2, 0, 0.02)
+    dA, dB = dev_copy(A, dev), dev_copy(B, dev)
+    outs = []
+    for _ in range(3):
+        dC = torch.zeros(M * N, dtype=torch.float32, device=dev)
+        lib.sgemm(M, N, K, 1.0, dA, K, dB, N, 0.0, dC, N, stream=stream())
+        outs.append(host(dC))
+    assert all(np.array_equal(outs[0].view(np.uint32), o.view(np.uint32)) for o in outs[1:])
+
+
+def test_sgemm_strided_operands(lib, orc, dev):
+    """lda/ldb/ldc larger than the row length, row-major sub-matrices."""
+    M, N, K = 5, 300, 200
+    lda, ldb, ldc = K + 9, N + 13, N + 7
+    A = u.uniform(orc, M * lda, 1).reshape(M, lda)
+    B = u.uniform(orc, K * ldb, 2).reshape(K, ldb)
+    C0 = u.uniform(orc, M * ldc, 3).reshape(M, ldc)
+    for (m, n) in ((M, N), (40, N)):
+        AA = u.uniform(orc, m * lda, 1).reshape(m, lda) if m != M else A
+        CC = u.uniform(orc, m * ldc, 3).reshape(m, ldc) if m != M else C0
+        dC = dev_copy(CC, dev)
+        lib.sgemm(m, n, K, 1.0, dev_copy(AA, dev), lda, dev_copy(B, dev), ldb, 1.0, dC, ldc, stream=stream())
+        got = host(dC)
+        want, scale = u.exact(AA[:, :K], B[:, :n], 1.0, 1.0, CC[:, :n])
+        u.assert_fp32_close(got[:, :n], want, scale, K, f"strided m={m}")
+        assert np.array_equal(got[:, n:], CC[:, n:]), "wrote outside the C block"
+
+
+# ---------------------------------------------------------------- fp32 tiles and transposes
+TILE = [(9, 13, 17), (16, 16, 16), (65, 17, 300), (128, 128, 128), (127, 127, 127), (256, 256, 256),
+        (128, 768, 768), (33, 1, 65), (100, 5, 1), (64, 64, 4096), (300, 70, 63)]
+
+
+@pytest.mark.parametrize("M,N,K", TILE)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_sgemm_tiles_and_transposes(lib, orc, dev, M, N, K, ta, tb):
+    opA = u.uniform(orc, M * K, 1).reshape(M, K)
+    opB = u.uniform(orc, K * N, 2).reshape(K, N)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    A = np.ascontiguousarray(opA.T) if ta else opA
+    B = np.ascontiguousarray(opB.T) if tb else opB
+    dC = dev_copy(C0, dev)
+    lib.sgemm(M, N, K, 2.5, dev_copy(A, dev), A.shape[1], dev_copy(B, dev), B.shape[1], -0.3, dC, N,
+              transA=ta, transB=tb, stream=stream())
+    want, scale = u.exact(opA, opB, 2.5, -0.3, C0)
+    u.assert_fp32_close(host(dC), want, scale, K, f"tile {M}x{N}x{K} ta={ta} tb={tb}")
+
+
+@pytest.mark.parametrize("M,N,K,ta", [(65536, 16, 256, 0), (65536, 64, 256, 0), (64, 64, 262144, 0),
+                                      (64, 64, 262144, 1)])
+def test_sgemm_configs_c3(lib, orc, dev, M, N, K, ta):
+    opA = u.uniform(orc, M * K, 1).reshape(M, K)
+    B = u.uniform(orc, K * N, 2).reshape(K, N)
+    A = np.ascontiguousarray(opA.T) if ta else opA
+    dC = dev_copy(np.full((M, N), np.nan, np.float32), dev)
+    lib.sgemm(M, N, K, 1.0, dev_copy(A, dev), A.shape[1], dev_copy(B, dev), N, 0.0, dC, N, transA=ta,
+              stream=stream())
+    want, scale = u.exact(opA, B)
+    u.assert_fp32_close(host(dC), want, scale, K, f"C3 {M}x{N}x{K} ta={ta}")
+
+
+def test_sgemm_naive_bitwise(lib, orc, dev):
+    """The kNaive kernel reproduces the reference's scalar loop bit for bit
+    (the oracle's naive loop is itself pinned to the reference build)."""
+    for M, N, K, alpha, beta in [(7, 13, 5, 1.0, 0.0), (3, 3, 1000, 2.5, -0.3), (33, 70, 129, 1.0, 0.5)]:
+        A, B, C0 = u.uniform(orc, M * K, 1), u.uniform(orc, K * N, 2), u.uniform(orc, M * N, 3)
+        Co = C0.copy()
+        orc.orc_gemm_naive_f32(M, N, K, alpha, u.ptr(A), K, u.ptr(B), N, beta, u.ptr(Co), N)
+        dC = dev_copy(C0, dev)
+        lib.sgemm_naive(M, N, K, alpha, dev_copy(A, dev), K, dev_copy(B, dev), N, beta, dC, N, stream=stream())
+        assert np.array_equal(host(dC).view(np.uint32), Co.view(np.uint32))
+
+
+# ---------------------------------------------------------------- bf16
+BF16 = [(1, 11008, 4096), (4, 11008, 4096), (32, 11008, 4096), (256, 11008, 4096), (3, 1001, 130), (8, 5, 7),
+        (9, 33, 250), (64, 100, 129), (1, 1, 1)]
+
+
+@pytest.mark.parametrize("M,N,K", BF16)
+def test_bf16_storage(lib, orc, dev, M, N, K):
+    A = u.bf16_bits(orc, u.normal(orc, M * K, 1)).reshape(M, K)
+    B = u.bf16_bits(orc, u.normal(orc, K * N, 2, 0, 0.02)).reshape(K, N)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    dA = dev_copy(A.view(np.int16), dev)
+    dB = dev_copy(B.view(np.int16), dev)
+    for beta in (0.0, 1.0):
+        dC = dev_copy(C0 if beta else np.full_like(C0, np.nan), dev)
+        lib.gemm_bf16(M, N, K, 1.0, dA, K, dB, N, beta, dC, N, stream=stream())
+        want, scale = u.exact(u.bf16_value(A), u.bf16_value(B), 1.0, beta, C0 if beta else None)
+        u.assert_fp32_close(host(dC), want, scale, K, f"bf16 {M}x{N}x{K} beta={beta}")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 11008, 4096), (4, 1000, 512), (7, 33, 65), (32, 300, 260), (256, 1024, 512)])
+def test_bf16_fp32_inputs(lib, orc, dev, M, N, K):
+    A = u.normal(orc, M * K, 1).reshape(M, K)
+    B = u.normal(orc, K * N, 2, 0, 0.02).reshape(K, N)
+    dC = torch.zeros(M * N, dtype=torch.float32, device=dev)
+    lib.gemm_bf16_f32in(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, 0.0, dC, N, stream=stream())
+    got = host(dC).reshape(M, N)
+    Ar, Br = u.bf16_value(u.bf16_bits(orc, A)), u.bf16_value(u.bf16_bits(orc, B))
+    want, scale = u.exact(Ar, Br)
+    u.assert_fp32_close(got, want, scale, K, "bf16 rounded in registers")
+    w2, s2 = u.exact(A, B)
+    assert (np.abs(got - w2) <= 1e-2 * s2 + 1e-30).all(), "bf16 vs unrounded fp32 beyond 1e-2"
+
+
+# ---------------------------------------------------------------- int8
+S8 = [(M, N, 4096) for M in (1, 8, 128) for N in (4096, 4093)]
+S8 += [(1, 1, 1), (3, 5, 15), (17, 33, 17), (16, 16, 255), (9, 100, 300), (40, 7, 1000), (130, 70, 64),
+       (2, 3, 257)]
+
+
+@pytest.mark.parametrize("M,N,K", S8)
+def test_int8_bit_exact(lib, orc, dev, M, N, K):
+    A = u.ints8(orc, M * K, 1).reshape(M, K)
+    B = u.ints8(orc, N * K, 2).reshape(N, K)
+    dC = torch.full((M, N), -7, dtype=torch.int32, device=dev)
+    lib.gemm_s8s8s32(M, N, K, dev_copy(A, dev), K, dev_copy(B, dev), K, dC, N, stream=stream())
+    want = (A.astype(np.float64) @ B.astype(np.float64).T).astype(np.int64)  # exact below 2^53
+    assert np.array_equal(host(dC).astype(np.int64), want)
+
+
+def test_int8_padded_strides_and_extremes(lib, orc, dev):
+    M, N, K = 9, 21, 300
+    lda, ldb, ldc = K + 5, K + 3, N + 2
+    A = u.ints8(orc, M * lda, 1, -128, 127).reshape(M, lda)
+    B = u.ints8(orc, N * ldb, 2, -128, 127).reshape(N, ldb)
+    A[0, :K] = -128
+    B[0, :K] = -128
+    dC = torch.full((M, ldc), 99, dtype=torch.int32, device=dev)
+    lib.gemm_s8s8s32(M, N, K, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, dC, ldc, stream=stream())
+    got = host(dC)
+    want = (A[:, :K].astype(np.float64) @ B[:, :K].astype(np.float64).T).astype(np.int64)
+    assert np.array_equal(got[:, :N].astype(np.int64), want)
+    assert (got[:, N:] == 99).all()
+    assert got[0, 0] == K * 128 * 128
+
+
+@pytest.mark.parametrize("M,N", [(1, 4096), (8, 4093), (128, 4093)])
+def test_int8_colscale(lib, orc, dev, M, N):
+    K = 4096
+    A, B = u.ints8(orc, M * K, 1).reshape(M, K), u.ints8(orc, N * K, 2).reshape(N, K)
+    s = u.uniform(orc, N, 4, 0.001, 0.01)
+    dC = torch.zeros((M, N), dtype=torch.float32, device=dev)
+    lib.gemm_s8s8f32_colscale(M, N, K, dev_copy(A, dev), K, dev_copy(B, dev), K, dev_copy(s, dev), dC, N,
+                              stream=stream())
+    acc = (A.astype(np.float64) @ B.astype(np.float64).T).astype(np.float32)
+    assert np.array_equal(host(dC), acc * s[None, :])
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (7, 13, 5), (3, 3, 1000), (13, 17, 19), (64, 300, 257)])
+def test_int8_dynamic_quant_matches_oracle(lib, orc, dev, M, N, K):
+    A, B, C0 = u.uniform(orc, M * K, 1), u.uniform(orc, K * N, 2), u.uniform(orc, M * N, 3)
+    for beta in (0.0, 0.5):
+        Co = C0.copy()
+        orc.orc_gemm_int8_dynq(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, beta, u.ptr(Co), N)
+        dC = dev_copy(C0, dev)
+        lib.gemm_int8_f32(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, beta, dC, N, stream=stream())
+        assert np.array_equal(host(dC).view(np.uint32), Co.view(np.uint32))
+
+
+# ---------------------------------------------------------------- saxpy, C++ and BLAS APIs on host memory
+def test_saxpy(lib, orc, dev):
+    for n, incx, incy in [(1, 1, 1), (1000, 1, 1), (777, 3, 2)]:
+        X, Y0 = u.uniform(orc, n * incx, 5), u.uniform(orc, n * incy, 6)
+        Yo = Y0.copy()
+        orc.orc_saxpy(n, 0.7, u.ptr(X), incx, u.ptr(Yo), incy, 1)
+        dY = dev_copy(Y0, dev)
+        lib.saxpy(n, 0.7, dev_copy(X, dev), incx, dY, incy, stream=stream())
+        assert np.array_equal(host(dY).view(np.uint32), Yo.view(np.uint32))
+        Yh = Y0.copy()
+        lib.so.cblas_saxpy(n, 0.7, X.ctypes.data, incx, Yh.ctypes.data, incy)
+        assert lib.last_status() == 0 and np.array_equal(Yh.view(np.uint32), Yo.view(np.uint32))
+
+
+CBLAS_SIZES = [(4, 4, 4), (16, 16, 16), (32, 64, 48), (128, 128, 128), (7, 13, 11), (1, 64, 32), (256, 256, 256)]
+
+
+@pytest.mark.parametrize("M,N,K", CBLAS_SIZES)
+def test_cblas_matrix_of_the_reference(lib, orc, M, N, K):
+    """Every Order x Trans case of tests/test_cblas.cpp:78-334 plus Fortran
+    sgemm_, on host arrays, against the oracle's restatement of
+    cblas_sgemm.cpp (explicit transposes + scalar loop)."""
+    b = u.binding()
+    for order in (101, 102):
+        for ta in (111, 112):
+            for tb in (111, 112):
+                rows_a, cols_a = (M, K) if ta == 111 else (K, M)
+                rows_b, cols_b = (K, N) if tb == 111 else (N, K)
+                if order == 102:
+                    rows_a, cols_a, rows_b, cols_b = cols_a, rows_a, cols_b, rows_b
+                A = u.uniform(orc, rows_a * cols_a, 1)
+                B = u.uniform(orc, rows_b * cols_b, 2)
+                crow, ccol = (M, N) if order == 101 else (N, M)
+                C0 = u.uniform(orc, crow * ccol, 3)
+                Co, Cg = C0.copy(), C0.copy()
+                orc.orc_cblas_sgemm(order, ta, tb, M, N, K, 2.5, u.ptr(A), cols_a, u.ptr(B), cols_b, -0.3,
+                                    u.ptr(Co), ccol)
+                lib.cblas_sgemm(order, ta, tb, M, N, K, 2.5, A, cols_a, B, cols_b, -0.3, Cg, ccol)
+                _, scale = u.exact(np.abs(A).reshape(1, -1)[:, :1], np.abs(B).reshape(1, -1)[:1, :1])
+                tol = K * 5e-4  # tests/test_cblas.cpp alpha/beta tolerance
+                assert np.abs(Cg - Co).max() < tol, (order, ta, tb)
+    # Fortran entry: column-major NN with alpha 1, beta 0
+    A = u.uniform(orc, M * K, 1)
+    B = u.uniform(orc, K * N, 2)
+    C = np.zeros(M * N, np.float32)
+    import ctypes
+
+    ci = lambda v: ctypes.byref(ctypes.c_int(v))  # noqa: E731
+    cf = lambda v: ctypes.byref(ctypes.c_float(v))  # noqa: E731
+    lib.so.sgemm_(ctypes.c_char_p(b"N"), ctypes.c_char_p(b"N"), ci(M), ci(N), ci(K), cf(1.0), A.ctypes.data,
+                  ci(M), B.ctypes.data, ci(K), cf(0.0), C.ctypes.data, ci(M))
+    want, scale = u.exact(A.reshape(K, M).T, B.reshape(N, K).T)
+    u.assert_fp32_close(C.reshape(N, M).T, want, scale, K, "sgemm_")
+
+
+def test_cxx_api_host_and_device_pointers(lib, orc, dev):
+    M, N, K = 5, 1009, 2048
+    A, B, C0 = u.normal(orc, M * K, 1, 0, .02), u.normal(orc, K * N, 2, 0, .02), u.uniform(orc, M * N, 3)
+    want, scale = u.exact(A.reshape(M, K), B.reshape(K, N), 1.0, 1.0, C0.reshape(M, N))
+    Ch = C0.copy()
+    lib.gemm_fp32(M, N, K, 1.0, A, K, B, N, 1.0, Ch, N)
+    u.assert_fp32_close(Ch.reshape(M, N), want, scale, K, "gemm_fp32 host")
+    dC = dev_copy(C0, dev)
+    lib.gemm_fp32(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, 1.0, dC, N)
+    u.assert_fp32_close(host(dC).reshape(M, N), want, scale, K, "gemm_fp32 device")
+    Cn, Co = C0.copy(), C0.copy()
+    lib.gemm_fp32(M, N, K, 1.0, A, K, B, N, 1.0, Cn, N, algo="kNaive")
+    orc.orc_gemm_naive_f32(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 1.0, u.ptr(Co), N)
+    assert np.array_equal(Cn.view(np.uint32), Co.view(np.uint32))
+    # bf16 on fp32 storage, native bf16, fp32-API int8, native int8
+    Cb = np.zeros(M * N, np.float32)
+    lib.cxx["gemm_bf16"](M, N, K, 1.0, A.ctypes.data, K, B.ctypes.data, N, 0.0, Cb.ctypes.data, N)
+    assert lib.last_status() == 0
+    w2, s2 = u.exact(A.reshape(M, K), B.reshape(K, N))
+    assert (np.abs(Cb.reshape(M, N) - w2) <= 1e-2 * s2).all()
+    Ab, Bb = u.bf16_bits(orc, A), u.bf16_bits(orc, B)
+    Cbb = np.zeros(M * N, np.float32)
+    lib.cxx["gemm_bf16_bf16bf16f32"](M, N, K, 1.0, Ab.ctypes.data, K, Bb.ctypes.data, N, 0.0, Cbb.ctypes.data, N)
+    wb, sb = u.exact(u.bf16_value(Ab).reshape(M, K), u.bf16_value(Bb).reshape(K, N))
+    u.assert_fp32_close(Cbb.reshape(M, N), wb, sb, K, "gemm_bf16_bf16bf16f32 host")
+    Ci, Cio = C0.copy(), C0.copy()
+    lib.cxx["gemm_int8"](M, N, K, 1.0, A.ctypes.data, K, B.ctypes.data, N, 0.5, Ci.ctypes.data, N)
+    orc.orc_gemm_int8_dynq(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 0.5, u.ptr(Cio), N)
+    assert np.array_equal(Ci.view(np.uint32), Cio.view(np.uint32))
+    A8, B8 = u.ints8(orc, M * K, 1), u.ints8(orc, N * K, 2)
+    C8 = np.zeros(M * N, np.int32)
+    lib.cxx["gemm_int8_int8int8int32"](M, N, K, A8.ctypes.data, K, B8.ctypes.data, K, C8.ctypes.data, N)
+    assert lib.last_status() == 0
+    assert np.array_equal(C8.reshape(M, N), (A8.reshape(M, K).astype(np.int64) @ B8.reshape(N, K).T.astype(np.int64)))
+
+
+def test_empty_problems_do_not_touch_c(lib, dev):
+    C = torch.full((4, 4), 3.0, device=dev)
+    A = torch.ones(16, device=dev)
+    for M, N, K in ((0, 4, 4), (4, 0, 4), (4, 4, 0), (-1, 4, 4)):
+        lib.sgemm(M, N, K, 1.0, A, 4, A, 4, 0.0, C, 4, stream=stream())
+    assert (host(C) == 3.0).all()
