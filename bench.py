@@ -19,9 +19,11 @@ touched once per step and a step's working set exceeds the 256 MB Infinity
 Cache (extra copies are rotated when it would not), so nothing is served from
 the cache between two launches of the same shape.
 
-`roofline` is for the kernel with the largest share of the step time:
-achieved = its algorithmic bytes (or flops) per launch / its mean launch
-time (HIP events around each launch).  `traffic` is filled from
+Timing uses HIP graphs replayed on one stream (a step = one graph replay), so
+host-side launch cost does not enter.  `roofline` is for the kernel with the
+largest share of the step time: achieved = its algorithmic bytes (or flops)
+per launch / its mean launch time, from HIP events around replays of a graph
+of 16 back-to-back launches of each shape (inter-kernel gaps included).  `traffic` is filled from
 profiles/<kernel>_<workload>_traffic.json when a rocprofv3 --pmc summary has
 been committed for it.
 
@@ -179,6 +181,13 @@ def kernel_key(lib, case):
 
 
 def run_gpu(args, wl_name):
+    """Time the workload with HIP graphs replayed on one stream.
+
+    Host-side launch cost (Python, ctypes, planning) would otherwise dominate
+    kernels of a few microseconds; a captured graph replays a whole step with
+    one host call.  The library's workspace for the stream is created by a
+    warm-up pass on that same stream before capture.
+    """
     import torch
 
     b = _binding()
@@ -190,53 +199,77 @@ def run_gpu(args, wl_name):
     # Rotate copies so one pass of every buffer exceeds 2x the 256 MB cache.
     copies = max(1, -(-(600 << 20) // step_bytes))
     bufs = [Buffers(torch, lib, c, copies, dev) for c in cases]
-    torch.cuda.synchronize()
-    s = torch.cuda.current_stream()
-    sp = s.cuda_stream
     keys = [kernel_key(lib, c) for c in cases]
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream(device=dev)  # default priority
+    sp = stream.cuda_stream
 
-    for w in range(args.warmup):
-        for bf in bufs:
-            bf.launch(lib, w % copies, sp)
+    with torch.cuda.stream(stream):
+        for w in range(max(1, args.warmup)):
+            for bf in bufs:
+                bf.launch(lib, w % copies, sp)
     torch.cuda.synchronize()
 
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in cases]
-          for _ in range(args.steps)]
+    def capture(launches):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for fn in launches:
+                fn()
+        return g
+
+    # one graph per buffer copy: a full step
+    step_graphs = [capture([lambda bf=bf, r=r: bf.launch(lib, r, sp) for bf in bufs]) for r in range(copies)]
+    # one graph per case: REP back-to-back launches, rotating copies
+    rep = 16
+    case_graphs = [capture([lambda bf=bf, i=i: bf.launch(lib, i % copies, sp) for i in range(rep)]) for bf in bufs]
+    torch.cuda.synchronize()
+
+    with torch.cuda.stream(stream):
+        for w in range(args.warmup):
+            step_graphs[w % copies].replay()
+    torch.cuda.synchronize()
+
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(s)
-    for st in range(args.steps):
-        r = (args.warmup + st) % copies
-        for i, bf in enumerate(bufs):
-            ev[st][i][0].record(s)
-            bf.launch(lib, r, sp)
-            ev[st][i][1].record(s)
-    t1.record(s)
+    with torch.cuda.stream(stream):
+        t0.record(stream)
+        for st in range(args.steps):
+            step_graphs[(args.warmup + st) % copies].replay()
+        t1.record(stream)
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
     ms_per_step = total_ms / args.steps
 
-    per_case = []
+    # per-case kernel time: events around graph replays on the launch stream
+    reps_timed = max(3, min(args.steps, 10))
+    per_case, launch_ms = [], []
     for i, c in enumerate(cases):
-        d = [ev[st][i][0].elapsed_time(ev[st][i][1]) for st in range(args.steps)]
+        samples = []
+        with torch.cuda.stream(stream):
+            case_graphs[i].replay()
+            for _ in range(reps_timed):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                case_graphs[i].replay()
+                e1.record(stream)
+                samples.append((e0, e1))
+        torch.cuda.synchronize()
+        d = [a.elapsed_time(bb) / rep for a, bb in samples]
         med = statistics.median(d)
+        launch_ms.append(sum(d) / len(d))
         per_case.append({
             "case": c.name, "M": c.M, "N": c.N, "K": c.K, "kernel": keys[i][0], "plan": keys[i][1],
-            "us_median": med * 1e3, "us_mean": sum(d) / len(d) * 1e3,
+            "us_median": med * 1e3, "us_mean": launch_ms[-1] * 1e3,
             "GBps": c.bytes_alg() / (med * 1e-3) / 1e9, "TFLOPs": c.flops_alg() / (med * 1e-3) / 1e12,
         })
     # dominant kernel instance: largest share of the per-launch time
     groups = {}
     for i, c in enumerate(cases):
-        k = keys[i][0]
-        g = groups.setdefault(k, {"ms": 0.0, "bytes": 0.0, "flops": 0.0, "launches": 0, "dtype": c.dtype,
-                                  "cases": []})
-        for st in range(args.steps):
-            g["ms"] += ev[st][i][0].elapsed_time(ev[st][i][1])
-            g["bytes"] += c.bytes_alg()
-            g["flops"] += c.flops_alg()
-            g["launches"] += 1
-        g["cases"].append(c.name)
+        g = groups.setdefault(keys[i][0], {"ms": 0.0, "bytes": 0.0, "flops": 0.0, "launches": 0,
+                                           "dtype": c.dtype})
+        g["ms"] += launch_ms[i]
+        g["bytes"] += c.bytes_alg()
+        g["flops"] += c.flops_alg()
+        g["launches"] += 1
     dom_key, dom = max(groups.items(), key=lambda kv: kv[1]["ms"])
     mean_s = dom["ms"] / dom["launches"] * 1e-3
     bytes_per = dom["bytes"] / dom["launches"]

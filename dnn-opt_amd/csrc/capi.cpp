@@ -4,6 +4,7 @@
 // takes the stream's workspace when the launch needs one, and enqueues the
 // kernel.  Nothing here falls back to the host: a failure is a status code.
 #include <hip/hip_runtime.h>
+#include <stdint.h>
 
 #include "dnnopt_hip.h"
 #include "host.h"
@@ -37,8 +38,12 @@ int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B
     a.K = K;
     a.alpha = alpha;
     a.beta = beta;
-    a.splits = (int)L.grid.y;
-    a.ncols_pad = (int)L.grid.x * skinny_tile_cols(L.mode);
+    const int T = L.tiles;
+    const int G = (int)L.grid.x;
+    a.tiles = T;
+    a.splits = (G + T - 1) / T;
+    a.ncols_pad = T * skinny_tile_cols(L.mode);
+    a.defer_reduce = L.defer_reduce;
     if (a.splits > 1) {
         void* part = nullptr;
         unsigned* tickets = nullptr;
@@ -47,7 +52,16 @@ int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B
         a.part = static_cast<float*>(part);
         a.tickets = tickets;
     }
-    return finish_launch(launch_skinny(L.mode, L.mr, L.nw, L.grid, a, s));
+    // bf16 rows start on 4-byte boundaries only when the matrix does and its
+    // row stride is even.
+    const bool bf16 = L.mode == kSkinnyBF16;
+    const int b_aligned = !bf16 || ((reinterpret_cast<uintptr_t>(B) & 3u) == 0 && (ldb & 1) == 0);
+    int a_layout = a_sk == 1 ? 0 : 1;
+    if (bf16 && ((reinterpret_cast<uintptr_t>(A) & 3u) != 0 || (a_sm & 1) != 0)) a_layout = 2;
+    int st = finish_launch(launch_skinny(L.mode, L.mr, L.nw, b_aligned, a_layout, L.grid, a, s));
+    if (st != DNNOPT_OK || !L.defer_reduce) return st;
+    return finish_launch(launch_skinny_reduce(a.part, G, T, skinny_tile_cols(L.mode), M, N, a.ncols_pad, alpha,
+                                              beta, C, ldc, s));
 }
 
 int run_tile(const Launch& L, int ta, int tb, const void* A, int lda, const void* B, int ldb, float* C, int ldc,
@@ -76,7 +90,8 @@ int run_tile(const Launch& L, int ta, int tb, const void* A, int lda, const void
         a.part = static_cast<float*>(part);
         a.tickets = tickets;
     }
-    int st = finish_launch(launch_tile(L.mode, L.cfg, ta, tb, L.grid, a, s));
+    const int aligned = L.mode != kTileBF16 || ((reinterpret_cast<uintptr_t>(A) & 3u) == 0 && (lda & 1) == 0);
+    int st = finish_launch(launch_tile(L.mode, L.cfg, ta, tb, aligned, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
     return finish_launch(launch_splitk_reduce(a.part, a.splits, (int)L.grid.x, (int)L.grid.y, L.bm, L.bn, M, N,
                                               alpha, beta, C, ldc, s));
@@ -204,6 +219,7 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
     a.N = N;
     a.K = K;
     a.splits = (int)L.grid.z;
+    a.defer_reduce = L.defer_reduce;
     if (a.splits > 1) {
         void* part = nullptr;
         unsigned* tickets = nullptr;
@@ -212,7 +228,12 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
         a.part = static_cast<int32_t*>(part);
         a.tickets = tickets;
     }
-    return finish_launch(launch_mfma_s8(L.cfg, epi, L.grid, a, s));
+    const int aligned = ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) == 0 &&
+                        (lda & 3) == 0 && (ldb & 3) == 0;
+    st = finish_launch(launch_mfma_s8(L.cfg, epi, aligned, L.grid, a, s));
+    if (st != DNNOPT_OK || !L.defer_reduce) return st;
+    return finish_launch(launch_s8_reduce(a.part, a.splits, (int)L.grid.x, (int)L.grid.y, L.bm, L.bn, M, N, epi,
+                                          scale, C, ldc, s));
 }
 
 int dnnopt_hip_gemm_s8s8s32(int M, int N, int K, const int8_t* A, int lda, const int8_t* B, int ldb, int32_t* C,
@@ -232,10 +253,12 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
     if (lda < K || ldb < N || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
     hipStream_t s = as_stream(stream);
-    // Staging (slot 1): [int32 acc M*N][qA M*K][qB N*K][2 absmax words].
-    const size_t acc_bytes = (size_t)M * N * 4;
-    const size_t qa_bytes = ((size_t)M * K + 255) & ~(size_t)255;
-    const size_t qb_bytes = ((size_t)N * K + 255) & ~(size_t)255;
+    // Staging (slot 1): [int32 acc M*N][qA M x ldq][qB N x ldq][2 absmax words];
+    // ldq pads K to 16 bytes so every quantized row is 16-byte aligned.
+    const int ldq = (K + 15) & ~15;
+    const size_t acc_bytes = ((size_t)M * N * 4 + 255) & ~(size_t)255;
+    const size_t qa_bytes = ((size_t)M * ldq + 255) & ~(size_t)255;
+    const size_t qb_bytes = ((size_t)N * ldq + 255) & ~(size_t)255;
     void* stage = nullptr;
     unsigned* unused = nullptr;
     int st = get_workspace(s, acc_bytes + qa_bytes + qb_bytes + 256, &stage, &unused, 1);
@@ -245,9 +268,9 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
     int8_t* qa = reinterpret_cast<int8_t*>(base + acc_bytes);
     int8_t* qb = reinterpret_cast<int8_t*>(base + acc_bytes + qa_bytes);
     unsigned* amax = reinterpret_cast<unsigned*>(base + acc_bytes + qa_bytes + qb_bytes);
-    st = finish_launch(launch_quant_prepare(A, lda, B, ldb, M, N, K, amax, qa, qb, s));
+    st = finish_launch(launch_quant_prepare(A, lda, B, ldb, M, N, K, ldq, amax, qa, qb, s));
     if (st != DNNOPT_OK) return st;
-    st = gemm_s8_common(0, M, N, K, qa, K, qb, K, nullptr, acc, N, stream);
+    st = gemm_s8_common(0, M, N, K, qa, ldq, qb, ldq, nullptr, acc, N, stream);
     if (st != DNNOPT_OK) return st;
     return finish_launch(launch_dequant(acc, M, N, amax, alpha, beta, C, ldc, s));
 }

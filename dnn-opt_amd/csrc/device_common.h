@@ -32,12 +32,71 @@ __device__ __forceinline__ u32x4 buf_load_x4(__amdgpu_buffer_rsrc_t r, uint32_t 
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// Cache-policy operand of the buffer intrinsics on gfx950: bit 0 = sc0,
+// bit 1 = nt, bit 4 = sc1.  sc0|sc1 is system scope: loads miss in every
+// cache level and stores write through to memory, which makes data written by
+// one workgroup visible to another on any XCD without an L2 writeback or
+// invalidate.  nt marks streaming data that is used once.
+constexpr int kAuxNT = 2;
+constexpr int kAuxCoherent = 17;
+
+__device__ __forceinline__ u32x4 buf_load_x4_stream(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAuxNT));
+}
+
+__device__ __forceinline__ f32x4 buf_load_x4_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAuxCoherent));
+}
+
+__device__ __forceinline__ void buf_store_x4_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kAuxCoherent);
+}
+
+__device__ __forceinline__ uint32_t buf_load_x1_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kAuxCoherent);
+}
+
+__device__ __forceinline__ void buf_store_x1_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kAuxCoherent);
+}
+
 __device__ __forceinline__ uint32_t buf_load_x1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
 
 __device__ __forceinline__ uint16_t buf_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+// Dword buffer loads ignore the two low address bits, so 16 bytes that do not
+// start on a 4-byte boundary (rows of an odd-length bf16 or int8 matrix) are
+// read as the enclosing aligned 20 bytes and funnel-shifted into place.  The
+// descriptor must start on a 4-byte boundary (see rsrc_aligned) and `off` is
+// the byte offset from it; shift 0 returns the aligned load unchanged.
+__device__ __forceinline__ u32x4 buf_load_x4_unaligned(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    const uint32_t sh = off & 3u;
+    const uint32_t o = off - sh;
+    const u32x4 v = buf_load_x4(r, o);
+    const uint32_t e = buf_load_x1(r, o + 16u);
+    u32x4 out;
+    out[0] = __builtin_amdgcn_alignbyte(v[1], v[0], sh);
+    out[1] = __builtin_amdgcn_alignbyte(v[2], v[1], sh);
+    out[2] = __builtin_amdgcn_alignbyte(v[3], v[2], sh);
+    out[3] = __builtin_amdgcn_alignbyte(e, v[3], sh);
+    return out;
+}
+
+// Descriptor for `bytes` bytes starting at `base`, with the start rounded
+// down to 4 bytes; *lo receives the bytes skipped (add it to every offset).
+// The range check of a dword load rejects a dword that extends past the
+// range, so the range is also rounded up to whole dwords: the extra bytes lie
+// in the same aligned dword (and page) as the last valid byte, and every
+// kernel masks or discards what it reads there.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_aligned(const void* base, size_t bytes, uint32_t* lo) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(base);
+    *lo = (uint32_t)(a & 3u);
+    const size_t total = (bytes + *lo + 3u) & ~(size_t)3u;
+    return make_rsrc(reinterpret_cast<const void*>(a - *lo), total > 0x7FFFFFFFull ? 0x7FFFFFFFu : (uint32_t)total);
 }
 
 __device__ __forceinline__ float as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
@@ -61,6 +120,25 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
     return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
+// Balanced split-k decomposition: workgroup g of G over T column tiles
+// (G >= T).  The first G % T tiles get G/T + 1 k-splits, the others G/T, and
+// workgroups are numbered tile by tile.
+struct SplitPos {
+    int tile, split, nsplit;
+};
+
+__host__ __device__ __forceinline__ SplitPos split_pos(int g, int G, int T) {
+    const int q = G / T, r = G % T;
+    const int big = r * (q + 1);
+    if (g < big) return SplitPos{g / (q + 1), g % (q + 1), q + 1};
+    const int h = g - big;
+    return SplitPos{r + h / q, h % q, q};
+}
+
+__host__ __device__ __forceinline__ int splits_of_tile(int t, int G, int T) {
+    return G / T + (t < G % T ? 1 : 0);
+}
+
 // Wave index as a scalar (lets the compiler keep per-wave addresses in SGPRs).
 __device__ __forceinline__ int wave_id() {
     return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -75,27 +153,30 @@ __device__ __forceinline__ float epilogue(float acc, float alpha, float beta, co
     return __builtin_fmaf(alpha, acc, beta * (*c));
 }
 
-// Cross-workgroup ticket: every workgroup of a split-K group calls this after
-// its partial results are stored.  Returns true in exactly one workgroup -- the
-// last to arrive -- after which that workgroup may read every partial.  The
-// release fence before the atomic makes this workgroup's partial stores
-// visible at device (agent) scope, across XCD L2s; the acquire fence in the
-// last workgroup makes the other workgroups' stores visible to it.  The last
-// workgroup resets the ticket so the next launch starts from zero.
+// Cross-workgroup ticket: every workgroup of a split-k group calls this after
+// storing its partial sums with coherent (sc0 sc1, write-through) stores.
+// Returns true in exactly one workgroup -- the last to arrive -- which then
+// reads every partial with coherent loads.
+//
+// Protocol: each wave waits until its own stores have completed (vmcnt(0):
+// a write-through store completes once memory holds it); the barrier then
+// puts all of them before thread 0's atomic increment, which is performed at
+// memory (system scope).  The workgroup that draws the last ticket reads the
+// partials only after observing it, with loads that bypass every cache.  No
+// agent-scope fence is used: on gfx950 those are whole-L2 writebacks and
+// invalidates.  The last workgroup resets the ticket for the next launch.
 __device__ __forceinline__ bool split_ticket(unsigned* ticket, unsigned nsplits, int* lds_flag) {
-    __threadfence();
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are in memory
     __syncthreads();
     if (threadIdx.x == 0) {
-        unsigned t = atomicAdd(ticket, 1u);
-        bool last = (t == nsplits - 1);
+        const unsigned t = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const bool last = (t == nsplits - 1);
         // Every other workgroup of the group has already taken its ticket.
-        if (last) atomicExch(ticket, 0u);
+        if (last) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         *lds_flag = last ? 1 : 0;
     }
     __syncthreads();
-    bool last = *lds_flag != 0;
-    if (last) __threadfence();
-    return last;
+    return *lds_flag != 0;
 }
 
 }  // namespace dnnopt_dev

@@ -19,7 +19,8 @@
 //     large M, split-k as above.
 // Tunables (environment, read once, for sweeps):
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
-//   DNNOPT_MAX_SPLITS (default 256).
+//   DNNOPT_SKINNY_WGS_PER_CU (default 2), DNNOPT_SKINNY_WGS (force G),
+//   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel).
 #include <stdlib.h>
 #include <string.h>
 
@@ -50,10 +51,27 @@ int skinny_nw() {
     }();
     return v;
 }
+int skinny_wgs_per_cu() {
+    static int v = env_int("DNNOPT_SKINNY_WGS_PER_CU", 2);
+    return v;
+}
 int max_splits() {
     static int v = env_int("DNNOPT_MAX_SPLITS", 256);
     return v;
 }
+
+}  // namespace
+
+int split_reduce_mode() {
+    static int v = [] {
+        const char* e = getenv("DNNOPT_SPLIT_REDUCE");
+        if (e && *e) return atoi(e) ? 1 : 0;
+        return 1;
+    }();
+    return v;
+}
+
+namespace {
 
 // Splits beyond this are reduced by a separate kernel rather than by the
 // last-arriving workgroup.
@@ -82,27 +100,47 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
     *L = Launch{};
     const int tw = skinny_tile_cols(mode);
     const int es = skinny_elem_bytes(mode);
-    const int nw = skinny_nw();
-    const long long tiles = ceil_div(N, tw);
-    const long long target_waves = (long long)num_cus() * waves_per_cu();
-    long long s = ceil_div(target_waves, tiles * nw);
-    // Each wave should own at least one unrolled step of rows.
+    const long long T = ceil_div(N, tw);
+    const long long cus = num_cus();
+    // Every wave should own at least one unrolled step of rows; problems too
+    // small to give every CU a workgroup of 8 such waves use 4-wave groups.
+    int nw = skinny_nw();
+    if (!getenv("DNNOPT_SKINNY_NW") && T * std::max<long long>(1, K / (8ll * kSkinnyUnroll)) < cus) nw = 4;
     const long long smax = std::max<long long>(1, K / ((long long)nw * kSkinnyUnroll));
-    s = std::max<long long>(1, std::min<long long>({s, smax, (long long)kTicketSplitLimit * 2}));
-    // Keep per-workgroup buffer offsets inside 31 bits.
-    while (s < K && ceil_div(K, s) * (long long)ldb * es + (long long)tw * es >= 0x7FFFFFFFll) s *= 2;
-    if (ceil_div(K, s) * (long long)ldb * es + (long long)tw * es >= 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
-    if (s > 1 && tiles > kMaxTickets) s = 1;
+    // G workgroups, about skinny_wgs_per_cu() per CU, shared by the T column
+    // tiles as G/T or G/T + 1 k-splits each (balanced work per workgroup).
+    // When there is more than one CU's worth of work, G is a whole multiple
+    // of the CU count so that no CU runs one workgroup more than the others.
+    const long long g_target = cus * skinny_wgs_per_cu();
+    long long G;
+    if (T >= g_target) {
+        G = T;
+    } else {
+        G = std::min<long long>(g_target, T * smax);
+        if (G >= cus) G = std::max<long long>(T, G / cus * cus);
+    }
+    static const int forced = env_int("DNNOPT_SKINNY_WGS", 0);
+    if (forced > 0) G = std::min<long long>(std::max<long long>(forced, T), T * smax);
+    G = std::max<long long>(G, T);
+    // Keep per-workgroup buffer offsets inside 31 bits: more splits shorten
+    // the k-range of a workgroup.
+    auto span_ok = [&](long long g) { return ceil_div(K, g / T) * (long long)ldb * es + (long long)tw * es < 0x7FFFFFFFll; };
+    while (!span_ok(G) && G / T < K) G += T;
+    if (!span_ok(G) || G > 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
+    if (G > T && T > kMaxTickets && !split_reduce_mode()) return DNNOPT_ERR_UNSUPPORTED;
+    const long long smax_tile = ceil_div(G, T);
     L->mode = mode;
     L->mr = M;
     L->nw = nw;
-    L->grid = dim3((unsigned)tiles, (unsigned)s, 1);
-    L->part_bytes = s > 1 ? (size_t)s * M * tiles * tw * sizeof(float) : 0;
-    L->tickets = s > 1 ? (int)tiles : 0;
+    L->tiles = (int)T;
+    L->grid = dim3((unsigned)G, 1, 1);
+    L->defer_reduce = (G > T && split_reduce_mode()) ? 1 : 0;
+    L->part_bytes = G > T ? (size_t)smax_tile * M * T * tw * sizeof(float) : 0;
+    L->tickets = (G > T && !L->defer_reduce) ? (int)T : 0;
     const int kernel = mode == kSkinnyF32 ? DNNOPT_K_SKINNY_F32
                        : mode == kSkinnyBF16 ? DNNOPT_K_SKINNY_BF16
                                              : DNNOPT_K_SKINNY_F2B;
-    fill_pub(L, kernel, "dnnopt_skinny", M, tw, (int)s, nw * 64);
+    fill_pub(L, kernel, "dnnopt_skinny", M, tw, (int)smax_tile, nw * 64);
     return DNNOPT_OK;
 }
 
@@ -150,7 +188,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     L->bm = bm;
     L->bn = bn;
     L->grid = dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
-    L->defer_reduce = (s > kTicketSplitLimit || (s > 1 && tiles > kMaxTickets)) ? 1 : 0;
+    L->defer_reduce = (s > 1 && (split_reduce_mode() || s > kTicketSplitLimit || tiles > kMaxTickets)) ? 1 : 0;
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(float) : 0;
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
     const int kernel = mode == kTileF32 ? DNNOPT_K_TILE_F32 : DNNOPT_K_TILE_BF16;
@@ -174,14 +212,15 @@ int plan_s8(int epi, int M, int N, int K, Launch* L) {
         s = std::min<long long>({s, std::max<long long>(1, nblk / c.kw), (long long)kTicketSplitLimit});
         s = std::max<long long>(1, s);
     }
-    if (s > 1 && tiles > kMaxTickets) s = 1;
+    if (s > 1 && tiles > kMaxTickets && !split_reduce_mode()) s = 1;
+    L->defer_reduce = (s > 1 && split_reduce_mode()) ? 1 : 0;
     L->mode = epi;
     L->cfg = cfg;
     L->bm = bm;
     L->bn = bn;
     L->grid = dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(int32_t) : 0;
-    L->tickets = s > 1 ? (int)tiles : 0;
+    L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
     fill_pub(L, DNNOPT_K_MFMA_S8, "dnnopt_mfma_s8", bm, bn, (int)s, waves_per_wg * 64);
     return DNNOPT_OK;
 }

@@ -31,11 +31,16 @@ struct Launch {
     int mr = 0, nw = 0;  // skinny
     int cfg = 0;         // tile / int8 configuration index
     int bm = 0, bn = 0;  // tile shape
+    int tiles = 0;       // skinny: column tiles T (the grid has G >= T workgroups)
     dim3 grid;
     size_t part_bytes = 0;
     int tickets = 0;
     int defer_reduce = 0;
 };
+
+// Split-k reduction strategy: 0 = last-arriving workgroup (ticket),
+// 1 = separate reduce kernel.  DNNOPT_SPLIT_REDUCE overrides the default.
+int split_reduce_mode();
 
 int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L);
 int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L);

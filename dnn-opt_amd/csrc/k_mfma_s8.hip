@@ -39,7 +39,15 @@ __device__ __forceinline__ i32x4 mask_chunk(i32x4 v, int valid) {
 
 }  // namespace
 
-template <int MT, int NT, int WM, int WN, int KW, int EPI>
+// AL = 1: all rows of A and B start on 4-byte boundaries; AL = 0: rows are
+// read with funnel-shifted loads.
+template <int AL>
+__device__ __forceinline__ i32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (AL) return __builtin_bit_cast(i32x4, buf_load_x4(r, off));
+    return __builtin_bit_cast(i32x4, buf_load_x4_unaligned(r, off));
+}
+
+template <int MT, int NT, int WM, int WN, int KW, int EPI, int AL>
 __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
     constexpr int BM = WM * MT * 16;
     constexpr int BN = WN * NT * 16;
@@ -64,19 +72,20 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
     const int8_t* bbase = p.B + (size_t)n0 * p.ldb;
     const size_t arem = (size_t)(p.M - 1 - m0) * p.lda + p.K;
     const size_t brem = (size_t)(p.N - 1 - n0) * p.ldb + p.K;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(abase, arem > 0x7FFFFFFFull ? 0x7FFFFFFFu : (uint32_t)arem);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase, brem > 0x7FFFFFFFull ? 0x7FFFFFFFu : (uint32_t)brem);
+    uint32_t alo = 0, blo = 0;
+    const __amdgpu_buffer_rsrc_t ra = rsrc_aligned(abase, arem, &alo);
+    const __amdgpu_buffer_rsrc_t rb = rsrc_aligned(bbase, brem, &blo);
 
     uint32_t arow[MT], brow[NT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         const int ml = (wm * MT + mt) * 16 + r;
-        arow[mt] = (m0 + ml < p.M) ? (uint32_t)ml * p.lda : kOobOffset;
+        arow[mt] = (m0 + ml < p.M) ? (uint32_t)ml * p.lda + alo : kOobOffset;
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const int nl = (wn * NT + nt) * 16 + r;
-        brow[nt] = (n0 + nl < p.N) ? (uint32_t)nl * p.ldb : kOobOffset;
+        brow[nt] = (n0 + nl < p.N) ? (uint32_t)nl * p.ldb + blo : kOobOffset;
     }
 
     const int nblk = (p.K + 255) / 256;
@@ -100,12 +109,12 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const uint32_t off = (kc < p.K && arow[mt] != kOobOffset) ? arow[mt] + kc : kOobOffset;
-                a[mt][j] = __builtin_bit_cast(i32x4, buf_load_x4(ra, off));
+                a[mt][j] = load16<AL>(ra, off);
             }
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const uint32_t off = (brow[nt] != kOobOffset) ? brow[nt] + kc : kOobOffset;
-                b[nt][j] = __builtin_bit_cast(i32x4, buf_load_x4(rb, off));
+                b[nt][j] = load16<AL>(rb, off);
             }
         }
         if (blk * 256 + 256 > p.K) {
@@ -155,8 +164,12 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
     const int tiles = gridDim.x * gridDim.y;
     const int tile_id = tile_m * gridDim.x + tile_n;
     if (p.splits > 1) {
+        // Partials are written through to memory (coherent stores) so the
+        // reducing workgroup can read them without cache maintenance.
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(
+            p.part, (uint32_t)min<size_t>((size_t)p.splits * tiles * BM * BN * 4, 0x7FFFFFFFull));
         if (wk == 0) {
-            int32_t* mine = p.part + ((size_t)split * tiles + tile_id) * (BM * BN);
+            const size_t base = ((size_t)split * tiles + tile_id) * (BM * BN);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -165,9 +178,10 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
                     for (int i = 0; i < 4; ++i) {
                         const int ml = (wm * MT + mt) * 16 + 4 * g + i;
                         const int nl = (wn * NT + nt) * 16 + r;
-                        mine[ml * BN + nl] = acc[mt][nt][i];
+                        buf_store_x1_coherent(rp, (uint32_t)((base + ml * BN + nl) * 4), (uint32_t)acc[mt][nt][i]);
                     }
         }
+        if (p.defer_reduce) return;
         if (!split_ticket(&p.tickets[tile_id], (unsigned)p.splits, &last_flag)) return;
         if (wk != 0) return;
 #pragma unroll
@@ -180,7 +194,8 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
                     const int nl = (wn * NT + nt) * 16 + r;
                     int32_t s = 0;
                     for (int sp = 0; sp < p.splits; ++sp)
-                        s += p.part[((size_t)sp * tiles + tile_id) * (BM * BN) + ml * BN + nl];
+                        s += (int32_t)buf_load_x1_coherent(
+                            rp, (uint32_t)((((size_t)sp * tiles + tile_id) * (BM * BN) + ml * BN + nl) * 4));
                     acc[mt][nt][i] = s;
                 }
     } else if (wk != 0) {
@@ -218,21 +233,22 @@ static const S8Config kS8Configs[] = {
 int s8_config_count() { return (int)(sizeof(kS8Configs) / sizeof(kS8Configs[0])); }
 S8Config s8_config(int idx) { return kS8Configs[idx]; }
 
-template <int EPI>
-static hipError_t launch_s8_epi(int cfg, dim3 grid, const S8Args& a, hipStream_t s) {
+template <int EPI, int AL>
+static hipError_t launch_s8_cfg(int cfg, dim3 grid, const S8Args& a, hipStream_t s) {
     switch (cfg) {
-        case 0: hipLaunchKernelGGL((dnnopt_mfma_s8<1, 1, 1, 4, 2, EPI>), grid, dim3(512), 0, s, a); break;
-        case 1: hipLaunchKernelGGL((dnnopt_mfma_s8<1, 2, 1, 2, 4, EPI>), grid, dim3(512), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 2, 2, 2, 1, EPI>), grid, dim3(256), 0, s, a); break;
-        case 3: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 2, 4, 2, 1, EPI>), grid, dim3(512), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 4, 4, 1, 1, EPI>), grid, dim3(256), 0, s, a); break;
+        case 0: hipLaunchKernelGGL((dnnopt_mfma_s8<1, 1, 1, 4, 2, EPI, AL>), grid, dim3(512), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((dnnopt_mfma_s8<1, 2, 1, 2, 4, EPI, AL>), grid, dim3(512), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 2, 2, 2, 1, EPI, AL>), grid, dim3(256), 0, s, a); break;
+        case 3: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 2, 4, 2, 1, EPI, AL>), grid, dim3(512), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 4, 4, 1, 1, EPI, AL>), grid, dim3(256), 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_mfma_s8(int cfg_idx, int epi, dim3 grid, const S8Args& a, hipStream_t s) {
-    return epi ? launch_s8_epi<1>(cfg_idx, grid, a, s) : launch_s8_epi<0>(cfg_idx, grid, a, s);
+hipError_t launch_mfma_s8(int cfg_idx, int epi, int aligned, dim3 grid, const S8Args& a, hipStream_t s) {
+    if (epi) return aligned ? launch_s8_cfg<1, 1>(cfg_idx, grid, a, s) : launch_s8_cfg<1, 0>(cfg_idx, grid, a, s);
+    return aligned ? launch_s8_cfg<0, 1>(cfg_idx, grid, a, s) : launch_s8_cfg<0, 0>(cfg_idx, grid, a, s);
 }
 
 }  // namespace dnnopt_hip

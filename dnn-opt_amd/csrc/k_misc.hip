@@ -11,6 +11,7 @@ namespace dnnopt_hip {
 // (no fused multiply-add), then alpha*acc + beta*C with C always read: the
 // reference's scalar loop (src/gemm/gemm.cpp:88-100) as compiled for a target
 // without FMA contraction.  Used for GemmAlgo::kNaive.
+#pragma clang fp contract(off)
 __global__ __launch_bounds__(256) void dnnopt_naive_f32(int M, int N, int K, float alpha, const float* A,
                                                        int lda, const float* B, int ldb, float beta, float* C,
                                                        int ldc) {
@@ -19,10 +20,16 @@ __global__ __launch_bounds__(256) void dnnopt_naive_f32(int M, int N, int K, flo
     if (i >= M || j >= N) return;
     const float* a = A + (size_t)i * lda;
     float acc = 0.0f;
-    for (int k = 0; k < K; ++k) acc = __fadd_rn(acc, __fmul_rn(a[k], B[(size_t)k * ldb + j]));
+    for (int k = 0; k < K; ++k) {
+        const float prod = a[k] * B[(size_t)k * ldb + j];
+        acc = acc + prod;
+    }
     float* c = C + (size_t)i * ldc + j;
-    *c = __fadd_rn(__fmul_rn(alpha, acc), __fmul_rn(beta, *c));
+    const float t0 = alpha * acc;
+    const float t1 = beta * *c;
+    *c = t0 + t1;
 }
+#pragma clang fp contract(on)
 
 // Y[i*incy] = fma(alpha, X[i*incx], Y[i*incy])  (src/blas/cblas_saxpy.cpp:17-49
 // computes the same fused update on its NEON path).
@@ -106,7 +113,15 @@ __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restr
     if (valid && s_lo < s_hi) {
         const float* src = part + (size_t)tile_id * bm * bn + local;
         s = src[(size_t)s_lo * stride];
-        for (int sp = s_lo + 1; sp < s_hi; ++sp) s += src[(size_t)sp * stride];
+        int sp = s_lo + 1;
+        for (; sp + 8 <= s_hi; sp += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(sp + u) * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
+        for (; sp < s_hi; ++sp) s += src[(size_t)sp * stride];
     }
     red[q][o] = s;
     __syncthreads();
@@ -124,6 +139,78 @@ hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int 
     const unsigned blocks = (unsigned)((outs + 31) / 32);
     hipLaunchKernelGGL(dnnopt_splitk_reduce, dim3(blocks), dim3(256), 0, s, part, splits, tiles_n,
                        tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc);
+    return hipGetLastError();
+}
+
+// Sum the k-split partials of the skinny kernel, [split][M][ncols_pad], in
+// ascending split order and apply the reference epilogue.  Column tile t of T
+// (width tw) has splits_of_tile(t, G, T) partials.  All loads of an output
+// are issued before the first add.
+__global__ __launch_bounds__(256) void dnnopt_skinny_reduce(const float* __restrict__ part, int G, int T, int tw,
+                                                           int M, int N, int ncols_pad, float alpha, float beta,
+                                                           float* C, int ldc) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int m = blockIdx.y;
+    if (n >= N) return;
+    const int splits = splits_of_tile(n / tw, G, T);
+    const float* src = part + (size_t)m * ncols_pad + n;
+    const size_t stride = (size_t)M * ncols_pad;
+    float s = src[0];
+    int sp = 1;
+    for (; sp + 16 <= splits; sp += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = src[(size_t)(sp + u) * stride];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) s += v[u];
+    }
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+        if (sp + u < splits) v[u] = src[(size_t)(sp + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+        if (sp + u < splits) s += v[u];
+    float* c = C + (size_t)m * ldc + n;
+    *c = epilogue(s, alpha, beta, c);
+}
+
+// Sum exact int32 partial tiles [split][tile][bm*bn] and store C.
+__global__ __launch_bounds__(256) void dnnopt_s8_reduce(const int32_t* __restrict__ part, int splits, int tiles_n,
+                                                       int tiles, int bm, int bn, int M, int N, int epi,
+                                                       const float* scale, void* C, int ldc) {
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long long)M * N) return;
+    const int m = (int)(idx / N), n = (int)(idx % N);
+    const int tile_id = (m / bm) * tiles_n + n / bn;
+    const int32_t* src = part + (size_t)tile_id * bm * bn + (size_t)(m % bm) * bn + (n % bn);
+    const size_t stride = (size_t)tiles * bm * bn;
+    int32_t s = 0;
+    int sp = 0;
+    for (; sp + 8 <= splits; sp += 8) {
+        int32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(sp + u) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; sp < splits; ++sp) s += src[sp * stride];
+    if (epi) static_cast<float*>(C)[(size_t)m * ldc + n] = (float)s * scale[n];
+    else static_cast<int32_t*>(C)[(size_t)m * ldc + n] = s;
+}
+
+hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, int N, int ncols_pad,
+                                float alpha, float beta, float* C, int ldc, hipStream_t s) {
+    hipLaunchKernelGGL(dnnopt_skinny_reduce, dim3((N + 255) / 256, M), dim3(256), 0, s, part, G, T, tw, M, N,
+                       ncols_pad, alpha, beta, C, ldc);
+    return hipGetLastError();
+}
+
+hipError_t launch_s8_reduce(const int32_t* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
+                            int N, int epi, const float* scale, void* C, int ldc, hipStream_t s) {
+    const long long outs = (long long)M * N;
+    hipLaunchKernelGGL(dnnopt_s8_reduce, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, part, splits,
+                       tiles_n, tiles_n * tiles_m, bm, bn, M, N, epi, scale, C, ldc);
     return hipGetLastError();
 }
 

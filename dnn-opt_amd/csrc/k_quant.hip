@@ -93,15 +93,15 @@ static unsigned grid_for(long long total) {
     return (unsigned)b;
 }
 
-hipError_t launch_quant_prepare(const float* A, int lda, const float* B, int ldb, int M, int N, int K,
+hipError_t launch_quant_prepare(const float* A, int lda, const float* B, int ldb, int M, int N, int K, int ldq,
                                 unsigned* amax, int8_t* qA, int8_t* qB, hipStream_t s) {
     hipLaunchKernelGGL(dnnopt_zero_u32, dim3(1), dim3(64), 0, s, amax, 2);
     hipLaunchKernelGGL(dnnopt_absmax, dim3(grid_for((long long)M * K)), dim3(256), 0, s, A, M, K, lda, amax);
     hipLaunchKernelGGL(dnnopt_absmax, dim3(grid_for((long long)K * N)), dim3(256), 0, s, B, K, N, ldb, amax + 1);
     hipLaunchKernelGGL(dnnopt_quantize, dim3(grid_for((long long)M * K)), dim3(256), 0, s, A, M, K, lda, 0, amax,
-                       qA, K);
+                       qA, ldq);
     hipLaunchKernelGGL(dnnopt_quantize, dim3(grid_for((long long)K * N)), dim3(256), 0, s, B, K, N, ldb, 1,
-                       amax + 1, qB, K);
+                       amax + 1, qB, ldq);
     return hipGetLastError();
 }
 

@@ -59,6 +59,14 @@ __device__ __forceinline__ void unpack_b(const u32x4& raw, float* out) {
     }
 }
 
+// B is read exactly once: non-temporal loads keep it from displacing data
+// that is reused (A, partial sums) in the caches.
+template <int AL>
+__device__ __forceinline__ u32x4 load_row(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (AL) return buf_load_x4_stream(r, off);
+    return buf_load_x4_unaligned(r, off);
+}
+
 template <int MODE>
 __device__ __forceinline__ float load_a(const void* A, size_t idx) {
     if constexpr (MODE == kSkinnyBF16) {
@@ -70,12 +78,60 @@ __device__ __forceinline__ float load_a(const void* A, size_t idx) {
     }
 }
 
-template <int MR, int NW, int MODE>
+// A values of rows m < MR at k, k+1, ..., k+UG-1 into av[m][u].  A is tiny
+// and uniform across the wave, so these are scalar loads; the layouts give
+// the compiler constant offsets from one base so it merges them into wide
+// s_load_dwordxN that are issued together with the B loads.
+//   AK = 0: A row-major (k contiguous), 4-byte aligned rows
+//   AK = 1: A stored K x M (m contiguous), fp32
+//   AK = 2: any layout, element by element (bf16 rows off 4-byte alignment)
+template <int MR, int UG, int MODE, int AK>
+__device__ __forceinline__ void load_a_block(const SkinnyArgs& p, int k, float (&av)[MR][UG]) {
+    if constexpr (AK == 0 && MODE == kSkinnyBF16) {
+        static_assert(UG % 2 == 0, "bf16 A groups load whole dwords");
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const uint32_t* ap = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.A) +
+                                                                   (size_t)m * p.a_sm + k);
+#pragma unroll
+            for (int d = 0; d < UG / 2; ++d) {
+                const uint32_t w2 = ap[d];
+                av[m][2 * d] = bf16_lo(w2);
+                av[m][2 * d + 1] = bf16_hi(w2);
+            }
+        }
+    } else if constexpr (AK == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const float* ap = static_cast<const float*>(p.A) + (size_t)m * p.a_sm + k;
+#pragma unroll
+            for (int u = 0; u < UG; ++u) av[m][u] = MODE == kSkinnyF2B ? round_bf16(ap[u]) : ap[u];
+        }
+    } else if constexpr (AK == 1) {
+#pragma unroll
+        for (int u = 0; u < UG; ++u) {
+            const float* ap = static_cast<const float*>(p.A) + (size_t)(k + u) * p.a_sk;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) av[m][u] = MODE == kSkinnyF2B ? round_bf16(ap[m]) : ap[m];
+        }
+    } else {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int u = 0; u < UG; ++u) av[m][u] = load_a<MODE>(p.A, (size_t)m * p.a_sm + (size_t)(k + u) * p.a_sk);
+    }
+}
+
+// AL = 1: every row of B starts on a 4-byte boundary (always true for fp32);
+// AL = 0: bf16 rows may start on a 2-byte boundary and are funnel-shifted.
+// AK: layout of A, see load_a_block.
+template <int MR, int NW, int MODE, int AL, int AK>
 __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     constexpr int VEC = SkinnyTraits<MODE>::VEC;
     constexpr int ES = SkinnyTraits<MODE>::ES;
     constexpr int TW = 64 * VEC;
-    constexpr int U = kSkinnyUnroll;
+    constexpr int U = kSkinnyUnroll;  // rows of B in flight per wave
+    constexpr int UG = 8;             // rows per group of A values
     constexpr int NT = NW * 64;
     // LDS reduction in passes of G rows, at most 32 KiB of LDS per pass.
     constexpr int GMAX = 32768 / (NW * TW * 4) > 0 ? 32768 / (NW * TW * 4) : 1;
@@ -88,22 +144,32 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
 
     const int lane = lane_id();
     const int w = wave_id();
-    const int tile = blockIdx.x;
-    const int split = blockIdx.y;
+    // Workgroup -> (column tile, k-split): the grid has G = gridDim.x
+    // workgroups for T column tiles, and every tile gets G/T or G/T + 1
+    // k-splits, so each workgroup streams (nearly) the same number of bytes
+    // whatever T is.
+    const SplitPos sp = split_pos((int)blockIdx.x, (int)gridDim.x, p.tiles);
+    const int tile = sp.tile;
+    const int split = sp.split;
+    const int nsplit = sp.nsplit;
     const int col0 = tile * TW;
-    const long long chunks = (long long)p.splits * NW;
+    // k is cut into blocks of U rows; chunk cw (wave w of split `split`)
+    // owns a contiguous run of blocks, so every chunk but the last starts and
+    // ends on a multiple of U.
+    const long long nblk = (p.K + U - 1) / U;
+    const long long chunks = (long long)nsplit * NW;
     const long long cw = (long long)split * NW + w;
-    const int k_lo = (int)(((long long)p.K * cw) / chunks);
-    const int k_hi = (int)(((long long)p.K * (cw + 1)) / chunks);
-    const int kb = (int)(((long long)p.K * ((long long)split * NW)) / chunks);
+    const int k_lo = (int)((nblk * cw) / chunks) * U;
+    const int k_hi = min(p.K, (int)((nblk * (cw + 1)) / chunks) * U);
+    const int kb = (int)((nblk * ((long long)split * NW)) / chunks) * U;
 
     // Buffer range: from row kb, column col0 to the last element of B.
     const char* bbase = static_cast<const char*>(p.B) + ((size_t)kb * p.ldb + col0) * ES;
     const size_t remain = ((size_t)(p.K - 1 - kb) * p.ldb + (size_t)(p.N - col0)) * ES;
-    const uint32_t nrec = remain > 0x7FFFFFFFull ? 0x7FFFFFFFu : (uint32_t)remain;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(bbase, nrec);
+    uint32_t base_lo = 0;
+    const __amdgpu_buffer_rsrc_t rs = rsrc_aligned(bbase, remain, &base_lo);
     const uint32_t rowbytes = (uint32_t)p.ldb * ES;
-    const uint32_t lane_off = (uint32_t)lane * VEC * ES;
+    const uint32_t lane_off = (uint32_t)lane * VEC * ES + base_lo;
 
     float acc[MR][VEC];
 #pragma unroll
@@ -115,21 +181,24 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     for (; k + U <= k_hi; k += U) {
         u32x4 raw[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) raw[u] = buf_load_x4(rs, (uint32_t)(k + u - kb) * rowbytes + lane_off);
+        for (int u = 0; u < U; ++u) raw[u] = load_row<AL>(rs, (uint32_t)(k + u - kb) * rowbytes + lane_off);
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            float bv[VEC];
-            unpack_b<MODE>(raw[u], bv);
+        for (int g0 = 0; g0 < U; g0 += UG) {
+            float av[MR][UG];
+            load_a_block<MR, UG, MODE, AK>(p, k + g0, av);
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const float a = load_a<MODE>(p.A, (size_t)m * p.a_sm + (size_t)(k + u) * p.a_sk);
+            for (int u = 0; u < UG; ++u) {
+                float bv[VEC];
+                unpack_b<MODE>(raw[g0 + u], bv);
 #pragma unroll
-                for (int v = 0; v < VEC; ++v) acc[m][v] = __builtin_fmaf(a, bv[v], acc[m][v]);
+                for (int m = 0; m < MR; ++m)
+#pragma unroll
+                    for (int v = 0; v < VEC; ++v) acc[m][v] = __builtin_fmaf(av[m][u], bv[v], acc[m][v]);
             }
         }
     }
     for (; k < k_hi; ++k) {
-        const u32x4 raw = buf_load_x4(rs, (uint32_t)(k - kb) * rowbytes + lane_off);
+        const u32x4 raw = load_row<AL>(rs, (uint32_t)(k - kb) * rowbytes + lane_off);
         float bv[VEC];
         unpack_b<MODE>(raw, bv);
 #pragma unroll
@@ -140,8 +209,12 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
         }
     }
 
-    // Reduce the NW waves of this workgroup, waves in ascending order.
-    float out[P][I];
+    // Reduce the NW waves of this workgroup, waves in ascending order.  Each
+    // thread owns float4 groups of 4 consecutive columns of one row; LDS is
+    // used in passes of G rows.
+    constexpr int Q = TW / 4;                 // float4 groups per row of the tile
+    constexpr int I4 = (G * Q + NT - 1) / NT; // groups per thread per pass
+    f32x4 out[P][I4];
 #pragma unroll
     for (int pass = 0; pass < P; ++pass) {
         if (pass) __syncthreads();
@@ -158,99 +231,128 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
         }
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < I; ++i) {
-            const int idx = (int)threadIdx.x + i * NT;
-            const int g = idx / TW;
-            const int col = idx % TW;
-            float s = 0.0f;
-            if (idx < G * TW && pass * G + g < MR) {
-                s = red[g * TW + col];
+        for (int i = 0; i < I4; ++i) {
+            const int gi = (int)threadIdx.x + i * NT;
+            const int g = gi / Q, c4 = gi % Q;
+            f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+            if (gi < G * Q && pass * G + g < MR) {
+                sum = *reinterpret_cast<const f32x4*>(&red[g * TW + c4 * 4]);
 #pragma unroll
-                for (int w2 = 1; w2 < NW; ++w2) s += red[(w2 * G + g) * TW + col];
+                for (int w2 = 1; w2 < NW; ++w2) sum += *reinterpret_cast<const f32x4*>(&red[(w2 * G + g) * TW + c4 * 4]);
             }
-            out[pass][i] = s;
+            out[pass][i] = sum;
         }
     }
 
-    if (p.splits == 1) {
+    auto store_c = [&](int m, int c4, const f32x4& v) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int n = col0 + c4 * 4 + e;
+            if (n < p.N) {
+                float* c = p.C + (size_t)m * p.ldc + n;
+                *c = epilogue(v[e], p.alpha, p.beta, c);
+            }
+        }
+    };
+
+    if (nsplit == 1) {
 #pragma unroll
         for (int pass = 0; pass < P; ++pass)
 #pragma unroll
-            for (int i = 0; i < I; ++i) {
-                const int idx = (int)threadIdx.x + i * NT;
-                const int m = pass * G + idx / TW;
-                const int n = col0 + idx % TW;
-                if (idx < G * TW && m < MR && n < p.N) {
-                    float* c = p.C + (size_t)m * p.ldc + n;
-                    *c = epilogue(out[pass][i], p.alpha, p.beta, c);
-                }
+            for (int i = 0; i < I4; ++i) {
+                const int gi = (int)threadIdx.x + i * NT;
+                const int m = pass * G + gi / Q;
+                if (gi < G * Q && m < MR) store_c(m, gi % Q, out[pass][i]);
             }
         return;
     }
 
-    // Split-k: publish this workgroup's partial sums, last arrival reduces.
-    float* mine = p.part + (size_t)split * MR * p.ncols_pad;
+    // Split-k: publish this workgroup's partial sums [split][MR][ncols_pad].
+    // They are written through to memory (sc0 sc1) so that the workgroup that
+    // reduces them -- here or in a separate kernel -- reads them without any
+    // cache maintenance.
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(p.part, (uint32_t)min<size_t>((size_t)p.splits * MR * p.ncols_pad * 4, 0x7FFFFFFFull));
 #pragma unroll
     for (int pass = 0; pass < P; ++pass)
 #pragma unroll
-        for (int i = 0; i < I; ++i) {
-            const int idx = (int)threadIdx.x + i * NT;
-            const int m = pass * G + idx / TW;
-            if (idx < G * TW && m < MR) mine[(size_t)m * p.ncols_pad + col0 + idx % TW] = out[pass][i];
+        for (int i = 0; i < I4; ++i) {
+            const int gi = (int)threadIdx.x + i * NT;
+            const int m = pass * G + gi / Q;
+            if (gi < G * Q && m < MR) {
+                const uint32_t off = (uint32_t)((((size_t)split * MR + m) * p.ncols_pad + col0 + (gi % Q) * 4) * 4);
+                buf_store_x4_coherent(rp, off, out[pass][i]);
+            }
         }
-    if (!split_ticket(&p.tickets[tile], (unsigned)p.splits, &last_flag)) return;
+    if (p.defer_reduce) return;
+    if (!split_ticket(&p.tickets[tile], (unsigned)nsplit, &last_flag)) return;
 
+    // Last workgroup of the tile: add the partials in split order.
 #pragma unroll
     for (int pass = 0; pass < P; ++pass)
 #pragma unroll
-        for (int i = 0; i < I; ++i) {
-            const int idx = (int)threadIdx.x + i * NT;
-            const int m = pass * G + idx / TW;
-            const int n = col0 + idx % TW;
-            if (idx < G * TW && m < MR && n < p.N) {
-                const float* src = p.part + (size_t)m * p.ncols_pad + n;
-                const size_t stride = (size_t)MR * p.ncols_pad;
-                float s = src[0];
-                for (int sp = 1; sp < p.splits; ++sp) s += src[sp * stride];
-                float* c = p.C + (size_t)m * p.ldc + n;
-                *c = epilogue(s, p.alpha, p.beta, c);
+        for (int i = 0; i < I4; ++i) {
+            const int gi = (int)threadIdx.x + i * NT;
+            const int m = pass * G + gi / Q;
+            if (gi < G * Q && m < MR) {
+                const uint32_t off0 = (uint32_t)((((size_t)m) * p.ncols_pad + col0 + (gi % Q) * 4) * 4);
+                const uint32_t stride = (uint32_t)((size_t)MR * p.ncols_pad * 4);
+                f32x4 sum = buf_load_x4_coherent(rp, off0);
+                int j = 1;
+                for (; j + 8 <= nsplit; j += 8) {
+                    f32x4 v[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) v[u] = buf_load_x4_coherent(rp, off0 + (uint32_t)(j + u) * stride);
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) sum += v[u];
+                }
+                for (; j < nsplit; ++j) sum += buf_load_x4_coherent(rp, off0 + (uint32_t)j * stride);
+                store_c(m, gi % Q, sum);
             }
         }
 }
 
 // ---------------------------------------------------------------- launch table
-template <int MODE, int NW>
+template <int MODE, int NW, int AL, int AK>
 static hipError_t launch_mr(int mr, dim3 grid, const SkinnyArgs& a, hipStream_t s) {
     dim3 block(NW * 64);
     switch (mr) {
-        case 1: hipLaunchKernelGGL((dnnopt_skinny<1, NW, MODE>), grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL((dnnopt_skinny<2, NW, MODE>), grid, block, 0, s, a); break;
-        case 3: hipLaunchKernelGGL((dnnopt_skinny<3, NW, MODE>), grid, block, 0, s, a); break;
-        case 4: hipLaunchKernelGGL((dnnopt_skinny<4, NW, MODE>), grid, block, 0, s, a); break;
-        case 5: hipLaunchKernelGGL((dnnopt_skinny<5, NW, MODE>), grid, block, 0, s, a); break;
-        case 6: hipLaunchKernelGGL((dnnopt_skinny<6, NW, MODE>), grid, block, 0, s, a); break;
-        case 7: hipLaunchKernelGGL((dnnopt_skinny<7, NW, MODE>), grid, block, 0, s, a); break;
-        case 8: hipLaunchKernelGGL((dnnopt_skinny<8, NW, MODE>), grid, block, 0, s, a); break;
+        case 1: hipLaunchKernelGGL((dnnopt_skinny<1, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((dnnopt_skinny<2, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL((dnnopt_skinny<3, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((dnnopt_skinny<4, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
+        case 5: hipLaunchKernelGGL((dnnopt_skinny<5, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
+        case 6: hipLaunchKernelGGL((dnnopt_skinny<6, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
+        case 7: hipLaunchKernelGGL((dnnopt_skinny<7, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
+        case 8: hipLaunchKernelGGL((dnnopt_skinny<8, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-template <int MODE>
+template <int MODE, int AL, int AK>
 static hipError_t launch_nw(int mr, int nw, dim3 grid, const SkinnyArgs& a, hipStream_t s) {
     switch (nw) {
-        case 4: return launch_mr<MODE, 4>(mr, grid, a, s);
-        case 8: return launch_mr<MODE, 8>(mr, grid, a, s);
-        case 16: return launch_mr<MODE, 16>(mr, grid, a, s);
+        case 4: return launch_mr<MODE, 4, AL, AK>(mr, grid, a, s);
+        case 8: return launch_mr<MODE, 8, AL, AK>(mr, grid, a, s);
+        case 16: return launch_mr<MODE, 16, AL, AK>(mr, grid, a, s);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_skinny(int mode, int mr, int nw, dim3 grid, const SkinnyArgs& a, hipStream_t s) {
+hipError_t launch_skinny(int mode, int mr, int nw, int b_aligned, int a_layout, dim3 grid, const SkinnyArgs& a,
+                         hipStream_t s) {
     switch (mode) {
-        case kSkinnyF32: return launch_nw<kSkinnyF32>(mr, nw, grid, a, s);
-        case kSkinnyBF16: return launch_nw<kSkinnyBF16>(mr, nw, grid, a, s);
-        case kSkinnyF2B: return launch_nw<kSkinnyF2B>(mr, nw, grid, a, s);
+        case kSkinnyF32:
+            return a_layout == 1 ? launch_nw<kSkinnyF32, 1, 1>(mr, nw, grid, a, s)
+                                 : launch_nw<kSkinnyF32, 1, 0>(mr, nw, grid, a, s);
+        case kSkinnyBF16:
+            if (b_aligned)
+                return a_layout == 2 ? launch_nw<kSkinnyBF16, 1, 2>(mr, nw, grid, a, s)
+                                     : launch_nw<kSkinnyBF16, 1, 0>(mr, nw, grid, a, s);
+            return a_layout == 2 ? launch_nw<kSkinnyBF16, 0, 2>(mr, nw, grid, a, s)
+                                 : launch_nw<kSkinnyBF16, 0, 0>(mr, nw, grid, a, s);
+        case kSkinnyF2B: return launch_nw<kSkinnyF2B, 1, 0>(mr, nw, grid, a, s);
         default: return hipErrorInvalidValue;
     }
 }

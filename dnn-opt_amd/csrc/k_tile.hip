@@ -100,8 +100,12 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
     const int tiles = gridDim.x * gridDim.y;
     const int tile_id = tile_m * gridDim.x + tile_n;
     if (p.splits > 1) {
+        // Partials are written through to memory (coherent stores) so the
+        // reducing workgroup can read them without cache maintenance.
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(
+            p.part, (uint32_t)min<size_t>((size_t)p.splits * tiles * S::BM * S::BN * 4, 0x7FFFFFFFull));
         if (wk == 0) {
-            float* mine = p.part + ((size_t)split * tiles + tile_id) * (S::BM * S::BN);
+            const size_t base = ((size_t)split * tiles + tile_id) * (S::BM * S::BN);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -110,7 +114,7 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
                     for (int i = 0; i < 4; ++i) {
                         const int ml = (wm * MT + mt) * 16 + 4 * g + i;
                         const int nl = (wn * NT + nt) * 16 + r;
-                        mine[ml * S::BN + nl] = acc[mt][nt][i];
+                        buf_store_x1_coherent(rp, (uint32_t)((base + ml * S::BN + nl) * 4), as_u32(acc[mt][nt][i]));
                     }
         }
         if (p.defer_reduce) return;
@@ -124,10 +128,11 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
                 for (int i = 0; i < 4; ++i) {
                     const int ml = (wm * MT + mt) * 16 + 4 * g + i;
                     const int nl = (wn * NT + nt) * 16 + r;
-                    const float* src = p.part + (size_t)tile_id * (S::BM * S::BN) + ml * S::BN + nl;
+                    const size_t off0 = (size_t)tile_id * (S::BM * S::BN) + ml * S::BN + nl;
                     const size_t stride = (size_t)tiles * (S::BM * S::BN);
-                    float s = src[0];
-                    for (int sp = 1; sp < p.splits; ++sp) s += src[sp * stride];
+                    float s = as_f32(buf_load_x1_coherent(rp, (uint32_t)(off0 * 4)));
+                    for (int sp = 1; sp < p.splits; ++sp)
+                        s += as_f32(buf_load_x1_coherent(rp, (uint32_t)((off0 + sp * stride) * 4)));
                     acc[mt][nt][i] = s;
                 }
     } else if (wk != 0) {
@@ -255,7 +260,9 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_f32(TileArgs p) {
 // ---------------------------------------------------------------- bf16
 // MODE kTileBF16: A, B hold bf16 bit patterns.  MODE kTileF2B: A, B are fp32
 // and are rounded to bf16 (nearest even, reference formula) on load.
-template <int MT, int NT, int WM, int WN, int KW, int MODE>
+// AL = 0: rows of a bf16-storage A may start on a 2-byte boundary and are
+// read with funnel-shifted loads.
+template <int MT, int NT, int WM, int WN, int KW, int MODE, int AL>
 __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) {
     using S = TileShape<MT, NT, WM, WN, KW>;
     constexpr int KB = 128;
@@ -281,7 +288,8 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
     const size_t arem = (size_t)(p.M - 1 - m0) * p.lda + (p.K - ks);
     const char* bbase = B + ((size_t)ks * p.ldb + n0) * ES;
     const size_t brem = (size_t)(p.K - 1 - ks) * p.ldb + (p.N - n0);
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(abase, clamp_rec(arem * ES));
+    uint32_t alo = 0;
+    const __amdgpu_buffer_rsrc_t ra = rsrc_aligned(abase, arem * ES, &alo);
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase, clamp_rec(brem * ES));
 
     int mloc[MT], nloc[NT];
@@ -313,13 +321,17 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 if constexpr (MODE == kTileBF16) {
-                    const uint32_t off = (mval[mt] && kvalid > 0) ? ((uint32_t)mloc[mt] * p.lda + ko) * 2u : kOobOffset;
-                    a[mt][j] = buf_load_x4(ra, off);
+                    const uint32_t off =
+                        (mval[mt] && kvalid > 0) ? ((uint32_t)mloc[mt] * p.lda + ko) * 2u + alo : kOobOffset;
+                    if constexpr (AL) a[mt][j] = buf_load_x4(ra, off);
+                    else a[mt][j] = buf_load_x4_unaligned(ra, off);
                     if (kvalid < 8) a[mt][j] = keep_halves(a[mt][j], kvalid);
                 } else {
-                    const uint32_t off = (mval[mt] && kvalid > 0) ? ((uint32_t)mloc[mt] * p.lda + ko) * 4u : kOobOffset;
+                    const uint32_t off =
+                        (mval[mt] && kvalid > 0) ? ((uint32_t)mloc[mt] * p.lda + ko) * 4u + alo : kOobOffset;
                     u32x4 lo = buf_load_x4(ra, off);
                     u32x4 hi = buf_load_x4(ra, (mval[mt] && kvalid > 4) ? off + 16u : kOobOffset);
+                    (void)AL;
                     if (kvalid < 4) lo = keep_dwords(lo, kvalid);
                     if (kvalid < 8) hi = keep_dwords(hi, kvalid - 4);
 #pragma unroll
@@ -382,13 +394,14 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
             else if (!ta && tb) hipLaunchKernelGGL((dnnopt_tile_f32<MT, NT, WM, WN, KW, 0, 1>), grid, blk, 0, s, a); \
             else hipLaunchKernelGGL((dnnopt_tile_f32<MT, NT, WM, WN, KW, 1, 1>), grid, blk, 0, s, a);    \
         } else if (mode == kTileBF16) {                                                                  \
-            hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileBF16>), grid, blk, 0, s, a);    \
+            if (al) hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileBF16, 1>), grid, blk, 0, s, a); \
+            else hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileBF16, 0>), grid, blk, 0, s, a);    \
         } else {                                                                                         \
-            hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileF2B>), grid, blk, 0, s, a);     \
+            hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileF2B, 1>), grid, blk, 0, s, a);  \
         }                                                                                                \
         break;
 
-hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, dim3 grid, const TileArgs& a, hipStream_t s) {
+hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid, const TileArgs& a, hipStream_t s) {
     if (mode != kTileF32 && (ta || tb)) return hipErrorInvalidValue;
     const TileConfig c = kTileConfigs[cfg_idx];
     const dim3 blk(c.wm * c.wn * c.kw * 64);

@@ -31,16 +31,21 @@ struct SkinnyArgs {
     int ldb, ldc;
     int M, N, K;
     float alpha, beta;
-    int splits;
+    int splits;         // most k-splits of any tile (partial buffer rows)
     int ncols_pad;
+    int defer_reduce;   // splits > 1: 1 = only store partials (a reduce kernel follows)
+    int tiles;          // column tiles T; the grid has G >= T workgroups
 };
 
-constexpr int kSkinnyUnroll = 8;
+constexpr int kSkinnyUnroll = 16;
 inline int skinny_tile_cols(int mode) { return mode == kSkinnyBF16 ? 512 : 256; }
 inline int skinny_elem_bytes(int mode) { return mode == kSkinnyBF16 ? 2 : 4; }
 
-hipError_t launch_skinny(int mode, int mr, int nw, dim3 grid, const SkinnyArgs& a,
-                         hipStream_t s);
+// b_aligned: every row of B starts on a 4-byte boundary (checked by the host).
+// a_layout: 0 = A row-major with 4-byte aligned rows, 1 = A stored K x M (fp32),
+// 2 = bf16 A rows off 4-byte alignment (element loads).
+hipError_t launch_skinny(int mode, int mr, int nw, int b_aligned, int a_layout, dim3 grid,
+                         const SkinnyArgs& a, hipStream_t s);
 
 // ---------------------------------------------------------------- int8 MFMA
 // Exact s8 x s8 -> s32 with B stored N x K.  Each wave owns MT x NT tiles of
@@ -57,6 +62,7 @@ struct S8Args {
     int lda, ldb, ldc;
     int M, N, K;
     int splits;
+    int defer_reduce;    // splits > 1: 1 = only store partials (a reduce kernel follows)
 };
 
 struct S8Config {
@@ -65,7 +71,8 @@ struct S8Config {
 // Index into the table of built int8 configurations.
 int s8_config_count();
 S8Config s8_config(int idx);
-hipError_t launch_mfma_s8(int cfg_idx, int epi, dim3 grid, const S8Args& a, hipStream_t s);
+// aligned: all rows of A and B start on 4-byte boundaries (checked by the host).
+hipError_t launch_mfma_s8(int cfg_idx, int epi, int aligned, dim3 grid, const S8Args& a, hipStream_t s);
 
 // ---------------------------------------------------------------- fp32 / bf16 tiles
 // Row-major C (M x N) = alpha * op(A) op(B) + beta * C with MFMA tiles.
@@ -96,7 +103,8 @@ struct TileConfig {
 };
 int tile_config_count();
 TileConfig tile_config(int idx);
-hipError_t launch_tile(int mode, int cfg_idx, int transA, int transB, dim3 grid,
+// aligned: all rows of A start on 4-byte boundaries (matters for bf16 storage).
+hipError_t launch_tile(int mode, int cfg_idx, int transA, int transB, int aligned, dim3 grid,
                        const TileArgs& a, hipStream_t s);
 
 // ---------------------------------------------------------------- small kernels
@@ -111,9 +119,17 @@ hipError_t launch_fill(void* dst, size_t n, int dtype, int dist, uint64_t seed,
 // A (M x K) and B (K x N, written transposed as N x K), then after the int8
 // GEMM dequantize the int32 accumulators into C.
 hipError_t launch_quant_prepare(const float* A, int lda, const float* B, int ldb, int M, int N, int K,
-                                unsigned* amax, int8_t* qA, int8_t* qB, hipStream_t s);
+                                int ldq, unsigned* amax, int8_t* qA, int8_t* qB, hipStream_t s);
 hipError_t launch_dequant(const int32_t* acc, int M, int N, const unsigned* amax, float alpha,
                           float beta, float* C, int ldc, hipStream_t s);
+// Reduce skinny partials [split][M][ncols_pad] into C (epilogue applied);
+// tile t (of T, tile width tw) has splits_of_tile(t, G, T) partials.
+hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, int N, int ncols_pad,
+                                float alpha, float beta, float* C, int ldc, hipStream_t s);
+// Reduce int8 partial tiles [splits][tiles][bm*bn] (exact int32) into C:
+// epi 0 stores int32, epi 1 stores (float)acc * scale[n].
+hipError_t launch_s8_reduce(const int32_t* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
+                            int N, int epi, const float* scale, void* C, int ldc, hipStream_t s);
 // Reduce partial tiles [splits][tiles_m*tiles_n][bm*bn] into C (epilogue applied).
 hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm,
                                 int bn, int M, int N, float alpha, float beta, float* C, int ldc,

@@ -39,7 +39,14 @@ DNNOPT_SYNTH_FN uint64_t tensor_key(uint64_t seed, uint32_t tensor_id) {
 
 DNNOPT_SYNTH_FN uint64_t draw(uint64_t key, uint64_t i) { return mix64(key + (i + 1) * kGamma); }
 
+#if defined(__clang__)
+#define DNNOPT_NO_CONTRACT _Pragma("clang fp contract(off)")
+#else
+#define DNNOPT_NO_CONTRACT
+#endif
+
 DNNOPT_SYNTH_FN float uniform_value(uint64_t key, uint64_t i, double lo, double hi) {
+    DNNOPT_NO_CONTRACT
     const double u = (double)(draw(key, i) >> 40) * (1.0 / 16777216.0);
     const double span = hi - lo;
     const double scaled = span * u;
@@ -47,6 +54,7 @@ DNNOPT_SYNTH_FN float uniform_value(uint64_t key, uint64_t i, double lo, double 
 }
 
 DNNOPT_SYNTH_FN float normal_value(uint64_t key, uint64_t i, double mu, double sigma) {
+    DNNOPT_NO_CONTRACT
     const double u1 = (double)((draw(key, 2 * i) >> 40) + 1) * (1.0 / 16777216.0);
     const double u2 = (double)(draw(key, 2 * i + 1) >> 40) * (1.0 / 16777216.0);
     const double rad = sqrt(-2.0 * log(u1));

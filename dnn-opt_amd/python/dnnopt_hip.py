@@ -138,6 +138,26 @@ def _ptr(x):
     raise TypeError(f"cannot take the address of {type(x)!r}")
 
 
+def _share_torch_hip_runtime():
+    """When PyTorch-ROCm is installed, initialise its HIP runtime first.
+
+    The torch wheel ships its own libamdhip64 under the same soname as the
+    system one this library links.  Whichever copy a process loads first is
+    the one every later library binds to; loading the system copy first
+    leaves torch with a second, device-less runtime.  Letting torch go first
+    gives the process a single HIP runtime shared by torch tensors (device
+    memory, streams) and these kernels.
+    """
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        return
+    try:
+        torch.cuda.is_available()
+    except Exception:  # pragma: no cover - torch without a usable backend
+        pass
+
+
 class Lib:
     """Loaded libdnnopt_blas.so with typed entry points."""
 
@@ -145,6 +165,7 @@ class Lib:
         if not os.path.exists(path):
             raise FileNotFoundError(f"{path} is not built; run __graft_entry__.build() or make -C dnn-opt_amd")
         self.path = path
+        _share_torch_hip_runtime()
         self.so = ctypes.CDLL(path)
         for table in (C_ABI, BLAS_ABI):
             for name, (res, args) in table.items():

@@ -77,7 +77,12 @@ def test_plans_for_the_configs(lib):
         for N in (1009, 4099, 11003):
             p = lib.plan_sgemm(M, N, 2048)
             assert p["kernel"] == b.K_SKINNY_F32 and p["rows"] == M
-            assert p["grid_x"] == -(-N // 256)
+            tiles = -(-N // 256)
+            # G >= T workgroups, each tile split G/T or G/T + 1 ways
+            assert p["grid_x"] >= tiles and p["splits"] == -(-p["grid_x"] // tiles)
+            # more than one CU's worth of work: a whole number of workgroups per CU
+            if p["grid_x"] >= 256:
+                assert p["grid_x"] % 256 == 0 or p["grid_x"] == tiles
     assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TILE_F32
     p = lib.plan_sgemm(64, 64, 262144, transA=1)
     assert p["kernel"] == b.K_TILE_F32 and p["splits"] > 16

@@ -329,3 +329,47 @@ def test_empty_problems_do_not_touch_c(lib, dev):
     for M, N, K in ((0, 4, 4), (4, 0, 4), (4, 4, 0), (-1, 4, 4)):
         lib.sgemm(M, N, K, 1.0, A, 4, A, 4, 0.0, C, 4, stream=stream())
     assert (host(C) == 3.0).all()
+
+
+@pytest.mark.parametrize("kind,M,N,K", [("f32", 1, 4096, 4096), ("f32", 7, 1009, 2048), ("f32", 3, 257, 5000),
+                                        ("s8", 1, 4096, 4096), ("s8", 128, 4093, 4096), ("bf16", 4, 11008, 4096),
+                                        ("f32t", 64, 64, 262144)])
+def test_split_k_repeatable(lib, orc, dev, kind, M, N, K):
+    """Split-k launches reduce partial sums across workgroups; 25 repetitions
+    must agree bit for bit with each other and with the exact result."""
+    if kind == "s8":
+        A, B = u.ints8(orc, M * K, 1).reshape(M, K), u.ints8(orc, N * K, 2).reshape(N, K)
+        dA, dB = dev_copy(A, dev), dev_copy(B, dev)
+        want = (A.astype(np.float64) @ B.astype(np.float64).T).astype(np.int64)
+        outs = []
+        for _ in range(25):
+            dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+            lib.gemm_s8s8s32(M, N, K, dA, K, dB, K, dC, N, stream=stream())
+            outs.append(dC)
+        for o in outs:
+            assert np.array_equal(host(o).astype(np.int64), want)
+        return
+    if kind == "bf16":
+        A = u.bf16_bits(orc, u.normal(orc, M * K, 1)).reshape(M, K)
+        B = u.bf16_bits(orc, u.normal(orc, K * N, 2, 0, 0.02)).reshape(K, N)
+        dA, dB = dev_copy(A.view(np.int16), dev), dev_copy(B.view(np.int16), dev)
+        run = lambda dC: lib.gemm_bf16(M, N, K, 1.0, dA, K, dB, N, 0.0, dC, N, stream=stream())  # noqa: E731
+        want, scale = u.exact(u.bf16_value(A), u.bf16_value(B))
+    else:
+        ta = 1 if kind == "f32t" else 0
+        opA = u.uniform(orc, M * K, 1).reshape(M, K)
+        B = u.uniform(orc, K * N, 2).reshape(K, N)
+        A = np.ascontiguousarray(opA.T) if ta else opA
+        dA, dB = dev_copy(A, dev), dev_copy(B, dev)
+        run = lambda dC: lib.sgemm(M, N, K, 1.0, dA, A.shape[1], dB, N, 0.0, dC, N, transA=ta,  # noqa: E731
+                                   stream=stream())
+        want, scale = u.exact(opA, B)
+    outs = []
+    for _ in range(25):
+        dC = torch.full((M, N), np.nan, dtype=torch.float32, device=dev)
+        run(dC)
+        outs.append(dC)
+    first = host(outs[0])
+    u.assert_fp32_close(first, want, scale, K, f"split-k {kind} {M}x{N}x{K}")
+    for o in outs[1:]:
+        assert np.array_equal(host(o).view(np.uint32), first.view(np.uint32))
