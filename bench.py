@@ -399,12 +399,12 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "all"])
-    ap.add_argument("--detail", default=os.path.join(ROOT, "gpurun_out", "bench_detail.jsonl"))
+    ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "(multi-GPU sharding is described in DESIGN.md, not run).", file=sys.stderr)
+              "sharding across GPUs is not built.", file=sys.stderr)
         sys.exit(2)
 
     names = ["c1", "c2", "c3", "c4", "c5"] if args.workload == "all" else [args.workload]
@@ -431,7 +431,7 @@ def main():
         "cpu_baseline": cpu,
     }
     if args.detail:
-        os.makedirs(os.path.dirname(args.detail), exist_ok=True)
+        os.makedirs(os.path.dirname(os.path.abspath(args.detail)), exist_ok=True)
         with open(args.detail, "a") as f:
             for wl, rr in results.items():
                 f.write(json.dumps({"workload": wl, "desc": rr["desc"], "GBps_step": rr["value"],

@@ -37,7 +37,10 @@ struct SkinnyArgs {
     int tiles;          // column tiles T; the grid has G >= T workgroups
 };
 
-constexpr int kSkinnyUnroll = 16;
+#ifndef DNNOPT_SKINNY_UNROLL
+#define DNNOPT_SKINNY_UNROLL 16
+#endif
+constexpr int kSkinnyUnroll = DNNOPT_SKINNY_UNROLL;  // rows of B in flight per wave
 inline int skinny_tile_cols(int mode) { return mode == kSkinnyBF16 ? 512 : 256; }
 inline int skinny_elem_bytes(int mode) { return mode == kSkinnyBF16 ? 2 : 4; }
 

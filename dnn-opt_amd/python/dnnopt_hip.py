@@ -23,7 +23,9 @@ import os
 from ctypes import POINTER, c_char, c_double, c_float, c_int, c_size_t, c_uint16, c_uint32, c_uint64, c_void_p
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(PKG_DIR, "lib", "libdnnopt_blas.so")
+# DNNOPT_HIP_LIB selects another build of the library (e.g. a variant built
+# with different compile-time tunables); the default is this package's lib/.
+LIB_PATH = os.environ.get("DNNOPT_HIP_LIB") or os.path.join(PKG_DIR, "lib", "libdnnopt_blas.so")
 
 OK, ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_OUT_OF_MEMORY = range(6)
 
