@@ -155,6 +155,9 @@ __global__ __launch_bounds__(256) void dnnopt_skinny_reduce(const float* __restr
     const int splits = splits_of_tile(n / tw, G, T);
     const float* src = part + (size_t)m * ncols_pad + n;
     const size_t stride = (size_t)M * ncols_pad;
+    float* c = C + (size_t)m * ldc + n;
+    // C is requested together with the partials (one memory round trip).
+    const float c_old = beta != 0.0f ? *c : 0.0f;
     float s = src[0];
     int sp = 1;
     for (; sp + 16 <= splits; sp += 16) {
@@ -171,8 +174,7 @@ __global__ __launch_bounds__(256) void dnnopt_skinny_reduce(const float* __restr
 #pragma unroll
     for (int u = 0; u < 16; ++u)
         if (sp + u < splits) s += v[u];
-    float* c = C + (size_t)m * ldc + n;
-    *c = epilogue(s, alpha, beta, c);
+    *c = beta == 0.0f ? alpha * s : __builtin_fmaf(alpha, s, beta * c_old);
 }
 
 // Sum exact int32 partial tiles [split][tile][bm*bn] and store C.

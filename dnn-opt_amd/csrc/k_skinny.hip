@@ -137,7 +137,6 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     constexpr int GMAX = 32768 / (NW * TW * 4) > 0 ? 32768 / (NW * TW * 4) : 1;
     constexpr int G = MR < GMAX ? MR : GMAX;
     constexpr int P = (MR + G - 1) / G;
-    constexpr int I = (G * TW + NT - 1) / NT;
 
     __shared__ float red[NW * G * TW];
     __shared__ int last_flag;
@@ -170,6 +169,25 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     const __amdgpu_buffer_rsrc_t rs = rsrc_aligned(bbase, remain, &base_lo);
     const uint32_t rowbytes = (uint32_t)p.ldb * ES;
     const uint32_t lane_off = (uint32_t)lane * VEC * ES + base_lo;
+
+    // Unsplit tiles store C directly: fetch the C values of this thread's
+    // outputs now so that the read overlaps the main loop.
+    constexpr int QG = TW / 4;                  // float4 groups per row of the tile
+    constexpr int I4 = (G * QG + NT - 1) / NT;  // groups per thread per reduction pass
+    float c_pre[P][I4][4];
+#pragma unroll
+    for (int pass = 0; pass < P; ++pass)
+#pragma unroll
+        for (int i = 0; i < I4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                c_pre[pass][i][e] = 0.0f;
+                const int gi = (int)threadIdx.x + i * NT;
+                const int m = pass * G + gi / QG;
+                const int n = col0 + (gi % QG) * 4 + e;
+                if (nsplit == 1 && p.beta != 0.0f && gi < G * QG && m < MR && n < p.N)
+                    c_pre[pass][i][e] = p.C[(size_t)m * p.ldc + n];
+            }
 
     float acc[MR][VEC];
 #pragma unroll
@@ -212,8 +230,7 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     // Reduce the NW waves of this workgroup, waves in ascending order.  Each
     // thread owns float4 groups of 4 consecutive columns of one row; LDS is
     // used in passes of G rows.
-    constexpr int Q = TW / 4;                 // float4 groups per row of the tile
-    constexpr int I4 = (G * Q + NT - 1) / NT; // groups per thread per pass
+    constexpr int Q = QG;
     f32x4 out[P][I4];
 #pragma unroll
     for (int pass = 0; pass < P; ++pass) {
@@ -244,17 +261,6 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
         }
     }
 
-    auto store_c = [&](int m, int c4, const f32x4& v) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int n = col0 + c4 * 4 + e;
-            if (n < p.N) {
-                float* c = p.C + (size_t)m * p.ldc + n;
-                *c = epilogue(v[e], p.alpha, p.beta, c);
-            }
-        }
-    };
-
     if (nsplit == 1) {
 #pragma unroll
         for (int pass = 0; pass < P; ++pass)
@@ -262,7 +268,16 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
             for (int i = 0; i < I4; ++i) {
                 const int gi = (int)threadIdx.x + i * NT;
                 const int m = pass * G + gi / Q;
-                if (gi < G * Q && m < MR) store_c(m, gi % Q, out[pass][i]);
+                if (gi < G * Q && m < MR) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int n = col0 + (gi % Q) * 4 + e;
+                        if (n < p.N)
+                            p.C[(size_t)m * p.ldc + n] = p.beta == 0.0f ? p.alpha * out[pass][i][e]
+                                                                        : __builtin_fmaf(p.alpha, out[pass][i][e],
+                                                                                         p.beta * c_pre[pass][i][e]);
+                    }
+                }
             }
         return;
     }
@@ -287,29 +302,67 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     if (p.defer_reduce) return;
     if (!split_ticket(&p.tickets[tile], (unsigned)nsplit, &last_flag)) return;
 
-    // Last workgroup of the tile: add the partials in split order.
+    // Last workgroup of the tile: add the partials in split order.  Each
+    // thread owns float4 outputs of the whole tile; C (for beta != 0) and a
+    // chunk of CH partials per output are requested before any is used, so
+    // the tail costs one memory round trip per CH splits.
+    constexpr int OUTS = MR * QG;
+    constexpr int OPT = (OUTS + NT - 1) / NT;
+    constexpr int CH = OPT == 1 ? 16 : 8;
+    const uint32_t stride = (uint32_t)((size_t)MR * p.ncols_pad * 4);
+    uint32_t off0[OPT];
+    float c_old[OPT][4];
 #pragma unroll
-    for (int pass = 0; pass < P; ++pass)
+    for (int o = 0; o < OPT; ++o) {
+        const int idx = (int)threadIdx.x + o * NT;
+        const int m = idx / QG, n0 = col0 + (idx % QG) * 4;
+        off0[o] = idx < OUTS ? (uint32_t)(((size_t)m * p.ncols_pad + n0) * 4) : kOobOffset;
 #pragma unroll
-        for (int i = 0; i < I4; ++i) {
-            const int gi = (int)threadIdx.x + i * NT;
-            const int m = pass * G + gi / Q;
-            if (gi < G * Q && m < MR) {
-                const uint32_t off0 = (uint32_t)((((size_t)m) * p.ncols_pad + col0 + (gi % Q) * 4) * 4);
-                const uint32_t stride = (uint32_t)((size_t)MR * p.ncols_pad * 4);
-                f32x4 sum = buf_load_x4_coherent(rp, off0);
-                int j = 1;
-                for (; j + 8 <= nsplit; j += 8) {
-                    f32x4 v[8];
+        for (int e = 0; e < 4; ++e)
+            c_old[o][e] = (idx < OUTS && p.beta != 0.0f && n0 + e < p.N) ? p.C[(size_t)m * p.ldc + n0 + e] : 0.0f;
+    }
+    auto chunk = [&](int j, f32x4 (&v)[OPT][CH]) {
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) v[u] = buf_load_x4_coherent(rp, off0 + (uint32_t)(j + u) * stride);
+        for (int o = 0; o < OPT; ++o)
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) sum += v[u];
-                }
-                for (; j < nsplit; ++j) sum += buf_load_x4_coherent(rp, off0 + (uint32_t)j * stride);
-                store_c(m, gi % Q, sum);
-            }
+            for (int u = 0; u < CH; ++u)
+                v[o][u] = buf_load_x4_coherent(rp, j + u < nsplit && off0[o] != kOobOffset
+                                                       ? off0[o] + (uint32_t)(j + u) * stride
+                                                       : kOobOffset);
+    };
+    f32x4 sum[OPT];
+    {
+        f32x4 v[OPT][CH];
+        chunk(0, v);
+#pragma unroll
+        for (int o = 0; o < OPT; ++o) {
+            sum[o] = v[o][0];
+#pragma unroll
+            for (int u = 1; u < CH; ++u)
+                if (u < nsplit) sum[o] += v[o][u];
         }
+    }
+    for (int j = CH; j < nsplit; j += CH) {
+        f32x4 v[OPT][CH];
+        chunk(j, v);
+#pragma unroll
+        for (int o = 0; o < OPT; ++o)
+#pragma unroll
+            for (int u = 0; u < CH; ++u)
+                if (j + u < nsplit) sum[o] += v[o][u];
+    }
+#pragma unroll
+    for (int o = 0; o < OPT; ++o) {
+        const int idx = (int)threadIdx.x + o * NT;
+        const int m = idx / QG, n0 = col0 + (idx % QG) * 4;
+        if (idx < OUTS) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (n0 + e < p.N)
+                    p.C[(size_t)m * p.ldc + n0 + e] = p.beta == 0.0f ? p.alpha * sum[o][e]
+                                                                     : __builtin_fmaf(p.alpha, sum[o][e], p.beta * c_old[o][e]);
+        }
+    }
 }
 
 // ---------------------------------------------------------------- launch table
