@@ -298,9 +298,12 @@ def run_gpu(args, wl_name):
     }
 
 
+def _traffic_file_stem(kernel):
+    return kernel.replace("<", "_").replace(">", "").replace(", ", "_").replace("[", "_").replace("]", "")
+
+
 def read_traffic(kernel, wl):
-    safe = kernel.replace("<", "_").replace(">", "").replace(", ", "_").replace("[", "_").replace("]", "")
-    path = os.path.join(ROOT, "profiles", f"{safe}_{wl}_traffic.json")
+    path = os.path.join(ROOT, "profiles", f"{_traffic_file_stem(kernel)}_{wl}_traffic.json")
     if not os.path.exists(path):
         return None
     try:
@@ -392,6 +395,99 @@ def cpu_baseline(cases, budget_s=20.0):
     }
 
 
+def _short_kernel_name(name):
+    """'void dnnopt_hip::dnnopt_skinny<7, 8, 0, 1, 0>(dnnopt_hip::SkinnyArgs)' -> 'dnnopt_skinny<7, 8, 0, 1, 0>'."""
+    name = name.strip()
+    if name.startswith("void "):
+        name = name[5:]
+    depth, cut = 0, len(name)
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            cut = i
+            break
+    return name[:cut].replace("dnnopt_hip::", "")
+
+
+def rocprof_summary(kernel, workload, trace_csv, pmc=None):
+    """Summarise rocprofv3 CSV output for one kernel instance.
+
+    trace_csv: *_kernel_trace.csv of `rocprofv3 --kernel-trace --stats -f csv`.
+    pmc: optional (fetch_csv, write_csv, copy_fetch_csv, copy_write_csv) from
+    `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of the same command
+    and of `bench.py --copy-calibration`.  Each launch of `kernel` (a name
+    prefix, e.g. 'dnnopt_skinny<7, 8, 0') is counted together with a reduce
+    kernel dispatched right after it.  Returns (text, traffic dict or None).
+    """
+    import csv
+
+    def rows(path):
+        with open(path, newline="") as f:
+            return list(csv.DictReader(f))
+
+    lines = []
+    tr = rows(trace_csv)
+    tr.sort(key=lambda r: int(r["Start_Timestamp"]))
+    groups = {}
+    for r in tr:
+        nm = _short_kernel_name(r["Kernel_Name"])
+        key = (nm, int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])), int(r["Grid_Size_Y"]),
+               int(r["Grid_Size_Z"]), int(r["Workgroup_Size_X"]))
+        groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    lines.append(f"{'kernel':<44} {'grid (workgroups x,y,z)':>24} {'block':>5} {'calls':>6} {'avg_us':>8} "
+                 f"{'min_us':>8} {'max_us':>8}")
+    for (nm, gx, gy, gz, bs), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{nm:<44} {f'{gx},{gy},{gz}':>24} {bs:>5} {len(d):>6} {sum(d) / len(d):8.2f} {min(d):8.2f} "
+                     f"{max(d):8.2f}")
+    dom = [sum(d) / len(d) for (nm, *_), d in groups.items() if nm.startswith(kernel)]
+    traffic = None
+    if pmc:
+        fetch_csv, write_csv, cfetch_csv, cwrite_csv = pmc
+
+        def per_launch(path):
+            rr = rows(path)
+            rr.sort(key=lambda r: int(r["Dispatch_Id"]))
+            vals = []
+            for i, r in enumerate(rr):
+                if _short_kernel_name(r["Kernel_Name"]).startswith(kernel):
+                    v = float(r["Counter_Value"])
+                    if i + 1 < len(rr) and "reduce" in rr[i + 1]["Kernel_Name"]:
+                        v += float(rr[i + 1]["Counter_Value"])
+                    vals.append(v)
+            return sum(vals) / len(vals) if vals else None, len(vals)
+
+        def calib(path):
+            rr = [r for r in rows(path) if "copy" in r["Kernel_Name"].lower()]
+            return sum(float(r["Counter_Value"]) for r in rr) / len(rr) if rr else None
+
+        fk, nf = per_launch(fetch_csv)
+        wk, nw = per_launch(write_csv)
+        copy_kib = (1 << 30) / 1024.0  # bench.py --copy-calibration 1024
+        cf, cw = calib(cfetch_csv), calib(cwrite_csv)
+        if fk is not None and wk is not None and cf and cw:
+            fs, ws = copy_kib / cf, copy_kib / cw
+            traffic = {
+                "kernel": kernel, "workload": workload, "launches_fetch": nf, "launches_write": nw,
+                "fetch_kib_per_launch": round(fk, 1), "write_kib_per_launch": round(wk, 1),
+                "copy_1gib_fetch_kib": round(cf, 1), "copy_1gib_write_kib": round(cw, 1),
+                "fetch_scale": round(fs, 4), "write_scale": round(ws, 4),
+                "traffic_bytes_per_launch": int(round((fk * fs + wk * ws) * 1024)),
+            }
+            lines.append("")
+            lines.append(f"HBM traffic of {kernel}* (+ its reduce kernel) per launch, mean of {nf}/{nw} launches:")
+            lines.append(f"  FETCH_SIZE {fk:.1f} KiB x {fs:.4f} + WRITE_SIZE {wk:.1f} KiB x {ws:.4f} = "
+                         f"{traffic['traffic_bytes_per_launch'] / 1e6:.2f} MB")
+            lines.append(f"  (scales: a 1 GiB device copy reads FETCH_SIZE {cf:.1f} KiB, WRITE_SIZE {cw:.1f} KiB)")
+    if dom:
+        lines.append("")
+        lines.append(f"rocprof mean duration of {kernel}* launches: "
+                     + ", ".join(f"{x:.2f} us" for x in dom))
+    return "\n".join(lines) + "\n", traffic
+
+
 def copy_calibration(mib):
     """Plain copies of a known size: what FETCH_SIZE / WRITE_SIZE read for
     them scales the counters of the GEMM kernels to bytes."""
@@ -419,9 +515,24 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (scale for HBM byte counters)")
+    ap.add_argument("--rocprof-summary", nargs="+", metavar="ARG",
+                    help="KERNEL WORKLOAD TRACE_CSV [FETCH_CSV WRITE_CSV COPY_FETCH_CSV COPY_WRITE_CSV]: print a "
+                         "summary of rocprofv3 CSV output (no GPU use); with the counter files also write "
+                         "profiles/<kernel>_<workload>_traffic.json")
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.rocprof_summary:
+        a = args.rocprof_summary
+        text, traffic = rocprof_summary(a[0], a[1], a[2], tuple(a[3:7]) if len(a) >= 7 else None)
+        print(text, end="")
+        if traffic:
+            path = os.path.join(ROOT, "profiles", f"{_traffic_file_stem(a[0])}_{a[1]}_traffic.json")
+            os.makedirs(os.path.dirname(path), exist_ok=True)
+            with open(path, "w") as f:
+                json.dump(traffic, f, indent=1)
+                f.write("\n")
         return
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
