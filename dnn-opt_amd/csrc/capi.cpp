@@ -64,8 +64,16 @@ int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B
                                               beta, C, ldc, s));
 }
 
-int run_tile(const Launch& L, int ta, int tb, const void* A, int lda, const void* B, int ldb, float* C, int ldc,
+int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const void* B, int ldb, float* C, int ldc,
              int M, int N, int K, float alpha, float beta, hipStream_t s) {
+    Launch L = L0;
+    // The LDS-staged bf16 kernel reads whole dwords: bf16 operands must start
+    // on 4-byte boundaries, else the register-only kernel serves the call.
+    if (L.cfg >= kTileFirstLds && L.mode == kTileBF16 &&
+        ((reinterpret_cast<uintptr_t>(A) & 3u) != 0 || (reinterpret_cast<uintptr_t>(B) & 3u) != 0)) {
+        const int st = plan_tile(L.mode, ta, tb, M, N, K, lda, ldb, &L, false);
+        if (st != DNNOPT_OK) return st;
+    }
     TileArgs a{};
     a.A = A;
     a.B = B;
@@ -90,7 +98,8 @@ int run_tile(const Launch& L, int ta, int tb, const void* A, int lda, const void
         a.part = static_cast<float*>(part);
         a.tickets = tickets;
     }
-    const int aligned = L.mode != kTileBF16 || ((reinterpret_cast<uintptr_t>(A) & 3u) == 0 && (lda & 1) == 0);
+    const int aligned = L.cfg >= kTileFirstLds ||
+                        L.mode != kTileBF16 || ((reinterpret_cast<uintptr_t>(A) & 3u) == 0 && (lda & 1) == 0);
     int st = finish_launch(launch_tile(L.mode, L.cfg, ta, tb, aligned, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
     return finish_launch(launch_splitk_reduce(a.part, a.splits, (int)L.grid.x, (int)L.grid.y, L.bm, L.bn, M, N,

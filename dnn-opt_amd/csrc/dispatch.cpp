@@ -12,15 +12,19 @@
 //     over column tiles, over the waves of a workgroup and, when there are too
 //     few column tiles to occupy the chip, over k across workgroups (split-k
 //     with a ticketed, ordered reduction) -- about eight waves per CU.
-//   * M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for N <= 16,
-//     64 x 64 otherwise); split-k when the tile count cannot occupy the CUs,
-//     with a separate reduce kernel once the split count is large.
+//   * M > 8 bf16 with 4-byte aligned rows: LDS-staged MFMA tiles (128 x 128
+//     above M = 64, 64 x 128, 32 x 128 below), split-k only when the tiles
+//     leave more than half of the CUs idle.
+//   * other M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for
+//     N <= 16, 64 x 64 otherwise); split-k when the tile count cannot occupy
+//     the CUs, with a separate reduce kernel once the split count is large.
 //   * int8 (B as N x K): MFMA tiles of 16 rows for M <= 16, 128 x 64 for
 //     large M, split-k as above.
 // Tunables (environment, read once, for sweeps):
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
 //   DNNOPT_SKINNY_WGS_PER_CU (default 2), DNNOPT_SKINNY_WGS (force G),
-//   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel).
+//   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel),
+//   DNNOPT_TILE_SPLITS (force the k-splits of a tile launch).
 #include <stdlib.h>
 #include <string.h>
 
@@ -144,10 +148,18 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
     return DNNOPT_OK;
 }
 
-int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L) {
+int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, bool lds_ok) {
     *L = Launch{};
+    const long long es = mode == kTileBF16 ? 2 : 4;
+    // bf16 GEMMs with 4-byte aligned rows go through the LDS-staged kernel.
+    const bool lds = mode != kTileF32 && lds_ok && !transA && !transB &&
+                     (mode == kTileF2B || ((lda & 1) == 0 && (ldb & 1) == 0)) &&
+                     ((long long)(M + 128) * lda + K) * es < 0x7FFFFFFFll &&
+                     ((long long)K * ldb + N) * es < 0x7FFFFFFFll;
     int cfg;
-    if (mode == kTileF32 && N <= 16) {
+    if (lds) {
+        cfg = M > 64 ? 5 : (M > 32 ? 7 : 6);
+    } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
     } else if (mode == kTileF32 && N <= 64 && M >= 4096) {
         cfg = 1;
@@ -158,22 +170,33 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     }
     const TileConfig c = tile_config(cfg);
     const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
-    const int kb = mode == kTileF32 ? 64 : 128;
+    const int kb = (mode == kTileF32 || lds) ? 64 : 128;
     const long long tn = ceil_div(N, bn), tm = ceil_div(M, bm), tiles = tn * tm;
     const long long nblk = ceil_div(K, kb);
     const int waves_per_wg = c.wm * c.wn * c.kw;
-    const long long target_wgs = (long long)num_cus() * waves_per_cu() / waves_per_wg;
+    const long long cus = num_cus();
     long long s = 1;
-    if (tiles < target_wgs) {
-        s = ceil_div(target_wgs, tiles);
-        s = std::min<long long>({s, std::max<long long>(1, nblk / (2 * c.kw)), (long long)max_splits()});
-        s = std::max<long long>(1, s);
+    static const int forced_splits = env_int("DNNOPT_TILE_SPLITS", 0);
+    if (lds) {
+        // One LDS-staged workgroup per CU is the unit of work; split k only
+        // when the tiles leave more than half of the CUs idle.
+        if (tiles * 2 < cus) s = std::min<long long>({ceil_div(cus, tiles), std::max<long long>(1, nblk / 2),
+                                                      (long long)max_splits()});
+    } else {
+        const long long target_wgs = cus * waves_per_cu() / waves_per_wg;
+        if (tiles < target_wgs) {
+            s = ceil_div(target_wgs, tiles);
+            s = std::min<long long>({s, std::max<long long>(1, nblk / (2 * c.kw)), (long long)max_splits()});
+            s = std::max<long long>(1, s);
+        }
     }
+    if (forced_splits > 0) s = std::min<long long>(forced_splits, nblk);
     // Per-workgroup buffer offsets must fit in 31 bits: an operand read along
     // its rows spans one tile of rows, one read along k spans the k-range of
-    // one workgroup.  More splits shorten that range.
-    const long long es = mode == kTileBF16 ? 2 : 4;
+    // one workgroup.  More splits shorten that range.  (The LDS kernel
+    // addresses k from 0; its spans were checked above.)
     auto span_ok = [&](long long splits) {
+        if (lds) return true;
         const long long kext = ceil_div(nblk, splits) * kb;
         const long long a = transA ? kext * lda : (long long)bm * lda;
         const long long b = transB ? (long long)bn * ldb : kext * ldb;
@@ -192,8 +215,8 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(float) : 0;
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
     const int kernel = mode == kTileF32 ? DNNOPT_K_TILE_F32 : DNNOPT_K_TILE_BF16;
-    fill_pub(L, kernel, mode == kTileF32 ? "dnnopt_tile_f32" : "dnnopt_tile_bf16", bm, bn, (int)s,
-             waves_per_wg * 64);
+    fill_pub(L, kernel, mode == kTileF32 ? "dnnopt_tile_f32" : (lds ? "dnnopt_tile_bf16_lds" : "dnnopt_tile_bf16"), bm,
+             bn, (int)s, waves_per_wg * 64);
     return DNNOPT_OK;
 }
 

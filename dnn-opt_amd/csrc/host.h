@@ -43,7 +43,10 @@ struct Launch {
 int split_reduce_mode();
 
 int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L);
-int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L);
+// lds_ok = false keeps bf16 GEMMs off the LDS-staged kernel (operands whose
+// rows do not start on 4-byte boundaries).
+int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L,
+              bool lds_ok = true);
 int plan_s8(int epi, int M, int N, int K, Launch* L);
 
 // Route an fp32 GEMM to a kernel family (skinny or tile).

@@ -90,53 +90,58 @@ hipError_t launch_fill(void* dst, size_t n, int dtype, int dist, uint64_t seed, 
 
 namespace dnnopt_hip {
 
-// Reduce k-split partial tiles written as [split][tile][BM*BN] (tile =
-// tile_m * tiles_n + tile_n) into C with the reference epilogue.  Each output
-// is summed by Q threads over interleaved ranges of splits, then the Q
-// partial sums are added in ascending split-range order through LDS, so the
-// order is fixed and the result reproducible.  Used when there are too many
-// k-splits for the last-arriving workgroup to reduce alone.
+// Sum k-split partial tiles [split][tile][bm*bn] (tile = tile_m * tiles_n +
+// tile_n, row-major inside a tile) into C with the reference epilogue.  One
+// thread per 4 consecutive columns of a tile row: the partial reads of a
+// warp are contiguous, C (for beta != 0) and up to 8 splits are requested
+// before the first add, and splits are added in ascending order -- the same
+// order as the last-arriving-workgroup reduction, so both give the same bits.
 __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restrict__ part, int splits,
                                                            int tiles_n, int tiles, int bm, int bn, int M, int N,
                                                            float alpha, float beta, float* C, int ldc) {
-    constexpr int Q = 8, OUTS = 256 / Q;
-    __shared__ float red[Q][OUTS];
-    const int o = threadIdx.x % OUTS, q = threadIdx.x / OUTS;
-    const long long idx = (long long)blockIdx.x * OUTS + o;
-    const bool valid = idx < (long long)M * N;
-    const int m = valid ? (int)(idx / N) : 0, n = valid ? (int)(idx % N) : 0;
-    const int tile_id = (m / bm) * tiles_n + n / bn;
-    const size_t local = (size_t)(m % bm) * bn + (n % bn);
-    const size_t stride = (size_t)tiles * bm * bn;
-    const int s_lo = (int)((long long)splits * q / Q), s_hi = (int)((long long)splits * (q + 1) / Q);
-    float s = 0.0f;
-    if (valid && s_lo < s_hi) {
-        const float* src = part + (size_t)tile_id * bm * bn + local;
-        s = src[(size_t)s_lo * stride];
-        int sp = s_lo + 1;
-        for (; sp + 8 <= s_hi; sp += 8) {
-            float v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(sp + u) * stride];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) s += v[u];
-        }
-        for (; sp < s_hi; ++sp) s += src[(size_t)sp * stride];
-    }
-    red[q][o] = s;
-    __syncthreads();
-    if (q != 0 || !valid) return;
-    float t = red[0][o];
-    for (int qq = 1; qq < Q; ++qq)
-        if ((long long)splits * qq / Q < (long long)splits * (qq + 1) / Q) t += red[qq][o];
+    const int per_tile = bm * bn / 4;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (long long)tiles * per_tile) return;
+    const int tile = (int)(idx / per_tile);
+    const int loc = (int)(idx % per_tile) * 4;
+    const int m = (tile / tiles_n) * bm + loc / bn;
+    const int n = (tile % tiles_n) * bn + loc % bn;
+    if (m >= M || n >= N) return;
     float* c = C + (size_t)m * ldc + n;
-    *c = epilogue(t, alpha, beta, c);
+    float c_old[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (beta != 0.0f) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (n + e < N) c_old[e] = c[e];
+    }
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4* src = reinterpret_cast<const f4*>(part) + idx;
+    const size_t stride = (size_t)tiles * per_tile;
+    f4 s = src[0];
+    int sp = 1;
+    for (; sp + 8 <= splits; sp += 8) {
+        f4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(sp + u) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    f4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+        if (sp + u < splits) v[u] = src[(size_t)(sp + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+        if (sp + u < splits) s += v[u];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (n + e < N) c[e] = beta == 0.0f ? alpha * s[e] : __builtin_fmaf(alpha, s[e], beta * c_old[e]);
 }
 
 hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
                                 int N, float alpha, float beta, float* C, int ldc, hipStream_t s) {
-    const long long outs = (long long)M * N;
-    const unsigned blocks = (unsigned)((outs + 31) / 32);
+    const long long quads = (long long)tiles_n * tiles_m * bm * bn / 4;
+    const unsigned blocks = (unsigned)((quads + 255) / 256);
     hipLaunchKernelGGL(dnnopt_splitk_reduce, dim3(blocks), dim3(256), 0, s, part, splits, tiles_n,
                        tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc);
     return hipGetLastError();

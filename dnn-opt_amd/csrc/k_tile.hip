@@ -59,7 +59,7 @@ struct TileShape {
     static constexpr int BM = WM * MT * 16;
     static constexpr int BN = WN * NT * 16;
     static constexpr int SUB = MT * NT * 4;
-    static constexpr int RED = (KW > 1 ? (KW - 1) : 1) * WM * WN * SUB * 64;
+    static constexpr int RED = KW > 1 ? (KW - 1) * WM * WN * SUB * 64 : 1;
 };
 
 // Combine k-split waves (LDS) and k-split workgroups (ticket), then apply the
@@ -373,6 +373,175 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
     tile_finish<MT, NT, WM, WN, KW>(p, acc, red, &last_flag, w, lane);
 }
 
+// ---------------------------------------------------------------- bf16, LDS-staged
+// Row-major A (M x K) and B (K x N) through LDS, double-buffered in k-blocks
+// of 64.  Per block a workgroup stages A as BM rows x 64 k and B transposed
+// as BN columns x 64 k, both k-contiguous, so that every MFMA operand is one
+// 16-byte LDS read.  The transpose happens on the way into LDS: a thread
+// loads 4 consecutive rows x 8 columns of B (four 16-byte global loads),
+// regroups them into 8 column runs of 4 k (v_perm_b32) and writes those with
+// 8-byte LDS stores.  16-byte chunks of an LDS row are XOR-swizzled by the
+// row index so that the 16 rows read by one MFMA operand, and the columns
+// written by one store, fall in different banks.  The next block's global
+// loads are issued before the current block's MFMAs.
+//
+// Requirements (checked by the host): rows of A and B start on 4-byte
+// boundaries (even lda, ldb and 4-byte aligned pointers for bf16 storage).
+namespace {
+
+template <int MODE>
+__device__ __forceinline__ u32x4 load8_bf16(__amdgpu_buffer_rsrc_t r, uint32_t elem_off, bool ok) {
+    // 8 consecutive elements as bf16 bits (MODE kTileF2B: fp32 rounded).
+    if constexpr (MODE == kTileBF16) {
+        return buf_load_x4(r, ok ? elem_off * 2u : kOobOffset);
+    } else {
+        const u32x4 lo = buf_load_x4(r, ok ? elem_off * 4u : kOobOffset);
+        const u32x4 hi = buf_load_x4(r, ok ? elem_off * 4u + 16u : kOobOffset);
+        u32x4 out;
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            out[d] = (uint32_t)f32_to_bf16_bits(as_f32(lo[2 * d])) |
+                     ((uint32_t)f32_to_bf16_bits(as_f32(lo[2 * d + 1])) << 16);
+            out[d + 2] = (uint32_t)f32_to_bf16_bits(as_f32(hi[2 * d])) |
+                         ((uint32_t)f32_to_bf16_bits(as_f32(hi[2 * d + 1])) << 16);
+        }
+        return out;
+    }
+}
+
+// Physical 16-byte chunk of logical chunk c (0..7) in LDS row `row`.
+__device__ __forceinline__ int swz_a(int row, int c) { return c ^ (row & 7); }
+__device__ __forceinline__ int swz_b(int n, int c) { return c ^ ((n ^ (n >> 3)) & 7); }
+
+}  // namespace
+
+template <int MT, int NT, int WM, int WN, int MODE>
+__global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) {
+    using S = TileShape<MT, NT, WM, WN, 1>;
+    constexpr int BM = S::BM, BN = S::BN, BK = 64;
+    constexpr int NTH = WM * WN * 64;
+    constexpr int ROWB = BK * 2;  // bytes of one LDS row (64 bf16)
+    constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
+    constexpr int AU = BM * 8 / NTH;           // A chunks (8 k) per thread
+    constexpr int BU = (BN / 8) * 16 / NTH;    // B units (4 k x 8 n) per thread
+    static_assert(AU * NTH == BM * 8 && BU * NTH == (BN / 8) * 16, "tile / thread count mismatch");
+    __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+    __shared__ float red_unused[1];
+    __shared__ int last_flag;
+
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+    const int w = wave_id();
+    const int wn = w % WN, wm = w / WN;
+    const int t = (int)threadIdx.x;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    const int nblk = (p.K + BK - 1) / BK;
+    const int b_lo = (int)(((long long)nblk * blockIdx.z) / p.splits);
+    const int b_hi = (int)(((long long)nblk * (blockIdx.z + 1)) / p.splits);
+
+    constexpr int ES = MODE == kTileBF16 ? 2 : 4;
+    const char* abase = static_cast<const char*>(p.A) + (size_t)m0 * p.lda * ES;
+    const char* bbase = static_cast<const char*>(p.B) + (size_t)n0 * ES;
+    // Ranges end at the last element of each operand, rounded up to a whole
+    // dword: the range check of a dword load drops a dword that extends past
+    // the range, and the last element may share its dword with the next.
+    const __amdgpu_buffer_rsrc_t ra =
+        make_rsrc(abase, clamp_rec((((size_t)(p.M - 1 - m0) * p.lda + p.K) * ES + 3) & ~(size_t)3));
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(bbase, clamp_rec((((size_t)(p.K - 1) * p.ldb + (p.N - n0)) * ES + 3) & ~(size_t)3));
+
+    u32x4 sa[AU], sb[BU][4];
+    auto load_stage = [&](int blk) {
+        const int k0 = blk * BK;
+#pragma unroll
+        for (int i = 0; i < AU; ++i) {
+            const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
+            const int kk = k0 + 8 * c;
+            const int kvalid = p.K - kk;
+            sa[i] = load8_bf16<MODE>(ra, (uint32_t)row * p.lda + kk, m0 + row < p.M && kvalid > 0);
+            if (kvalid < 8) sa[i] = keep_halves(sa[i], kvalid);
+        }
+#pragma unroll
+        for (int i = 0; i < BU; ++i) {
+            const int u = t + i * NTH, cg = u % (BN / 8), kg = u / (BN / 8);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int k = k0 + 4 * kg + q;
+                sb[i][q] = load8_bf16<MODE>(rb, (uint32_t)k * p.ldb + 8 * cg, k < p.K);
+            }
+        }
+    };
+    auto write_stage = [&](int buf) {
+        char* As = lds + buf * STAGE;
+        char* Bs = As + A_BYTES;
+#pragma unroll
+        for (int i = 0; i < AU; ++i) {
+            const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
+            *reinterpret_cast<u32x4*>(As + row * ROWB + swz_a(row, c) * 16) = sa[i];
+        }
+#pragma unroll
+        for (int i = 0; i < BU; ++i) {
+            const int u = t + i * NTH, cg = u % (BN / 8), kg = u / (BN / 8);
+            const int c = kg >> 1, half = kg & 1;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int n = 8 * cg + j;
+                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                u32x2 v;
+                v[0] = __builtin_amdgcn_perm(sb[i][1][j >> 1], sb[i][0][j >> 1], sel);
+                v[1] = __builtin_amdgcn_perm(sb[i][3][j >> 1], sb[i][2][j >> 1], sel);
+                *reinterpret_cast<u32x2*>(Bs + n * ROWB + swz_b(n, c) * 16 + half * 8) = v;
+            }
+        }
+    };
+
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if (b_lo < b_hi) {
+        load_stage(b_lo);
+        write_stage(0);
+    }
+    __syncthreads();
+    for (int blk = b_lo; blk < b_hi; ++blk) {
+        const int cur = (blk - b_lo) & 1;
+        const bool more = blk + 1 < b_hi;
+        if (more) load_stage(blk + 1);
+        const char* As = lds + cur * STAGE;
+        const char* Bs = As + A_BYTES;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int c = kk * 4 + g;
+            u32x4 af[MT], bfr[NT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int row = (wm * MT + mt) * 16 + r;
+                af[mt] = *reinterpret_cast<const u32x4*>(As + row * ROWB + swz_a(row, c) * 16);
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int n = (wn * NT + nt) * 16 + r;
+                bfr[nt] = *reinterpret_cast<const u32x4*>(Bs + n * ROWB + swz_b(n, c) * 16);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[mt]),
+                                                                         __builtin_bit_cast(bf16x8, bfr[nt]),
+                                                                         acc[mt][nt], 0, 0, 0);
+        }
+        if (more) write_stage(cur ^ 1);
+        __syncthreads();
+    }
+
+    tile_finish<MT, NT, WM, WN, 1>(p, acc, red_unused, &last_flag, w, lane);
+}
+
 // ---------------------------------------------------------------- launch table
 // {MT, NT, WM, WN, KW}
 static const TileConfig kTileConfigs[] = {
@@ -381,6 +550,9 @@ static const TileConfig kTileConfigs[] = {
     {2, 2, 2, 2, 1},  // 2: 64 x 64   general / split-k
     {2, 2, 2, 2, 2},  // 3: 64 x 64   k split over 2 waves
     {2, 4, 2, 2, 1},  // 4: 64 x 128
+    {4, 4, 2, 2, 1},  // 5: 128 x 128  bf16 through LDS
+    {2, 2, 1, 4, 1},  // 6: 32 x 128   bf16 through LDS, small M
+    {2, 4, 2, 2, 1},  // 7: 64 x 128   bf16 through LDS
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -401,16 +573,28 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
         }                                                                                                \
         break;
 
+#define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN)                                                         \
+    case IDX:                                                                                              \
+        if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, kTileBF16>), grid, blk, 0, s, a); \
+        else if (mode == kTileF2B) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, kTileF2B>), grid, blk, 0, s, a); \
+        else return hipErrorInvalidValue;                                                                  \
+        break;
+
 hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid, const TileArgs& a, hipStream_t s) {
     if (mode != kTileF32 && (ta || tb)) return hipErrorInvalidValue;
+    if (cfg_idx < 0 || cfg_idx >= tile_config_count()) return hipErrorInvalidValue;
     const TileConfig c = kTileConfigs[cfg_idx];
     const dim3 blk(c.wm * c.wn * c.kw * 64);
+    if (cfg_idx >= kTileFirstLds && !al) return hipErrorInvalidValue;
     switch (cfg_idx) {
         DNNOPT_TILE_CASE(0, 1, 1, 4, 1, 1)
         DNNOPT_TILE_CASE(1, 1, 4, 4, 1, 1)
         DNNOPT_TILE_CASE(2, 2, 2, 2, 2, 1)
         DNNOPT_TILE_CASE(3, 2, 2, 2, 2, 2)
         DNNOPT_TILE_CASE(4, 2, 4, 2, 2, 1)
+        DNNOPT_TILE_LDS_CASE(5, 4, 4, 2, 2)
+        DNNOPT_TILE_LDS_CASE(6, 2, 2, 1, 4)
+        DNNOPT_TILE_LDS_CASE(7, 2, 4, 2, 2)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

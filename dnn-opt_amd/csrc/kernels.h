@@ -106,6 +106,9 @@ struct TileConfig {
 };
 int tile_config_count();
 TileConfig tile_config(int idx);
+// Configurations from this index on are the LDS-staged bf16 kernels: bf16 or
+// fp32-rounded modes only, no transposes, rows of A and B 4-byte aligned.
+constexpr int kTileFirstLds = 5;
 // aligned: all rows of A start on 4-byte boundaries (matters for bf16 storage).
 hipError_t launch_tile(int mode, int cfg_idx, int transA, int transB, int aligned, dim3 grid,
                        const TileArgs& a, hipStream_t s);

@@ -163,6 +163,50 @@ def test_bf16_storage(lib, orc, dev, M, N, K):
         u.assert_fp32_close(host(dC), want, scale, K, f"bf16 {M}x{N}x{K} beta={beta}")
 
 
+# LDS-staged bf16 tiles: ragged M/N/K (K tails inside a 64-k block), padded
+# even strides, k split across workgroups (few tiles), exact tile multiples.
+LDS = [(100, 1001, 129, 1, 1), (33, 130, 8192, 0, 0), (17, 4096, 300, 2, 0), (256, 256, 64, 0, 0),
+       (129, 127, 1000, 0, 1), (64, 64, 64, 0, 0), (300, 600, 70, 4, 8)]
+
+
+@pytest.mark.parametrize("M,N,K,pa,pb", LDS)
+@pytest.mark.parametrize("mode", ["bf16", "f2b"])
+def test_bf16_lds_tiles(lib, orc, dev, M, N, K, pa, pb, mode):
+    lda, ldb = K + pa, N + pb
+    p = lib.plan_bf16(M, N, K, fp32_inputs=int(mode == "f2b"))
+    if (K % 2 == 0 and N % 2 == 0) or mode == "f2b":
+        assert p["name"] == "dnnopt_tile_bf16_lds", p
+    A32 = u.normal(orc, M * lda, 1).reshape(M, lda)
+    B32 = u.normal(orc, K * ldb, 2, 0, 0.02).reshape(K, ldb)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    A, B = u.bf16_bits(orc, A32), u.bf16_bits(orc, B32)
+    want, scale = u.exact(u.bf16_value(A)[:, :K], u.bf16_value(B)[:, :N], 0.5, 1.0, C0)
+    dC = dev_copy(C0, dev)
+    if mode == "bf16":
+        lib.gemm_bf16(M, N, K, 0.5, dev_copy(A.view(np.int16), dev), lda, dev_copy(B.view(np.int16), dev), ldb, 1.0,
+                      dC, N, stream=stream())
+    else:
+        lib.gemm_bf16_f32in(M, N, K, 0.5, dev_copy(A32, dev), lda, dev_copy(B32, dev), ldb, 1.0, dC, N,
+                            stream=stream())
+    u.assert_fp32_close(host(dC), want, scale, K, f"lds {mode} {M}x{N}x{K}")
+
+
+def test_bf16_lds_misaligned_falls_back(lib, orc, dev):
+    """bf16 operands 2 bytes off a 4-byte boundary take the register-only tiles."""
+    M, N, K = 128, 512, 256
+    A = u.bf16_bits(orc, u.normal(orc, M * K + 1, 1))
+    B = u.bf16_bits(orc, u.normal(orc, K * N + 1, 2, 0, 0.02))
+    dA, dB = dev_copy(A.view(np.int16), dev), dev_copy(B.view(np.int16), dev)
+    want, scale = u.exact(u.bf16_value(A[1:]).reshape(M, K), u.bf16_value(B[1:]).reshape(K, N))
+    for a_off, b_off in ((2, 0), (0, 2), (2, 2)):
+        dC = torch.zeros((M, N), dtype=torch.float32, device=dev)
+        AA = A[1:] if a_off else A[:-1]
+        BB = B[1:] if b_off else B[:-1]
+        want, scale = u.exact(u.bf16_value(AA).reshape(M, K), u.bf16_value(BB).reshape(K, N))
+        lib.gemm_bf16(M, N, K, 1.0, dA.data_ptr() + a_off, K, dB.data_ptr() + b_off, N, 0.0, dC, N, stream=stream())
+        u.assert_fp32_close(host(dC), want, scale, K, f"misaligned a+{a_off} b+{b_off}")
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 11008, 4096), (4, 1000, 512), (7, 33, 65), (32, 300, 260), (256, 1024, 512)])
 def test_bf16_fp32_inputs(lib, orc, dev, M, N, K):
     A = u.normal(orc, M * K, 1).reshape(M, K)
