@@ -195,6 +195,11 @@ def run_gpu(args, wl_name):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     desc, cases = workload(wl_name)
+    if args.cases:
+        keep = set(args.cases.split(","))
+        cases = [c for c in cases if c.name in keep]
+        if not cases:
+            raise SystemExit(f"bench.py: no case of {wl_name} is named in --cases {args.cases}")
     step_bytes = sum(c.bytes_alg() for c in cases)
     # Rotate copies so one pass of every buffer exceeds 2x the 256 MB cache.
     copies = max(1, -(-(600 << 20) // step_bytes))
@@ -513,6 +518,7 @@ def main():
     ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "all"])
     ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (scale for HBM byte counters)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="ARG",

@@ -12,9 +12,9 @@
 //     over column tiles, over the waves of a workgroup and, when there are too
 //     few column tiles to occupy the chip, over k across workgroups (split-k
 //     with a ticketed, ordered reduction) -- about eight waves per CU.
-//   * M > 8 bf16 with 4-byte aligned rows: LDS-staged MFMA tiles (128 x 128
-//     above M = 64, 64 x 128, 32 x 128 below), split-k only when the tiles
-//     leave more than half of the CUs idle.
+//   * M > 8 bf16 with 4-byte aligned rows: LDS-staged MFMA tiles (128 x 96
+//     with 8 waves above M = 64, 64 x 128 and 32 x 128 below), split-k only
+//     when the tiles leave more than half of the CUs idle.
 //   * other M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for
 //     N <= 16, 64 x 64 otherwise); split-k when the tile count cannot occupy
 //     the CUs, with a separate reduce kernel once the split count is large.
@@ -24,7 +24,8 @@
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
 //   DNNOPT_SKINNY_WGS_PER_CU (default 2), DNNOPT_SKINNY_WGS (force G),
 //   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel),
-//   DNNOPT_TILE_SPLITS (force the k-splits of a tile launch).
+//   DNNOPT_TILE_SPLITS (force the k-splits of a tile launch), DNNOPT_TILE_CFG
+//   (force an LDS-staged bf16 tile configuration, index 5 and up).
 #include <stdlib.h>
 #include <string.h>
 
@@ -157,8 +158,10 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
                      ((long long)(M + 128) * lda + K) * es < 0x7FFFFFFFll &&
                      ((long long)K * ldb + N) * es < 0x7FFFFFFFll;
     int cfg;
+    static const int forced_cfg = env_int("DNNOPT_TILE_CFG", 0);
     if (lds) {
-        cfg = M > 64 ? 5 : (M > 32 ? 7 : 6);
+        cfg = M > 64 ? 13 : (M > 32 ? 7 : 6);
+        if (forced_cfg >= kTileFirstLds && forced_cfg < tile_config_count()) cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
     } else if (mode == kTileF32 && N <= 64 && M >= 4096) {

@@ -389,24 +389,17 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
 // boundaries (even lda, ldb and 4-byte aligned pointers for bf16 storage).
 namespace {
 
-template <int MODE>
-__device__ __forceinline__ u32x4 load8_bf16(__amdgpu_buffer_rsrc_t r, uint32_t elem_off, bool ok) {
-    // 8 consecutive elements as bf16 bits (MODE kTileF2B: fp32 rounded).
-    if constexpr (MODE == kTileBF16) {
-        return buf_load_x4(r, ok ? elem_off * 2u : kOobOffset);
-    } else {
-        const u32x4 lo = buf_load_x4(r, ok ? elem_off * 4u : kOobOffset);
-        const u32x4 hi = buf_load_x4(r, ok ? elem_off * 4u + 16u : kOobOffset);
-        u32x4 out;
+// 8 fp32 values (two 16-byte loads) rounded to bf16 (reference formula) and
+// packed as 8 bf16 bit patterns.
+__device__ __forceinline__ u32x4 pack_bf16x8(const u32x4& lo, const u32x4& hi) {
+    u32x4 out;
 #pragma unroll
-        for (int d = 0; d < 2; ++d) {
-            out[d] = (uint32_t)f32_to_bf16_bits(as_f32(lo[2 * d])) |
-                     ((uint32_t)f32_to_bf16_bits(as_f32(lo[2 * d + 1])) << 16);
-            out[d + 2] = (uint32_t)f32_to_bf16_bits(as_f32(hi[2 * d])) |
-                         ((uint32_t)f32_to_bf16_bits(as_f32(hi[2 * d + 1])) << 16);
-        }
-        return out;
+    for (int d = 0; d < 2; ++d) {
+        out[d] = (uint32_t)f32_to_bf16_bits(as_f32(lo[2 * d])) | ((uint32_t)f32_to_bf16_bits(as_f32(lo[2 * d + 1])) << 16);
+        out[d + 2] =
+            (uint32_t)f32_to_bf16_bits(as_f32(hi[2 * d])) | ((uint32_t)f32_to_bf16_bits(as_f32(hi[2 * d + 1])) << 16);
     }
+    return out;
 }
 
 // Physical 16-byte chunk of logical chunk c (0..7) in LDS row `row`.
@@ -415,17 +408,21 @@ __device__ __forceinline__ int swz_b(int n, int c) { return c ^ ((n ^ (n >> 3)) 
 
 }  // namespace
 
-template <int MT, int NT, int WM, int WN, int MODE>
+template <int MT, int NT, int WM, int WN, int D, int MODE>
 __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) {
     using S = TileShape<MT, NT, WM, WN, 1>;
     constexpr int BM = S::BM, BN = S::BN, BK = 64;
     constexpr int NTH = WM * WN * 64;
     constexpr int ROWB = BK * 2;  // bytes of one LDS row (64 bf16)
     constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
-    constexpr int AU = BM * 8 / NTH;           // A chunks (8 k) per thread
-    constexpr int BU = (BN / 8) * 16 / NTH;    // B units (4 k x 8 n) per thread
-    static_assert(AU * NTH == BM * 8 && BU * NTH == (BN / 8) * 16, "tile / thread count mismatch");
-    __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+    constexpr int ACH = BM * 8;                // A chunks (8 k) per block
+    constexpr int BUN = (BN / 8) * 16;         // B units (4 k x 8 n) per block
+    constexpr int AU = (ACH + NTH - 1) / NTH;  // per thread
+    constexpr int BU = (BUN + NTH - 1) / NTH;
+    // The two k-block stages, reused after the main loop to stage C rows.
+    constexpr int CROW = BN + 4;  // floats per staged C row (padding spreads the banks)
+    constexpr int LDS_BYTES = 2 * STAGE > BM * CROW * 4 ? 2 * STAGE : BM * CROW * 4;
+    __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
     __shared__ float red_unused[1];
     __shared__ int last_flag;
 
@@ -450,48 +447,98 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     const __amdgpu_buffer_rsrc_t rb =
         make_rsrc(bbase, clamp_rec((((size_t)(p.K - 1) * p.ldb + (p.N - n0)) * ES + 3) & ~(size_t)3));
 
-    u32x4 sa[AU], sb[BU][4];
-    auto load_stage = [&](int blk) {
-        const int k0 = blk * BK;
+    // Per-thread offsets that do not change from block to block are computed
+    // once: global element offsets of this thread's A chunks and B rows (an
+    // out-of-range offset for rows past M), LDS byte offsets of its stores
+    // and of the wave's operand reads.
+    uint32_t a_off[AU], b_off[BU][4];
+    int a_lds[AU], b_lds[BU][8];
+    int a_c[AU];
+#pragma unroll
+    for (int i = 0; i < AU; ++i) {
+        const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
+        const bool ok = (ACH % NTH == 0 || idx < ACH) && m0 + row < p.M;
+        a_off[i] = ok ? ((uint32_t)row * p.lda + 8 * c) * ES : kOobOffset;
+        a_lds[i] = row * ROWB + swz_a(row, c) * 16;
+        a_c[i] = 8 * c;
+    }
+#pragma unroll
+    for (int i = 0; i < BU; ++i) {
+        const int u = t + i * NTH, cg = u % (BN / 8), kg = u / (BN / 8);
+        const bool ok = BUN % NTH == 0 || u < BUN;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b_off[i][q] = ok ? ((uint32_t)(4 * kg + q) * p.ldb + 8 * cg) * ES : kOobOffset;
+        const int c = kg >> 1, half = kg & 1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int n = 8 * cg + j;
+            b_lds[i][j] = ok ? n * ROWB + swz_b(n, c) * 16 + half * 8 : -1;
+        }
+    }
+
+    // Register ring of D k-blocks: block i of this workgroup lives in slot
+    // i % D from its load until it is written to LDS.  Loads run ahead of the
+    // range by up to D - 1 blocks; those re-read the last block (never used),
+    // so every load is unconditional and the compiler waits for exactly the
+    // loads each LDS store needs.
+    u32x4 sa[D][AU], sb[D][BU][4];
+    auto load_stage = [&](int blk, int slot) {
+        const int bc = blk < b_hi ? blk : b_hi - 1;
+        const uint32_t ka = (uint32_t)bc * BK * ES;
+        const uint32_t kb = (uint32_t)bc * BK * p.ldb * ES;
 #pragma unroll
         for (int i = 0; i < AU; ++i) {
-            const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
-            const int kk = k0 + 8 * c;
-            const int kvalid = p.K - kk;
-            sa[i] = load8_bf16<MODE>(ra, (uint32_t)row * p.lda + kk, m0 + row < p.M && kvalid > 0);
-            if (kvalid < 8) sa[i] = keep_halves(sa[i], kvalid);
-        }
-#pragma unroll
-        for (int i = 0; i < BU; ++i) {
-            const int u = t + i * NTH, cg = u % (BN / 8), kg = u / (BN / 8);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int k = k0 + 4 * kg + q;
-                sb[i][q] = load8_bf16<MODE>(rb, (uint32_t)k * p.ldb + 8 * cg, k < p.K);
+            if constexpr (MODE == kTileBF16) {
+                sa[slot][i] = buf_load_x4(ra, a_off[i] + ka);
+            } else {
+                const u32x4 lo = buf_load_x4(ra, a_off[i] + ka);
+                const u32x4 hi = buf_load_x4(ra, a_off[i] + ka + 16u);
+                sa[slot][i] = pack_bf16x8(lo, hi);
             }
         }
+#pragma unroll
+        for (int i = 0; i < BU; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if constexpr (MODE == kTileBF16) {
+                    sb[slot][i][q] = buf_load_x4(rb, b_off[i][q] + kb);
+                } else {
+                    const u32x4 lo = buf_load_x4(rb, b_off[i][q] + kb);
+                    const u32x4 hi = buf_load_x4(rb, b_off[i][q] + kb + 16u);
+                    sb[slot][i][q] = pack_bf16x8(lo, hi);
+                }
+            }
     };
-    auto write_stage = [&](int buf) {
+    auto write_stage = [&](int slot, int buf, int blk) {
         char* As = lds + buf * STAGE;
         char* Bs = As + A_BYTES;
+        // Only the block holding k = K - 1 has A elements past K (the next
+        // row's data): zero them.  B rows past K read as zero (out of range).
+        const bool tail = (blk + 1) * BK > p.K;
 #pragma unroll
         for (int i = 0; i < AU; ++i) {
-            const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
-            *reinterpret_cast<u32x4*>(As + row * ROWB + swz_a(row, c) * 16) = sa[i];
+            u32x4 v = sa[slot][i];
+            if (tail) {
+                const int kvalid = p.K - (blk * BK + a_c[i]);
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const int keep = kvalid - 2 * d;
+                    v[d] = keep >= 2 ? v[d] : (keep == 1 ? (v[d] & 0xFFFFu) : 0u);
+                }
+            }
+            if (ACH % NTH == 0 || t + i * NTH < ACH) *reinterpret_cast<u32x4*>(As + a_lds[i]) = v;
         }
 #pragma unroll
         for (int i = 0; i < BU; ++i) {
-            const int u = t + i * NTH, cg = u % (BN / 8), kg = u / (BN / 8);
-            const int c = kg >> 1, half = kg & 1;
+            if (BUN % NTH != 0 && t + i * NTH >= BUN) continue;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int n = 8 * cg + j;
                 const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
                 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
                 u32x2 v;
-                v[0] = __builtin_amdgcn_perm(sb[i][1][j >> 1], sb[i][0][j >> 1], sel);
-                v[1] = __builtin_amdgcn_perm(sb[i][3][j >> 1], sb[i][2][j >> 1], sel);
-                *reinterpret_cast<u32x2*>(Bs + n * ROWB + swz_b(n, c) * 16 + half * 8) = v;
+                v[0] = __builtin_amdgcn_perm(sb[slot][i][1][j >> 1], sb[slot][i][0][j >> 1], sel);
+                v[1] = __builtin_amdgcn_perm(sb[slot][i][3][j >> 1], sb[slot][i][2][j >> 1], sel);
+                *reinterpret_cast<u32x2*>(Bs + b_lds[i][j]) = v;
             }
         }
     };
@@ -502,31 +549,30 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    if (b_lo < b_hi) {
-        load_stage(b_lo);
-        write_stage(0);
+    int a_rd[2][MT], b_rd[2][NT];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        const int c = kk * 4 + g;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int row = (wm * MT + mt) * 16 + r;
+            a_rd[kk][mt] = row * ROWB + swz_a(row, c) * 16;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int n = (wn * NT + nt) * 16 + r;
+            b_rd[kk][nt] = A_BYTES + n * ROWB + swz_b(n, c) * 16;
+        }
     }
-    __syncthreads();
-    for (int blk = b_lo; blk < b_hi; ++blk) {
-        const int cur = (blk - b_lo) & 1;
-        const bool more = blk + 1 < b_hi;
-        if (more) load_stage(blk + 1);
-        const char* As = lds + cur * STAGE;
-        const char* Bs = As + A_BYTES;
+    auto compute = [&](int buf) {
+        const char* St = lds + buf * STAGE;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-            const int c = kk * 4 + g;
             u32x4 af[MT], bfr[NT];
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                const int row = (wm * MT + mt) * 16 + r;
-                af[mt] = *reinterpret_cast<const u32x4*>(As + row * ROWB + swz_a(row, c) * 16);
-            }
+            for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const u32x4*>(St + a_rd[kk][mt]);
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                const int n = (wn * NT + nt) * 16 + r;
-                bfr[nt] = *reinterpret_cast<const u32x4*>(Bs + n * ROWB + swz_b(n, c) * 16);
-            }
+            for (int nt = 0; nt < NT; ++nt) bfr[nt] = *reinterpret_cast<const u32x4*>(St + b_rd[kk][nt]);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -535,11 +581,79 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
                                                                          __builtin_bit_cast(bf16x8, bfr[nt]),
                                                                          acc[mt][nt], 0, 0, 0);
         }
-        if (more) write_stage(cur ^ 1);
-        __syncthreads();
+    };
+
+    // Block i (relative to b_lo) is loaded D iterations ahead, written to LDS
+    // buffer i & 1 at the end of iteration i - 1 and consumed in iteration i.
+    // Full groups of D iterations run without conditionals, so the compiler
+    // can wait for exactly the loads each LDS write needs.
+    const int nb = b_hi - b_lo;
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_stage(b_lo + d, d);
+    write_stage(0, 0, b_lo);
+    __syncthreads();
+    int i0 = 0;
+    for (; i0 + D <= nb; i0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int i = i0 + d;
+            load_stage(b_lo + i + D, d);
+            compute(i & 1);
+            write_stage((d + 1) % D, (i + 1) & 1, b_lo + i + 1);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const int i = i0 + d;
+        if (i < nb) {
+            compute(i & 1);
+            write_stage((d + 1) % D, (i + 1) & 1, b_lo + i + 1);
+            __syncthreads();
+        }
     }
 
-    tile_finish<MT, NT, WM, WN, 1>(p, acc, red_unused, &last_flag, w, lane);
+    if (p.splits > 1) {
+        tile_finish<MT, NT, WM, WN, 1>(p, acc, red_unused, &last_flag, w, lane);
+        return;
+    }
+    // Unsplit tile: stage the BM x BN accumulators in LDS (the main loop
+    // ended with a barrier, so the stages are free), then write C row by row
+    // with 16-byte accesses -- the MFMA layout would store 4 rows x 16
+    // columns per instruction.
+    float* Cs = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                Cs[((wm * MT + mt) * 16 + 4 * g + i) * CROW + (wn * NT + nt) * 16 + r] = acc[mt][nt][i];
+    __syncthreads();
+    constexpr int Q4 = BN / 4;  // float4 groups per row
+    const __amdgpu_buffer_rsrc_t rc = make_rsrc(
+        p.C + (size_t)m0 * p.ldc + n0, clamp_rec(((size_t)(p.M - 1 - m0) * p.ldc + (p.N - n0)) * 4));
+    for (int e = t; e < BM * Q4; e += NTH) {
+        const int row = e / Q4, q = e % Q4;
+        const int m = m0 + row, n = n0 + 4 * q;
+        if (m >= p.M || n >= p.N) continue;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(&Cs[row * CROW + 4 * q]);
+        const uint32_t off = ((uint32_t)row * p.ldc + 4 * q) * 4u;
+        if (n + 4 <= p.N) {
+            f32x4 out;
+            if (p.beta == 0.0f) {
+                out = p.alpha * v;
+            } else {
+                const f32x4 c_old = __builtin_bit_cast(f32x4, buf_load_x4(rc, off));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) out[k] = __builtin_fmaf(p.alpha, v[k], p.beta * c_old[k]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, out), rc, off, 0, 0);
+        } else {
+            float* c = p.C + (size_t)m * p.ldc + n;
+            for (int k = 0; k < p.N - n; ++k) c[k] = epilogue(v[k], p.alpha, p.beta, c + k);
+        }
+    }
 }
 
 // ---------------------------------------------------------------- launch table
@@ -550,9 +664,15 @@ static const TileConfig kTileConfigs[] = {
     {2, 2, 2, 2, 1},  // 2: 64 x 64   general / split-k
     {2, 2, 2, 2, 2},  // 3: 64 x 64   k split over 2 waves
     {2, 4, 2, 2, 1},  // 4: 64 x 128
-    {4, 4, 2, 2, 1},  // 5: 128 x 128  bf16 through LDS
-    {2, 2, 1, 4, 1},  // 6: 32 x 128   bf16 through LDS, small M
-    {2, 4, 2, 2, 1},  // 7: 64 x 128   bf16 through LDS
+    {4, 4, 2, 2, 1, 2},  // 5: 128 x 128  bf16 through LDS
+    {2, 2, 1, 4, 1, 2},  // 6: 32 x 128   bf16 through LDS, small M
+    {2, 4, 2, 2, 1, 2},  // 7: 64 x 128   bf16 through LDS
+    {4, 4, 2, 2, 1, 3},  // 8: 128 x 128  bf16 through LDS, 3 blocks ahead
+    {4, 4, 2, 2, 1, 4},  // 9: 128 x 128  bf16 through LDS, 4 blocks ahead
+    {2, 2, 1, 4, 1, 4},  // 10: 32 x 128  bf16 through LDS, 4 blocks ahead
+    {2, 4, 2, 2, 1, 4},  // 11: 64 x 128  bf16 through LDS, 4 blocks ahead
+    {4, 2, 2, 4, 1, 3},  // 12: 128 x 128 bf16 through LDS, 8 waves, 3 blocks ahead
+    {2, 3, 4, 2, 1, 3},  // 13: 128 x 96  bf16 through LDS, 8 waves, 3 blocks ahead
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -573,10 +693,10 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
         }                                                                                                \
         break;
 
-#define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN)                                                         \
+#define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN, D)                                                      \
     case IDX:                                                                                              \
-        if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, kTileBF16>), grid, blk, 0, s, a); \
-        else if (mode == kTileF2B) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, kTileF2B>), grid, blk, 0, s, a); \
+        if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16>), grid, blk, 0, s, a); \
+        else if (mode == kTileF2B) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileF2B>), grid, blk, 0, s, a); \
         else return hipErrorInvalidValue;                                                                  \
         break;
 
@@ -592,9 +712,15 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_CASE(2, 2, 2, 2, 2, 1)
         DNNOPT_TILE_CASE(3, 2, 2, 2, 2, 2)
         DNNOPT_TILE_CASE(4, 2, 4, 2, 2, 1)
-        DNNOPT_TILE_LDS_CASE(5, 4, 4, 2, 2)
-        DNNOPT_TILE_LDS_CASE(6, 2, 2, 1, 4)
-        DNNOPT_TILE_LDS_CASE(7, 2, 4, 2, 2)
+        DNNOPT_TILE_LDS_CASE(5, 4, 4, 2, 2, 2)
+        DNNOPT_TILE_LDS_CASE(6, 2, 2, 1, 4, 2)
+        DNNOPT_TILE_LDS_CASE(7, 2, 4, 2, 2, 2)
+        DNNOPT_TILE_LDS_CASE(8, 4, 4, 2, 2, 3)
+        DNNOPT_TILE_LDS_CASE(9, 4, 4, 2, 2, 4)
+        DNNOPT_TILE_LDS_CASE(10, 2, 2, 1, 4, 4)
+        DNNOPT_TILE_LDS_CASE(11, 2, 4, 2, 2, 4)
+        DNNOPT_TILE_LDS_CASE(12, 4, 2, 2, 4, 3)
+        DNNOPT_TILE_LDS_CASE(13, 2, 3, 4, 2, 3)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -103,6 +103,7 @@ struct TileArgs {
 
 struct TileConfig {
     int mt, nt, wm, wn, kw;
+    int depth;  // LDS-staged kernels: k-blocks loaded ahead (register ring)
 };
 int tile_config_count();
 TileConfig tile_config(int idx);
