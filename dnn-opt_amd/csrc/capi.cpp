@@ -210,8 +210,10 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
     if (!A || !B || !C || (epi && !scale)) return DNNOPT_ERR_INVALID_ARG;
     if (lda < K || ldb < K || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    const int aligned = ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) == 0 &&
+                        (lda & 3) == 0 && (ldb & 3) == 0;
     Launch L;
-    int st = plan_s8(epi, M, N, K, &L);
+    int st = plan_s8(epi, M, N, K, &L, aligned != 0);
     if (st != DNNOPT_OK) return st;
     if ((long long)L.bm * lda + K >= 0x7FFFFFFFll || (long long)L.bn * ldb + K >= 0x7FFFFFFFll)
         return DNNOPT_ERR_UNSUPPORTED;
@@ -237,8 +239,6 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
         a.part = static_cast<int32_t*>(part);
         a.tickets = tickets;
     }
-    const int aligned = ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) == 0 &&
-                        (lda & 3) == 0 && (ldb & 3) == 0;
     st = finish_launch(launch_mfma_s8(L.cfg, epi, aligned, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
     return finish_launch(launch_s8_reduce(a.part, a.splits, (int)L.grid.x, (int)L.grid.y, L.bm, L.bn, M, N, epi,

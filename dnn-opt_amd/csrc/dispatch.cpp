@@ -18,14 +18,17 @@
 //   * other M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for
 //     N <= 16, 64 x 64 otherwise); split-k when the tile count cannot occupy
 //     the CUs, with a separate reduce kernel once the split count is large.
-//   * int8 (B as N x K): MFMA tiles of 16 rows for M <= 16, 128 x 64 for
-//     large M, split-k as above.
+//   * int8 (B as N x K): 16 x 16 MFMA tiles with k split over the waves of a
+//     workgroup for M <= 16; 32 x 32 tiles staged through LDS above that
+//     (4-byte aligned rows), split-k only when the tiles leave more than half
+//     of the CUs idle.
 // Tunables (environment, read once, for sweeps):
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
 //   DNNOPT_SKINNY_WGS_PER_CU (default 2), DNNOPT_SKINNY_WGS (force G),
 //   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel),
 //   DNNOPT_TILE_SPLITS (force the k-splits of a tile launch), DNNOPT_TILE_CFG
-//   (force an LDS-staged bf16 tile configuration, index 5 and up).
+//   (force an LDS-staged bf16 tile configuration, index 5 and up),
+//   DNNOPT_S8_CFG / DNNOPT_S8_SPLITS (force the int8 configuration / splits).
 #include <stdlib.h>
 #include <string.h>
 
@@ -223,23 +226,40 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     return DNNOPT_OK;
 }
 
-int plan_s8(int epi, int M, int N, int K, Launch* L) {
+int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok) {
     *L = Launch{};
-    const int cfg = M <= 16 ? 1 : (M >= 128 ? 3 : 2);
+    static const int forced_cfg = env_int("DNNOPT_S8_CFG", -1);
+    static const int forced_splits = env_int("DNNOPT_S8_SPLITS", 0);
+    // M <= 16: 16 x 16 tiles with k split over the 8 waves of a workgroup
+    // (one launch, no partial sums); larger M: 32 x 32 tiles through LDS.
+    int cfg = M <= 16 ? 5 : 13;
+    if (forced_cfg >= 0 && forced_cfg < s8_config_count()) cfg = forced_cfg;
+    if (cfg >= kS8FirstLds && !lds_ok) cfg = M <= 16 ? 5 : (M >= 128 ? 3 : 2);
+    const bool lds = cfg >= kS8FirstLds;
     const S8Config c = s8_config(cfg);
     const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
     const long long tn = ceil_div(N, bn), tm = ceil_div(M, bm), tiles = tn * tm;
-    const long long nblk = ceil_div(K, 256);
+    const int kb = lds ? 128 : 256;
+    const long long nblk = ceil_div(K, kb);
     const int waves_per_wg = c.wm * c.wn * c.kw;
-    const long long target_wgs = (long long)num_cus() * waves_per_cu() / waves_per_wg;
+    const long long cus = num_cus();
     long long s = 1;
-    if (tiles < target_wgs) {
-        s = ceil_div(target_wgs, tiles);
-        s = std::min<long long>({s, std::max<long long>(1, nblk / c.kw), (long long)kTicketSplitLimit});
-        s = std::max<long long>(1, s);
+    if (lds) {
+        if (tiles * 2 < cus) s = std::min<long long>({ceil_div(cus, tiles), std::max<long long>(1, nblk / 2),
+                                                      (long long)max_splits()});
+    } else {
+        const long long target_wgs = cus * waves_per_cu() / waves_per_wg;
+        if (tiles < target_wgs) {
+            s = ceil_div(target_wgs, tiles);
+            s = std::min<long long>({s, std::max<long long>(1, nblk / c.kw), (long long)kTicketSplitLimit});
+            s = std::max<long long>(1, s);
+        }
     }
-    if (s > 1 && tiles > kMaxTickets && !split_reduce_mode()) s = 1;
-    L->defer_reduce = (s > 1 && split_reduce_mode()) ? 1 : 0;
+    if (forced_splits > 0) s = std::min<long long>(forced_splits, std::max<long long>(1, nblk / c.kw));
+    if (s > 1 && tiles > kMaxTickets && !split_reduce_mode() && !lds) s = 1;
+    if (tm > 65535 || s > 65535) return DNNOPT_ERR_UNSUPPORTED;
+    // The LDS-staged kernel always hands its k-splits to the reduce kernel.
+    L->defer_reduce = (s > 1 && (split_reduce_mode() || lds)) ? 1 : 0;
     L->mode = epi;
     L->cfg = cfg;
     L->bm = bm;
@@ -247,7 +267,7 @@ int plan_s8(int epi, int M, int N, int K, Launch* L) {
     L->grid = dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(int32_t) : 0;
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
-    fill_pub(L, DNNOPT_K_MFMA_S8, "dnnopt_mfma_s8", bm, bn, (int)s, waves_per_wg * 64);
+    fill_pub(L, DNNOPT_K_MFMA_S8, lds ? "dnnopt_s8_lds" : "dnnopt_mfma_s8", bm, bn, (int)s, waves_per_wg * 64);
     return DNNOPT_OK;
 }
 

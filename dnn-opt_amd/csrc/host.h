@@ -47,7 +47,9 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L);
 // rows do not start on 4-byte boundaries).
 int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L,
               bool lds_ok = true);
-int plan_s8(int epi, int M, int N, int K, Launch* L);
+// lds_ok = false keeps int8 GEMMs off the LDS-staged kernel (rows of A or B
+// not on 4-byte boundaries).
+int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok = true);
 
 // Route an fp32 GEMM to a kernel family (skinny or tile).
 int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L);

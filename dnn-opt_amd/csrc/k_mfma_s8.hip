@@ -100,8 +100,9 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = i32x4{0, 0, 0, 0};
 
-    for (int blk = b_lo; blk < b_hi; ++blk) {
-        i32x4 a[MT][4], b[NT][4];
+    // Operands of one 256-byte k block, loaded one block ahead of the MFMAs
+    // that consume them (two register sets, alternating).
+    auto load_blk = [&](int blk, i32x4 (&a)[MT][4], i32x4 (&b)[NT][4]) {
         const int kbase = blk * 256 + 16 * g;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -117,7 +118,10 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
                 b[nt][j] = load16<AL>(rb, off);
             }
         }
+    };
+    auto compute_blk = [&](int blk, i32x4 (&a)[MT][4], i32x4 (&b)[NT][4]) {
         if (blk * 256 + 256 > p.K) {
+            const int kbase = blk * 256 + 16 * g;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -130,7 +134,19 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
 #pragma unroll
                 for (int nt = 0; nt < NT; ++nt)
                     acc[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt][j], b[nt][j], acc[mt][nt], 0, 0, 0);
+    };
+    i32x4 a0[MT][4], b0[NT][4], a1[MT][4], b1[NT][4];
+    if (b_lo < b_hi) load_blk(b_lo, a0, b0);
+    int blk = b_lo;
+    for (; blk + 2 <= b_hi; blk += 2) {
+        load_blk(blk + 1, a1, b1);
+        compute_blk(blk, a0, b0);
+        // The block after this pair, or (at the end) the last block again,
+        // so that the load is unconditional.
+        load_blk(min(blk + 2, b_hi - 1), a0, b0);
+        compute_blk(blk + 1, a1, b1);
     }
+    if (blk < b_hi) compute_blk(blk, a0, b0);
 
     // Waves that split k inside the workgroup: add into the wk == 0 wave.
     if constexpr (KW > 1) {
@@ -220,6 +236,205 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
             }
 }
 
+// ---------------------------------------------------------------- LDS-staged
+// Both operands are k-contiguous, so A and B tiles are staged in LDS the same
+// way: k-blocks of 128 bytes, one LDS row of 128 bytes per operand row, the
+// 16-byte chunks of a row XOR-swizzled by the row index so that the 16 rows
+// read by one MFMA operand fall in different banks.  Each operand row is
+// read from global memory once per workgroup (the register kernel reads it
+// once per wave), the next D - 1 blocks are in flight while one is consumed,
+// and C is written through LDS in whole rows.
+namespace {
+__device__ __forceinline__ int swz16(int row, int c) { return c ^ (row & 7); }
+}  // namespace
+
+template <int MT, int NT, int WM, int WN, int D, int EPI>
+__global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
+    constexpr int BM = WM * MT * 16, BN = WN * NT * 16, BK = 128;
+    constexpr int NTH = WM * WN * 64;
+    constexpr int ROWB = BK;
+    constexpr int A_BYTES = BM * ROWB, STAGE = (BM + BN) * ROWB;
+    constexpr int ACH = BM * 8, BCH = BN * 8;  // 16-byte chunks per block
+    constexpr int AU = (ACH + NTH - 1) / NTH, BU = (BCH + NTH - 1) / NTH;
+    constexpr int CROW = BN + 4;
+    constexpr int LDS_BYTES = 2 * STAGE > BM * CROW * 4 ? 2 * STAGE : BM * CROW * 4;
+    __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
+
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+    const int w = wave_id();
+    const int wn = w % WN, wm = w / WN;
+    const int t = (int)threadIdx.x;
+    const int tile_n = blockIdx.x, tile_m = blockIdx.y, split = blockIdx.z;
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+    const int nblk = (p.K + BK - 1) / BK;
+    const int b_lo = (int)(((long long)nblk * split) / p.splits);
+    const int b_hi = (int)(((long long)nblk * (split + 1)) / p.splits);
+
+    // Ranges end at the last byte of each operand, rounded up to a dword.
+    const __amdgpu_buffer_rsrc_t ra =
+        make_rsrc(p.A + (size_t)m0 * p.lda,
+                  (uint32_t)min<size_t>(((size_t)(p.M - 1 - m0) * p.lda + p.K + 3) & ~(size_t)3, 0x7FFFFFFFull));
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(p.B + (size_t)n0 * p.ldb,
+                  (uint32_t)min<size_t>(((size_t)(p.N - 1 - n0) * p.ldb + p.K + 3) & ~(size_t)3, 0x7FFFFFFFull));
+
+    uint32_t a_off[AU], b_off[BU];
+    int a_lds[AU], b_lds[BU], a_c[AU];
+#pragma unroll
+    for (int i = 0; i < AU; ++i) {
+        const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
+        const bool ok = (ACH % NTH == 0 || idx < ACH) && m0 + row < p.M;
+        a_off[i] = ok ? (uint32_t)row * p.lda + 16 * c : kOobOffset;
+        a_lds[i] = row * ROWB + swz16(row, c) * 16;
+        a_c[i] = 16 * c;
+    }
+#pragma unroll
+    for (int i = 0; i < BU; ++i) {
+        const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
+        const bool ok = (BCH % NTH == 0 || idx < BCH) && n0 + row < p.N;
+        b_off[i] = ok ? (uint32_t)row * p.ldb + 16 * c : kOobOffset;
+        b_lds[i] = A_BYTES + row * ROWB + swz16(row, c) * 16;
+    }
+
+    i32x4 sa[D][AU], sb[D][BU];
+    auto load_stage = [&](int blk, int slot) {
+        const uint32_t k0 = (uint32_t)(blk < b_hi ? blk : b_hi - 1) * BK;
+#pragma unroll
+        for (int i = 0; i < AU; ++i) sa[slot][i] = __builtin_bit_cast(i32x4, buf_load_x4(ra, a_off[i] + k0));
+#pragma unroll
+        for (int i = 0; i < BU; ++i) sb[slot][i] = __builtin_bit_cast(i32x4, buf_load_x4(rb, b_off[i] + k0));
+    };
+    auto write_stage = [&](int slot, int buf, int blk) {
+        char* St = lds + buf * STAGE;
+        // Bytes of A past K (the next row's data) are zeroed in the block
+        // that holds k = K - 1, which zeroes their products whatever B holds.
+        const bool tail = (blk + 1) * BK > p.K;
+#pragma unroll
+        for (int i = 0; i < AU; ++i) {
+            i32x4 v = sa[slot][i];
+            if (tail) v = mask_chunk(v, p.K - (blk * BK + a_c[i]));
+            if (ACH % NTH == 0 || t + i * NTH < ACH) *reinterpret_cast<i32x4*>(St + a_lds[i]) = v;
+        }
+#pragma unroll
+        for (int i = 0; i < BU; ++i)
+            if (BCH % NTH == 0 || t + i * NTH < BCH) *reinterpret_cast<i32x4*>(St + b_lds[i]) = sb[slot][i];
+    };
+
+    int a_rd[2][MT], b_rd[2][NT];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        const int c = kk * 4 + g;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int row = (wm * MT + mt) * 16 + r;
+            a_rd[kk][mt] = row * ROWB + swz16(row, c) * 16;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int row = (wn * NT + nt) * 16 + r;
+            b_rd[kk][nt] = A_BYTES + row * ROWB + swz16(row, c) * 16;
+        }
+    }
+    i32x4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = i32x4{0, 0, 0, 0};
+    auto compute = [&](int buf) {
+        const char* St = lds + buf * STAGE;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            i32x4 af[MT], bfr[NT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const i32x4*>(St + a_rd[kk][mt]);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) bfr[nt] = *reinterpret_cast<const i32x4*>(St + b_rd[kk][nt]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[mt], bfr[nt], acc[mt][nt], 0, 0, 0);
+        }
+    };
+
+    const int nb = b_hi - b_lo;
+#pragma unroll
+    for (int d = 0; d < D; ++d) load_stage(b_lo + d, d);
+    write_stage(0, 0, b_lo);
+    __syncthreads();
+    int i0 = 0;
+    for (; i0 + D <= nb; i0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int i = i0 + d;
+            load_stage(b_lo + i + D, d);
+            compute(i & 1);
+            write_stage((d + 1) % D, (i + 1) & 1, b_lo + i + 1);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        const int i = i0 + d;
+        if (i < nb) {
+            compute(i & 1);
+            write_stage((d + 1) % D, (i + 1) & 1, b_lo + i + 1);
+            __syncthreads();
+        }
+    }
+
+    // Stage the accumulators in LDS (row-major tile), then write whole rows.
+    int32_t* Cs = reinterpret_cast<int32_t*>(lds);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                Cs[((wm * MT + mt) * 16 + 4 * g + i) * CROW + (wn * NT + nt) * 16 + r] = acc[mt][nt][i];
+    __syncthreads();
+    constexpr int Q4 = BN / 4;
+    if (p.splits > 1) {
+        // Exact int32 partial tile [split][tile][BM * BN], summed by the
+        // reduce kernel that follows.
+        const int tiles = gridDim.x * gridDim.y;
+        const int tile_id = tile_m * gridDim.x + tile_n;
+        int32_t* part = p.part + ((size_t)split * tiles + tile_id) * (BM * BN);
+        for (int e = t; e < BM * Q4; e += NTH) {
+            const int row = e / Q4, q = e % Q4;
+            *reinterpret_cast<i32x4*>(part + row * BN + 4 * q) = *reinterpret_cast<const i32x4*>(&Cs[row * CROW + 4 * q]);
+        }
+        return;
+    }
+    const size_t esz = EPI == 0 ? 4 : 4;
+    const __amdgpu_buffer_rsrc_t rc =
+        make_rsrc(static_cast<char*>(p.C) + ((size_t)m0 * p.ldc + n0) * esz,
+                  (uint32_t)min<size_t>(((size_t)(p.M - 1 - m0) * p.ldc + (p.N - n0)) * esz, 0x7FFFFFFFull));
+    for (int e = t; e < BM * Q4; e += NTH) {
+        const int row = e / Q4, q = e % Q4;
+        const int m = m0 + row, n = n0 + 4 * q;
+        if (m >= p.M || n >= p.N) continue;
+        const i32x4 v = *reinterpret_cast<const i32x4*>(&Cs[row * CROW + 4 * q]);
+        const uint32_t off = ((uint32_t)row * p.ldc + 4 * q) * 4u;
+        if (n + 4 <= p.N) {
+            u32x4 out;
+            if constexpr (EPI == 0) {
+                out = __builtin_bit_cast(u32x4, v);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) out[k] = as_u32((float)v[k] * p.scale[n + k]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(out, rc, off, 0, 0);
+        } else {
+            for (int k = 0; k < p.N - n; ++k) {
+                if constexpr (EPI == 0) static_cast<int32_t*>(p.C)[(size_t)m * p.ldc + n + k] = v[k];
+                else static_cast<float*>(p.C)[(size_t)m * p.ldc + n + k] = (float)v[k] * p.scale[n + k];
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- launch table
 // {MT, NT, WM, WN, KW}
 static const S8Config kS8Configs[] = {
@@ -228,6 +443,17 @@ static const S8Config kS8Configs[] = {
     {2, 2, 2, 2, 1},  // 2: 64 x 64 tiles
     {2, 2, 4, 2, 1},  // 3: 128 x 64 tiles
     {2, 4, 4, 1, 1},  // 4: 128 x 64 tiles, 4 waves
+    {1, 1, 1, 1, 8},  // 5: M <= 16, 16 x 16 tiles, k split over 8 waves
+    {2, 1, 2, 2, 2},  // 6: 64 x 32 tiles, k split over 2 waves
+    {2, 1, 4, 2, 1},  // 7: 128 x 32 tiles, 8 waves
+    {1, 1, 4, 2, 1},  // 8: 64 x 32 tiles, 8 waves
+    {1, 1, 1, 2, 4},  // 9: M <= 16, 16 x 32 tiles, k split over 4 waves
+    {2, 2, 2, 2, 1, 2},  // 10: 64 x 64 through LDS
+    {2, 1, 2, 2, 1, 2},  // 11: 64 x 32 through LDS
+    {2, 2, 4, 2, 1, 2},  // 12: 128 x 64 through LDS, 8 waves
+    {1, 1, 2, 2, 1, 3},  // 13: 32 x 32 through LDS, 3 blocks ahead
+    {2, 1, 2, 4, 1, 2},  // 14: 64 x 64 through LDS, 8 waves
+    {1, 1, 1, 4, 1, 3},  // 15: 16 x 64 through LDS (M <= 16)
 };
 
 int s8_config_count() { return (int)(sizeof(kS8Configs) / sizeof(kS8Configs[0])); }
@@ -241,12 +467,25 @@ static hipError_t launch_s8_cfg(int cfg, dim3 grid, const S8Args& a, hipStream_t
         case 2: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 2, 2, 2, 1, EPI, AL>), grid, dim3(256), 0, s, a); break;
         case 3: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 2, 4, 2, 1, EPI, AL>), grid, dim3(512), 0, s, a); break;
         case 4: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 4, 4, 1, 1, EPI, AL>), grid, dim3(256), 0, s, a); break;
+        case 5: hipLaunchKernelGGL((dnnopt_mfma_s8<1, 1, 1, 1, 8, EPI, AL>), grid, dim3(512), 0, s, a); break;
+        case 6: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 1, 2, 2, 2, EPI, AL>), grid, dim3(512), 0, s, a); break;
+        case 7: hipLaunchKernelGGL((dnnopt_mfma_s8<2, 1, 4, 2, 1, EPI, AL>), grid, dim3(512), 0, s, a); break;
+        case 8: hipLaunchKernelGGL((dnnopt_mfma_s8<1, 1, 4, 2, 1, EPI, AL>), grid, dim3(512), 0, s, a); break;
+        case 9: hipLaunchKernelGGL((dnnopt_mfma_s8<1, 1, 1, 2, 4, EPI, AL>), grid, dim3(512), 0, s, a); break;
+        case 10: hipLaunchKernelGGL((dnnopt_s8_lds<2, 2, 2, 2, 2, EPI>), grid, dim3(256), 0, s, a); break;
+        case 11: hipLaunchKernelGGL((dnnopt_s8_lds<2, 1, 2, 2, 2, EPI>), grid, dim3(256), 0, s, a); break;
+        case 12: hipLaunchKernelGGL((dnnopt_s8_lds<2, 2, 4, 2, 2, EPI>), grid, dim3(512), 0, s, a); break;
+        case 13: hipLaunchKernelGGL((dnnopt_s8_lds<1, 1, 2, 2, 3, EPI>), grid, dim3(256), 0, s, a); break;
+        case 14: hipLaunchKernelGGL((dnnopt_s8_lds<2, 1, 2, 4, 2, EPI>), grid, dim3(512), 0, s, a); break;
+        case 15: hipLaunchKernelGGL((dnnopt_s8_lds<1, 1, 1, 4, 3, EPI>), grid, dim3(256), 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
 hipError_t launch_mfma_s8(int cfg_idx, int epi, int aligned, dim3 grid, const S8Args& a, hipStream_t s) {
+    if (cfg_idx < 0 || cfg_idx >= s8_config_count()) return hipErrorInvalidValue;
+    if (cfg_idx >= kS8FirstLds && !aligned) return hipErrorInvalidValue;
     if (epi) return aligned ? launch_s8_cfg<1, 1>(cfg_idx, grid, a, s) : launch_s8_cfg<1, 0>(cfg_idx, grid, a, s);
     return aligned ? launch_s8_cfg<0, 1>(cfg_idx, grid, a, s) : launch_s8_cfg<0, 0>(cfg_idx, grid, a, s);
 }

@@ -93,46 +93,66 @@ namespace dnnopt_hip {
 // Sum k-split partial tiles [split][tile][bm*bn] (tile = tile_m * tiles_n +
 // tile_n, row-major inside a tile) into C with the reference epilogue.  One
 // thread per 4 consecutive columns of a tile row: the partial reads of a
-// warp are contiguous, C (for beta != 0) and up to 8 splits are requested
-// before the first add, and splits are added in ascending order -- the same
-// order as the last-arriving-workgroup reduction, so both give the same bits.
+// wave are contiguous and C (for beta != 0) is requested with the partials.
+// Q = 1 (up to 16 splits): splits are added in ascending order -- the order
+// of the last-arriving-workgroup reduction, so both give the same bits.
+// Q > 1 (many splits): Q threads per output each add an ascending range of
+// splits, and the Q range sums are added in ascending order through LDS; the
+// order is fixed, so the result is still reproducible.
+template <int Q>
 __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restrict__ part, int splits,
                                                            int tiles_n, int tiles, int bm, int bn, int M, int N,
                                                            float alpha, float beta, float* C, int ldc) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int OUTS = 256 / Q;
+    __shared__ f4 red[Q > 1 ? Q * OUTS : 1];
+    const int o = threadIdx.x % OUTS, q = threadIdx.x / OUTS;
     const int per_tile = bm * bn / 4;
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (long long)tiles * per_tile) return;
-    const int tile = (int)(idx / per_tile);
-    const int loc = (int)(idx % per_tile) * 4;
+    const long long idx = (long long)blockIdx.x * OUTS + o;
+    const bool valid = idx < (long long)tiles * per_tile;
+    const int tile = valid ? (int)(idx / per_tile) : 0;
+    const int loc = valid ? (int)(idx % per_tile) * 4 : 0;
     const int m = (tile / tiles_n) * bm + loc / bn;
     const int n = (tile % tiles_n) * bn + loc % bn;
-    if (m >= M || n >= N) return;
+    const bool live = valid && m < M && n < N;
     float* c = C + (size_t)m * ldc + n;
     float c_old[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (beta != 0.0f) {
+    if (live && q == 0 && beta != 0.0f) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             if (n + e < N) c_old[e] = c[e];
     }
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    const f4* src = reinterpret_cast<const f4*>(part) + idx;
-    const size_t stride = (size_t)tiles * per_tile;
-    f4 s = src[0];
-    int sp = 1;
-    for (; sp + 8 <= splits; sp += 8) {
+    const int s_lo = (int)((long long)splits * q / Q), s_hi = (int)((long long)splits * (q + 1) / Q);
+    f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live && s_lo < s_hi) {
+        const f4* src = reinterpret_cast<const f4*>(part) + idx;
+        const size_t stride = (size_t)tiles * per_tile;
+        s = src[(size_t)s_lo * stride];
+        int sp = s_lo + 1;
+        for (; sp + 8 <= s_hi; sp += 8) {
+            f4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(sp + u) * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
         f4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(sp + u) * stride];
+        for (int u = 0; u < 8; ++u)
+            if (sp + u < s_hi) v[u] = src[(size_t)(sp + u) * stride];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) s += v[u];
+        for (int u = 0; u < 8; ++u)
+            if (sp + u < s_hi) s += v[u];
     }
-    f4 v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-        if (sp + u < splits) v[u] = src[(size_t)(sp + u) * stride];
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-        if (sp + u < splits) s += v[u];
+    if constexpr (Q > 1) {
+        red[q * OUTS + o] = s;
+        __syncthreads();
+        if (q != 0) return;
+        s = red[o];
+        for (int qq = 1; qq < Q; ++qq)
+            if ((long long)splits * qq / Q < (long long)splits * (qq + 1) / Q) s += red[qq * OUTS + o];
+    }
+    if (!live) return;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
         if (n + e < N) c[e] = beta == 0.0f ? alpha * s[e] : __builtin_fmaf(alpha, s[e], beta * c_old[e]);
@@ -141,9 +161,13 @@ __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restr
 hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
                                 int N, float alpha, float beta, float* C, int ldc, hipStream_t s) {
     const long long quads = (long long)tiles_n * tiles_m * bm * bn / 4;
-    const unsigned blocks = (unsigned)((quads + 255) / 256);
-    hipLaunchKernelGGL(dnnopt_splitk_reduce, dim3(blocks), dim3(256), 0, s, part, splits, tiles_n,
-                       tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc);
+    if (splits <= 16) {
+        hipLaunchKernelGGL(dnnopt_splitk_reduce<1>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, part,
+                           splits, tiles_n, tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc);
+    } else {
+        hipLaunchKernelGGL(dnnopt_splitk_reduce<16>, dim3((unsigned)((quads + 15) / 16)), dim3(256), 0, s, part,
+                           splits, tiles_n, tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc);
+    }
     return hipGetLastError();
 }
 

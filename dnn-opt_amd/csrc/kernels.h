@@ -70,7 +70,11 @@ struct S8Args {
 
 struct S8Config {
     int mt, nt, wm, wn, kw;
+    int depth;  // LDS-staged configurations: k-blocks loaded ahead
 };
+// Configurations from this index on stage both operands through LDS; they
+// need 4-byte aligned rows and reduce k-splits with the reduce kernel only.
+constexpr int kS8FirstLds = 10;
 // Index into the table of built int8 configurations.
 int s8_config_count();
 S8Config s8_config(int idx);
