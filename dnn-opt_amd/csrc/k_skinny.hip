@@ -168,7 +168,9 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     uint32_t base_lo = 0;
     const __amdgpu_buffer_rsrc_t rs = rsrc_aligned(bbase, remain, &base_lo);
     const uint32_t rowbytes = (uint32_t)p.ldb * ES;
-    const uint32_t lane_off = (uint32_t)lane * VEC * ES + base_lo;
+    // Lanes whose columns all lie past N read nothing (out-of-range offset)
+    // instead of the next row's data.
+    const uint32_t lane_off = col0 + lane * VEC < p.N ? (uint32_t)lane * VEC * ES + base_lo : kOobOffset;
 
     // Unsplit tiles store C directly: fetch the C values of this thread's
     // outputs now so that the read overlaps the main loop.
@@ -195,15 +197,15 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) acc[m][v] = 0.0f;
 
-    int k = k_lo;
-    for (; k + U <= k_hi; k += U) {
-        u32x4 raw[U];
+    auto load_block = [&](u32x4 (&raw)[U], int k0) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) raw[u] = load_row<AL>(rs, (uint32_t)(k + u - kb) * rowbytes + lane_off);
+        for (int u = 0; u < U; ++u) raw[u] = load_row<AL>(rs, (uint32_t)(k0 + u - kb) * rowbytes + lane_off);
+    };
+    auto compute_block = [&](const u32x4 (&raw)[U], int k0) {
 #pragma unroll
         for (int g0 = 0; g0 < U; g0 += UG) {
             float av[MR][UG];
-            load_a_block<MR, UG, MODE, AK>(p, k + g0, av);
+            load_a_block<MR, UG, MODE, AK>(p, k0 + g0, av);
 #pragma unroll
             for (int u = 0; u < UG; ++u) {
                 float bv[VEC];
@@ -214,7 +216,36 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
                     for (int v = 0; v < VEC; ++v) acc[m][v] = __builtin_fmaf(av[m][u], bv[v], acc[m][v]);
             }
         }
+    };
+
+    int k = k_lo;
+#if DNNOPT_SKINNY_PIPE
+    // Two blocks of U rows alternate: the loads of the next block are in
+    // flight while the current one is consumed.  At the end of the range the
+    // prefetch re-reads the last whole block (unused), keeping every load
+    // unconditional.
+    if (k + U <= k_hi) {
+        const int k_last = k_lo + ((k_hi - k_lo) / U - 1) * U;  // last whole block
+        u32x4 r0[U], r1[U];
+        load_block(r0, k);
+        for (; k + 2 * U <= k_hi; k += 2 * U) {
+            load_block(r1, k + U);
+            compute_block(r0, k);
+            load_block(r0, min(k + 2 * U, k_last));
+            compute_block(r1, k + U);
+        }
+        if (k + U <= k_hi) {
+            compute_block(r0, k);
+            k += U;
+        }
     }
+#else
+    for (; k + U <= k_hi; k += U) {
+        u32x4 raw[U];
+        load_block(raw, k);
+        compute_block(raw, k);
+    }
+#endif
     for (; k < k_hi; ++k) {
         const u32x4 raw = load_row<AL>(rs, (uint32_t)(k - kb) * rowbytes + lane_off);
         float bv[VEC];

@@ -40,7 +40,10 @@ struct SkinnyArgs {
 #ifndef DNNOPT_SKINNY_UNROLL
 #define DNNOPT_SKINNY_UNROLL 16
 #endif
-constexpr int kSkinnyUnroll = DNNOPT_SKINNY_UNROLL;  // rows of B in flight per wave
+constexpr int kSkinnyUnroll = DNNOPT_SKINNY_UNROLL;  // rows of B per load block of a wave
+#ifndef DNNOPT_SKINNY_PIPE
+#define DNNOPT_SKINNY_PIPE 0  // 1: double-buffered load blocks
+#endif
 inline int skinny_tile_cols(int mode) { return mode == kSkinnyBF16 ? 512 : 256; }
 inline int skinny_elem_bytes(int mode) { return mode == kSkinnyBF16 ? 2 : 4; }
 
