@@ -411,12 +411,16 @@ __device__ __forceinline__ int swz_b(int n, int c) { return c ^ ((n ^ (n >> 3)) 
 template <int MT, int NT, int WM, int WN, int D, int MODE>
 __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) {
     using S = TileShape<MT, NT, WM, WN, 1>;
-    constexpr int BM = S::BM, BN = S::BN, BK = 64;
+    constexpr int BM = S::BM, BN = S::BN;
+    // k per block: DNNOPT_LDS_KB when both stages fit in 128 KiB of LDS.
+    constexpr int BK = (BM + BN) * DNNOPT_LDS_KB * 2 * 2 <= 131072 ? DNNOPT_LDS_KB : 64;
     constexpr int NTH = WM * WN * 64;
-    constexpr int ROWB = BK * 2;  // bytes of one LDS row (64 bf16)
+    constexpr int ROWB = BK * 2;  // bytes of one LDS row (BK bf16)
+    constexpr int CPR = ROWB / 16;  // 16-byte chunks per LDS row
+    constexpr int KK = BK / 32;     // MFMA k-steps per block
     constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
-    constexpr int ACH = BM * 8;                // A chunks (8 k) per block
-    constexpr int BUN = (BN / 8) * 16;         // B units (4 k x 8 n) per block
+    constexpr int ACH = BM * CPR;              // A chunks (8 k) per block
+    constexpr int BUN = (BN / 8) * (BK / 4);   // B units (4 k x 8 n) per block
     constexpr int AU = (ACH + NTH - 1) / NTH;  // per thread
     constexpr int BU = (BUN + NTH - 1) / NTH;
     // The two k-block stages, reused after the main loop to stage C rows.
@@ -456,7 +460,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     int a_c[AU];
 #pragma unroll
     for (int i = 0; i < AU; ++i) {
-        const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
+        const int idx = t + i * NTH, row = idx / CPR, c = idx % CPR;
         const bool ok = (ACH % NTH == 0 || idx < ACH) && m0 + row < p.M;
         a_off[i] = ok ? ((uint32_t)row * p.lda + 8 * c) * ES : kOobOffset;
         a_lds[i] = row * ROWB + swz_a(row, c) * 16;
@@ -549,9 +553,9 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    int a_rd[2][MT], b_rd[2][NT];
+    int a_rd[KK][MT], b_rd[KK][NT];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < KK; ++kk) {
         const int c = kk * 4 + g;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -567,7 +571,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     auto compute = [&](int buf) {
         const char* St = lds + buf * STAGE;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < KK; ++kk) {
             u32x4 af[MT], bfr[NT];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const u32x4*>(St + a_rd[kk][mt]);
@@ -673,6 +677,8 @@ static const TileConfig kTileConfigs[] = {
     {2, 4, 2, 2, 1, 4},  // 11: 64 x 128  bf16 through LDS, 4 blocks ahead
     {4, 2, 2, 4, 1, 3},  // 12: 128 x 128 bf16 through LDS, 8 waves, 3 blocks ahead
     {2, 3, 4, 2, 1, 3},  // 13: 128 x 96  bf16 through LDS, 8 waves, 3 blocks ahead
+    {2, 3, 4, 2, 1, 2},  // 14: 128 x 96  bf16 through LDS, 8 waves
+    {4, 2, 2, 4, 1, 2},  // 15: 128 x 128 bf16 through LDS, 8 waves
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -721,6 +727,8 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_LDS_CASE(11, 2, 4, 2, 2, 4)
         DNNOPT_TILE_LDS_CASE(12, 4, 2, 2, 4, 3)
         DNNOPT_TILE_LDS_CASE(13, 2, 3, 4, 2, 3)
+        DNNOPT_TILE_LDS_CASE(14, 2, 3, 4, 2, 2)
+        DNNOPT_TILE_LDS_CASE(15, 4, 2, 2, 4, 2)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -114,6 +114,9 @@ struct TileConfig {
 };
 int tile_config_count();
 TileConfig tile_config(int idx);
+#ifndef DNNOPT_LDS_KB
+#define DNNOPT_LDS_KB 64  // k per LDS stage of the bf16 tile kernel (64 or 128)
+#endif
 // Configurations from this index on are the LDS-staged bf16 kernels: bf16 or
 // fp32-rounded modes only, no transposes, rows of A and B 4-byte aligned.
 constexpr int kTileFirstLds = 5;
