@@ -88,6 +88,8 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
     a.beta = beta;
     a.transA = ta;
     a.transB = tb;
+    a.tiles_n = L.tn;
+    a.tiles_m = L.tm;
     a.splits = (int)L.grid.z;
     a.defer_reduce = L.defer_reduce;
     if (a.splits > 1) {
@@ -102,8 +104,7 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
                         L.mode != kTileBF16 || ((reinterpret_cast<uintptr_t>(A) & 3u) == 0 && (lda & 1) == 0);
     int st = finish_launch(launch_tile(L.mode, L.cfg, ta, tb, aligned, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
-    return finish_launch(launch_splitk_reduce(a.part, a.splits, (int)L.grid.x, (int)L.grid.y, L.bm, L.bn, M, N,
-                                              alpha, beta, C, ldc, s));
+    return finish_launch(launch_splitk_reduce(a.part, a.splits, L.tn, L.tm, L.bm, L.bn, M, N, alpha, beta, C, ldc, s));
 }
 
 bool dims_ok(int M, int N, int K) { return M > 0 && N > 0 && K > 0; }
@@ -231,6 +232,8 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
     a.K = K;
     a.splits = (int)L.grid.z;
     a.defer_reduce = L.defer_reduce;
+    a.tiles_n = L.tn;
+    a.tiles_m = L.tm;
     if (a.splits > 1) {
         void* part = nullptr;
         unsigned* tickets = nullptr;
@@ -241,8 +244,7 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
     }
     st = finish_launch(launch_mfma_s8(L.cfg, epi, aligned, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
-    return finish_launch(launch_s8_reduce(a.part, a.splits, (int)L.grid.x, (int)L.grid.y, L.bm, L.bn, M, N, epi,
-                                          scale, C, ldc, s));
+    return finish_launch(launch_s8_reduce(a.part, a.splits, L.tn, L.tm, L.bm, L.bn, M, N, epi, scale, C, ldc, s));
 }
 
 int dnnopt_hip_gemm_s8s8s32(int M, int N, int K, const int8_t* A, int lda, const int8_t* B, int ldb, int32_t* C,

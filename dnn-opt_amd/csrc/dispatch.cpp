@@ -216,8 +216,11 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     L->cfg = cfg;
     L->bm = bm;
     L->bn = bn;
-    L->grid = dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
-    L->defer_reduce = (s > 1 && (split_reduce_mode() || s > kTicketSplitLimit || tiles > kMaxTickets)) ? 1 : 0;
+    L->tn = (int)tn;
+    L->tm = (int)tm;
+    // LDS-staged tiles are launched as one XCD-ordered row of workgroups.
+    L->grid = lds ? dim3((unsigned)xcd_grid((int)tn, (int)tm), 1, (unsigned)s) : dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
+    L->defer_reduce = (s > 1 && (split_reduce_mode() || s > kTicketSplitLimit || tiles > kMaxTickets || lds)) ? 1 : 0;
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(float) : 0;
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
     const int kernel = mode == kTileF32 ? DNNOPT_K_TILE_F32 : DNNOPT_K_TILE_BF16;
@@ -264,7 +267,9 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok) {
     L->cfg = cfg;
     L->bm = bm;
     L->bn = bn;
-    L->grid = dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
+    L->tn = (int)tn;
+    L->tm = (int)tm;
+    L->grid = lds ? dim3((unsigned)xcd_grid((int)tn, (int)tm), 1, (unsigned)s) : dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(int32_t) : 0;
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
     fill_pub(L, DNNOPT_K_MFMA_S8, lds ? "dnnopt_s8_lds" : "dnnopt_mfma_s8", bm, bn, (int)s, waves_per_wg * 64);

@@ -31,6 +31,7 @@ struct Launch {
     int mr = 0, nw = 0;  // skinny
     int cfg = 0;         // tile / int8 configuration index
     int bm = 0, bn = 0;  // tile shape
+    int tn = 0, tm = 0;  // tile grid (column tiles, row tiles)
     int tiles = 0;       // skinny: column tiles T (the grid has G >= T workgroups)
     dim3 grid;
     size_t part_bytes = 0;

@@ -264,7 +264,9 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     const int w = wave_id();
     const int wn = w % WN, wm = w / WN;
     const int t = (int)threadIdx.x;
-    const int tile_n = blockIdx.x, tile_m = blockIdx.y, split = blockIdx.z;
+    const TileXY tile = xcd_tile((int)blockIdx.x, p.tiles_n, p.tiles_m);
+    if (!tile.ok) return;
+    const int tile_n = tile.n, tile_m = tile.m, split = blockIdx.z;
     const int m0 = tile_m * BM, n0 = tile_n * BN;
 
     const int nblk = (p.K + BK - 1) / BK;
@@ -398,8 +400,8 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     if (p.splits > 1) {
         // Exact int32 partial tile [split][tile][BM * BN], summed by the
         // reduce kernel that follows.
-        const int tiles = gridDim.x * gridDim.y;
-        const int tile_id = tile_m * gridDim.x + tile_n;
+        const int tiles = p.tiles_n * p.tiles_m;
+        const int tile_id = tile_m * p.tiles_n + tile_n;
         int32_t* part = p.part + ((size_t)split * tiles + tile_id) * (BM * BN);
         for (int e = t; e < BM * Q4; e += NTH) {
             const int row = e / Q4, q = e % Q4;

@@ -66,7 +66,8 @@ struct TileShape {
 // epilogue.  Shared by the fp32 and bf16 kernels.
 template <int MT, int NT, int WM, int WN, int KW>
 __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][NT], float* red,
-                                            int* last_flag, int w, int lane) {
+                                            int* last_flag, int w, int lane, int tile_n, int tile_m, int tiles_n,
+                                            int tiles) {
     using S = TileShape<MT, NT, WM, WN, KW>;
     const int r = lane & 15, g = lane >> 4;
     const int wn = w % WN, wm = (w / WN) % WM, wk = w / (WN * WM);
@@ -96,9 +97,8 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
         }
     }
 
-    const int tile_n = blockIdx.x, tile_m = blockIdx.y, split = blockIdx.z;
-    const int tiles = gridDim.x * gridDim.y;
-    const int tile_id = tile_m * gridDim.x + tile_n;
+    const int split = blockIdx.z;
+    const int tile_id = tile_m * tiles_n + tile_n;
     if (p.splits > 1) {
         // Partials are written through to memory (coherent stores) so the
         // reducing workgroup can read them without cache maintenance.
@@ -254,7 +254,8 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_f32(TileArgs p) {
                                                                           acc[mt][nt], 0, 0, 0);
     }
 
-    tile_finish<MT, NT, WM, WN, KW>(p, acc, red, &last_flag, w, lane);
+    tile_finish<MT, NT, WM, WN, KW>(p, acc, red, &last_flag, w, lane, blockIdx.x, blockIdx.y, gridDim.x,
+                                    gridDim.x * gridDim.y);
 }
 
 // ---------------------------------------------------------------- bf16
@@ -370,7 +371,8 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
                                                                          acc[mt][nt], 0, 0, 0);
     }
 
-    tile_finish<MT, NT, WM, WN, KW>(p, acc, red, &last_flag, w, lane);
+    tile_finish<MT, NT, WM, WN, KW>(p, acc, red, &last_flag, w, lane, blockIdx.x, blockIdx.y, gridDim.x,
+                                    gridDim.x * gridDim.y);
 }
 
 // ---------------------------------------------------------------- bf16, LDS-staged
@@ -434,7 +436,9 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     const int w = wave_id();
     const int wn = w % WN, wm = w / WN;
     const int t = (int)threadIdx.x;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const TileXY tile = xcd_tile((int)blockIdx.x, p.tiles_n, p.tiles_m);
+    if (!tile.ok) return;
+    const int m0 = tile.m * BM, n0 = tile.n * BN;
 
     const int nblk = (p.K + BK - 1) / BK;
     const int b_lo = (int)(((long long)nblk * blockIdx.z) / p.splits);
@@ -618,7 +622,8 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     }
 
     if (p.splits > 1) {
-        tile_finish<MT, NT, WM, WN, 1>(p, acc, red_unused, &last_flag, w, lane);
+        tile_finish<MT, NT, WM, WN, 1>(p, acc, red_unused, &last_flag, w, lane, tile.n, tile.m, p.tiles_n,
+                                       p.tiles_n * p.tiles_m);
         return;
     }
     // Unsplit tile: stage the BM x BN accumulators in LDS (the main loop

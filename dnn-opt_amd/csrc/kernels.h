@@ -69,6 +69,7 @@ struct S8Args {
     int M, N, K;
     int splits;
     int defer_reduce;    // splits > 1: 1 = only store partials (a reduce kernel follows)
+    int tiles_n, tiles_m;  // LDS-staged kernel: tile grid (blockIdx.x is XCD-ordered, see xcd_tile)
 };
 
 struct S8Config {
@@ -106,7 +107,27 @@ struct TileArgs {
     int transA, transB;
     int splits;
     int defer_reduce;   // splits > 1: 1 = only store partials (a reduce kernel follows)
+    int tiles_n, tiles_m;  // LDS-staged kernels: tile grid (blockIdx.x is a linear, XCD-ordered index)
 };
+
+// LDS-staged kernels walk the tiles in an XCD-aware order: workgroup L runs on
+// XCD L % 8 (the hardware dispatches workgroups to XCDs round robin) and
+// takes the tiles of the column strips n = x, x + 8, x + 16, ... with all
+// their row tiles back to back, so the row tiles that share a strip of B run
+// together on one XCD and share its L2.  Workgroups past the last tile of
+// their XCD exit.  The order affects speed only, never which tiles exist.
+struct TileXY {
+    int n, m;
+    bool ok;
+};
+__host__ __device__ inline TileXY xcd_tile(int L, int tn, int tm) {
+    const int x = L & 7, j = L >> 3;
+    const int strips = tn > x ? (tn - x + 7) >> 3 : 0;  // tiles n = x (mod 8)
+    if (j >= strips * tm) return TileXY{0, 0, false};
+    return TileXY{(j / tm) * 8 + x, j % tm, true};
+}
+// Workgroups to launch for a tn x tm tile grid in that order.
+inline int xcd_grid(int tn, int tm) { return 8 * ((tn + 7) / 8) * tm; }
 
 struct TileConfig {
     int mt, nt, wm, wn, kw;
