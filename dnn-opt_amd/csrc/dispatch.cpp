@@ -242,7 +242,7 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok) {
     const S8Config c = s8_config(cfg);
     const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
     const long long tn = ceil_div(N, bn), tm = ceil_div(M, bm), tiles = tn * tm;
-    const int kb = lds ? 128 : 256;
+    const int kb = lds ? (c.kblk > 0 ? c.kblk : 128) : 256;
     const long long nblk = ceil_div(K, kb);
     const int waves_per_wg = c.wm * c.wn * c.kw;
     const long long cus = num_cus();

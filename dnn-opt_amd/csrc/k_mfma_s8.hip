@@ -248,13 +248,15 @@ namespace {
 __device__ __forceinline__ int swz16(int row, int c) { return c ^ (row & 7); }
 }  // namespace
 
-template <int MT, int NT, int WM, int WN, int D, int EPI>
+template <int MT, int NT, int WM, int WN, int D, int EPI, int BK = 128>
 __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
-    constexpr int BM = WM * MT * 16, BN = WN * NT * 16, BK = 128;
+    constexpr int BM = WM * MT * 16, BN = WN * NT * 16;  // BK: bytes (= k) per block
     constexpr int NTH = WM * WN * 64;
     constexpr int ROWB = BK;
+    constexpr int CPR = ROWB / 16;  // 16-byte chunks per LDS row
+    constexpr int KK = BK / 64;     // MFMA k-steps per block
     constexpr int A_BYTES = BM * ROWB, STAGE = (BM + BN) * ROWB;
-    constexpr int ACH = BM * 8, BCH = BN * 8;  // 16-byte chunks per block
+    constexpr int ACH = BM * CPR, BCH = BN * CPR;  // 16-byte chunks per block
     constexpr int AU = (ACH + NTH - 1) / NTH, BU = (BCH + NTH - 1) / NTH;
     constexpr int CROW = BN + 4;
     constexpr int LDS_BYTES = 2 * STAGE > BM * CROW * 4 ? 2 * STAGE : BM * CROW * 4;
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     int a_lds[AU], b_lds[BU], a_c[AU];
 #pragma unroll
     for (int i = 0; i < AU; ++i) {
-        const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
+        const int idx = t + i * NTH, row = idx / CPR, c = idx % CPR;
         const bool ok = (ACH % NTH == 0 || idx < ACH) && m0 + row < p.M;
         a_off[i] = ok ? (uint32_t)row * p.lda + 16 * c : kOobOffset;
         a_lds[i] = row * ROWB + swz16(row, c) * 16;
@@ -293,7 +295,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     }
 #pragma unroll
     for (int i = 0; i < BU; ++i) {
-        const int idx = t + i * NTH, row = idx >> 3, c = idx & 7;
+        const int idx = t + i * NTH, row = idx / CPR, c = idx % CPR;
         const bool ok = (BCH % NTH == 0 || idx < BCH) && n0 + row < p.N;
         b_off[i] = ok ? (uint32_t)row * p.ldb + 16 * c : kOobOffset;
         b_lds[i] = A_BYTES + row * ROWB + swz16(row, c) * 16;
@@ -323,9 +325,9 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
             if (BCH % NTH == 0 || t + i * NTH < BCH) *reinterpret_cast<i32x4*>(St + b_lds[i]) = sb[slot][i];
     };
 
-    int a_rd[2][MT], b_rd[2][NT];
+    int a_rd[KK][MT], b_rd[KK][NT];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < KK; ++kk) {
         const int c = kk * 4 + g;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
@@ -346,7 +348,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     auto compute = [&](int buf) {
         const char* St = lds + buf * STAGE;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < KK; ++kk) {
             i32x4 af[MT], bfr[NT];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const i32x4*>(St + a_rd[kk][mt]);
@@ -361,9 +363,11 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     };
 
     const int nb = b_hi - b_lo;
+    if (nb > 0) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_stage(b_lo + d, d);
-    write_stage(0, 0, b_lo);
+        for (int d = 0; d < D; ++d) load_stage(b_lo + d, d);
+        write_stage(0, 0, b_lo);
+    }
     __syncthreads();
     int i0 = 0;
     for (; i0 + D <= nb; i0 += D) {
@@ -456,6 +460,11 @@ static const S8Config kS8Configs[] = {
     {1, 1, 2, 2, 1, 3},  // 13: 32 x 32 through LDS, 3 blocks ahead
     {2, 1, 2, 4, 1, 2},  // 14: 64 x 64 through LDS, 8 waves
     {1, 1, 1, 4, 1, 3},  // 15: 16 x 64 through LDS (M <= 16)
+    {2, 1, 2, 2, 1, 2, 512},  // 16: 64 x 32 through LDS, 512-byte k blocks
+    {1, 1, 2, 2, 1, 2, 512},  // 17: 32 x 32 through LDS, 512-byte k blocks
+    {2, 2, 2, 2, 1, 2, 512},  // 18: 64 x 64 through LDS, 512-byte k blocks
+    {1, 1, 1, 4, 1, 2, 512},  // 19: 16 x 64 through LDS, 512-byte k blocks (M <= 16)
+    {1, 1, 2, 2, 1, 2, 256},  // 20: 32 x 32 through LDS, 256-byte k blocks
 };
 
 int s8_config_count() { return (int)(sizeof(kS8Configs) / sizeof(kS8Configs[0])); }
@@ -480,6 +489,11 @@ static hipError_t launch_s8_cfg(int cfg, dim3 grid, const S8Args& a, hipStream_t
         case 13: hipLaunchKernelGGL((dnnopt_s8_lds<1, 1, 2, 2, 3, EPI>), grid, dim3(256), 0, s, a); break;
         case 14: hipLaunchKernelGGL((dnnopt_s8_lds<2, 1, 2, 4, 2, EPI>), grid, dim3(512), 0, s, a); break;
         case 15: hipLaunchKernelGGL((dnnopt_s8_lds<1, 1, 1, 4, 3, EPI>), grid, dim3(256), 0, s, a); break;
+        case 16: hipLaunchKernelGGL((dnnopt_s8_lds<2, 1, 2, 2, 2, EPI, 512>), grid, dim3(256), 0, s, a); break;
+        case 17: hipLaunchKernelGGL((dnnopt_s8_lds<1, 1, 2, 2, 2, EPI, 512>), grid, dim3(256), 0, s, a); break;
+        case 18: hipLaunchKernelGGL((dnnopt_s8_lds<2, 2, 2, 2, 2, EPI, 512>), grid, dim3(256), 0, s, a); break;
+        case 19: hipLaunchKernelGGL((dnnopt_s8_lds<1, 1, 1, 4, 2, EPI, 512>), grid, dim3(256), 0, s, a); break;
+        case 20: hipLaunchKernelGGL((dnnopt_s8_lds<1, 1, 2, 2, 2, EPI, 256>), grid, dim3(256), 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

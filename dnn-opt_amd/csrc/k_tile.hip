@@ -596,9 +596,11 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     // Full groups of D iterations run without conditionals, so the compiler
     // can wait for exactly the loads each LDS write needs.
     const int nb = b_hi - b_lo;
+    if (nb > 0) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) load_stage(b_lo + d, d);
-    write_stage(0, 0, b_lo);
+        for (int d = 0; d < D; ++d) load_stage(b_lo + d, d);
+        write_stage(0, 0, b_lo);
+    }
     __syncthreads();
     int i0 = 0;
     for (; i0 + D <= nb; i0 += D) {

@@ -75,6 +75,7 @@ struct S8Args {
 struct S8Config {
     int mt, nt, wm, wn, kw;
     int depth;  // LDS-staged configurations: k-blocks loaded ahead
+    int kblk;   // LDS-staged configurations: bytes of k per block (0 = 128)
 };
 // Configurations from this index on stage both operands through LDS; they
 // need 4-byte aligned rows and reduce k-splits with the reduce kernel only.
