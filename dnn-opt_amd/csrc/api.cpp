@@ -122,6 +122,11 @@ size_t extent(int rows, int cols, int ld, size_t esize) {
     return ((size_t)(rows - 1) * (size_t)ld + (size_t)cols) * esize;
 }
 
+// C has to be uploaded when the kernel reads it (beta != 0) or when its
+// extent has elements the GEMM does not write (row padding, ldc > N): the
+// whole extent is copied back.
+bool c_read_or_kept(float beta, int ldc, int N) { return beta != 0.0f || ldc != N; }
+
 int sgemm_any(int ta, int tb, int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
               float beta, float* C, int ldc, bool naive) {
     if (M <= 0 || N <= 0 || K <= 0) return DNNOPT_OK;
@@ -130,7 +135,7 @@ int sgemm_any(int ta, int tb, int M, int N, int K, float alpha, const float* A, 
     int st = DNNOPT_OK;
     Operand a = stage_in(A, ta ? extent(K, M, lda, 4) : extent(M, K, lda, 4), 0, true, &st);
     Operand b = stage_in(B, tb ? extent(N, K, ldb, 4) : extent(K, N, ldb, 4), 1, true, &st);
-    Operand c = stage_in(C, extent(M, N, ldc, 4), 2, naive || beta != 0.0f, &st);
+    Operand c = stage_in(C, extent(M, N, ldc, 4), 2, naive || c_read_or_kept(beta, ldc, N), &st);
     if (st != DNNOPT_OK) return st;
     if (naive)
         st = dnnopt_hip_sgemm_naive(M, N, K, alpha, (const float*)a.dev, lda, (const float*)b.dev, ldb, beta,
@@ -172,7 +177,7 @@ void gemm_bf16(int M, int N, int K, float alpha, const float* A, int lda, const 
         } else {
             Operand a = stage_in(A, extent(M, K, lda, 4), 0, true, &st);
             Operand b = stage_in(B, extent(K, N, ldb, 4), 1, true, &st);
-            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, beta != 0.0f, &st);
+            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), &st);
             if (st == DNNOPT_OK)
                 st = dnnopt_hip_gemm_bf16_f32in(M, N, K, alpha, (const float*)a.dev, lda, (const float*)b.dev, ldb,
                                                 beta, (float*)c.dev, ldc, nullptr);
@@ -194,7 +199,7 @@ void gemm_bf16_bf16bf16f32(int M, int N, int K, float alpha, const bfloat16_t* A
         } else {
             Operand a = stage_in(A, extent(M, K, lda, 2), 0, true, &st);
             Operand b = stage_in(B, extent(K, N, ldb, 2), 1, true, &st);
-            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, beta != 0.0f, &st);
+            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), &st);
             if (st == DNNOPT_OK)
                 st = dnnopt_hip_gemm_bf16(M, N, K, alpha, (const uint16_t*)a.dev, lda, (const uint16_t*)b.dev, ldb,
                                           beta, (float*)c.dev, ldc, nullptr);
@@ -216,7 +221,7 @@ void gemm_int8(int M, int N, int K, float alpha, const float* A, int lda, const 
         } else {
             Operand a = stage_in(A, extent(M, K, lda, 4), 0, true, &st);
             Operand b = stage_in(B, extent(K, N, ldb, 4), 1, true, &st);
-            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, beta != 0.0f, &st);
+            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), &st);
             if (st == DNNOPT_OK)
                 st = dnnopt_hip_gemm_int8_f32(M, N, K, alpha, (const float*)a.dev, lda, (const float*)b.dev, ldb,
                                               beta, (float*)c.dev, ldc, nullptr);

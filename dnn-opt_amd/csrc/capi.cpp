@@ -53,11 +53,11 @@ int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B
         a.tickets = tickets;
     }
     // bf16 rows start on 4-byte boundaries only when the matrix does and its
-    // row stride is even.
+    // row stride is even.  bf16 A stored K x M is read element by element.
     const bool bf16 = L.mode == kSkinnyBF16;
     const int b_aligned = !bf16 || ((reinterpret_cast<uintptr_t>(B) & 3u) == 0 && (ldb & 1) == 0);
     int a_layout = a_sk == 1 ? 0 : 1;
-    if (bf16 && ((reinterpret_cast<uintptr_t>(A) & 3u) != 0 || (a_sm & 1) != 0)) a_layout = 2;
+    if (bf16 && (a_sk != 1 || (reinterpret_cast<uintptr_t>(A) & 3u) != 0 || (a_sm & 1) != 0)) a_layout = 2;
     int st = finish_launch(launch_skinny(L.mode, L.mr, L.nw, b_aligned, a_layout, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
     return finish_launch(launch_skinny_reduce(a.part, G, T, skinny_tile_cols(L.mode), M, N, a.ncols_pad, alpha,
@@ -70,7 +70,7 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
     // The LDS-staged bf16 kernel reads whole dwords: bf16 operands must start
     // on 4-byte boundaries, else the register-only kernel serves the call.
     if (L.cfg >= kTileFirstLds && L.mode == kTileBF16 &&
-        ((reinterpret_cast<uintptr_t>(A) & 3u) != 0 || (reinterpret_cast<uintptr_t>(B) & 3u) != 0)) {
+        ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) != 0) {
         const int st = plan_tile(L.mode, ta, tb, M, N, K, lda, ldb, &L, false);
         if (st != DNNOPT_OK) return st;
     }
@@ -100,8 +100,11 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
         a.part = static_cast<float*>(part);
         a.tickets = tickets;
     }
-    const int aligned = L.cfg >= kTileFirstLds ||
-                        L.mode != kTileBF16 || ((reinterpret_cast<uintptr_t>(A) & 3u) == 0 && (lda & 1) == 0);
+    // Register bf16 kernel: k-contiguous rows (A, and B stored N x K) that do
+    // not start on 4-byte boundaries are read with shifted loads.
+    const int aligned = L.cfg >= kTileFirstLds || L.mode != kTileBF16 ||
+                        ((reinterpret_cast<uintptr_t>(A) & 3u) == 0 && (lda & 1) == 0 &&
+                         (!tb || ((reinterpret_cast<uintptr_t>(B) & 3u) == 0 && (ldb & 1) == 0)));
     int st = finish_launch(launch_tile(L.mode, L.cfg, ta, tb, aligned, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
     return finish_launch(launch_splitk_reduce(a.part, a.splits, L.tn, L.tm, L.bm, L.bn, M, N, alpha, beta, C, ldc, s));
@@ -113,7 +116,7 @@ bool dims_ok(int M, int N, int K) { return M > 0 && N > 0 && K > 0; }
 
 extern "C" {
 
-int dnnopt_hip_abi_version(void) { return 1; }
+int dnnopt_hip_abi_version(void) { return 2; }
 
 int dnnopt_hip_device_count(void) { return visible_devices(); }
 
@@ -200,6 +203,40 @@ int dnnopt_hip_gemm_bf16(int M, int N, int K, float alpha, const uint16_t* A, in
     return gemm_bf16_common(0, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream);
 }
 
+int dnnopt_hip_gemm_bf16_ex(int transA, int transB, int M, int N, int K, float alpha, const uint16_t* A, int lda,
+                            const uint16_t* B, int ldb, float beta, float* C, int ldc, void* stream) {
+    if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return DNNOPT_ERR_INVALID_ARG;
+    if (!dims_ok(M, N, K)) return DNNOPT_OK;
+    if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
+    if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    hipStream_t s = as_stream(stream);
+    Launch L;
+    if (transA && !transB && M <= 8) {
+        // The skinny kernel reads a K x M A in place (A is M*K elements).
+        int st = plan_bf16(0, M, N, K, lda, ldb, &L);
+        if (st != DNNOPT_OK) return st;
+        return run_skinny(L, A, 1, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+    }
+    if (transA) {
+        // MFMA tiles read k-contiguous rows of A: transpose the K x M A into
+        // workspace (M x K, even row stride so rows stay 4-byte aligned).
+        const int ldt = (K + 1) & ~1;
+        void* ws = nullptr;
+        unsigned* unused = nullptr;
+        int st = get_workspace(s, (size_t)M * ldt * sizeof(uint16_t), &ws, &unused, kSlotTransA);
+        if (st != DNNOPT_OK) return st;
+        st = finish_launch(launch_transpose_u16(A, K, M, lda, static_cast<uint16_t*>(ws), ldt, s));
+        if (st != DNNOPT_OK) return st;
+        A = static_cast<const uint16_t*>(ws);
+        lda = ldt;
+    }
+    int st = plan_bf16(0, M, N, K, lda, ldb, &L, transB);
+    if (st != DNNOPT_OK) return st;
+    if (L.family == DNNOPT_K_SKINNY_BF16) return run_skinny(L, A, lda, 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+    return run_tile(L, 0, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+}
+
 int dnnopt_hip_gemm_bf16_f32in(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
                                float beta, float* C, int ldc, void* stream) {
     return gemm_bf16_common(1, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream);
@@ -272,7 +309,7 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
     const size_t qb_bytes = ((size_t)N * ldq + 255) & ~(size_t)255;
     void* stage = nullptr;
     unsigned* unused = nullptr;
-    int st = get_workspace(s, acc_bytes + qa_bytes + qb_bytes + 256, &stage, &unused, 1);
+    int st = get_workspace(s, acc_bytes + qa_bytes + qb_bytes + 256, &stage, &unused, kSlotQuant);
     if (st != DNNOPT_OK) return st;
     char* base = static_cast<char*>(stage);
     int32_t* acc = reinterpret_cast<int32_t*>(base);

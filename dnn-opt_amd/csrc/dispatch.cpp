@@ -155,11 +155,12 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
 int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, bool lds_ok) {
     *L = Launch{};
     const long long es = mode == kTileBF16 ? 2 : 4;
-    // bf16 GEMMs with 4-byte aligned rows go through the LDS-staged kernel.
-    const bool lds = mode != kTileF32 && lds_ok && !transA && !transB &&
+    // bf16 GEMMs with 4-byte aligned rows go through the LDS-staged kernel
+    // (B stored N x K too, for bf16 storage).
+    const bool lds = mode != kTileF32 && lds_ok && !transA && (!transB || mode == kTileBF16) &&
                      (mode == kTileF2B || ((lda & 1) == 0 && (ldb & 1) == 0)) &&
                      ((long long)(M + 128) * lda + K) * es < 0x7FFFFFFFll &&
-                     ((long long)K * ldb + N) * es < 0x7FFFFFFFll;
+                     (transB ? ((long long)(N + 128) * ldb + K) : ((long long)K * ldb + N)) * es < 0x7FFFFFFFll;
     int cfg;
     static const int forced_cfg = env_int("DNNOPT_TILE_CFG", 0);
     if (lds) {
@@ -281,9 +282,12 @@ int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, La
     return plan_tile(kTileF32, transA, transB, M, N, K, lda, ldb, L);
 }
 
-int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L) {
-    if (M <= 8) return plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L);
-    return plan_tile(fp32_inputs ? kTileF2B : kTileBF16, 0, 0, M, N, K, lda, ldb, L);
+int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB) {
+    // B stored N x K has k-contiguous columns: MFMA tiles read it in place
+    // for every M (the skinny kernel streams rows of a K x N B).
+    if (M <= 8 && !transB) return plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L);
+    if (transB && fp32_inputs) return DNNOPT_ERR_UNSUPPORTED;
+    return plan_tile(fp32_inputs ? kTileF2B : kTileBF16, 0, transB, M, N, K, lda, ldb, L);
 }
 
 }  // namespace dnnopt_hip

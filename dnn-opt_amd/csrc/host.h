@@ -54,7 +54,13 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok = true);
 
 // Route an fp32 GEMM to a kernel family (skinny or tile).
 int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L);
-// Route a bf16 GEMM (fp32_inputs: operands are fp32 and rounded in registers).
-int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L);
+// Route a bf16 GEMM (fp32_inputs: operands are fp32 and rounded in registers;
+// transB: B stored N x K, bf16 storage only).
+int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB = 0);
+
+// Workspace slots (get_workspace): 0 GEMM partials and tickets, 1 int8
+// quantization staging, 2 the column-major hook's temporary C, 3 transposed
+// bf16 A operands.
+constexpr int kSlotGemm = 0, kSlotQuant = 1, kSlotHookC = 2, kSlotTransA = 3;
 
 }  // namespace dnnopt_hip

@@ -263,8 +263,11 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_f32(TileArgs p) {
 // and are rounded to bf16 (nearest even, reference formula) on load.
 // AL = 0: rows of a bf16-storage A may start on a 2-byte boundary and are
 // read with funnel-shifted loads.
-template <int MT, int NT, int WM, int WN, int KW, int MODE, int AL>
+// TB = 1: B is stored N x K (k contiguous, bf16 storage only) and each
+// lane's 8 k of a column are one 16-byte load, like A's.
+template <int MT, int NT, int WM, int WN, int KW, int MODE, int AL, int TB = 0>
 __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) {
+    static_assert(!TB || MODE == kTileBF16, "B stored N x K needs bf16 storage");
     using S = TileShape<MT, NT, WM, WN, KW>;
     constexpr int KB = 128;
     constexpr int ES = MODE == kTileBF16 ? 2 : 4;
@@ -287,11 +290,11 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
     const char* B = static_cast<const char*>(p.B);
     const char* abase = A + ((size_t)m0 * p.lda + ks) * ES;
     const size_t arem = (size_t)(p.M - 1 - m0) * p.lda + (p.K - ks);
-    const char* bbase = B + ((size_t)ks * p.ldb + n0) * ES;
-    const size_t brem = (size_t)(p.K - 1 - ks) * p.ldb + (p.N - n0);
-    uint32_t alo = 0;
+    const char* bbase = TB ? B + ((size_t)n0 * p.ldb + ks) * ES : B + ((size_t)ks * p.ldb + n0) * ES;
+    const size_t brem = TB ? (size_t)(p.N - 1 - n0) * p.ldb + (p.K - ks) : (size_t)(p.K - 1 - ks) * p.ldb + (p.N - n0);
+    uint32_t alo = 0, blo = 0;
     const __amdgpu_buffer_rsrc_t ra = rsrc_aligned(abase, arem * ES, &alo);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase, clamp_rec(brem * ES));
+    const __amdgpu_buffer_rsrc_t rb = TB ? rsrc_aligned(bbase, brem * ES, &blo) : make_rsrc(bbase, clamp_rec(brem * ES));
 
     int mloc[MT], nloc[NT];
     bool mval[MT], nval[NT];
@@ -346,18 +349,27 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
             }
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                uint32_t h[8];
+                if constexpr (TB) {
+                    const uint32_t off =
+                        (nval[nt] && kvalid > 0) ? ((uint32_t)nloc[nt] * p.ldb + ko) * 2u + blo : kOobOffset;
+                    if constexpr (AL) b[nt][j] = buf_load_x4(rb, off);
+                    else b[nt][j] = buf_load_x4_unaligned(rb, off);
+                    if (kvalid < 8) b[nt][j] = keep_halves(b[nt][j], kvalid);
+                } else {
+                    uint32_t h[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const uint32_t off = (nval[nt] && e < kvalid) ? ((uint32_t)(ko + e) * p.ldb + nloc[nt]) * ES : kOobOffset;
-                    if constexpr (MODE == kTileBF16) {
-                        h[e] = buf_load_u16(rb, off);
-                    } else {
-                        h[e] = f32_to_bf16_bits(as_f32(buf_load_x1(rb, off)));
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t off =
+                            (nval[nt] && e < kvalid) ? ((uint32_t)(ko + e) * p.ldb + nloc[nt]) * ES : kOobOffset;
+                        if constexpr (MODE == kTileBF16) {
+                            h[e] = buf_load_u16(rb, off);
+                        } else {
+                            h[e] = f32_to_bf16_bits(as_f32(buf_load_x1(rb, off)));
+                        }
                     }
-                }
 #pragma unroll
-                for (int d = 0; d < 4; ++d) b[nt][j][d] = h[2 * d] | (h[2 * d + 1] << 16);
+                    for (int d = 0; d < 4; ++d) b[nt][j][d] = h[2 * d] | (h[2 * d + 1] << 16);
+                }
             }
         }
 #pragma unroll
@@ -387,6 +399,9 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
 // written by one store, fall in different banks.  The next block's global
 // loads are issued before the current block's MFMAs.
 //
+// TB = 1 (bf16 storage only): B is stored N x K.  Its rows are then staged
+// exactly like A's -- 16-byte chunks of 8 k, no transpose.
+//
 // Requirements (checked by the host): rows of A and B start on 4-byte
 // boundaries (even lda, ldb and 4-byte aligned pointers for bf16 storage).
 namespace {
@@ -410,8 +425,9 @@ __device__ __forceinline__ int swz_b(int n, int c) { return c ^ ((n ^ (n >> 3)) 
 
 }  // namespace
 
-template <int MT, int NT, int WM, int WN, int D, int MODE>
+template <int MT, int NT, int WM, int WN, int D, int MODE, int TB = 0>
 __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) {
+    static_assert(!TB || MODE == kTileBF16, "B stored N x K needs bf16 storage");
     using S = TileShape<MT, NT, WM, WN, 1>;
     constexpr int BM = S::BM, BN = S::BN;
     // k per block: DNNOPT_LDS_KB when both stages fit in 128 KiB of LDS.
@@ -422,7 +438,10 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     constexpr int KK = BK / 32;     // MFMA k-steps per block
     constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
     constexpr int ACH = BM * CPR;              // A chunks (8 k) per block
-    constexpr int BUN = (BN / 8) * (BK / 4);   // B units (4 k x 8 n) per block
+    // B units per block: 4 k x 8 n (stored K x N, 4 loads and 8 LDS stores
+    // each), or one 16-byte chunk of 8 k (stored N x K).
+    constexpr int BUN = TB ? BN * CPR : (BN / 8) * (BK / 4);
+    constexpr int BQ = TB ? 1 : 4, BL = TB ? 1 : 8;
     constexpr int AU = (ACH + NTH - 1) / NTH;  // per thread
     constexpr int BU = (BUN + NTH - 1) / NTH;
     // The two k-block stages, reused after the main loop to stage C rows.
@@ -446,22 +465,22 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
 
     constexpr int ES = MODE == kTileBF16 ? 2 : 4;
     const char* abase = static_cast<const char*>(p.A) + (size_t)m0 * p.lda * ES;
-    const char* bbase = static_cast<const char*>(p.B) + (size_t)n0 * ES;
+    const char* bbase = static_cast<const char*>(p.B) + (TB ? (size_t)n0 * p.ldb : (size_t)n0) * ES;
     // Ranges end at the last element of each operand, rounded up to a whole
     // dword: the range check of a dword load drops a dword that extends past
     // the range, and the last element may share its dword with the next.
     const __amdgpu_buffer_rsrc_t ra =
         make_rsrc(abase, clamp_rec((((size_t)(p.M - 1 - m0) * p.lda + p.K) * ES + 3) & ~(size_t)3));
-    const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(bbase, clamp_rec((((size_t)(p.K - 1) * p.ldb + (p.N - n0)) * ES + 3) & ~(size_t)3));
+    const size_t b_last = TB ? (size_t)(p.N - 1 - n0) * p.ldb + p.K : (size_t)(p.K - 1) * p.ldb + (p.N - n0);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase, clamp_rec((b_last * ES + 3) & ~(size_t)3));
 
     // Per-thread offsets that do not change from block to block are computed
     // once: global element offsets of this thread's A chunks and B rows (an
     // out-of-range offset for rows past M), LDS byte offsets of its stores
     // and of the wave's operand reads.
-    uint32_t a_off[AU], b_off[BU][4];
-    int a_lds[AU], b_lds[BU][8];
-    int a_c[AU];
+    uint32_t a_off[AU], b_off[BU][BQ];
+    int a_lds[AU], b_lds[BU][BL];
+    int a_c[AU], b_c[BU];
 #pragma unroll
     for (int i = 0; i < AU; ++i) {
         const int idx = t + i * NTH, row = idx / CPR, c = idx % CPR;
@@ -472,15 +491,25 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     }
 #pragma unroll
     for (int i = 0; i < BU; ++i) {
-        const int u = t + i * NTH, cg = u % (BN / 8), kg = u / (BN / 8);
-        const bool ok = BUN % NTH == 0 || u < BUN;
+        if constexpr (TB) {
+            const int idx = t + i * NTH, row = idx / CPR, c = idx % CPR;
+            const bool ok = (BUN % NTH == 0 || idx < BUN) && n0 + row < p.N;
+            b_off[i][0] = ok ? ((uint32_t)row * p.ldb + 8 * c) * ES : kOobOffset;
+            b_lds[i][0] = row * ROWB + swz_a(row, c) * 16;
+            b_c[i] = 8 * c;
+        } else {
+            const int u = t + i * NTH, cg = u % (BN / 8), kg = u / (BN / 8);
+            const bool ok = BUN % NTH == 0 || u < BUN;
+            b_c[i] = 0;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) b_off[i][q] = ok ? ((uint32_t)(4 * kg + q) * p.ldb + 8 * cg) * ES : kOobOffset;
-        const int c = kg >> 1, half = kg & 1;
+            for (int q = 0; q < BQ; ++q)
+                b_off[i][q] = ok ? ((uint32_t)(4 * kg + q) * p.ldb + 8 * cg) * ES : kOobOffset;
+            const int c = kg >> 1, half = kg & 1;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int n = 8 * cg + j;
-            b_lds[i][j] = ok ? n * ROWB + swz_b(n, c) * 16 + half * 8 : -1;
+            for (int j = 0; j < BL; ++j) {
+                const int n = 8 * cg + j;
+                b_lds[i][j] = ok ? n * ROWB + swz_b(n, c) * 16 + half * 8 : -1;
+            }
         }
     }
 
@@ -489,11 +518,11 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     // range by up to D - 1 blocks; those re-read the last block (never used),
     // so every load is unconditional and the compiler waits for exactly the
     // loads each LDS store needs.
-    u32x4 sa[D][AU], sb[D][BU][4];
+    u32x4 sa[D][AU], sb[D][BU][BQ];
     auto load_stage = [&](int blk, int slot) {
         const int bc = blk < b_hi ? blk : b_hi - 1;
         const uint32_t ka = (uint32_t)bc * BK * ES;
-        const uint32_t kb = (uint32_t)bc * BK * p.ldb * ES;
+        const uint32_t kb = TB ? ka : (uint32_t)bc * BK * p.ldb * ES;
 #pragma unroll
         for (int i = 0; i < AU; ++i) {
             if constexpr (MODE == kTileBF16) {
@@ -507,7 +536,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
 #pragma unroll
         for (int i = 0; i < BU; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < BQ; ++q) {
                 if constexpr (MODE == kTileBF16) {
                     sb[slot][i][q] = buf_load_x4(rb, b_off[i][q] + kb);
                 } else {
@@ -520,33 +549,41 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     auto write_stage = [&](int slot, int buf, int blk) {
         char* As = lds + buf * STAGE;
         char* Bs = As + A_BYTES;
-        // Only the block holding k = K - 1 has A elements past K (the next
-        // row's data): zero them.  B rows past K read as zero (out of range).
+        // Only the block holding k = K - 1 has elements of k-contiguous rows
+        // past K (the next row's data): zero them.  Rows of a K x N B past K
+        // read as zero (out of range).
         const bool tail = (blk + 1) * BK > p.K;
+        auto keep_k = [&](u32x4 v, int kvalid) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const int keep = kvalid - 2 * d;
+                v[d] = keep >= 2 ? v[d] : (keep == 1 ? (v[d] & 0xFFFFu) : 0u);
+            }
+            return v;
+        };
 #pragma unroll
         for (int i = 0; i < AU; ++i) {
             u32x4 v = sa[slot][i];
-            if (tail) {
-                const int kvalid = p.K - (blk * BK + a_c[i]);
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const int keep = kvalid - 2 * d;
-                    v[d] = keep >= 2 ? v[d] : (keep == 1 ? (v[d] & 0xFFFFu) : 0u);
-                }
-            }
+            if (tail) v = keep_k(v, p.K - (blk * BK + a_c[i]));
             if (ACH % NTH == 0 || t + i * NTH < ACH) *reinterpret_cast<u32x4*>(As + a_lds[i]) = v;
         }
 #pragma unroll
         for (int i = 0; i < BU; ++i) {
             if (BUN % NTH != 0 && t + i * NTH >= BUN) continue;
+            if constexpr (TB) {
+                u32x4 v = sb[slot][i][0];
+                if (tail) v = keep_k(v, p.K - (blk * BK + b_c[i]));
+                *reinterpret_cast<u32x4*>(Bs + b_lds[i][0]) = v;
+            } else {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-                typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-                u32x2 v;
-                v[0] = __builtin_amdgcn_perm(sb[slot][i][1][j >> 1], sb[slot][i][0][j >> 1], sel);
-                v[1] = __builtin_amdgcn_perm(sb[slot][i][3][j >> 1], sb[slot][i][2][j >> 1], sel);
-                *reinterpret_cast<u32x2*>(Bs + b_lds[i][j]) = v;
+                for (int j = 0; j < BL; ++j) {
+                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    u32x2 v;
+                    v[0] = __builtin_amdgcn_perm(sb[slot][i][1][j >> 1], sb[slot][i][0][j >> 1], sel);
+                    v[1] = __builtin_amdgcn_perm(sb[slot][i][3][j >> 1], sb[slot][i][2][j >> 1], sel);
+                    *reinterpret_cast<u32x2*>(Bs + b_lds[i][j]) = v;
+                }
             }
         }
     };
@@ -569,7 +606,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             const int n = (wn * NT + nt) * 16 + r;
-            b_rd[kk][nt] = A_BYTES + n * ROWB + swz_b(n, c) * 16;
+            b_rd[kk][nt] = A_BYTES + n * ROWB + (TB ? swz_a(n, c) : swz_b(n, c)) * 16;
         }
     }
     auto compute = [&](int buf) {
@@ -698,6 +735,9 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
             else if (ta && !tb) hipLaunchKernelGGL((dnnopt_tile_f32<MT, NT, WM, WN, KW, 1, 0>), grid, blk, 0, s, a); \
             else if (!ta && tb) hipLaunchKernelGGL((dnnopt_tile_f32<MT, NT, WM, WN, KW, 0, 1>), grid, blk, 0, s, a); \
             else hipLaunchKernelGGL((dnnopt_tile_f32<MT, NT, WM, WN, KW, 1, 1>), grid, blk, 0, s, a);    \
+        } else if (mode == kTileBF16 && tb) {                                                            \
+            if (al) hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileBF16, 1, 1>), grid, blk, 0, s, a); \
+            else hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileBF16, 0, 1>), grid, blk, 0, s, a);    \
         } else if (mode == kTileBF16) {                                                                  \
             if (al) hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileBF16, 1>), grid, blk, 0, s, a); \
             else hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileBF16, 0>), grid, blk, 0, s, a);    \
@@ -708,13 +748,15 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
 
 #define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN, D)                                                      \
     case IDX:                                                                                              \
-        if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16>), grid, blk, 0, s, a); \
+        if (mode == kTileBF16 && tb) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16, 1>), grid, blk, 0, s, a); \
+        else if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16>), grid, blk, 0, s, a); \
         else if (mode == kTileF2B) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileF2B>), grid, blk, 0, s, a); \
         else return hipErrorInvalidValue;                                                                  \
         break;
 
 hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid, const TileArgs& a, hipStream_t s) {
-    if (mode != kTileF32 && (ta || tb)) return hipErrorInvalidValue;
+    // Transposed operands: fp32 both, bf16 storage B only (stored N x K).
+    if (mode != kTileF32 && (ta || (tb && mode != kTileBF16))) return hipErrorInvalidValue;
     if (cfg_idx < 0 || cfg_idx >= tile_config_count()) return hipErrorInvalidValue;
     const TileConfig c = kTileConfigs[cfg_idx];
     const dim3 blk(c.wm * c.wn * c.kw * 64);

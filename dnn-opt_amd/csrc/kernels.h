@@ -140,9 +140,12 @@ TileConfig tile_config(int idx);
 #define DNNOPT_LDS_KB 64  // k per LDS stage of the bf16 tile kernel (64 or 128)
 #endif
 // Configurations from this index on are the LDS-staged bf16 kernels: bf16 or
-// fp32-rounded modes only, no transposes, rows of A and B 4-byte aligned.
+// fp32-rounded modes only, rows of A and B 4-byte aligned, no transposed A
+// (B stored N x K with bf16 storage).
 constexpr int kTileFirstLds = 5;
-// aligned: all rows of A start on 4-byte boundaries (matters for bf16 storage).
+// transA: fp32 only; transB: fp32, or bf16 storage with B stored N x K.
+// aligned: all k-contiguous rows (A; B stored N x K) start on 4-byte
+// boundaries (matters for bf16 storage).
 hipError_t launch_tile(int mode, int cfg_idx, int transA, int transB, int aligned, dim3 grid,
                        const TileArgs& a, hipStream_t s);
 
@@ -173,5 +176,19 @@ hipError_t launch_s8_reduce(const int32_t* part, int splits, int tiles_n, int ti
 hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm,
                                 int bn, int M, int N, float alpha, float beta, float* C, int ldc,
                                 hipStream_t s);
+
+// Column-major helpers of the oneDNN-hook entry points.  C(i, j) is at
+// C[j * ldc + i]; ldc < M means overlapping columns (see k_colmajor.hip).
+enum CmOp { kCmNone = 0, kCmZero = 1, kCmScale = 2 };
+// op on the M x N column-major C, then C += bias[i] (bias may be null).
+hipError_t launch_cm_fixup(float* C, int M, int N, long long ldc, int op, float beta, const float* bias,
+                           hipStream_t s);
+// T (N x M, row stride M) <- the N strided rows of C.
+hipError_t launch_cm_gather(const float* C, long long ldc, float* T, int M, int N, hipStream_t s);
+// Rows of T back into C at stride ldc < M, in row order (the last row wins).
+hipError_t launch_cm_scatter(const float* T, int M, int N, long long ldc, float* C, hipStream_t s);
+// dst (cols x rows, row stride ldd) = transpose of src (rows x cols, stride lds).
+hipError_t launch_transpose_u16(const uint16_t* src, int rows, int cols, long long lds, uint16_t* dst,
+                                long long ldd, hipStream_t s);
 
 }  // namespace dnnopt_hip

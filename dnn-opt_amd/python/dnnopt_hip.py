@@ -8,6 +8,9 @@ Host-side mirror of the reference's operator interface for this path:
   arrays or device pointers, synchronously.
 * ``cblas_sgemm`` / ``sgemm_`` / ``cblas_saxpy`` are the BLAS entry points
   (``include/dnnopt/blas/cblas.h:29-50``).
+* ``onednn_sgemm`` / ``onednn_gemm_bf16bf16f32`` are the column-major oneDNN
+  hook entry points (``integration/onednn/0001-dnnopt-integration.patch:279-370,
+  573-630``), with the hook's argument list (scalars by pointer).
 * ``Lib.sgemm``, ``Lib.gemm_bf16`` ... call the stream-ordered C-ABI of
   ``include/dnnopt_hip.h`` on device pointers and raise ``DnnoptError`` on a
   non-zero status.
@@ -20,7 +23,8 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char, c_double, c_float, c_int, c_size_t, c_uint16, c_uint32, c_uint64, c_void_p
+from ctypes import (POINTER, c_char, c_double, c_float, c_int, c_int64, c_size_t, c_uint16, c_uint32, c_uint64,
+                    c_void_p)
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 # DNNOPT_HIP_LIB selects another build of the library (e.g. a variant built
@@ -62,6 +66,8 @@ class Plan(ctypes.Structure):
 _F = c_float
 _I = c_int
 _P = c_void_p
+_L = c_int64
+_C = c_char
 
 # name -> (restype, argtypes); every symbol declared in include/dnnopt_hip.h
 # and the BLAS header, so a test can check the export list against this.
@@ -69,11 +75,16 @@ C_ABI = {
     "dnnopt_hip_sgemm": (_I, [_I, _I, _I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
     "dnnopt_hip_sgemm_naive": (_I, [_I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
     "dnnopt_hip_gemm_bf16": (_I, [_I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
+    "dnnopt_hip_gemm_bf16_ex": (_I, [_I, _I, _I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
     "dnnopt_hip_gemm_bf16_f32in": (_I, [_I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
     "dnnopt_hip_gemm_s8s8s32": (_I, [_I, _I, _I, _P, _I, _P, _I, _P, _I, _P]),
     "dnnopt_hip_gemm_s8s8f32_colscale": (_I, [_I, _I, _I, _P, _I, _P, _I, _P, _P, _I, _P]),
     "dnnopt_hip_gemm_int8_f32": (_I, [_I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
     "dnnopt_hip_saxpy": (_I, [_I, _F, _P, _I, _P, _I, _P]),
+    "dnnopt_hip_ext_sgemm": (_I, [_C, _C, _L, _L, _L, _F, _P, _L, _P, _L, _F, _P, _L, _P, _P]),
+    "dnnopt_hip_ext_gemm_bf16bf16f32": (_I, [_C, _C, _L, _L, _L, _F, _P, _L, _P, _L, _F, _P, _L, _P]),
+    "dnnopt_onednn_sgemm": (_I, [_P] * 14),
+    "dnnopt_onednn_gemm_bf16bf16f32": (_I, [_P] * 13),
     "dnnopt_hip_plan_sgemm": (_I, [_I, _I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_plan_gemm_bf16": (_I, [_I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_plan_gemm_s8": (_I, [_I, _I, _I, _I, POINTER(Plan)]),
@@ -228,6 +239,42 @@ class Lib:
             "dnnopt_hip_gemm_bf16",
         )
 
+    def gemm_bf16_ex(self, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, transA=0, transB=0, stream=None):
+        self._check(
+            self.so.dnnopt_hip_gemm_bf16_ex(transA, transB, M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta,
+                                            _ptr(C), ldc, stream),
+            "dnnopt_hip_gemm_bf16_ex",
+        )
+
+    def ext_sgemm(self, transa, transb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias=None, stream=None,
+                  check=True):
+        """Column-major oneDNN hook on device pointers; returns the status."""
+        st = self.so.dnnopt_hip_ext_sgemm(_char(transa), _char(transb), M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb,
+                                          beta, _ptr(C), ldc, _ptr(bias), stream)
+        if check:
+            self._check(st, "dnnopt_hip_ext_sgemm")
+        return st
+
+    def ext_gemm_bf16bf16f32(self, transa, transb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream=None,
+                             check=True):
+        st = self.so.dnnopt_hip_ext_gemm_bf16bf16f32(_char(transa), _char(transb), M, N, K, alpha, _ptr(A), lda,
+                                                     _ptr(B), ldb, beta, _ptr(C), ldc, stream)
+        if check:
+            self._check(st, "dnnopt_hip_ext_gemm_bf16bf16f32")
+        return st
+
+    def onednn_sgemm(self, transa, transb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias=None):
+        """The hook's own argument list (scalars by pointer); host or device
+        memory, synchronous.  Returns the status."""
+        sc = _HookScalars(transa, transb, M, N, K, alpha, lda, ldb, beta, ldc)
+        return self.so.dnnopt_onednn_sgemm(*sc.head(), _ptr(A), sc.ref("lda"), _ptr(B), sc.ref("ldb"),
+                                           sc.ref("beta"), _ptr(C), sc.ref("ldc"), _ptr(bias))
+
+    def onednn_gemm_bf16bf16f32(self, transa, transb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc):
+        sc = _HookScalars(transa, transb, M, N, K, alpha, lda, ldb, beta, ldc)
+        return self.so.dnnopt_onednn_gemm_bf16bf16f32(*sc.head(), _ptr(A), sc.ref("lda"), _ptr(B), sc.ref("ldb"),
+                                                      sc.ref("beta"), _ptr(C), sc.ref("ldc"))
+
     def gemm_bf16_f32in(self, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream=None):
         self._check(
             self.so.dnnopt_hip_gemm_bf16_f32in(M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C), ldc,
@@ -275,6 +322,28 @@ class Lib:
     def cblas_sgemm(self, order, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc):
         self.so.cblas_sgemm(order, ta, tb, M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta, _ptr(C), ldc)
         self._check(self.last_status(), "cblas_sgemm")
+
+
+def _char(c):
+    return c.encode() if isinstance(c, str) else bytes([c]) if isinstance(c, int) else c
+
+
+class _HookScalars:
+    """The scalars of a hook call kept alive as ctypes objects (the hook
+    takes every scalar by pointer, as oneDNN's extended_sgemm passes them)."""
+
+    def __init__(self, transa, transb, M, N, K, alpha, lda, ldb, beta, ldc):
+        self.v = {
+            "transa": c_char(_char(transa)), "transb": c_char(_char(transb)),
+            "M": c_int64(M), "N": c_int64(N), "K": c_int64(K), "alpha": c_float(alpha),
+            "lda": c_int64(lda), "ldb": c_int64(ldb), "beta": c_float(beta), "ldc": c_int64(ldc),
+        }
+
+    def ref(self, k):
+        return ctypes.cast(ctypes.byref(self.v[k]), c_void_p)
+
+    def head(self):
+        return [self.ref(k) for k in ("transa", "transb", "M", "N", "K", "alpha")]
 
 
 _LIB = None

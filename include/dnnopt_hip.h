@@ -73,6 +73,18 @@ int dnnopt_hip_gemm_bf16(int M, int N, int K,
                          const uint16_t* B, int ldb,
                          float beta, float* C, int ldc, void* stream);
 
+/* bf16 storage with operand transposes: with transA, A is stored K x M
+ * (lda >= M); with transB, B is stored N x K (ldb >= K).  Otherwise as
+ * dnnopt_hip_gemm_bf16.  Replaces the oneDNN hook's row-major bf16 helper
+ * dnnopt_gemm_bf16_row_major (integration/onednn/0001-dnnopt-integration.patch:
+ * 536-560), which copies transposed operands into temporaries: here B is read
+ * in place and a K x M A is read in place (M <= 8) or transposed on the
+ * device into library workspace. */
+int dnnopt_hip_gemm_bf16_ex(int transA, int transB, int M, int N, int K,
+                            float alpha, const uint16_t* A, int lda,
+                            const uint16_t* B, int ldb,
+                            float beta, float* C, int ldc, void* stream);
+
 /* fp32 storage, both operands rounded to bf16 (nearest even) in registers,
  * fp32 accumulation.  Replaces dnnopt::gemm_bf16 (src/gemm/gemm.cpp:379-416). */
 int dnnopt_hip_gemm_bf16_f32in(int M, int N, int K,
@@ -114,6 +126,50 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K,
  * (src/blas/cblas_saxpy.cpp:13-51): N <= 0 or alpha == 0 is a no-op. */
 int dnnopt_hip_saxpy(int N, float alpha, const float* X, int incX,
                      float* Y, int incY, void* stream);
+
+/* ---- oneDNN hook: column-major GEMMs ------------------------------------
+ * C (M x N, column-major: C(i,j) at C[j*ldc + i]) = alpha * op(A) * op(B)
+ * + beta * C, then C(i,j) += bias[i] when bias != NULL (fp32 only); op(A) is
+ * M x K, op(B) is K x N, column-major.  transa/transb are the BLAS letters:
+ * 'T'/'t' transposed, 'P'/'p' (packed, fp32 only) -> DNNOPT_ERR_UNSUPPORTED,
+ * anything else not transposed.  M == 0 or N == 0: nothing.  K == 0: C = 0
+ * (beta == 0, C not read) or C *= beta (beta != 1), then the bias.  ldc < M is
+ * accepted and gives the reference's result for overlapping columns.  Sizes
+ * are 64-bit as oneDNN's dim_t; values above INT_MAX ->
+ * DNNOPT_ERR_UNSUPPORTED.
+ * Replace the hook functions dnnopt_sgemm and dnnopt_gemm_bf16bf16f32 that
+ * the reference adds to oneDNN
+ * (integration/onednn/0001-dnnopt-integration.patch:279-370, 573-630). */
+
+/* Device pointers, enqueued on `stream` (as the GEMM entry points above). */
+int dnnopt_hip_ext_sgemm(char transa, char transb, int64_t M, int64_t N,
+                         int64_t K, float alpha, const float* A, int64_t lda,
+                         const float* B, int64_t ldb, float beta, float* C,
+                         int64_t ldc, const float* bias, void* stream);
+int dnnopt_hip_ext_gemm_bf16bf16f32(char transa, char transb, int64_t M,
+                                    int64_t N, int64_t K, float alpha,
+                                    const uint16_t* A, int64_t lda,
+                                    const uint16_t* B, int64_t ldb,
+                                    float beta, float* C, int64_t ldc,
+                                    void* stream);
+
+/* The hook's own argument list (every scalar by pointer, as oneDNN's
+ * extended_sgemm passes them), host or device memory, synchronous: returns
+ * when C holds the result.  A oneDNN build maps DNNOPT_OK to
+ * dnnl_success, DNNOPT_ERR_UNSUPPORTED to dnnl_unimplemented (its own
+ * fallback then runs) and other codes to dnnl_runtime_error. */
+int dnnopt_onednn_sgemm(const char* transa, const char* transb,
+                        const int64_t* M, const int64_t* N, const int64_t* K,
+                        const float* alpha, const float* A, const int64_t* lda,
+                        const float* B, const int64_t* ldb, const float* beta,
+                        float* C, const int64_t* ldc, const float* bias);
+int dnnopt_onednn_gemm_bf16bf16f32(const char* transa, const char* transb,
+                                   const int64_t* M, const int64_t* N,
+                                   const int64_t* K, const float* alpha,
+                                   const uint16_t* A, const int64_t* lda,
+                                   const uint16_t* B, const int64_t* ldb,
+                                   const float* beta, float* C,
+                                   const int64_t* ldc);
 
 /* ---- planning (host only; needs no device) ----------------------------- */
 

@@ -22,7 +22,8 @@
  *   orc_saxpy             bit-exact vs the reference's cblas_saxpy.cpp built
  *                         in oracle/_ref for the scalar (x86) build.
  *   orc_gemv_1xn_f32, orc_smallm_wide_f32, orc_adaptive_f32, orc_gemm_bf16,
- *   orc_gemm_int8_dynq, orc_cblas_sgemm:
+ *   orc_gemm_int8_dynq, orc_cblas_sgemm, orc_onednn_sgemm,
+ *   orc_onednn_gemm_bf16bf16f32:
  *                         the reference's NEON kernels cannot run here (no
  *                         AArch64 toolchain or emulator); pinned by exact
  *                         small-integer inputs (every rounding exact, so the
@@ -412,6 +413,106 @@ void orc_cblas_sgemm(int order, int trans_a, int trans_b, int M, int N, int K, f
         row_major(ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
     else
         row_major(tb, ta, N, M, K, alpha, B, ldb, A, lda, beta, C, ldc);
+}
+
+/* ------------------------------------------------------------------------
+ * oneDNN hook: integration/onednn/0001-dnnopt-integration.patch:279-370
+ * (dnnopt_sgemm, fp32 with bias) and 573-630 (dnnopt_gemm_bf16bf16f32).
+ * Column-major C (element (i, j) at C[j*ldc + i]).  The reference's steps, in
+ * its order: 'P'/'p' -> unimplemented (fp32 only); M or N zero -> nothing;
+ * K == 0 -> per column memset (beta == 0) or C *= beta (beta != 1), then the
+ * bias loop; otherwise the row-major problem of the swapped operands
+ * (patch:316-329) with transposed operands copied out first
+ * (patch:243-268, 536-560), through a temporary of row stride M when
+ * ldc < M (patch:330-352), then the bias loop (patch:355-362).  The
+ * row-major product is the scalar orc_gemm_naive_f32 / orc_gemm_bf16 (the
+ * reference calls its dispatcher there; kernels are compared to this by
+ * tolerance).  Returns 0, or 1 for "unimplemented".
+ * ---------------------------------------------------------------------- */
+static void transpose_u16(const uint16_t* src, uint16_t* dst, int rows, int cols, int ld_src, int ld_dst) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c) dst[(size_t)c * ld_dst + r] = src[(size_t)r * ld_src + c];
+}
+
+static void row_major_bf16(int ta, int tb, int M, int N, int K, float alpha, const uint16_t* A, int lda,
+                           const uint16_t* B, int ldb, float beta, float* C, int ldc) {
+    uint16_t* at = NULL;
+    uint16_t* bt = NULL;
+    if (ta) {
+        at = (uint16_t*)malloc((size_t)M * K * sizeof(uint16_t));
+        transpose_u16(A, at, K, M, lda, K);
+        A = at;
+        lda = K;
+    }
+    if (tb) {
+        bt = (uint16_t*)malloc((size_t)K * N * sizeof(uint16_t));
+        transpose_u16(B, bt, N, K, ldb, N);
+        B = bt;
+        ldb = N;
+    }
+    orc_gemm_bf16(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+    free(at);
+    free(bt);
+}
+
+static int onednn_hook(int bf16, char transa, char transb, int64_t M, int64_t N, int64_t K, float alpha,
+                       const void* A, int64_t lda, const void* B, int64_t ldb, float beta, float* C, int64_t ldc,
+                       const float* bias) {
+    if (!bf16 && (transa == 'P' || transa == 'p' || transb == 'P' || transb == 'p')) return 1;
+    if (M == 0 || N == 0) return 0;
+    if (K == 0) {
+        if (beta == 0.0f) {
+            for (int64_t j = 0; j < N; ++j) memset(C + j * ldc, 0, (size_t)M * sizeof(float));
+        } else if (beta != 1.0f) {
+            for (int64_t j = 0; j < N; ++j)
+                for (int64_t i = 0; i < M; ++i) C[j * ldc + i] *= beta;
+        }
+        if (bias)
+            for (int64_t j = 0; j < N; ++j)
+                for (int64_t i = 0; i < M; ++i) C[j * ldc + i] += bias[i];
+        return 0;
+    }
+    const int tA = transa == 'T' || transa == 't';
+    const int tB = transb == 'T' || transb == 't';
+    const int rm_M = (int)N, rm_N = (int)M, rm_K = (int)K;
+    float* out = C;
+    int ld_out = (int)ldc;
+    float* tmp = NULL;
+    if ((int)ldc < rm_N) {
+        tmp = (float*)malloc((size_t)rm_M * rm_N * sizeof(float));
+        if (beta != 0.0f)
+            for (int r = 0; r < rm_M; ++r)
+                for (int c = 0; c < rm_N; ++c) tmp[(size_t)r * rm_N + c] = C[(size_t)r * ldc + c];
+        out = tmp;
+        ld_out = rm_N;
+    }
+    if (bf16)
+        row_major_bf16(tB, tA, rm_M, rm_N, rm_K, alpha, (const uint16_t*)B, (int)ldb, (const uint16_t*)A, (int)lda,
+                       beta, out, ld_out);
+    else
+        row_major(tB, tA, rm_M, rm_N, rm_K, alpha, (const float*)B, (int)ldb, (const float*)A, (int)lda, beta, out,
+                  ld_out);
+    if (tmp) {
+        for (int r = 0; r < rm_M; ++r)
+            for (int c = 0; c < rm_N; ++c) C[(size_t)r * ldc + c] = tmp[(size_t)r * rm_N + c];
+        free(tmp);
+    }
+    if (bias)
+        for (int64_t j = 0; j < N; ++j)
+            for (int64_t i = 0; i < M; ++i) C[j * ldc + i] += bias[i];
+    return 0;
+}
+
+int orc_onednn_sgemm(char transa, char transb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
+                     int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
+                     const float* bias) {
+    return onednn_hook(0, transa, transb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias);
+}
+
+int orc_onednn_gemm_bf16bf16f32(char transa, char transb, int64_t M, int64_t N, int64_t K, float alpha,
+                                const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, float beta, float* C,
+                                int64_t ldc) {
+    return onednn_hook(1, transa, transb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, NULL);
 }
 
 /* cblas_saxpy: src/blas/cblas_saxpy.cpp:13-51 (fused update on the NEON

@@ -76,6 +76,11 @@ ORACLE_ABI = {
     "orc_gemm_int8_dynq": (None, [I, I, I, F, P, I, P, I, F, P, I]),
     "orc_cblas_sgemm": (None, [I, I, I, I, I, I, F, P, I, P, I, F, P, I]),
     "orc_saxpy": (None, [I, F, P, I, P, I, I]),
+    "orc_onednn_sgemm": (I, [ctypes.c_char, ctypes.c_char, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, F, P,
+                             ctypes.c_int64, P, ctypes.c_int64, F, P, ctypes.c_int64, P]),
+    "orc_onednn_gemm_bf16bf16f32": (I, [ctypes.c_char, ctypes.c_char, ctypes.c_int64, ctypes.c_int64,
+                                        ctypes.c_int64, F, P, ctypes.c_int64, P, ctypes.c_int64, F, P,
+                                        ctypes.c_int64]),
     "orc_max_threads": (I, []),
 }
 
@@ -177,3 +182,32 @@ def assert_fp32_close(got, want, scale, K, what=""):
             f"got {got[idx]!r} want {want[idx]!r} tol {tol[idx]!r}"
         )
     return float((err / np.maximum(scale, 1e-300)).max())
+
+
+# ---------------------------------------------------------------- column-major (oneDNN hook) layouts
+def cm_store(X: np.ndarray, ld: int, fill=0.0, dtype=np.float32) -> np.ndarray:
+    """Column-major storage of X (rows x cols) with leading dimension ld >= rows:
+    a flat buffer of cols * ld elements, X[i, j] at [j * ld + i]; the padding
+    rows hold `fill`."""
+    rows, cols = X.shape
+    buf = np.full((cols, ld), fill, dtype)
+    buf[:, :rows] = X.T
+    return buf.reshape(-1)
+
+
+def cm_load(buf: np.ndarray, rows: int, cols: int, ld: int) -> np.ndarray:
+    return buf.reshape(cols, ld)[:, :rows].T
+
+
+def hook_operands(opA: np.ndarray, opB: np.ndarray, ta: str, tb: str, pad=0, dtype=np.float32, fill=0.0):
+    """Stored A, B (flat column-major buffers) and lda, ldb for op(A) = opA
+    (M x K) and op(B) = opB (K x N) under the BLAS letters ta, tb."""
+    SA = opA.T if ta in "Tt" else opA
+    SB = opB.T if tb in "Tt" else opB
+    lda, ldb = SA.shape[0] + pad, SB.shape[0] + pad
+    return cm_store(SA, lda, fill, dtype), lda, cm_store(SB, ldb, fill, dtype), ldb
+
+
+def small_ints(orc, n, tid, lim=3, seed=SEED):
+    """Integers in [-lim, lim] as float32 (every product and short sum exact)."""
+    return np.rint(uniform(orc, n, tid, -lim - 0.499, lim + 0.499, seed)).astype(np.float32)

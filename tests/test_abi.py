@@ -29,7 +29,7 @@ def _exports(path):
 
 
 def test_library_loads(lib):
-    assert lib.so.dnnopt_hip_abi_version() == 1
+    assert lib.so.dnnopt_hip_abi_version() == 2
 
 
 def test_every_c_declaration_is_exported(lib):
@@ -152,6 +152,47 @@ def test_cxx_and_cblas_api_without_device(lib):
     # alpha == 0 and beta == 1 returns before anything (cblas_sgemm.cpp:115)
     lib.so.cblas_sgemm(101, 111, 111, 4, 4, 4, 0.0, A.ctypes.data, 4, A.ctypes.data, 4, 1.0, C.ctypes.data, 4)
     assert (C == 7.0).all()
+
+
+def test_hook_argument_checks(lib):
+    """The column-major hook entry points decide these before any device work
+    (same answers with or without a GPU)."""
+    b = u.binding()
+    A = np.ones(64, np.float32)
+    C = np.full(64, 7.0, np.float32)
+    ext = lambda *a, **k: lib.ext_sgemm(*a, check=False, **k)  # noqa: E731
+    # packed operands: unimplemented (the oneDNN side falls back), fp32 only
+    assert ext("P", "N", 4, 4, 4, 1.0, A, 4, A, 4, 0.0, C, 4) == b.ERR_UNSUPPORTED
+    assert ext("N", "p", 4, 4, 4, 1.0, A, 4, A, 4, 0.0, C, 4) == b.ERR_UNSUPPORTED
+    assert lib.onednn_sgemm("P", "N", 4, 4, 4, 1.0, A, 4, A, 4, 0.0, C, 4) == b.ERR_UNSUPPORTED
+    # M == 0 or N == 0: nothing, even with null pointers
+    assert ext("N", "N", 0, 4, 4, 1.0, None, 4, None, 4, 0.0, None, 4) == b.OK
+    assert lib.onednn_gemm_bf16bf16f32("N", "N", 4, 0, 4, 1.0, None, 4, None, 4, 0.0, None, 4) == b.OK
+    # negative sizes, ldc < 1, short leading dimensions (column-major: lda >= M
+    # for 'N', >= K for 'T'), null operands with K > 0
+    assert ext("N", "N", -1, 4, 4, 1.0, A, 4, A, 4, 0.0, C, 4) == b.ERR_INVALID_ARG
+    assert ext("N", "N", 4, 4, 4, 1.0, A, 4, A, 4, 0.0, C, 0) == b.ERR_INVALID_ARG
+    assert ext("N", "N", 4, 4, 4, 1.0, A, 3, A, 4, 0.0, C, 4) == b.ERR_INVALID_ARG
+    assert ext("T", "N", 4, 4, 5, 1.0, A, 4, A, 5, 0.0, C, 4) == b.ERR_INVALID_ARG
+    assert ext("N", "T", 4, 5, 4, 1.0, A, 4, A, 4, 0.0, C, 4) == b.ERR_INVALID_ARG
+    assert ext("N", "N", 4, 4, 4, 1.0, None, 4, A, 4, 0.0, C, 4) == b.ERR_INVALID_ARG
+    assert lib.onednn_sgemm("N", "N", 4, 4, 4, 1.0, A, 2, A, 4, 0.0, C, 4) == b.ERR_INVALID_ARG
+    # sizes beyond 32 bits
+    assert ext("N", "N", 1 << 31, 4, 4, 1.0, A, 1 << 31, A, 4, 0.0, C, 1 << 31) == b.ERR_UNSUPPORTED
+    # K == 0 with beta == 1 and no bias changes nothing (no device needed)
+    assert lib.onednn_sgemm("N", "N", 4, 4, 0, 1.0, None, 4, None, 1, 1.0, C, 4) == b.OK
+    assert (C == 7.0).all()
+
+
+@no_device
+def test_hook_without_device(lib):
+    b = u.binding()
+    A = np.ones(16, np.float32)
+    C = np.full(16, 7.0, np.float32)
+    assert lib.ext_sgemm("N", "N", 4, 4, 4, 1.0, A, 4, A, 4, 0.0, C, 4, check=False) == b.ERR_NO_DEVICE
+    assert lib.onednn_sgemm("T", "N", 4, 4, 4, 1.0, A, 4, A, 4, 0.0, C, 4) == b.ERR_NO_DEVICE
+    assert lib.onednn_sgemm("N", "N", 4, 4, 0, 1.0, None, 4, None, 1, 0.0, C, 4) == b.ERR_NO_DEVICE
+    assert lib.last_status() == b.ERR_NO_DEVICE and (C == 7.0).all()
 
 
 def test_thread_setters_round_trip(lib):

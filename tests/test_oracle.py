@@ -304,6 +304,158 @@ def test_cblas_early_exits(orc):
     assert C.tolist() == [1, 2, 3, 4]
 
 
+# ---------------------------------------------------------------- oneDNN hook (column-major)
+HOOK_T = [("N", "N"), ("T", "N"), ("N", "T"), ("t", "t")]
+
+
+def _hook(orc, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias=None, bf16=False):
+    if bf16:
+        return orc.orc_onednn_gemm_bf16bf16f32(ta.encode(), tb.encode(), M, N, K, alpha, u.ptr(A), lda, u.ptr(B), ldb,
+                                               beta, u.ptr(C), ldc)
+    return orc.orc_onednn_sgemm(ta.encode(), tb.encode(), M, N, K, alpha, u.ptr(A), lda, u.ptr(B), ldb, beta,
+                                u.ptr(C), ldc, None if bias is None else u.ptr(bias))
+
+
+@pytest.mark.parametrize("ta,tb", HOOK_T)
+@pytest.mark.parametrize("beta,with_bias,bf16", [(0.0, False, False), (1.0, True, False), (-2.0, True, False),
+                                                 (0.5, False, False), (0.0, False, True), (-2.0, False, True)])
+def test_onednn_hook_exact_on_integers(orc, ta, tb, beta, with_bias, bf16):
+    """Column-major C = alpha op(A) op(B) + beta C (+ bias[i]) on small
+    integers, where every rounding is exact: the result must equal the integer
+    closed form, and the padding rows of C (ldc > M) must be untouched.  The
+    shapes are all different, so a swapped or untransposed operand fails."""
+    M, N, K, ldc = 5, 7, 6, 9
+    opA = u.small_ints(orc, M * K, 1).reshape(M, K)
+    opB = u.small_ints(orc, K * N, 2).reshape(K, N)
+    C0 = u.small_ints(orc, M * N, 3).reshape(M, N)
+    bias = u.small_ints(orc, M, 4) if with_bias else None
+    alpha = 0.5
+    A, lda, B, ldb = u.hook_operands(opA, opB, ta, tb, pad=2)
+    if bf16:  # small integers are exact in bf16
+        A, B = u.bf16_bits(orc, A), u.bf16_bits(orc, B)
+    C = u.cm_store(C0, ldc, fill=12345.0)
+    assert _hook(orc, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, bf16) == 0
+    want = alpha * (opA.astype(np.float64) @ opB) + beta * C0
+    if with_bias:
+        want = want + bias[:, None]
+    assert np.array_equal(u.cm_load(C, M, N, ldc), want.astype(np.float32))
+    assert (C.reshape(N, ldc)[:, M:] == 12345.0).all()
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_onednn_hook_k_zero(orc, with_bias):
+    """K == 0: C = 0 (beta 0, C not read: NaN in, zeros out), C *= beta, or C
+    unchanged (beta 1); alpha is not used (NaN); then the bias."""
+    M, N, ldc = 4, 3, 6
+    bias = u.small_ints(orc, M, 4) if with_bias else None
+    add = bias[:, None] if with_bias else 0.0
+    C0 = u.small_ints(orc, M * N, 3).reshape(M, N)
+    nan = np.full(4, np.nan, np.float32)
+    for beta, want in [(0.0, np.zeros((M, N))), (1.0, C0), (-2.0, -2.0 * C0)]:
+        C = u.cm_store(np.full((M, N), np.nan, np.float32) if beta == 0.0 else C0, ldc, fill=7.0)
+        assert _hook(orc, "N", "N", M, N, 0, float("nan"), nan, M, nan, 1, beta, C, ldc, bias) == 0
+        assert np.array_equal(u.cm_load(C, M, N, ldc), (want + add).astype(np.float32)), beta
+        assert (C.reshape(N, ldc)[:, M:] == 7.0).all()
+
+
+def test_onednn_hook_early_exits(orc):
+    C = _f([1, 2, 3, 4])
+    nan = np.full(4, np.nan, np.float32)
+    assert _hook(orc, "N", "N", 0, 2, 2, 1.0, nan, 1, nan, 2, 0.0, C, 1) == 0
+    assert _hook(orc, "N", "N", 2, 0, 2, 1.0, nan, 2, nan, 2, 0.0, C, 2) == 0
+    assert _hook(orc, "P", "N", 2, 2, 2, 1.0, nan, 2, nan, 2, 0.0, C, 2) == 1
+    assert _hook(orc, "N", "p", 2, 2, 2, 1.0, nan, 2, nan, 2, 0.0, C, 2) == 1
+    assert C.tolist() == [1, 2, 3, 4]
+    # The bf16 hook has no packed check: 'P' reads as not transposed.
+    A = u.bf16_bits(orc, _f([1, 2, 3, 4]))
+    B = u.bf16_bits(orc, _f([1, 0, 0, 1]))
+    assert _hook(orc, "P", "N", 2, 2, 2, 1.0, A, 2, B, 2, 0.0, C, 2, bf16=True) == 0
+    assert C.tolist() == [1, 2, 3, 4]
+
+
+def _overlap_closed_form(opA, opB, C0flat, M, N, ldc, alpha, beta, bias):
+    """ldc < M, restated with numpy slices: the row-major rows C^T[r] (from
+    the rows of C as they were on entry) written back at stride ldc in row
+    order, then bias added column by column in order."""
+    flat = C0flat.astype(np.float64).copy()
+    G = np.stack([flat[r * ldc: r * ldc + M] for r in range(N)])
+    R = alpha * (opB.T.astype(np.float64) @ opA.T) + (beta * G if beta != 0.0 else 0.0)
+    for r in range(N):
+        flat[r * ldc: r * ldc + M] = R[r]
+    if bias is not None:
+        for j in range(N):
+            flat[j * ldc: j * ldc + M] += bias
+    return flat.astype(np.float32)
+
+
+@pytest.mark.parametrize("beta,with_bias", [(0.0, False), (0.5, True), (1.0, False)])
+def test_onednn_hook_overlapping_columns(orc, beta, with_bias):
+    M, N, K, ldc = 7, 5, 4, 3
+    opA = u.small_ints(orc, M * K, 1).reshape(M, K)
+    opB = u.small_ints(orc, K * N, 2).reshape(K, N)
+    total = (N - 1) * ldc + M
+    C0 = u.small_ints(orc, total, 3)
+    bias = u.small_ints(orc, M, 4) if with_bias else None
+    A, lda, B, ldb = u.hook_operands(opA, opB, "N", "T")
+    C = C0.copy()
+    assert _hook(orc, "N", "T", M, N, K, 1.0, A, lda, B, ldb, beta, C, ldc, bias) == 0
+    assert np.array_equal(C, _overlap_closed_form(opA, opB, C0, M, N, ldc, 1.0, beta, bias))
+
+
+def test_onednn_hook_overlap_k_zero(orc):
+    """K == 0 with ldc < M: scaling and bias apply once per covering column."""
+    M, N, ldc = 5, 4, 2
+    total = (N - 1) * ldc + M
+    C0 = u.small_ints(orc, total, 3)
+    bias = u.small_ints(orc, M, 4)
+    C = C0.copy()
+    nan = np.full(2, np.nan, np.float32)
+    assert _hook(orc, "N", "N", M, N, 0, 1.0, nan, M, nan, 1, -2.0, C, ldc, bias) == 0
+    want = C0.astype(np.float64)
+    for j in range(N):
+        want[j * ldc: j * ldc + M] *= -2.0
+    for j in range(N):
+        want[j * ldc: j * ldc + M] += bias
+    assert np.array_equal(C, want.astype(np.float32))
+
+
+def test_onednn_hook_random_tolerance(orc):
+    """Random inputs: the fp64 error bound, every transpose combination."""
+    M, N, K = 9, 13, 37
+    opA = u.uniform(orc, M * K, 1).reshape(M, K)
+    opB = u.uniform(orc, K * N, 2).reshape(K, N)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    bias = u.uniform(orc, M, 4)
+    for ta, tb in HOOK_T:
+        A, lda, B, ldb = u.hook_operands(opA, opB, ta, tb, pad=1)
+        C = u.cm_store(C0, M)
+        assert _hook(orc, ta, tb, M, N, K, 1.5, A, lda, B, ldb, 0.25, C, M, bias) == 0
+        want, scale = u.exact(opA, opB, 1.5, 0.25, C0)
+        u.assert_fp32_close(u.cm_load(C, M, N, M), want + bias[:, None], scale + np.abs(bias)[:, None], K + 1,
+                            f"hook {ta}{tb}")
+
+
+def test_onednn_hook_checks_catch_mistakes(orc):
+    """Plausible mistakes in a hook implementation change the exact integer
+    result: a 'T' operand read as not transposed (square A, so the call is
+    still well formed), the bias added along N instead of M, beta dropped."""
+    M, N, ldc = 5, 7, 5
+    sq = u.small_ints(orc, M * M, 5).reshape(M, M)
+    opB = u.small_ints(orc, M * N, 6).reshape(M, N)
+    C0 = u.small_ints(orc, M * N, 3).reshape(M, N)
+    bias = u.small_ints(orc, M, 4)
+    A, lda, B, ldb = u.hook_operands(sq, opB, "T", "N")
+    right, wrong = u.cm_store(C0, ldc), u.cm_store(C0, ldc)
+    _hook(orc, "T", "N", M, N, M, 1.0, A, lda, B, ldb, 1.0, right, ldc, bias)
+    _hook(orc, "N", "N", M, N, M, 1.0, A, lda, B, ldb, 1.0, wrong, ldc, bias)
+    want = sq.astype(np.float64) @ opB + C0 + bias[:, None]
+    assert np.array_equal(u.cm_load(right, M, N, ldc), want.astype(np.float32))
+    assert not np.array_equal(right, wrong)
+    bias_n = np.resize(bias, N)
+    assert not np.array_equal(want, sq.astype(np.float64) @ opB + C0 + bias_n[None, :])
+    assert not np.array_equal(want, sq.astype(np.float64) @ opB + bias[:, None])
+
+
 # ---------------------------------------------------------------- the checks catch mistakes
 def test_planted_mistakes_are_caught(orc):
     """Plant plausible mistakes in the oracle's output (on the CPU) and show
