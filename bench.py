@@ -69,9 +69,11 @@ class Case:
         self.dtype = dtype
 
     def sizes(self):
-        sa, sb = {"f32": (4, 4), "bf16": (2, 2), "f2b": (4, 4), "s8": (1, 1), "s8s": (1, 1)}[self.kind]
+        sa, sb = {"f32": (4, 4), "bf16": (2, 2), "f2b": (4, 4), "s8": (1, 1), "s8s": (1, 1), "hf32": (4, 4),
+                  "hbf16": (2, 2)}[self.kind]
         sc = 4
-        extra = 4 * self.N if self.kind == "s8s" else 0
+        # per-column scale (int8) or bias (hook) vector
+        extra = 4 * self.N if self.kind == "s8s" or (self.kind == "hf32" and self.init.get("bias")) else 0
         return sa, sb, sc, extra
 
     def bytes_alg(self):
@@ -113,6 +115,18 @@ def workload(name):
         cs.append(Case("c5_m128_n4093_scale", "s8s", 128, 4093, 4096, init={"A": ("i",), "B": ("i",)}, dtype="s8"))
         return ("C5: int8 s8 x s8 -> s32 (B as N x K), M in {1,8,128} x N in {4096,4093} x K=4096; "
                 "+ per-column fp32 scale", cs)
+    if name == "hook":
+        # oneDNN inner product through the column-major hook: extended_sgemm
+        # ('T', 'N', OC, MB, IC, W, IC, X, IC, dst, OC, bias).  The case's
+        # M, N, K are the row-major view: M = MB, N = OC, K = IC; B = W is
+        # stored N x K (weights as PyTorch/oneDNN keep them).
+        f = {"A": ("n", 0, 1), "B": ("n", 0, 0.02), "bias": True}
+        cs = [Case("hook_f32_mb1_oc4096_ic4096", "hf32", 1, 4096, 4096, init=f),
+              Case("hook_f32_mb7_oc11003_ic2048", "hf32", 7, 11003, 2048, init=f)]
+        cs += [Case(f"hook_bf16_mb{mb}_oc11008_ic4096", "hbf16", mb, 11008, 4096,
+                    init={"A": ("n", 0, 1), "B": ("n", 0, 0.02)}, dtype="bf16") for mb in (1, 32, 256)]
+        return ("oneDNN hook: column-major extended_sgemm / gemm_bf16bf16f32 ('T','N', M=OC, N=MB, K=IC), "
+                "weights OC x IC, fp32 with bias, beta=0", cs)
     raise SystemExit(f"unknown workload {name}")
 
 
@@ -122,7 +136,7 @@ class Buffers:
         self.case = case
         M, N, K = case.M, case.N, case.K
         tA = {"f32": torch.float32, "f2b": torch.float32, "bf16": torch.int16, "s8": torch.int8,
-              "s8s": torch.int8}[case.kind]
+              "s8s": torch.int8, "hf32": torch.float32, "hbf16": torch.int16}[case.kind]
         dt_code = {torch.float32: 0, torch.int16: 1, torch.int8: 2}[tA]
         a_elems = M * K
         b_elems = K * N
@@ -144,9 +158,10 @@ class Buffers:
             self.A.append(A)
             self.B.append(B)
             self.C.append(C)
-            if case.kind == "s8s":
+            if case.kind == "s8s" or (case.kind == "hf32" and case.init.get("bias")):
                 S = torch.empty(N, dtype=torch.float32, device=dev)
-                lib.fill(S, N, 0, 0, SEED + r, 4, 0.001, 0.01)
+                lo, hi = (0.001, 0.01) if case.kind == "s8s" else (-1.0, 1.0)
+                lib.fill(S, N, 0, 0, SEED + r, 4, lo, hi)
                 self.S.append(S)
 
     def launch(self, lib, r, stream):
@@ -162,6 +177,11 @@ class Buffers:
             lib.gemm_bf16_f32in(M, N, K, c.alpha, A, K, B, N, c.beta, C, N, stream=stream)
         elif c.kind == "s8":
             lib.gemm_s8s8s32(M, N, K, A, K, B, K, C, N, stream=stream)
+        elif c.kind == "hf32":
+            lib.ext_sgemm("T", "N", N, M, K, c.alpha, B, K, A, K, c.beta, C, N,
+                          bias=self.S[r] if self.S else None, stream=stream)
+        elif c.kind == "hbf16":
+            lib.ext_gemm_bf16bf16f32("T", "N", N, M, K, c.alpha, B, K, A, K, c.beta, C, N, stream=stream)
         else:
             lib.gemm_s8s8f32_colscale(M, N, K, A, K, B, K, self.S[r], C, N, stream=stream)
 
@@ -170,12 +190,16 @@ def kernel_key(lib, case):
     """Kernel template instance as rocprof names it (family<params>)."""
     if case.kind in ("f32",):
         p = lib.plan_sgemm(case.M, case.N, case.K, transA=case.ta)
+    elif case.kind == "hf32":
+        p = lib.plan_sgemm(case.M, case.N, case.K, transB=1)
+    elif case.kind == "hbf16":
+        p = lib.plan_bf16_ex(case.M, case.N, case.K, transB=1)
     elif case.kind in ("bf16", "f2b"):
         p = lib.plan_bf16(case.M, case.N, case.K, fp32_inputs=int(case.kind == "f2b"))
     else:
         p = lib.plan_s8(case.M, case.N, case.K, with_scale=int(case.kind == "s8s"))
     if p["name"] == "dnnopt_skinny":
-        mode = {"f32": 0, "bf16": 1, "f2b": 2}[case.kind]
+        mode = {"f32": 0, "bf16": 1, "f2b": 2, "hf32": 0, "hbf16": 1}[case.kind]
         return f"dnnopt_skinny<{case.M}, {p['block'] // 64}, {mode}>", p
     return f"{p['name']}[{p['rows']}x{p['cols']}]", p
 
@@ -515,7 +539,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "all"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "hook", "all"])
     ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
@@ -545,7 +569,7 @@ def main():
               "sharding across GPUs is not built.", file=sys.stderr)
         sys.exit(2)
 
-    names = ["c1", "c2", "c3", "c4", "c5"] if args.workload == "all" else [args.workload]
+    names = ["c1", "c2", "c3", "c4", "c5", "hook"] if args.workload == "all" else [args.workload]
     main_name = "c2" if args.workload == "all" else args.workload
     results = {}
     for wl in names:

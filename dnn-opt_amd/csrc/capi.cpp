@@ -149,6 +149,18 @@ int dnnopt_hip_plan_gemm_bf16(int fp32_inputs, int M, int N, int K, dnnopt_plan*
     return st;
 }
 
+int dnnopt_hip_plan_gemm_bf16_ex(int transA, int transB, int M, int N, int K, dnnopt_plan* out) {
+    if (!out || !dims_ok(M, N, K) || (transA != 0 && transA != 1) || (transB != 0 && transB != 1))
+        return DNNOPT_ERR_INVALID_ARG;
+    // As dnnopt_hip_gemm_bf16_ex with unpadded strides (a transposed A is
+    // first copied to an even row stride).
+    const int lda = transA ? (M <= 8 && !transB ? M : (K + 1) & ~1) : K;
+    Launch L;
+    int st = plan_bf16(0, M, N, K, lda, transB ? K : N, &L, transB);
+    if (st == DNNOPT_OK) *out = L.pub;
+    return st;
+}
+
 int dnnopt_hip_plan_gemm_s8(int with_scale, int M, int N, int K, dnnopt_plan* out) {
     if (!out || !dims_ok(M, N, K)) return DNNOPT_ERR_INVALID_ARG;
     Launch L;

@@ -87,6 +87,7 @@ C_ABI = {
     "dnnopt_onednn_gemm_bf16bf16f32": (_I, [_P] * 13),
     "dnnopt_hip_plan_sgemm": (_I, [_I, _I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_plan_gemm_bf16": (_I, [_I, _I, _I, _I, POINTER(Plan)]),
+    "dnnopt_hip_plan_gemm_bf16_ex": (_I, [_I, _I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_plan_gemm_s8": (_I, [_I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_fill": (_I, [_P, c_size_t, _I, _I, c_uint64, c_uint32, c_double, c_double, _P]),
     "dnnopt_hip_status_string": (ctypes.c_char_p, [_I]),
@@ -212,6 +213,11 @@ class Lib:
     def plan_bf16(self, M, N, K, fp32_inputs=0) -> dict:
         p = Plan()
         self._check(self.so.dnnopt_hip_plan_gemm_bf16(fp32_inputs, M, N, K, ctypes.byref(p)), "plan_bf16")
+        return p.as_dict()
+
+    def plan_bf16_ex(self, M, N, K, transA=0, transB=0) -> dict:
+        p = Plan()
+        self._check(self.so.dnnopt_hip_plan_gemm_bf16_ex(transA, transB, M, N, K, ctypes.byref(p)), "plan_bf16_ex")
         return p.as_dict()
 
     def plan_s8(self, M, N, K, with_scale=0) -> dict:

@@ -198,6 +198,8 @@ int dnnopt_hip_plan_sgemm(int transA, int transB, int M, int N, int K,
                           dnnopt_plan* out);
 int dnnopt_hip_plan_gemm_bf16(int fp32_inputs, int M, int N, int K,
                               dnnopt_plan* out);
+int dnnopt_hip_plan_gemm_bf16_ex(int transA, int transB, int M, int N, int K,
+                                 dnnopt_plan* out);
 int dnnopt_hip_plan_gemm_s8(int with_scale, int M, int N, int K,
                             dnnopt_plan* out);
 
