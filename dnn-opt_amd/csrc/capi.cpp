@@ -110,6 +110,27 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
     return finish_launch(launch_splitk_reduce(a.part, a.splits, L.tn, L.tm, L.bm, L.bn, M, N, alpha, beta, C, ldc, s));
 }
 
+int run_rowdot(const Launch& L, const void* A, int lda, const void* B, int ldb, float* C, int ldc, int M, int N,
+               int K, float alpha, float beta, hipStream_t s) {
+    RowdotArgs a{};
+    a.A = A;
+    a.B = B;
+    a.C = C;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.alpha = alpha;
+    a.beta = beta;
+    // bf16 rows start on 4-byte boundaries only when the matrix does and its
+    // row stride is even.
+    const int aligned = L.mode == 0 || (((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) == 0 &&
+                                        (lda & 1) == 0 && (ldb & 1) == 0);
+    return finish_launch(launch_rowdot(L.mode, L.mr, L.nw, aligned, L.grid, a, s));
+}
+
 bool dims_ok(int M, int N, int K) { return M > 0 && N > 0 && K > 0; }
 
 }  // namespace
@@ -182,6 +203,7 @@ int dnnopt_hip_sgemm(int transA, int transB, int M, int N, int K, float alpha, c
     hipStream_t s = as_stream(stream);
     if (L.family == DNNOPT_K_SKINNY_F32)
         return run_skinny(L, A, transA ? 1 : lda, transA ? lda : 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+    if (L.family == DNNOPT_K_ROWDOT_F32) return run_rowdot(L, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     return run_tile(L, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
 }
 
@@ -246,6 +268,7 @@ int dnnopt_hip_gemm_bf16_ex(int transA, int transB, int M, int N, int K, float a
     int st = plan_bf16(0, M, N, K, lda, ldb, &L, transB);
     if (st != DNNOPT_OK) return st;
     if (L.family == DNNOPT_K_SKINNY_BF16) return run_skinny(L, A, lda, 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+    if (L.family == DNNOPT_K_ROWDOT_BF16) return run_rowdot(L, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     return run_tile(L, 0, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
 }
 

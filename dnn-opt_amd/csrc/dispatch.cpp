@@ -8,6 +8,9 @@
 // On MI355X the questions are different: a launch must put enough bytes in
 // flight to cover HBM latency on every compute unit, and the shapes of this
 // path are almost all HBM-bound.  The rules:
+//   * M <= 8 with B stored N x K (fp32, bf16): the row-dot kernel streams the
+//     rows of B once; waves of a workgroup split k when there are too few
+//     rows to give every CU two workgroups.
 //   * M <= 8 (fp32, bf16): the skinny kernel streams B once.  Work is split
 //     over column tiles, over the waves of a workgroup and, when there are too
 //     few column tiles to occupy the chip, over k across workgroups (split-k
@@ -277,8 +280,35 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok) {
     return DNNOPT_OK;
 }
 
+int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
+    if (M < 1 || M > 8) return DNNOPT_ERR_UNSUPPORTED;
+    *L = Launch{};
+    const long long es = mode ? 2 : 4, R = rowdot_rows(M);
+    // Buffer offsets are 32-bit from the first row of a wave (B) and of A.
+    if ((R * ldb + K) * es >= 0x7FFFFFFFll || ((long long)(M - 1) * lda + K) * es >= 0x7FFFFFFFll)
+        return DNNOPT_ERR_UNSUPPORTED;
+    constexpr long long kSteps = 2;  // load steps a wave issues at once
+    const long long steps = ceil_div(ceil_div(K, 16 / es), 64);  // 1 KiB row steps
+    const long long cus = num_cus();
+    // Waves of a workgroup split k (kw ways) until there are two workgroups
+    // per CU, as long as each wave keeps whole multi-step k-ranges.
+    int kw = 1;
+    while (kw < 8 && ceil_div(N, (kRowdotWaves / kw) * R) < 2 * cus && steps / (2 * kw) >= kSteps) kw *= 2;
+    const long long rows_per_wg = (kRowdotWaves / kw) * R;
+    const long long G = ceil_div(N, rows_per_wg);
+    if (G > 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
+    L->mode = mode;
+    L->mr = M;
+    L->nw = kw;
+    L->grid = dim3((unsigned)G, 1, 1);
+    fill_pub(L, mode ? DNNOPT_K_ROWDOT_BF16 : DNNOPT_K_ROWDOT_F32, "dnnopt_rowdot", M, (int)rows_per_wg, 1,
+             kRowdotWaves * 64);
+    return DNNOPT_OK;
+}
+
 int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L) {
     if (M <= 8 && !transB) return plan_skinny(kSkinnyF32, M, N, K, ldb, L);
+    if (M <= 8 && !transA && plan_rowdot(0, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
     return plan_tile(kTileF32, transA, transB, M, N, K, lda, ldb, L);
 }
 
@@ -287,6 +317,7 @@ int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L,
     // for every M (the skinny kernel streams rows of a K x N B).
     if (M <= 8 && !transB) return plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L);
     if (transB && fp32_inputs) return DNNOPT_ERR_UNSUPPORTED;
+    if (M <= 8 && plan_rowdot(1, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
     return plan_tile(fp32_inputs ? kTileF2B : kTileBF16, 0, transB, M, N, K, lda, ldb, L);
 }
 

@@ -28,7 +28,7 @@ struct Launch {
     dnnopt_plan pub;
     int family = DNNOPT_K_NONE;
     int mode = 0;        // SkinnyMode / TileMode / int8 epilogue
-    int mr = 0, nw = 0;  // skinny
+    int mr = 0, nw = 0;  // skinny (rowdot: nw = waves splitting k)
     int cfg = 0;         // tile / int8 configuration index
     int bm = 0, bn = 0;  // tile shape
     int tn = 0, tm = 0;  // tile grid (column tiles, row tiles)
@@ -44,6 +44,8 @@ struct Launch {
 int split_reduce_mode();
 
 int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L);
+// M <= 8 against B stored N x K; mode 0 fp32, 1 bf16 storage.
+int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L);
 // lds_ok = false keeps bf16 GEMMs off the LDS-staged kernel (operands whose
 // rows do not start on 4-byte boundaries).
 int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L,

@@ -53,6 +53,25 @@ inline int skinny_elem_bytes(int mode) { return mode == kSkinnyBF16 ? 2 : 4; }
 hipError_t launch_skinny(int mode, int mr, int nw, int b_aligned, int a_layout, dim3 grid,
                          const SkinnyArgs& a, hipStream_t s);
 
+// ---------------------------------------------------------------- row dot (B stored N x K)
+// M <= 8 rows of a row-major A against B stored N x K (k contiguous): each
+// output is a dot product of two rows.  Workgroups of kRowdotWaves waves;
+// rowdot_rows(M) rows of B per wave; KW waves of a workgroup split k.
+struct RowdotArgs {
+    const void* A;
+    const void* B;
+    float* C;
+    int lda, ldb, ldc;
+    int M, N, K;
+    float alpha, beta;
+};
+constexpr int kRowdotWaves = 8;
+constexpr int rowdot_rows(int mr) { return mr <= 4 ? 4 : 2; }
+// mode 0 fp32, 1 bf16 storage; kw in {1, 2, 4, 8}; aligned: every row of A
+// and B starts on a 4-byte boundary (bf16).  grid.x = workgroups, each
+// covering (kRowdotWaves / kw) * rowdot_rows(M) rows of B.
+hipError_t launch_rowdot(int mode, int mr, int kw, int aligned, dim3 grid, const RowdotArgs& a, hipStream_t s);
+
 // ---------------------------------------------------------------- int8 MFMA
 // Exact s8 x s8 -> s32 with B stored N x K.  Each wave owns MT x NT tiles of
 // 16 x 16 outputs (v_mfma_i32_16x16x64_i8); a workgroup is WM x WN x KW waves

@@ -182,6 +182,8 @@ int dnnopt_onednn_gemm_bf16bf16f32(const char* transa, const char* transb,
 #define DNNOPT_K_TILE_F32    5  /* fp32 MFMA tiles (tall-skinny, split-K)   */
 #define DNNOPT_K_TILE_BF16   6  /* bf16 MFMA tiles                          */
 #define DNNOPT_K_NAIVE_F32   7  /* scalar reference kernel                  */
+#define DNNOPT_K_ROWDOT_F32  8  /* M <= 8, fp32 B stored N x K, rows once   */
+#define DNNOPT_K_ROWDOT_BF16 9  /* M <= 8, bf16 B stored N x K, rows once   */
 
 typedef struct dnnopt_plan {
     int kernel;             /* DNNOPT_K_* */

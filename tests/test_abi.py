@@ -106,6 +106,23 @@ def test_plan_split_never_exceeds_k(lib):
         assert p["splits"] <= max(1, -(-K // 64))
 
 
+def test_plans_for_weights_stored_n_by_k(lib):
+    """M <= 8 with B stored N x K (an inner product's weights) streams the rows
+    of B with the row-dot kernel; enough workgroups for two per CU."""
+    b = u.binding()
+    for M, N, K in ((1, 4096, 4096), (7, 11003, 2048), (3, 1009, 2048), (8, 5, 7)):
+        p = lib.plan_sgemm(M, N, K, transB=1)
+        assert p["kernel"] == b.K_ROWDOT_F32 and p["name"] == "dnnopt_rowdot", p
+        assert p["grid_x"] * p["cols"] >= N
+    p = lib.plan_sgemm(7, 11003, 2048, transB=1)
+    assert p["grid_x"] >= 256
+    assert lib.plan_bf16_ex(1, 11008, 4096, transB=1)["kernel"] == b.K_ROWDOT_BF16
+    assert lib.plan_bf16_ex(8, 11008, 4096, transA=1, transB=1)["kernel"] == b.K_ROWDOT_BF16
+    # transposed A (stored K x M) with B stored N x K stays on the MFMA tiles (fp32)
+    assert lib.plan_sgemm(4, 300, 64, transA=1, transB=1)["kernel"] == b.K_TILE_F32
+    assert lib.plan_bf16_ex(32, 11008, 4096, transB=1)["name"] == "dnnopt_tile_bf16_lds"
+
+
 def test_plan_rejects_bad_args(lib):
     b = u.binding()
     with pytest.raises(b.DnnoptError):

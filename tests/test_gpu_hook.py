@@ -76,6 +76,63 @@ def test_bf16_ex_misaligned_b_rows(lib, orc, dev):
     u.assert_fp32_close(host(dC), want, scale, K, "bf16_ex misaligned B")
 
 
+# ---------------------------------------------------------------- row dot: M <= 8, B stored N x K
+ROWDOT = [(M, N, K) for M in (1, 2, 3, 4, 5, 6, 7, 8) for (N, K) in ((1, 1), (5, 3), (257, 1000), (1009, 2051))]
+ROWDOT += [(1, 4096, 4096), (7, 11003, 2048), (4, 33, 65536)]
+
+
+@pytest.mark.parametrize("M,N,K", ROWDOT)
+def test_rowdot_fp32(lib, orc, dev, M, N, K):
+    """fp32 C = A B^T (+ beta C) with B stored N x K; the row padding past K
+    holds Inf and NaN, which must not reach any product."""
+    lda, ldb = K + 3, K + 5
+    A = np.full((M, lda), np.inf, np.float32)
+    B = np.full((N, ldb), np.nan, np.float32)
+    A[:, :K] = u.normal(orc, M * K, 1).reshape(M, K)
+    B[:, :K] = u.normal(orc, N * K, 2, 0, 0.02).reshape(N, K)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    p = lib.plan_sgemm(M, N, K, transB=1)
+    assert p["name"] == "dnnopt_rowdot", p
+    dA, dB = dev_copy(A, dev), dev_copy(B, dev)
+    for beta in (0.0, 0.5):
+        dC = dev_copy(C0 if beta else np.full_like(C0, np.nan), dev)
+        lib.sgemm(M, N, K, 1.5, dA, lda, dB, ldb, beta, dC, N, transB=1, stream=stream())
+        want, scale = u.exact(A[:, :K], B[:, :K].T, 1.5, beta, C0 if beta else None)
+        u.assert_fp32_close(host(dC), want, scale, K, f"rowdot f32 {M}x{N}x{K} beta={beta}")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 11008, 4096), (4, 1009, 2051), (8, 257, 1000), (3, 5, 3), (2, 64, 65536)])
+@pytest.mark.parametrize("odd", [0, 1])
+def test_rowdot_bf16(lib, orc, dev, M, N, K, odd):
+    """bf16 storage; odd strides put rows off 4-byte boundaries (shifted
+    loads).  Row padding holds bf16 Inf (0x7F80)."""
+    lda, ldb = K + 2 + odd, K + 4 + odd
+    A = np.full((M, lda), 0x7F80, np.uint16)
+    B = np.full((N, ldb), 0x7F80, np.uint16)
+    A[:, :K] = u.bf16_bits(orc, u.normal(orc, M * K, 1)).reshape(M, K)
+    B[:, :K] = u.bf16_bits(orc, u.normal(orc, N * K, 2, 0, 0.02)).reshape(N, K)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    dC = dev_copy(C0, dev)
+    lib.gemm_bf16_ex(M, N, K, 1.0, dev_copy(A.view(np.int16), dev), lda, dev_copy(B.view(np.int16), dev), ldb, 1.0,
+                     dC, N, transB=1, stream=stream())
+    want, scale = u.exact(u.bf16_value(A[:, :K]), u.bf16_value(B[:, :K]).T, 1.0, 1.0, C0)
+    u.assert_fp32_close(host(dC), want, scale, K, f"rowdot bf16 {M}x{N}x{K} odd={odd}")
+
+
+def test_rowdot_repeatable(lib, orc, dev):
+    M, N, K = 7, 1009, 4096
+    A, B = u.normal(orc, M * K, 1), u.normal(orc, N * K, 2, 0, 0.02)
+    dA, dB = dev_copy(A, dev), dev_copy(B, dev)
+    outs = []
+    for _ in range(10):
+        dC = torch.zeros((M, N), dtype=torch.float32, device=dev)
+        lib.sgemm(M, N, K, 1.0, dA, K, dB, K, 0.0, dC, N, transB=1, stream=stream())
+        outs.append(dC)
+    first = host(outs[0]).view(np.uint32)
+    for o in outs[1:]:
+        assert np.array_equal(host(o).view(np.uint32), first)
+
+
 # ---------------------------------------------------------------- column-major hook, device pointers
 HOOK = [(7, 1009, 2048), (31, 4096, 1024), (64, 300, 257), (1, 513, 77), (200, 3, 129), (16, 11008, 512)]
 
