@@ -4,7 +4,7 @@
                     [--detail FILE] [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input.  The
-default workload is BASELINE config C2 (the configuration the metric is
+default workload is config C2 (the configuration the headline metric is
 quoted on): fp32 C = A B + C for M in {2,3,5,7} x N in {1009,4099,11003},
 K = 2048, alpha = beta = 1, A, B ~ N(0, 0.02), C ~ U[-1, 1).  One step runs
 all twelve shapes once.  Other workloads (c1, c3, c4, c5) are selectable for
@@ -584,7 +584,7 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(r["ms_per_step"], 5), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
         "dtype": {"c4": "bf16", "c5": "s8"}.get(main_name, "f32"),
-        "data": "synthetic: SplitMix64 seed 42 (device generator), distributions of BASELINE.json",
+        "data": "synthetic: SplitMix64 seed 42 (device generator), distributions of the workload description",
         "config": {"workload": r["desc"], "shapes": len(r["cases"]), "bytes_per_step": r["step_bytes"],
                    "hbm_frac": round(r["value"] / HBM_PEAK_GBS, 4), "buffer_copies": r["copies"],
                    "parallelism": "1 GPU"},

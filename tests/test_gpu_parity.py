@@ -50,7 +50,7 @@ def test_sgemm_skinny(lib, orc, dev, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096)] + [(M, N, 2048) for M in (2, 3, 5, 7) for N in (1009, 4099, 11003)])
 def test_sgemm_configs_c1_c2(lib, orc, dev, M, N, K):
-    """Full BASELINE shapes: C1 (beta 0, C pre-filled NaN) and C2 (beta 1),
+    """Full benchmark shapes: C1 (beta 0, C pre-filled NaN) and C2 (beta 1),
     against fp64 and against the order-faithful oracle of the reference path."""
     if M == 1:
         A, B = u.uniform(orc, K, 1).reshape(1, K), u.uniform(orc, K * N, 2).reshape(K, N)
