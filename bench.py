@@ -426,7 +426,7 @@ def cpu_baseline(cases, budget_s=20.0):
 
 def _short_kernel_name(name):
     """'void dnnopt_hip::dnnopt_skinny<7, 8, 0, 1, 0>(dnnopt_hip::SkinnyArgs)' -> 'dnnopt_skinny<7, 8, 0, 1, 0>'."""
-    name = name.strip()
+    name = name.strip().replace("(anonymous namespace)::", "")
     if name.startswith("void "):
         name = name[5:]
     depth, cut = 0, len(name)
