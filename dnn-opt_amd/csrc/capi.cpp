@@ -24,8 +24,9 @@ int finish_launch(hipError_t e) {
 }
 
 int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B, int ldb, float* C, int ldc,
-               int M, int N, int K, float alpha, float beta, hipStream_t s) {
+               int M, int N, int K, float alpha, float beta, hipStream_t s, const float* bias = nullptr) {
     SkinnyArgs a{};
+    a.bias = bias;
     a.A = A;
     a.B = B;
     a.C = C;
@@ -61,11 +62,11 @@ int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B
     int st = finish_launch(launch_skinny(L.mode, L.mr, L.nw, b_aligned, a_layout, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
     return finish_launch(launch_skinny_reduce(a.part, G, T, skinny_tile_cols(L.mode), M, N, a.ncols_pad, alpha,
-                                              beta, C, ldc, s));
+                                              beta, C, ldc, bias, s));
 }
 
 int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const void* B, int ldb, float* C, int ldc,
-             int M, int N, int K, float alpha, float beta, hipStream_t s) {
+             int M, int N, int K, float alpha, float beta, hipStream_t s, const float* bias = nullptr) {
     Launch L = L0;
     // The LDS-staged bf16 kernel reads whole dwords: bf16 operands must start
     // on 4-byte boundaries, else the register-only kernel serves the call.
@@ -75,6 +76,7 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
         if (st != DNNOPT_OK) return st;
     }
     TileArgs a{};
+    a.bias = bias;
     a.A = A;
     a.B = B;
     a.C = C;
@@ -107,12 +109,14 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
                          (!tb || ((reinterpret_cast<uintptr_t>(B) & 3u) == 0 && (ldb & 1) == 0)));
     int st = finish_launch(launch_tile(L.mode, L.cfg, ta, tb, aligned, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
-    return finish_launch(launch_splitk_reduce(a.part, a.splits, L.tn, L.tm, L.bm, L.bn, M, N, alpha, beta, C, ldc, s));
+    return finish_launch(
+        launch_splitk_reduce(a.part, a.splits, L.tn, L.tm, L.bm, L.bn, M, N, alpha, beta, C, ldc, bias, s));
 }
 
 int run_rowdot(const Launch& L, const void* A, int lda, const void* B, int ldb, float* C, int ldc, int M, int N,
-               int K, float alpha, float beta, hipStream_t s) {
+               int K, float alpha, float beta, hipStream_t s, const float* bias = nullptr) {
     RowdotArgs a{};
+    a.bias = bias;
     a.A = A;
     a.B = B;
     a.C = C;
@@ -134,6 +138,27 @@ int run_rowdot(const Launch& L, const void* A, int lda, const void* B, int ldb, 
 bool dims_ok(int M, int N, int K) { return M > 0 && N > 0 && K > 0; }
 
 }  // namespace
+
+namespace dnnopt_hip {
+
+int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda, const float* B,
+               int ldb, float beta, float* C, int ldc, const float* bias, hipStream_t s) {
+    if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return DNNOPT_ERR_INVALID_ARG;
+    if (!dims_ok(M, N, K)) return DNNOPT_OK;
+    if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
+    if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    Launch L;
+    int st = plan_sgemm(transA, transB, M, N, K, lda, ldb, &L);
+    if (st != DNNOPT_OK) return st;
+    if (L.family == DNNOPT_K_SKINNY_F32)
+        return run_skinny(L, A, transA ? 1 : lda, transA ? lda : 1, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
+    if (L.family == DNNOPT_K_ROWDOT_F32)
+        return run_rowdot(L, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
+    return run_tile(L, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
+}
+
+}  // namespace dnnopt_hip
 
 extern "C" {
 
@@ -192,19 +217,7 @@ int dnnopt_hip_plan_gemm_s8(int with_scale, int M, int N, int K, dnnopt_plan* ou
 
 int dnnopt_hip_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
                      const float* B, int ldb, float beta, float* C, int ldc, void* stream) {
-    if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return DNNOPT_ERR_INVALID_ARG;
-    if (!dims_ok(M, N, K)) return DNNOPT_OK;
-    if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
-    if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N) return DNNOPT_ERR_INVALID_ARG;
-    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
-    Launch L;
-    int st = plan_sgemm(transA, transB, M, N, K, lda, ldb, &L);
-    if (st != DNNOPT_OK) return st;
-    hipStream_t s = as_stream(stream);
-    if (L.family == DNNOPT_K_SKINNY_F32)
-        return run_skinny(L, A, transA ? 1 : lda, transA ? lda : 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
-    if (L.family == DNNOPT_K_ROWDOT_F32) return run_rowdot(L, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
-    return run_tile(L, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+    return sgemm_bias(transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, nullptr, as_stream(stream));
 }
 
 int dnnopt_hip_sgemm_naive(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,

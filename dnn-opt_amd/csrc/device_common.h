@@ -153,6 +153,13 @@ __device__ __forceinline__ float epilogue(float acc, float alpha, float beta, co
     return __builtin_fmaf(alpha, acc, beta * (*c));
 }
 
+// Per-column bias added to a finished output as its own rounding (nothing
+// when bias is null): the oneDNN hook adds its bias to the completed C
+// (integration/onednn/0001-dnnopt-integration.patch:355-362).
+__device__ __forceinline__ float add_bias(float y, const float* bias, int n) {
+    return bias ? __fadd_rn(y, bias[n]) : y;
+}
+
 // Cross-workgroup ticket: every workgroup of a split-k group calls this after
 // storing its partial sums with coherent (sc0 sc1, write-through) stores.
 // Returns true in exactly one workgroup -- the last to arrive -- which then

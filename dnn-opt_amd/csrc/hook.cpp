@@ -84,16 +84,21 @@ int ext_common(bool bf16, char transa, char transb, int64_t M, int64_t N, int64_
             if (st != DNNOPT_OK) return st;
         }
     }
+    // The bias is one addition after each output's epilogue: fused into the
+    // GEMM when C is written in place (bias[i] is column i of C^T); after the
+    // write-back when columns overlap (the bias loop then runs per covering
+    // column, as the reference's does).
+    const float* fused_bias = Cw == C ? bias : nullptr;
     int st = bf16 ? dnnopt_hip_gemm_bf16_ex(tB, tA, n, m, k, alpha, static_cast<const uint16_t*>(B), (int)ldb,
                                             static_cast<const uint16_t*>(A), (int)lda, beta, Cw, ldw, stream)
-                  : dnnopt_hip_sgemm(tB, tA, n, m, k, alpha, static_cast<const float*>(B), (int)ldb,
-                                     static_cast<const float*>(A), (int)lda, beta, Cw, ldw, stream);
+                  : sgemm_bias(tB, tA, n, m, k, alpha, static_cast<const float*>(B), (int)ldb,
+                               static_cast<const float*>(A), (int)lda, beta, Cw, ldw, fused_bias, s);
     if (st != DNNOPT_OK) return st;
     if (Cw != C) {
         st = launch_status(launch_cm_scatter(Cw, m, n, ldc, C, s));
         if (st != DNNOPT_OK) return st;
     }
-    if (bias) return launch_status(launch_cm_fixup(C, m, n, ldc, kCmNone, 0.0f, bias, s));
+    if (bias && !fused_bias) return launch_status(launch_cm_fixup(C, m, n, ldc, kCmNone, 0.0f, bias, s));
     return DNNOPT_OK;
 }
 

@@ -54,6 +54,11 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
 // not on 4-byte boundaries).
 int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok = true);
 
+// fp32 GEMM of dnnopt_hip_sgemm with an optional per-column bias added to
+// each finished output (one more rounding): C = epilogue + bias[n].
+int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda, const float* B,
+               int ldb, float beta, float* C, int ldc, const float* bias, hipStream_t s);
+
 // Route an fp32 GEMM to a kernel family (skinny or tile).
 int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L);
 // Route a bf16 GEMM (fp32_inputs: operands are fp32 and rounded in registers;

@@ -102,7 +102,8 @@ namespace dnnopt_hip {
 template <int Q>
 __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restrict__ part, int splits,
                                                            int tiles_n, int tiles, int bm, int bn, int M, int N,
-                                                           float alpha, float beta, float* C, int ldc) {
+                                                           float alpha, float beta, float* C, int ldc,
+                                                           const float* bias) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     constexpr int OUTS = 256 / Q;
     __shared__ f4 red[Q > 1 ? Q * OUTS : 1];
@@ -155,18 +156,20 @@ __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restr
     if (!live) return;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        if (n + e < N) c[e] = beta == 0.0f ? alpha * s[e] : __builtin_fmaf(alpha, s[e], beta * c_old[e]);
+        if (n + e < N)
+            c[e] = add_bias(beta == 0.0f ? alpha * s[e] : __builtin_fmaf(alpha, s[e], beta * c_old[e]), bias, n + e);
 }
 
 hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
-                                int N, float alpha, float beta, float* C, int ldc, hipStream_t s) {
+                                int N, float alpha, float beta, float* C, int ldc, const float* bias,
+                                hipStream_t s) {
     const long long quads = (long long)tiles_n * tiles_m * bm * bn / 4;
     if (splits <= 16) {
         hipLaunchKernelGGL(dnnopt_splitk_reduce<1>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, part,
-                           splits, tiles_n, tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc);
+                           splits, tiles_n, tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc, bias);
     } else {
         hipLaunchKernelGGL(dnnopt_splitk_reduce<16>, dim3((unsigned)((quads + 15) / 16)), dim3(256), 0, s, part,
-                           splits, tiles_n, tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc);
+                           splits, tiles_n, tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc, bias);
     }
     return hipGetLastError();
 }
@@ -177,7 +180,7 @@ hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int 
 // are issued before the first add.
 __global__ __launch_bounds__(256) void dnnopt_skinny_reduce(const float* __restrict__ part, int G, int T, int tw,
                                                            int M, int N, int ncols_pad, float alpha, float beta,
-                                                           float* C, int ldc) {
+                                                           float* C, int ldc, const float* bias) {
     const int n = blockIdx.x * 256 + threadIdx.x;
     const int m = blockIdx.y;
     if (n >= N) return;
@@ -203,7 +206,7 @@ __global__ __launch_bounds__(256) void dnnopt_skinny_reduce(const float* __restr
 #pragma unroll
     for (int u = 0; u < 16; ++u)
         if (sp + u < splits) s += v[u];
-    *c = beta == 0.0f ? alpha * s : __builtin_fmaf(alpha, s, beta * c_old);
+    *c = add_bias(beta == 0.0f ? alpha * s : __builtin_fmaf(alpha, s, beta * c_old), bias, n);
 }
 
 // Sum exact int32 partial tiles [split][tile][bm*bn] and store C.
@@ -231,9 +234,9 @@ __global__ __launch_bounds__(256) void dnnopt_s8_reduce(const int32_t* __restric
 }
 
 hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, int N, int ncols_pad,
-                                float alpha, float beta, float* C, int ldc, hipStream_t s) {
+                                float alpha, float beta, float* C, int ldc, const float* bias, hipStream_t s) {
     hipLaunchKernelGGL(dnnopt_skinny_reduce, dim3((N + 255) / 256, M), dim3(256), 0, s, part, G, T, tw, M, N,
-                       ncols_pad, alpha, beta, C, ldc);
+                       ncols_pad, alpha, beta, C, ldc, bias);
     return hipGetLastError();
 }
 

@@ -209,7 +209,7 @@ __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
                 if (mm * R + rr == lane) v = acc[mm][rr];
     }
     float* c = p.C + (size_t)m * p.ldc + n0 + r;
-    *c = epilogue(v, p.alpha, p.beta, c);
+    *c = add_bias(epilogue(v, p.alpha, p.beta, c), p.bias, n0 + r);
 }
 
 }  // namespace

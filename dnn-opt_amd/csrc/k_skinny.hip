@@ -304,9 +304,11 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
                     for (int e = 0; e < 4; ++e) {
                         const int n = col0 + (gi % Q) * 4 + e;
                         if (n < p.N)
-                            p.C[(size_t)m * p.ldc + n] = p.beta == 0.0f ? p.alpha * out[pass][i][e]
-                                                                        : __builtin_fmaf(p.alpha, out[pass][i][e],
-                                                                                         p.beta * c_pre[pass][i][e]);
+                            p.C[(size_t)m * p.ldc + n] =
+                                add_bias(p.beta == 0.0f ? p.alpha * out[pass][i][e]
+                                                        : __builtin_fmaf(p.alpha, out[pass][i][e],
+                                                                         p.beta * c_pre[pass][i][e]),
+                                         p.bias, n);
                     }
                 }
             }
@@ -390,8 +392,10 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (n0 + e < p.N)
-                    p.C[(size_t)m * p.ldc + n0 + e] = p.beta == 0.0f ? p.alpha * sum[o][e]
-                                                                     : __builtin_fmaf(p.alpha, sum[o][e], p.beta * c_old[o][e]);
+                    p.C[(size_t)m * p.ldc + n0 + e] =
+                        add_bias(p.beta == 0.0f ? p.alpha * sum[o][e]
+                                                : __builtin_fmaf(p.alpha, sum[o][e], p.beta * c_old[o][e]),
+                                 p.bias, n0 + e);
         }
     }
 }

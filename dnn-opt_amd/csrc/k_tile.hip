@@ -150,7 +150,7 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
                 const int n = n0 + (wn * NT + nt) * 16 + r;
                 if (m < p.M && n < p.N) {
                     float* c = p.C + (size_t)m * p.ldc + n;
-                    *c = epilogue(acc[mt][nt][i], p.alpha, p.beta, c);
+                    *c = add_bias(epilogue(acc[mt][nt][i], p.alpha, p.beta, c), p.bias, n);
                 }
             }
 }
@@ -696,10 +696,14 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
 #pragma unroll
                 for (int k = 0; k < 4; ++k) out[k] = __builtin_fmaf(p.alpha, v[k], p.beta * c_old[k]);
             }
+            if (p.bias) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) out[k] = __fadd_rn(out[k], p.bias[n + k]);
+            }
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, out), rc, off, 0, 0);
         } else {
             float* c = p.C + (size_t)m * p.ldc + n;
-            for (int k = 0; k < p.N - n; ++k) c[k] = epilogue(v[k], p.alpha, p.beta, c + k);
+            for (int k = 0; k < p.N - n; ++k) c[k] = add_bias(epilogue(v[k], p.alpha, p.beta, c + k), p.bias, n + k);
         }
     }
 }

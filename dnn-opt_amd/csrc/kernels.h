@@ -35,6 +35,7 @@ struct SkinnyArgs {
     int ncols_pad;
     int defer_reduce;   // splits > 1: 1 = only store partials (a reduce kernel follows)
     int tiles;          // column tiles T; the grid has G >= T workgroups
+    const float* bias;  // per-column bias added after the epilogue (or null)
 };
 
 #ifndef DNNOPT_SKINNY_UNROLL
@@ -64,6 +65,7 @@ struct RowdotArgs {
     int lda, ldb, ldc;
     int M, N, K;
     float alpha, beta;
+    const float* bias;  // per-column bias added after the epilogue (or null)
 };
 constexpr int kRowdotWaves = 8;
 constexpr int rowdot_rows(int mr) { return mr <= 4 ? 4 : 2; }
@@ -128,6 +130,7 @@ struct TileArgs {
     int splits;
     int defer_reduce;   // splits > 1: 1 = only store partials (a reduce kernel follows)
     int tiles_n, tiles_m;  // LDS-staged kernels: tile grid (blockIdx.x is a linear, XCD-ordered index)
+    const float* bias;     // per-column bias added after the epilogue (or null)
 };
 
 // LDS-staged kernels walk the tiles in an XCD-aware order: workgroup L runs on
@@ -186,7 +189,7 @@ hipError_t launch_dequant(const int32_t* acc, int M, int N, const unsigned* amax
 // Reduce skinny partials [split][M][ncols_pad] into C (epilogue applied);
 // tile t (of T, tile width tw) has splits_of_tile(t, G, T) partials.
 hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, int N, int ncols_pad,
-                                float alpha, float beta, float* C, int ldc, hipStream_t s);
+                                float alpha, float beta, float* C, int ldc, const float* bias, hipStream_t s);
 // Reduce int8 partial tiles [splits][tiles][bm*bn] (exact int32) into C:
 // epi 0 stores int32, epi 1 stores (float)acc * scale[n].
 hipError_t launch_s8_reduce(const int32_t* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
@@ -194,7 +197,7 @@ hipError_t launch_s8_reduce(const int32_t* part, int splits, int tiles_n, int ti
 // Reduce partial tiles [splits][tiles_m*tiles_n][bm*bn] into C (epilogue applied).
 hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm,
                                 int bn, int M, int N, float alpha, float beta, float* C, int ldc,
-                                hipStream_t s);
+                                const float* bias, hipStream_t s);
 
 // Column-major helpers of the oneDNN-hook entry points.  C(i, j) is at
 // C[j * ldc + i]; ldc < M means overlapping columns (see k_colmajor.hip).

@@ -134,7 +134,11 @@ def test_rowdot_repeatable(lib, orc, dev):
 
 
 # ---------------------------------------------------------------- column-major hook, device pointers
-HOOK = [(7, 1009, 2048), (31, 4096, 1024), (64, 300, 257), (1, 513, 77), (200, 3, 129), (16, 11008, 512)]
+# Column-major (M, N, K): the row-major problem is N x M x K, so these reach
+# the fp32 tiles (with and without k-splits), the skinny kernel (with
+# k-splits: (4099, 3, 2048)) and, for transa = 'T', the row-dot kernel.
+HOOK = [(7, 1009, 2048), (31, 4096, 1024), (64, 300, 257), (1, 513, 77), (200, 3, 129), (16, 11008, 512),
+        (4099, 3, 2048), (16, 20, 65536)]
 
 
 def _hook_case(orc, M, N, K, ta, tb, pad, bf16):
@@ -272,3 +276,19 @@ def test_cxx_host_padded_c_beta_zero(lib, orc, dev):
         want, scale = u.exact(A.reshape(M, K), B.reshape(K, N))
         tol = u.fp32_tol(K, scale) if fn == "gemm_fp32" else 1e-2 * scale
         assert (np.abs(C[:, :N] - want) <= tol).all(), fn
+
+
+def test_ticket_reduction_mode(dev):
+    """The split-k reduction by the last-arriving workgroup (the library's
+    alternative to the reduce kernel, selected with DNNOPT_SPLIT_REDUCE=0 at
+    load time) gives the same results, bias included: checked in one child
+    process."""
+    import os
+    import subprocess
+    import sys
+
+    env = dict(os.environ, DNNOPT_SPLIT_REDUCE="0")
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ticket_mode_check.py")
+    r = subprocess.run([sys.executable, "-u", script], env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
+    assert "ticket mode ok" in r.stdout
