@@ -30,7 +30,9 @@ been committed for it.
 `cpu_baseline` times the oracle's restatement of the reference's CPU path
 (oracle/liboracle.so) on the host, on every shape of the workload once per
 run (2 warmup runs, 5 timed runs, median -- the reference's
-dnnopt::benchmark method).
+dnnopt::benchmark method).  `cpu_reference` times the reference's literal
+portable fallback (its naive loops, built from its own sources into
+oracle/_ref) on a bounded sample, when that build is present.
 """
 
 from __future__ import annotations
@@ -343,6 +345,61 @@ def read_traffic(kernel, wl):
 
 
 # ---------------------------------------------------------------- CPU baseline
+def cpu_reference(cases, budget_s=10.0):
+    """Time the reference's literal portable fallback on the host: its own
+    naive loops (src/gemm/gemm.cpp:88-100 for fp32, the scalar loop of
+    src/gemm/gemm_int8_native.cpp:239-247 for int8), compiled from the
+    reference sources into oracle/_ref/libref.so.  None when that build is
+    absent.  Single-threaded, as the loops are."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import _util as u
+
+    ref = u.load_ref()
+    if ref is None:
+        return None
+    orc = u.load_oracle()
+    prepared = []
+    for c in cases:
+        M, N, K = c.M, c.N, c.K
+        if c.kind == "f32":
+            A, B, C = u.uniform(orc, M * K, 1), u.uniform(orc, K * N, 2), u.uniform(orc, M * N, 3)
+
+            def run(A=A, B=B, C=C, c=c):
+                ref.ref_gemm_naive_f32(c.M, c.N, c.K, c.alpha, u.ptr(A), c.K, u.ptr(B), c.N, c.beta, u.ptr(C), c.N)
+        elif c.kind in ("s8", "s8s"):
+            A, B = u.ints8(orc, M * K, 1), u.ints8(orc, N * K, 2)
+            C = np.empty(M * N, np.int32)
+
+            def run(A=A, B=B, C=C, c=c):
+                ref.ref_gemm_s8s8s32(c.M, c.N, c.K, u.ptr(A), c.K, u.ptr(B), c.K, u.ptr(C), c.N)
+        else:
+            continue
+        prepared.append((c, run))
+    if not prepared:
+        return None
+    # bounded sample: whole passes over the shapes while they fit the budget,
+    # else the first shapes that fit
+    times, used = [], []
+    t_all = time.perf_counter()
+    for c, run in prepared:
+        t = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t)
+        used.append(c)
+        if time.perf_counter() - t_all > budget_s:
+            break
+    total_bytes = sum(c.bytes_alg() for c in used)
+    med = sum(times)
+    return {
+        "value": round(total_bytes / med / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "reference",
+        "sample": (f"{len(used)} of {len(prepared)} shapes of the workload once ({total_bytes / 1e6:.0f} MB "
+                   f"algorithmic, {med:.1f} s): the reference's own naive loops built from its sources "
+                   f"(oracle/_ref), single-threaded"),
+    }
+
+
 def cpu_baseline(cases, budget_s=20.0):
     """Time the oracle's restatement of the reference CPU path on the host."""
     import ctypes
@@ -579,6 +636,7 @@ def main():
               f"dominant {r['roofline']['kernel']} frac {r['roofline']['frac']}", file=sys.stderr, flush=True)
     r = results[main_name]
     cpu = None if args.no_cpu else cpu_baseline(r["cases"])
+    cpu_ref = None if args.no_cpu else cpu_reference(r["cases"])
     line = {
         "metric": METRIC, "value": round(r["value"], 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(r["ms_per_step"], 5), "higher_is_better": True,
@@ -591,6 +649,7 @@ def main():
         "roofline": {k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac", "traffic")},
         "roofline_kernel": {k: r["roofline"][k] for k in ("kernel", "launch_us", "bytes_per_launch")},
         "cpu_baseline": cpu,
+        "cpu_reference": cpu_ref,
     }
     if args.detail:
         os.makedirs(os.path.dirname(os.path.abspath(args.detail)), exist_ok=True)
