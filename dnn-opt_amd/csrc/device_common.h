@@ -23,6 +23,13 @@ constexpr int kRsrcWord3 = 0x00020000;
 // Offset used to force an out-of-range (zero-returning) buffer read.
 constexpr uint32_t kOobOffset = 0x80000000u;
 
+// Buffer range in bytes, clamped to 2^31 - 1.  Written as a plain select:
+// the HIP min() template for 64-bit values is not recognised as wave-uniform,
+// which turns every load through the descriptor into a readfirstlane loop.
+__device__ __forceinline__ uint32_t range31(size_t bytes) {
+    return bytes > 0x7FFFFFFFull ? 0x7FFFFFFFu : (uint32_t)bytes;
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                              kRsrcWord3);
@@ -54,6 +61,10 @@ __device__ __forceinline__ void buf_store_x4_coherent(__amdgpu_buffer_rsrc_t r, 
 
 __device__ __forceinline__ uint32_t buf_load_x1_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kAuxCoherent);
+}
+
+__device__ __forceinline__ void buf_store_x1(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
 }
 
 __device__ __forceinline__ void buf_store_x1_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {

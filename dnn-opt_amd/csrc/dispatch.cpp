@@ -18,6 +18,8 @@
 //   * M > 8 bf16 with 4-byte aligned rows: LDS-staged MFMA tiles (128 x 96
 //     with 8 waves above M = 64, 64 x 128 and 32 x 128 below), split-k only
 //     when the tiles leave more than half of the CUs idle.
+//   * fp32 with M >= 4096, 16 < N <= 64 and B small enough for LDS: B
+//     resident in LDS, persistent workgroups stream A (k_tall.hip).
 //   * other M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for
 //     N <= 16, 64 x 64 otherwise); split-k when the tile count cannot occupy
 //     the CUs, with a separate reduce kernel once the split count is large.
@@ -31,7 +33,8 @@
 //   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel),
 //   DNNOPT_TILE_SPLITS (force the k-splits of a tile launch), DNNOPT_TILE_CFG
 //   (force an LDS-staged bf16 tile configuration, index 5 and up),
-//   DNNOPT_S8_CFG / DNNOPT_S8_SPLITS (force the int8 configuration / splits).
+//   DNNOPT_S8_CFG / DNNOPT_S8_SPLITS (force the int8 configuration / splits),
+//   DNNOPT_TALL=0 (keep tall-skinny fp32 GEMMs on the register-only tiles).
 #include <stdlib.h>
 #include <string.h>
 
@@ -306,9 +309,38 @@ int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
     return DNNOPT_OK;
 }
 
+int plan_tall(int transB, int M, int N, int K, int lda, Launch* L) {
+    *L = Launch{};
+    // N <= 16 streams faster through the register tiles (64 x 16), whose
+    // per-k re-reads of B are small at that width.
+    if (N <= 16 || N > 64 || M < 4096) return DNNOPT_ERR_UNSUPPORTED;
+    const int nt = (N + 15) / 16;
+    const size_t lds = tall_lds_bytes(nt, K);
+    if (lds > 65536) return DNNOPT_ERR_UNSUPPORTED;
+    if (((long long)(M - 1) * lda + K) * 4 >= 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
+    // Persistent: as many 4-wave workgroups as fit (LDS-limited), no more
+    // than there are 32-row tiles for their waves.
+    const long long per_cu = std::max<long long>(1, std::min<long long>(4, 160 * 1024 / (long long)lds));
+    const long long tiles = ceil_div(M, 32);
+    static const int wgs_per_cu = env_int("DNNOPT_TALL_WGS_PER_CU", 0);
+    const long long want = num_cus() * (wgs_per_cu > 0 ? std::min<long long>(wgs_per_cu, per_cu) : per_cu);
+    const long long G = std::max<long long>(1, std::min<long long>(want, ceil_div(tiles, tall_waves())));
+    L->cfg = nt;
+    L->lds = lds;
+    L->mode = transB;
+    L->grid = dim3((unsigned)G, 1, 1);
+    fill_pub(L, DNNOPT_K_TALL_F32, "dnnopt_tall_f32", 32, 16 * nt, 1, tall_waves() * 64);
+    return DNNOPT_OK;
+}
+
 int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L) {
     if (M <= 8 && !transB) return plan_skinny(kSkinnyF32, M, N, K, ldb, L);
     if (M <= 8 && !transA && plan_rowdot(0, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
+    static const bool tall_ok = [] {
+        const char* e = getenv("DNNOPT_TALL");
+        return !(e && *e && atoi(e) == 0);
+    }();
+    if (tall_ok && !transA && plan_tall(transB, M, N, K, lda, L) == DNNOPT_OK) return DNNOPT_OK;
     return plan_tile(kTileF32, transA, transB, M, N, K, lda, ldb, L);
 }
 

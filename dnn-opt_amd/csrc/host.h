@@ -29,7 +29,8 @@ struct Launch {
     int family = DNNOPT_K_NONE;
     int mode = 0;        // SkinnyMode / TileMode / int8 epilogue
     int mr = 0, nw = 0;  // skinny (rowdot: nw = waves splitting k)
-    int cfg = 0;         // tile / int8 configuration index
+    int cfg = 0;         // tile / int8 configuration index (tall: column tiles nt)
+    size_t lds = 0;      // dynamic LDS bytes (tall)
     int bm = 0, bn = 0;  // tile shape
     int tn = 0, tm = 0;  // tile grid (column tiles, row tiles)
     int tiles = 0;       // skinny: column tiles T (the grid has G >= T workgroups)
@@ -44,6 +45,8 @@ struct Launch {
 int split_reduce_mode();
 
 int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L);
+// fp32, large M, N <= 64, B small enough to stay in LDS (no transposed A).
+int plan_tall(int transB, int M, int N, int K, int lda, Launch* L);
 // M <= 8 against B stored N x K; mode 0 fp32, 1 bf16 storage.
 int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L);
 // lds_ok = false keeps bf16 GEMMs off the LDS-staged kernel (operands whose

@@ -183,7 +183,7 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
         // Partials are written through to memory (coherent stores) so the
         // reducing workgroup can read them without cache maintenance.
         const __amdgpu_buffer_rsrc_t rp = make_rsrc(
-            p.part, (uint32_t)min<size_t>((size_t)p.splits * tiles * BM * BN * 4, 0x7FFFFFFFull));
+            p.part, range31((size_t)p.splits * tiles * BM * BN * 4));
         if (wk == 0) {
             const size_t base = ((size_t)split * tiles + tile_id) * (BM * BN);
 #pragma unroll
@@ -278,10 +278,10 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     // Ranges end at the last byte of each operand, rounded up to a dword.
     const __amdgpu_buffer_rsrc_t ra =
         make_rsrc(p.A + (size_t)m0 * p.lda,
-                  (uint32_t)min<size_t>(((size_t)(p.M - 1 - m0) * p.lda + p.K + 3) & ~(size_t)3, 0x7FFFFFFFull));
+                  range31(((size_t)(p.M - 1 - m0) * p.lda + p.K + 3) & ~(size_t)3));
     const __amdgpu_buffer_rsrc_t rb =
         make_rsrc(p.B + (size_t)n0 * p.ldb,
-                  (uint32_t)min<size_t>(((size_t)(p.N - 1 - n0) * p.ldb + p.K + 3) & ~(size_t)3, 0x7FFFFFFFull));
+                  range31(((size_t)(p.N - 1 - n0) * p.ldb + p.K + 3) & ~(size_t)3));
 
     uint32_t a_off[AU], b_off[BU];
     int a_lds[AU], b_lds[BU], a_c[AU];
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     const size_t esz = EPI == 0 ? 4 : 4;
     const __amdgpu_buffer_rsrc_t rc =
         make_rsrc(static_cast<char*>(p.C) + ((size_t)m0 * p.ldc + n0) * esz,
-                  (uint32_t)min<size_t>(((size_t)(p.M - 1 - m0) * p.ldc + (p.N - n0)) * esz, 0x7FFFFFFFull));
+                  range31(((size_t)(p.M - 1 - m0) * p.ldc + (p.N - n0)) * esz));
     for (int e = t; e < BM * Q4; e += NTH) {
         const int row = e / Q4, q = e % Q4;
         const int m = m0 + row, n = n0 + 4 * q;

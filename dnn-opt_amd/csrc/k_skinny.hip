@@ -320,7 +320,7 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     // reduces them -- here or in a separate kernel -- reads them without any
     // cache maintenance.
     const __amdgpu_buffer_rsrc_t rp =
-        make_rsrc(p.part, (uint32_t)min<size_t>((size_t)p.splits * MR * p.ncols_pad * 4, 0x7FFFFFFFull));
+        make_rsrc(p.part, range31((size_t)p.splits * MR * p.ncols_pad * 4));
 #pragma unroll
     for (int pass = 0; pass < P; ++pass)
 #pragma unroll

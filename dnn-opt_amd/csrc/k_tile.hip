@@ -103,7 +103,7 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
         // Partials are written through to memory (coherent stores) so the
         // reducing workgroup can read them without cache maintenance.
         const __amdgpu_buffer_rsrc_t rp = make_rsrc(
-            p.part, (uint32_t)min<size_t>((size_t)p.splits * tiles * S::BM * S::BN * 4, 0x7FFFFFFFull));
+            p.part, range31((size_t)p.splits * tiles * S::BM * S::BN * 4));
         if (wk == 0) {
             const size_t base = ((size_t)split * tiles + tile_id) * (S::BM * S::BN);
 #pragma unroll

@@ -74,6 +74,24 @@ constexpr int rowdot_rows(int mr) { return mr <= 4 ? 4 : 2; }
 // covering (kRowdotWaves / kw) * rowdot_rows(M) rows of B.
 hipError_t launch_rowdot(int mode, int mr, int kw, int aligned, dim3 grid, const RowdotArgs& a, hipStream_t s);
 
+// ---------------------------------------------------------------- tall-skinny fp32, B in LDS
+// Large M, N <= 16 * nt (nt in {1, 2, 3, 4}), all of B staged in LDS
+// (ceil(K / 16) * 16 * 16 * nt * 4 bytes <= 64 KiB); persistent workgroups
+// of 4 waves stream row tiles of A (32 rows per wave).  A rows must fit
+// 32-bit buffer offsets: ((M - 1) * lda + K) * 4 < 2^31.
+struct TallArgs {
+    const float* A;
+    const float* B;
+    float* C;
+    int lda, ldb, ldc;
+    int M, N, K;
+    float alpha, beta;
+    const float* bias;  // per-column bias added after the epilogue (or null)
+};
+inline size_t tall_lds_bytes(int nt, int K) { return (size_t)((K + 15) / 16) * 16 * 16 * nt * 4; }
+int tall_waves();  // waves per workgroup of the tall kernel
+hipError_t launch_tall_f32(int nt, int tb, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s);
+
 // ---------------------------------------------------------------- int8 MFMA
 // Exact s8 x s8 -> s32 with B stored N x K.  Each wave owns MT x NT tiles of
 // 16 x 16 outputs (v_mfma_i32_16x16x64_i8); a workgroup is WM x WN x KW waves

@@ -84,6 +84,7 @@ def test_plans_for_the_configs(lib):
             if p["grid_x"] >= 256:
                 assert p["grid_x"] % 256 == 0 or p["grid_x"] == tiles
     assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TILE_F32
+    assert lib.plan_sgemm(65536, 64, 256)["kernel"] == b.K_TALL_F32
     p = lib.plan_sgemm(64, 64, 262144, transA=1)
     assert p["kernel"] == b.K_TILE_F32 and p["splits"] > 16
     for M in (1, 4):
@@ -121,6 +122,21 @@ def test_plans_for_weights_stored_n_by_k(lib):
     # transposed A (stored K x M) with B stored N x K stays on the MFMA tiles (fp32)
     assert lib.plan_sgemm(4, 300, 64, transA=1, transB=1)["kernel"] == b.K_TILE_F32
     assert lib.plan_bf16_ex(32, 11008, 4096, transB=1)["name"] == "dnnopt_tile_bf16_lds"
+
+
+def test_plans_for_tall_skinny(lib):
+    """Large M with N <= 64 and B small enough for LDS: the B-resident kernel;
+    B too large for LDS or transposed A: the MFMA tiles."""
+    b = u.binding()
+    for M, N, K in ((65536, 17, 256), (65536, 64, 256), (4096, 20, 512), (100000, 33, 300), (8192, 48, 333)):
+        p = lib.plan_sgemm(M, N, K)
+        assert p["kernel"] == b.K_TALL_F32 and p["cols"] >= N, p
+        assert p["grid_x"] * 4 * 32 >= min(M, p["grid_x"] * 4 * 32)
+    assert lib.plan_sgemm(65536, 64, 257)["kernel"] == b.K_TILE_F32   # 272 x 64 x 4 bytes > 64 KiB
+    assert lib.plan_sgemm(65536, 64, 256, transA=1)["kernel"] == b.K_TILE_F32
+    assert lib.plan_sgemm(1000, 64, 256)["kernel"] == b.K_TILE_F32    # too few rows
+    assert lib.plan_sgemm(65536, 65, 64)["kernel"] == b.K_TILE_F32
+    assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TILE_F32   # N <= 16: register tiles
 
 
 def test_plan_rejects_bad_args(lib):

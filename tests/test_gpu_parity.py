@@ -132,6 +132,38 @@ def test_sgemm_configs_c3(lib, orc, dev, M, N, K, ta):
     u.assert_fp32_close(host(dC), want, scale, K, f"C3 {M}x{N}x{K} ta={ta}")
 
 
+# Tall-skinny fp32 with B resident in LDS: every column-tile width, ragged N
+# and K (K tails inside a 16-k chunk, N not a multiple of 16), padded strides,
+# B stored K x N or N x K, more row tiles than waves and fewer.
+# (N <= 16 goes to the register tiles; kept here as ragged tall-skinny cases.)
+TALL = [(65536, 64, 256, 0, 0), (65536, 16, 256, 1, 0), (8192, 33, 300, 0, 3), (5000, 64, 17, 2, 1),
+        (4096, 1, 1024, 0, 0), (100003, 7, 64, 1, 2), (20000, 48, 333, 0, 0), (4097, 17, 5, 3, 0),
+        (6000, 60, 250, 1, 1), (70000, 32, 128, 0, 0)]
+
+
+@pytest.mark.parametrize("M,N,K,pa,pb", TALL)
+@pytest.mark.parametrize("tb", [0, 1])
+def test_sgemm_tall_skinny(lib, orc, dev, M, N, K, pa, pb, tb):
+    p = lib.plan_sgemm(M, N, K, transB=tb)
+    assert p["name"] == ("dnnopt_tall_f32" if N > 16 else "dnnopt_tile_f32"), p
+    lda = K + pa
+    opA = np.zeros((M, lda), np.float32)
+    opA[:, :K] = u.uniform(orc, M * K, 1).reshape(M, K)
+    opA[:, K:] = np.inf  # row padding past K must never reach a product
+    opB = u.uniform(orc, K * N, 2).reshape(K, N)
+    SB = opB.T if tb else opB
+    ldb = SB.shape[1] + pb
+    B = np.zeros((SB.shape[0], ldb), np.float32)
+    B[:, :SB.shape[1]] = SB
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    for beta in (0.0, 0.75):
+        dC = dev_copy(C0 if beta else np.full_like(C0, np.nan), dev)
+        lib.sgemm(M, N, K, 1.25, dev_copy(opA, dev), lda, dev_copy(B, dev), ldb, beta, dC, N, transB=tb,
+                  stream=stream())
+        want, scale = u.exact(opA[:, :K], opB, 1.25, beta, C0 if beta else None)
+        u.assert_fp32_close(host(dC), want, scale, K, f"tall {M}x{N}x{K} tb={tb} beta={beta}")
+
+
 def test_sgemm_naive_bitwise(lib, orc, dev):
     """The kNaive kernel reproduces the reference's scalar loop bit for bit
     (the oracle's naive loop is itself pinned to the reference build)."""
