@@ -227,9 +227,13 @@ def run_gpu(args, wl_name):
         if not cases:
             raise SystemExit(f"bench.py: no case of {wl_name} is named in --cases {args.cases}")
     step_bytes = sum(c.bytes_alg() for c in cases)
-    # Rotate copies so one pass of every buffer exceeds 2x the 256 MB cache.
+    # Rotate copies so that one pass over the buffers a graph touches exceeds
+    # 2x the 256 MB Infinity Cache: the step graphs rotate `copies` copies of
+    # every case, the per-case graphs rotate that case's own copies, so each
+    # case gets enough copies for its own rotation to exceed 600 MB as well.
     copies = max(1, -(-(600 << 20) // step_bytes))
-    bufs = [Buffers(torch, lib, c, copies, dev) for c in cases]
+    case_copies = [max(copies, -(-(600 << 20) // c.bytes_alg())) for c in cases]
+    bufs = [Buffers(torch, lib, c, cc, dev) for c, cc in zip(cases, case_copies)]
     keys = [kernel_key(lib, c) for c in cases]
     torch.cuda.synchronize()
     stream = torch.cuda.Stream(device=dev)  # default priority
@@ -250,9 +254,11 @@ def run_gpu(args, wl_name):
 
     # one graph per buffer copy: a full step
     step_graphs = [capture([lambda bf=bf, r=r: bf.launch(lib, r, sp) for bf in bufs]) for r in range(copies)]
-    # one graph per case: REP back-to-back launches, rotating copies
-    rep = 16
-    case_graphs = [capture([lambda bf=bf, i=i: bf.launch(lib, i % copies, sp) for i in range(rep)]) for bf in bufs]
+    # one graph per case: back-to-back launches over all of the case's copies
+    # (at least 16 launches)
+    reps = [max(16, cc) for cc in case_copies]
+    case_graphs = [capture([lambda bf=bf, i=i, cc=cc: bf.launch(lib, i % cc, sp) for i in range(rp)])
+                   for bf, cc, rp in zip(bufs, case_copies, reps)]
     torch.cuda.synchronize()
 
     with torch.cuda.stream(stream):
@@ -284,7 +290,7 @@ def run_gpu(args, wl_name):
                 e1.record(stream)
                 samples.append((e0, e1))
         torch.cuda.synchronize()
-        d = [a.elapsed_time(bb) / rep for a, bb in samples]
+        d = [a.elapsed_time(bb) / reps[i] for a, bb in samples]
         med = statistics.median(d)
         launch_ms.append(sum(d) / len(d))
         per_case.append({

@@ -16,17 +16,18 @@
 //     few column tiles to occupy the chip, over k across workgroups (split-k
 //     with a ticketed, ordered reduction) -- about eight waves per CU.
 //   * M > 8 bf16 with 4-byte aligned rows: LDS-staged MFMA tiles (128 x 96
-//     with 8 waves above M = 64, 64 x 128 and 32 x 128 below), split-k only
-//     when the tiles leave more than half of the CUs idle.
+//     with 8 waves above M = 128; 64 x 128, 64 x 64 and 32 x 64 tiles with
+//     128-k blocks below), split-k only when the tiles leave more than half
+//     of the CUs idle.
 //   * fp32 with M >= 4096, 16 < N <= 64 and B small enough for LDS: B
 //     resident in LDS, persistent workgroups stream A (k_tall.hip).
 //   * other M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for
 //     N <= 16, 64 x 64 otherwise); split-k when the tile count cannot occupy
 //     the CUs, with a separate reduce kernel once the split count is large.
 //   * int8 (B as N x K): 16 x 16 MFMA tiles with k split over the waves of a
-//     workgroup for M <= 16; 32 x 32 tiles staged through LDS above that
-//     (4-byte aligned rows), split-k only when the tiles leave more than half
-//     of the CUs idle.
+//     workgroup for M <= 16; 32 x 32 tiles staged through LDS (256-byte
+//     k-blocks) above that (4-byte aligned rows), split-k only when the tiles
+//     leave more than half of the CUs idle.
 // Tunables (environment, read once, for sweeps):
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
 //   DNNOPT_SKINNY_WGS_PER_CU (default 2), DNNOPT_SKINNY_WGS (force G),
@@ -170,7 +171,9 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     int cfg;
     static const int forced_cfg = env_int("DNNOPT_TILE_CFG", 0);
     if (lds) {
-        cfg = M > 64 ? 13 : (M > 32 ? 7 : 6);
+        // 128 k per LDS block below M = 128 (fewer barriers, more bytes per
+        // block in flight); measured on MI355X at N = 11008, K = 4096.
+        cfg = M > 128 ? 13 : (M > 64 ? 23 : (M > 32 ? 21 : 19));
         if (forced_cfg >= kTileFirstLds && forced_cfg < tile_config_count()) cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
@@ -183,7 +186,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     }
     const TileConfig c = tile_config(cfg);
     const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
-    const int kb = (mode == kTileF32 || lds) ? 64 : 128;
+    const int kb = lds ? tile_lds_bk(bm, bn, c.kblk) : (mode == kTileF32 ? 64 : 128);
     const long long tn = ceil_div(N, bn), tm = ceil_div(M, bm), tiles = tn * tm;
     const long long nblk = ceil_div(K, kb);
     const int waves_per_wg = c.wm * c.wn * c.kw;
@@ -241,8 +244,9 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok) {
     static const int forced_cfg = env_int("DNNOPT_S8_CFG", -1);
     static const int forced_splits = env_int("DNNOPT_S8_SPLITS", 0);
     // M <= 16: 16 x 16 tiles with k split over the 8 waves of a workgroup
-    // (one launch, no partial sums); larger M: 32 x 32 tiles through LDS.
-    int cfg = M <= 16 ? 5 : 13;
+    // (one launch, no partial sums); larger M: 32 x 32 tiles through LDS with
+    // 256-byte k-blocks.
+    int cfg = M <= 16 ? 5 : 20;
     if (forced_cfg >= 0 && forced_cfg < s8_config_count()) cfg = forced_cfg;
     if (cfg >= kS8FirstLds && !lds_ok) cfg = M <= 16 ? 5 : (M >= 128 ? 3 : 2);
     const bool lds = cfg >= kS8FirstLds;

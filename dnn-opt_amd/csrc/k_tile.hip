@@ -425,13 +425,13 @@ __device__ __forceinline__ int swz_b(int n, int c) { return c ^ ((n ^ (n >> 3)) 
 
 }  // namespace
 
-template <int MT, int NT, int WM, int WN, int D, int MODE, int TB = 0>
+template <int MT, int NT, int WM, int WN, int D, int MODE, int TB = 0, int KB0 = 0>
 __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) {
     static_assert(!TB || MODE == kTileBF16, "B stored N x K needs bf16 storage");
     using S = TileShape<MT, NT, WM, WN, 1>;
     constexpr int BM = S::BM, BN = S::BN;
     // k per block: DNNOPT_LDS_KB when both stages fit in 128 KiB of LDS.
-    constexpr int BK = (BM + BN) * DNNOPT_LDS_KB * 2 * 2 <= 131072 ? DNNOPT_LDS_KB : 64;
+    constexpr int BK = tile_lds_bk(BM, BN, KB0);
     constexpr int NTH = WM * WN * 64;
     constexpr int ROWB = BK * 2;  // bytes of one LDS row (BK bf16)
     constexpr int CPR = ROWB / 16;  // 16-byte chunks per LDS row
@@ -727,6 +727,14 @@ static const TileConfig kTileConfigs[] = {
     {2, 3, 4, 2, 1, 3},  // 13: 128 x 96  bf16 through LDS, 8 waves, 3 blocks ahead
     {2, 3, 4, 2, 1, 2},  // 14: 128 x 96  bf16 through LDS, 8 waves
     {4, 2, 2, 4, 1, 2},  // 15: 128 x 128 bf16 through LDS, 8 waves
+    {2, 1, 1, 4, 1, 2, 256},  // 16: 32 x 64  bf16 through LDS, 256 k per block
+    {2, 2, 1, 2, 1, 2, 256},  // 17: 32 x 64  bf16 through LDS, 2 waves, 256 k per block
+    {2, 2, 1, 4, 1, 2, 128},  // 18: 32 x 128 bf16 through LDS, 128 k per block
+    {2, 1, 1, 4, 1, 3, 128},  // 19: 32 x 64  bf16 through LDS, 128 k per block, 3 ahead
+    {2, 3, 4, 2, 1, 2, 128},  // 20: 128 x 96 bf16 through LDS, 8 waves, 128 k per block
+    {2, 2, 2, 2, 1, 3, 128},  // 21: 64 x 64  bf16 through LDS, 128 k per block, 3 ahead
+    {2, 4, 2, 2, 1, 2, 128},  // 22: 64 x 128 bf16 through LDS, 128 k per block
+    {2, 2, 2, 4, 1, 2, 128},  // 23: 64 x 128 bf16 through LDS, 8 waves, 128 k per block
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -750,11 +758,11 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
         }                                                                                                \
         break;
 
-#define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN, D)                                                      \
+#define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN, D, KB)                                                  \
     case IDX:                                                                                              \
-        if (mode == kTileBF16 && tb) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16, 1>), grid, blk, 0, s, a); \
-        else if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16>), grid, blk, 0, s, a); \
-        else if (mode == kTileF2B) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileF2B>), grid, blk, 0, s, a); \
+        if (mode == kTileBF16 && tb) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16, 1, KB>), grid, blk, 0, s, a); \
+        else if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16, 0, KB>), grid, blk, 0, s, a); \
+        else if (mode == kTileF2B) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileF2B, 0, KB>), grid, blk, 0, s, a); \
         else return hipErrorInvalidValue;                                                                  \
         break;
 
@@ -771,17 +779,25 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_CASE(2, 2, 2, 2, 2, 1)
         DNNOPT_TILE_CASE(3, 2, 2, 2, 2, 2)
         DNNOPT_TILE_CASE(4, 2, 4, 2, 2, 1)
-        DNNOPT_TILE_LDS_CASE(5, 4, 4, 2, 2, 2)
-        DNNOPT_TILE_LDS_CASE(6, 2, 2, 1, 4, 2)
-        DNNOPT_TILE_LDS_CASE(7, 2, 4, 2, 2, 2)
-        DNNOPT_TILE_LDS_CASE(8, 4, 4, 2, 2, 3)
-        DNNOPT_TILE_LDS_CASE(9, 4, 4, 2, 2, 4)
-        DNNOPT_TILE_LDS_CASE(10, 2, 2, 1, 4, 4)
-        DNNOPT_TILE_LDS_CASE(11, 2, 4, 2, 2, 4)
-        DNNOPT_TILE_LDS_CASE(12, 4, 2, 2, 4, 3)
-        DNNOPT_TILE_LDS_CASE(13, 2, 3, 4, 2, 3)
-        DNNOPT_TILE_LDS_CASE(14, 2, 3, 4, 2, 2)
-        DNNOPT_TILE_LDS_CASE(15, 4, 2, 2, 4, 2)
+        DNNOPT_TILE_LDS_CASE(5, 4, 4, 2, 2, 2, 0)
+        DNNOPT_TILE_LDS_CASE(6, 2, 2, 1, 4, 2, 0)
+        DNNOPT_TILE_LDS_CASE(7, 2, 4, 2, 2, 2, 0)
+        DNNOPT_TILE_LDS_CASE(8, 4, 4, 2, 2, 3, 0)
+        DNNOPT_TILE_LDS_CASE(9, 4, 4, 2, 2, 4, 0)
+        DNNOPT_TILE_LDS_CASE(10, 2, 2, 1, 4, 4, 0)
+        DNNOPT_TILE_LDS_CASE(11, 2, 4, 2, 2, 4, 0)
+        DNNOPT_TILE_LDS_CASE(12, 4, 2, 2, 4, 3, 0)
+        DNNOPT_TILE_LDS_CASE(13, 2, 3, 4, 2, 3, 0)
+        DNNOPT_TILE_LDS_CASE(14, 2, 3, 4, 2, 2, 0)
+        DNNOPT_TILE_LDS_CASE(15, 4, 2, 2, 4, 2, 0)
+        DNNOPT_TILE_LDS_CASE(16, 2, 1, 1, 4, 2, 256)
+        DNNOPT_TILE_LDS_CASE(17, 2, 2, 1, 2, 2, 256)
+        DNNOPT_TILE_LDS_CASE(18, 2, 2, 1, 4, 2, 128)
+        DNNOPT_TILE_LDS_CASE(19, 2, 1, 1, 4, 3, 128)
+        DNNOPT_TILE_LDS_CASE(20, 2, 3, 4, 2, 2, 128)
+        DNNOPT_TILE_LDS_CASE(21, 2, 2, 2, 2, 3, 128)
+        DNNOPT_TILE_LDS_CASE(22, 2, 4, 2, 2, 2, 128)
+        DNNOPT_TILE_LDS_CASE(23, 2, 2, 2, 4, 2, 128)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

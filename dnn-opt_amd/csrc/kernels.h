@@ -173,6 +173,7 @@ inline int xcd_grid(int tn, int tm) { return 8 * ((tn + 7) / 8) * tm; }
 struct TileConfig {
     int mt, nt, wm, wn, kw;
     int depth;  // LDS-staged kernels: k-blocks loaded ahead (register ring)
+    int kblk;   // LDS-staged kernels: k per block (0 = DNNOPT_LDS_KB)
 };
 int tile_config_count();
 TileConfig tile_config(int idx);
@@ -183,6 +184,11 @@ TileConfig tile_config(int idx);
 // fp32-rounded modes only, rows of A and B 4-byte aligned, no transposed A
 // (B stored N x K with bf16 storage).
 constexpr int kTileFirstLds = 5;
+// k per LDS block of an LDS-staged configuration: its kblk (or
+// DNNOPT_LDS_KB) when both stages fit in 128 KiB of LDS, else 64.
+constexpr int tile_lds_bk(int bm, int bn, int kblk) {
+    return (bm + bn) * (kblk > 0 ? kblk : DNNOPT_LDS_KB) * 2 * 2 <= 131072 ? (kblk > 0 ? kblk : DNNOPT_LDS_KB) : 64;
+}
 // transA: fp32 only; transB: fp32, or bf16 storage with B stored N x K.
 // aligned: all k-contiguous rows (A; B stored N x K) start on 4-byte
 // boundaries (matters for bf16 storage).
