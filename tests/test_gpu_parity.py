@@ -449,3 +449,48 @@ def test_split_k_repeatable(lib, orc, dev, kind, M, N, K):
     u.assert_fp32_close(first, want, scale, K, f"split-k {kind} {M}x{N}x{K}")
     for o in outs[1:]:
         assert np.array_equal(host(o).view(np.uint32), first.view(np.uint32))
+
+
+# ---------------------------------------------------------------- shapes outside the benchmark configs
+# N == 1, tall-skinny N <= 7, K <= 16, M in 8..31 with moderate N, and mixes:
+# every entry point must route each to a kernel that gives the right result.
+EDGE = [(65536, 1, 256), (5000, 1, 3), (40000, 7, 300), (20000, 3, 16), (1000, 5, 1), (12, 700, 16), (9, 1000, 5),
+        (31, 257, 1000), (17, 64, 8192), (8, 1, 1), (24, 33, 7), (300, 2, 2049)]
+
+
+@pytest.mark.parametrize("M,N,K", EDGE)
+def test_edge_shapes_every_entry_point(lib, orc, dev, M, N, K):
+    A32 = u.uniform(orc, M * K, 1).reshape(M, K)
+    B32 = u.uniform(orc, K * N, 2).reshape(K, N)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    # fp32, every transpose combination
+    for ta in (0, 1):
+        for tb in (0, 1):
+            A = np.ascontiguousarray(A32.T) if ta else A32
+            B = np.ascontiguousarray(B32.T) if tb else B32
+            dC = dev_copy(C0, dev)
+            lib.sgemm(M, N, K, 0.5, dev_copy(A, dev), A.shape[1], dev_copy(B, dev), B.shape[1], 2.0, dC, N,
+                      transA=ta, transB=tb, stream=stream())
+            want, scale = u.exact(A32, B32, 0.5, 2.0, C0)
+            u.assert_fp32_close(host(dC), want, scale, K, f"f32 edge {M}x{N}x{K} ta={ta} tb={tb}")
+    # bf16 storage, every transpose combination
+    Ab, Bb = u.bf16_bits(orc, A32), u.bf16_bits(orc, B32)
+    want, scale = u.exact(u.bf16_value(Ab), u.bf16_value(Bb), 1.0, 1.0, C0)
+    for ta in (0, 1):
+        for tb in (0, 1):
+            A = np.ascontiguousarray(Ab.T) if ta else Ab
+            B = np.ascontiguousarray(Bb.T) if tb else Bb
+            dC = dev_copy(C0, dev)
+            lib.gemm_bf16_ex(M, N, K, 1.0, dev_copy(A.view(np.int16), dev), A.shape[1],
+                             dev_copy(B.view(np.int16), dev), B.shape[1], 1.0, dC, N, transA=ta, transB=tb,
+                             stream=stream())
+            u.assert_fp32_close(host(dC), want, scale, K, f"bf16 edge {M}x{N}x{K} ta={ta} tb={tb}")
+    # fp32 storage rounded to bf16 in registers
+    dC = dev_copy(C0, dev)
+    lib.gemm_bf16_f32in(M, N, K, 1.0, dev_copy(A32, dev), K, dev_copy(B32, dev), N, 1.0, dC, N, stream=stream())
+    u.assert_fp32_close(host(dC), want, scale, K, f"f2b edge {M}x{N}x{K}")
+    # int8, exact
+    A8, B8 = u.ints8(orc, M * K, 1).reshape(M, K), u.ints8(orc, N * K, 2).reshape(N, K)
+    dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+    lib.gemm_s8s8s32(M, N, K, dev_copy(A8, dev), K, dev_copy(B8, dev), K, dC, N, stream=stream())
+    assert np.array_equal(host(dC).astype(np.int64), A8.astype(np.int64) @ B8.T.astype(np.int64))
