@@ -167,8 +167,20 @@ __device__ __forceinline__ float epilogue(float acc, float alpha, float beta, co
 // Per-column bias added to a finished output as its own rounding (nothing
 // when bias is null): the oneDNN hook adds its bias to the completed C
 // (integration/onednn/0001-dnnopt-integration.patch:355-362).
+//
+// add_rn / mul_rn round on their own: contraction is off inside them, so the
+// compiler cannot fuse them with a product or sum computed before (a plain
+// a + b after y = alpha * acc may otherwise become one fma).
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
 __device__ __forceinline__ float add_bias(float y, const float* bias, int n) {
-    return bias ? __fadd_rn(y, bias[n]) : y;
+    return bias ? add_rn(y, bias[n]) : y;
 }
 
 // Cross-workgroup ticket: every workgroup of a split-k group calls this after

@@ -322,18 +322,25 @@ int plan_tall(int transB, int M, int N, int K, int lda, Launch* L) {
     const size_t lds = tall_lds_bytes(nt, K);
     if (lds > 65536) return DNNOPT_ERR_UNSUPPORTED;
     if (((long long)(M - 1) * lda + K) * 4 >= 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
-    // Persistent: as many 4-wave workgroups as fit (LDS-limited), no more
-    // than there are 32-row tiles for their waves.
+    // Each wave runs its row tiles as one serial chain of MFMAs, so the kernel
+    // needs about one tile for every wave of one workgroup per CU; with fewer
+    // (M below ~48K rows on 256 CUs) the register tiles, which spread the same
+    // work over more waves, are faster.
+    const long long tiles = ceil_div(M, tall_tile_rows());
+    if (tiles * 4 < 3LL * num_cus() * tall_waves()) return DNNOPT_ERR_UNSUPPORTED;
+    // Persistent: one workgroup per CU by default, no more than there are row
+    // tiles for their waves.  More row tiles per wave keep loads, MFMAs and
+    // stores of different tiles overlapped; a second workgroup per CU (more
+    // waves, one tile each) measured slower at every K.
     const long long per_cu = std::max<long long>(1, std::min<long long>(4, 160 * 1024 / (long long)lds));
-    const long long tiles = ceil_div(M, 32);
-    static const int wgs_per_cu = env_int("DNNOPT_TALL_WGS_PER_CU", 0);
-    const long long want = num_cus() * (wgs_per_cu > 0 ? std::min<long long>(wgs_per_cu, per_cu) : per_cu);
+    static const int wgs_per_cu = env_int("DNNOPT_TALL_WGS_PER_CU", 1);
+    const long long want = num_cus() * std::min<long long>(std::max(wgs_per_cu, 1), per_cu);
     const long long G = std::max<long long>(1, std::min<long long>(want, ceil_div(tiles, tall_waves())));
     L->cfg = nt;
     L->lds = lds;
     L->mode = transB;
     L->grid = dim3((unsigned)G, 1, 1);
-    fill_pub(L, DNNOPT_K_TALL_F32, "dnnopt_tall_f32", 32, 16 * nt, 1, tall_waves() * 64);
+    fill_pub(L, DNNOPT_K_TALL_F32, "dnnopt_tall_f32", tall_tile_rows(), 16 * nt, 1, tall_waves() * 64);
     return DNNOPT_OK;
 }
 

@@ -50,8 +50,8 @@ __global__ __launch_bounds__(kThreads) void dnnopt_cm_fixup(float* C, int M, int
             const int i = (int)(e - j * M);
             float* c = C + j * ldc + i;
             float v = op == kCmZero ? 0.0f : *c;
-            if (op == kCmScale) v = __fmul_rn(v, beta);
-            if (bias) v = __fadd_rn(v, bias[i]);
+            if (op == kCmScale) v = mul_rn(v, beta);
+            if (bias) v = add_rn(v, bias[i]);
             *c = v;
         }
         return;
@@ -62,9 +62,9 @@ __global__ __launch_bounds__(kThreads) void dnnopt_cm_fixup(float* C, int M, int
         covering(e, M, N, ldc, &jlo, &jhi);
         float v = op == kCmZero ? 0.0f : C[e];
         if (op == kCmScale)
-            for (long long j = jlo; j <= jhi; ++j) v = __fmul_rn(v, beta);
+            for (long long j = jlo; j <= jhi; ++j) v = mul_rn(v, beta);
         if (bias)
-            for (long long j = jlo; j <= jhi; ++j) v = __fadd_rn(v, bias[e - j * ldc]);
+            for (long long j = jlo; j <= jhi; ++j) v = add_rn(v, bias[e - j * ldc]);
         C[e] = v;
     }
 }

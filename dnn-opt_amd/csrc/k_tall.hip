@@ -41,10 +41,14 @@ namespace {
 #define DNNOPT_TALL_WAVES 8
 #endif
 #ifndef DNNOPT_TALL_D
-#define DNNOPT_TALL_D 4
+#define DNNOPT_TALL_D 2
+#endif
+#ifndef DNNOPT_TALL_RT
+#define DNNOPT_TALL_RT 2
 #endif
 constexpr int kTallWaves = DNNOPT_TALL_WAVES;
 constexpr int kTallD = DNNOPT_TALL_D;
+constexpr int kTallRT = DNNOPT_TALL_RT;
 
 __device__ __forceinline__ u32x4 keep_first(u32x4 v, int valid) {
     u32x4 r;
@@ -56,8 +60,9 @@ __device__ __forceinline__ u32x4 keep_first(u32x4 v, int valid) {
 }  // namespace
 
 // NT column tiles of 16 (N <= 16 * NT), RT row tiles of 16 per wave, D
-// chunks of A in flight, TB: B stored N x K, BETA: C is read (beta != 0).
-template <int NT, int RT, int D, int TB, int BETA>
+// chunks of A in flight, TB: B stored N x K, BETA: C is read (beta != 0),
+// KFULL: K % 16 == 0 (no partial chunk to mask).
+template <int NT, int RT, int D, int TB, int BETA, int KFULL>
 __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
     constexpr int NP = 16 * NT;
     extern __shared__ __attribute__((aligned(16))) float bsm[];
@@ -70,60 +75,91 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
     const int my_tiles = gw < tiles ? (tiles - 1 - gw) / GW + 1 : 0;
     const int total = my_tiles * KC;
 
+    // A's range ends at the last element of row M - 1, so every row >= M
+    // (a partial last tile, chunks past this wave's last tile) reads zero:
+    // row * lda + k >= M * lda >= (M - 1) * lda + K.  Offsets are split into a
+    // per-lane constant and a wave-uniform part kept in scalar registers.
     const __amdgpu_buffer_rsrc_t ra =
         make_rsrc(p.A, range31(((size_t)(p.M - 1) * p.lda + p.K) * 4));
-
-    // A chunk `i` of this wave: row tile gw + (i / KC) * GW, k = 16 * (i % KC).
-    u32x4 ring[D][RT];
-    auto load = [&](int i, int slot) {
-        const int ic = i < total ? i : total - 1;  // past the end: re-read the last chunk (unused)
-        const int ti = gw + (ic / KC) * GW, kc = ic % KC;
-        const int kq = kc * 16 + 4 * g;
+    uint32_t lane_a[RT];
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            const int row = ti * 16 * RT + rt * 16 + r;
-            const uint32_t off = (row < p.M && kq < p.K) ? ((uint32_t)row * p.lda + kq) * 4u : kOobOffset;
-            ring[slot][rt] = buf_load_x4(ra, off);
+    for (int rt = 0; rt < RT; ++rt) lane_a[rt] = ((uint32_t)(rt * 16 + r) * p.lda + 4 * g) * 4u;
+    const uint32_t tile_step = (uint32_t)(16 * RT) * (uint32_t)GW * (uint32_t)p.lda * 4u;  // next tile of this wave
+    // Load cursor: byte offset of (row tile, chunk) for the next load, and its
+    // chunk number.  Past the wave's last chunk it runs on into rows that are
+    // out of range or unused; no load faults and no such chunk is consumed.
+    uint32_t l_off = (uint32_t)gw * (uint32_t)(16 * RT) * (uint32_t)p.lda * 4u;
+    int l_kc = 0;
+
+    u32x4 ring[D][RT];
+    auto load = [&](int slot) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) ring[slot][rt] = buf_load_x4(ra, lane_a[rt] + l_off);
+        l_off += 64u;
+        if (++l_kc == KC) {
+            l_kc = 0;
+            l_off += tile_step - (uint32_t)KC * 64u;
         }
     };
     // First chunks of A go out before B is staged.
     if (total > 0) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) load(d, d);
+        for (int d = 0; d < D; ++d) load(d);
     }
 
-    // Stage B: unit u = (k quad kq, column n) -> 4 floats at bsm[(kq * NP + n) * 4].
+    // Stage B.  Both layouts have KC * 16 * NP / 4 16-byte units, at most
+    // kStageU per thread (the host caps the LDS image at 64 KiB); every
+    // thread issues all its loads before its first LDS write, so staging
+    // costs one L2 round trip rather than one per unit.
     {
-        const int KQ = KC * 4;
         const __amdgpu_buffer_rsrc_t rb = make_rsrc(
             p.B, range31((TB ? (size_t)(p.N - 1) * p.ldb + p.K : (size_t)(p.K - 1) * p.ldb + p.N) * 4));
-        for (int u = (int)threadIdx.x; u < KQ * NP; u += kTallWaves * 64) {
-            const int kq = u / NP, n = u % NP;
-            const int k0 = 4 * kq;
-            if constexpr (TB) {
-                const uint32_t off = (n < p.N && k0 < p.K) ? ((uint32_t)n * p.ldb + k0) * 4u : kOobOffset;
-                *reinterpret_cast<u32x4*>(&bsm[(size_t)u * 4]) = keep_first(buf_load_x4(rb, off), p.K - k0);
+        constexpr int kStageU = 65536 / 16 / (kTallWaves * 64);
+        const int units = KC * 4 * NP;
+        u32x4 v[kStageU];
+        if constexpr (TB) {
+            // unit u = (k quad kq, column n) -> 4 floats at bsm[(kq * NP + n) * 4]
+#pragma unroll
+            for (int j = 0; j < kStageU; ++j) {
+                const int u = (int)threadIdx.x + j * kTallWaves * 64;
+                const int kq = u / NP, n = u % NP, k0 = 4 * kq;
+                const uint32_t off = (u < units && n < p.N && k0 < p.K) ? ((uint32_t)n * p.ldb + k0) * 4u : kOobOffset;
+                v[j] = buf_load_x4(rb, off);
             }
-        }
-        if constexpr (!TB) {
-            // B stored K x N: unit = (k, 4 columns), one 16-byte load spread
-            // over the 4 column slots of quad k / 4.  Columns past N (in the
-            // last partial group, or past the padded width) are zero.
+#pragma unroll
+            for (int j = 0; j < kStageU; ++j) {
+                const int u = (int)threadIdx.x + j * kTallWaves * 64;
+                if (u < units) *reinterpret_cast<u32x4*>(&bsm[(size_t)u * 4]) = keep_first(v[j], p.K - 4 * (u / NP));
+            }
+        } else {
+            // B stored K x N: unit u = (k, 4 columns from n0), one 16-byte
+            // load spread over the 4 column slots of quad k / 4.  Columns past
+            // N (in the last partial group, or past the padded width) and rows
+            // past K are zero (out-of-range offsets read 0).
             const int NQ = NP / 4;
-            for (int u = (int)threadIdx.x; u < KQ * 4 * NQ; u += kTallWaves * 64) {
+            const bool vec = (p.ldb & 3) == 0;
+#pragma unroll
+            for (int j = 0; j < kStageU; ++j) {
+                const int u = (int)threadIdx.x + j * kTallWaves * 64;
                 const int k = u / NQ, n0 = (u % NQ) * 4;
-                u32x4 v = {0u, 0u, 0u, 0u};
-                if (k < p.K) {
-                    if (n0 + 4 <= p.N && ((p.ldb & 3) == 0)) {
-                        v = buf_load_x4(rb, ((uint32_t)k * p.ldb + n0) * 4u);
-                    } else {
+                const bool row_ok = u < units && k < p.K;
+                if (vec && n0 + 4 <= p.N) {
+                    v[j] = buf_load_x4(rb, row_ok ? ((uint32_t)k * p.ldb + n0) * 4u : kOobOffset);
+                } else {
 #pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            v[c] = n0 + c < p.N ? buf_load_x1(rb, ((uint32_t)k * p.ldb + n0 + c) * 4u) : 0u;
-                    }
+                    for (int c = 0; c < 4; ++c)
+                        v[j][c] = buf_load_x1(rb, (row_ok && n0 + c < p.N) ? ((uint32_t)k * p.ldb + n0 + c) * 4u
+                                                                            : kOobOffset);
                 }
+            }
 #pragma unroll
-                for (int c = 0; c < 4; ++c) bsm[((size_t)(k >> 2) * NP + n0 + c) * 4 + (k & 3)] = as_f32(v[c]);
+            for (int j = 0; j < kStageU; ++j) {
+                const int u = (int)threadIdx.x + j * kTallWaves * 64;
+                const int k = u / NQ, n0 = (u % NQ) * 4;
+                if (u < units) {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) bsm[((size_t)(k >> 2) * NP + n0 + c) * 4 + (k & 3)] = as_f32(v[j][c]);
+                }
             }
         }
     }
@@ -135,26 +171,42 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
     float biasv[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) biasv[nt] = (has_bias && nt * 16 + r < p.N) ? p.bias[nt * 16 + r] : 0.0f;
+    // C's range ends at the last element of row M - 1: rows >= M of a partial
+    // tile fall outside it (m * ldc + n >= M * ldc), columns >= N are masked
+    // explicitly (they may lie inside the range, in C's padding).
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.C, range31(((size_t)(p.M - 1) * p.ldc + p.N) * 4));
+    uint32_t lane_c[RT * 4];
+#pragma unroll
+    for (int q = 0; q < RT * 4; ++q)
+        lane_c[q] = ((uint32_t)((q >> 2) * 16 + 4 * g + (q & 3)) * (uint32_t)p.ldc + (uint32_t)r) * 4u;
+    bool col_ok[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) col_ok[nt] = nt * 16 + r < p.N;
 
     f32x4 acc[RT][NT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int ktail = p.K - (KC - 1) * 16;  // k of the last chunk (1..16)
+    // LDS byte offset of this lane's B fragment in chunk 0; chunk kc adds
+    // kc * 4 * NP * 16 bytes, column tile nt adds nt * 256.
+    const uint32_t lane_b = (uint32_t)(g * NP + r) * 16u;
+    // Compute cursor: chunk number and first row of the tile in progress.
+    int c_kc = 0;
+    int c_row0 = gw * 16 * RT;
 
-    auto step = [&](int i, const u32x4 (&a)[RT]) {
-        const int kc = i % KC;
-        if (kc == 0) {
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt) acc[rt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+    auto step = [&](const u32x4 (&a)[RT]) {
         u32x4 av[RT];
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) av[rt] = (kc == KC - 1 && ktail < 16) ? keep_first(a[rt], ktail - 4 * g) : a[rt];
+        for (int rt = 0; rt < RT; ++rt) {
+            if constexpr (KFULL) av[rt] = a[rt];
+            else av[rt] = c_kc == KC - 1 ? keep_first(a[rt], ktail - 4 * g) : a[rt];
+        }
+        const char* bp = reinterpret_cast<const char*>(bsm) + lane_b + (uint32_t)c_kc * (uint32_t)(NP * 64);
         u32x4 bv[NT];
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-            bv[nt] = *reinterpret_cast<const u32x4*>(&bsm[((size_t)(kc * 4 + g) * NP + nt * 16 + r) * 4]);
+        for (int nt = 0; nt < NT; ++nt) bv[nt] = *reinterpret_cast<const u32x4*>(bp + nt * 256);
 #pragma unroll
         for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -163,23 +215,28 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
                 for (int nt = 0; nt < NT; ++nt)
                     acc[rt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(as_f32(av[rt][c]), as_f32(bv[nt][c]),
                                                                       acc[rt][nt], 0, 0, 0);
-        if (kc == KC - 1) {
-            const int ti = gw + (i / KC) * GW;
+        if (c_kc == KC - 1) {
+            const uint32_t s_c = (uint32_t)c_row0 * (uint32_t)p.ldc * 4u;
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t row_off = s_c + lane_c[rt * 4 + e];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int m = ti * 16 * RT + rt * 16 + 4 * g + e;
-                        const int n = nt * 16 + r;
-                        const uint32_t off = (m < p.M && n < p.N) ? ((uint32_t)m * p.ldc + n) * 4u : kOobOffset;
+                    for (int nt = 0; nt < NT; ++nt) {
+                        const uint32_t off = col_ok[nt] ? row_off + nt * 64u : kOobOffset;
                         float v;
                         if constexpr (BETA) v = __builtin_fmaf(p.alpha, acc[rt][nt][e], p.beta * as_f32(buf_load_x1(rc, off)));
                         else v = p.alpha * acc[rt][nt][e];
-                        if (has_bias) v = __fadd_rn(v, biasv[nt]);
+                        if (has_bias) v = add_rn(v, biasv[nt]);
                         buf_store_x1(rc, off, as_u32(v));
+                        acc[rt][nt][e] = 0.0f;
                     }
+                }
+            c_kc = 0;
+            c_row0 += 16 * RT * GW;
+        } else {
+            ++c_kc;
         }
     };
 
@@ -192,8 +249,8 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
             u32x4 a[RT];
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) a[rt] = ring[d][rt];
-            load(i0 + d + D, d);
-            step(i0 + d, a);
+            load(d);
+            step(a);
         }
     }
 #pragma unroll
@@ -202,34 +259,45 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
             u32x4 a[RT];
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) a[rt] = ring[d][rt];
-            step(i0 + d, a);
+            step(a);
         }
     }
 }
 
 int tall_waves() { return kTallWaves; }
+int tall_tile_rows() { return 16 * kTallRT; }
 
-template <int BETA>
+template <int BETA, int KFULL>
 static hipError_t launch_tall_beta(int nt, int tb, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s) {
     const dim3 blk(kTallWaves * 64);
+#define DNNOPT_TALL_CASE(NT, TB)                                                                               \
+    case NT * 2 + TB:                                                                                          \
+        hipLaunchKernelGGL((dnnopt_tall_f32<NT, kTallRT, kTallD, TB, BETA, KFULL>), grid, blk, lds_bytes, s, a); \
+        break;
     switch (nt * 2 + (tb ? 1 : 0)) {
-        case 2: hipLaunchKernelGGL((dnnopt_tall_f32<1, 2, kTallD, 0, BETA>), grid, blk, lds_bytes, s, a); break;
-        case 3: hipLaunchKernelGGL((dnnopt_tall_f32<1, 2, kTallD, 1, BETA>), grid, blk, lds_bytes, s, a); break;
-        case 4: hipLaunchKernelGGL((dnnopt_tall_f32<2, 2, kTallD, 0, BETA>), grid, blk, lds_bytes, s, a); break;
-        case 5: hipLaunchKernelGGL((dnnopt_tall_f32<2, 2, kTallD, 1, BETA>), grid, blk, lds_bytes, s, a); break;
-        case 6: hipLaunchKernelGGL((dnnopt_tall_f32<3, 2, kTallD, 0, BETA>), grid, blk, lds_bytes, s, a); break;
-        case 7: hipLaunchKernelGGL((dnnopt_tall_f32<3, 2, kTallD, 1, BETA>), grid, blk, lds_bytes, s, a); break;
-        case 8: hipLaunchKernelGGL((dnnopt_tall_f32<4, 2, kTallD, 0, BETA>), grid, blk, lds_bytes, s, a); break;
-        case 9: hipLaunchKernelGGL((dnnopt_tall_f32<4, 2, kTallD, 1, BETA>), grid, blk, lds_bytes, s, a); break;
+        DNNOPT_TALL_CASE(1, 0)
+        DNNOPT_TALL_CASE(1, 1)
+        DNNOPT_TALL_CASE(2, 0)
+        DNNOPT_TALL_CASE(2, 1)
+        DNNOPT_TALL_CASE(3, 0)
+        DNNOPT_TALL_CASE(3, 1)
+        DNNOPT_TALL_CASE(4, 0)
+        DNNOPT_TALL_CASE(4, 1)
         default: return hipErrorInvalidValue;
     }
+#undef DNNOPT_TALL_CASE
     return hipGetLastError();
 }
 
 hipError_t launch_tall_f32(int nt, int tb, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s) {
-    if (lds_bytes > 65536) return hipErrorInvalidValue;
-    return a.beta == 0.0f ? launch_tall_beta<0>(nt, tb, grid, lds_bytes, a, s)
-                          : launch_tall_beta<1>(nt, tb, grid, lds_bytes, a, s);
+    // The kernel stages all of B: the image must fit the 64 KiB its staging
+    // loop is sized for, and the launch must provide it.
+    const size_t need = tall_lds_bytes(nt, a.K);
+    if (need > 65536 || lds_bytes < need) return hipErrorInvalidValue;
+    const bool kfull = a.K % 16 == 0;
+    if (a.beta == 0.0f)
+        return kfull ? launch_tall_beta<0, 1>(nt, tb, grid, lds_bytes, a, s) : launch_tall_beta<0, 0>(nt, tb, grid, lds_bytes, a, s);
+    return kfull ? launch_tall_beta<1, 1>(nt, tb, grid, lds_bytes, a, s) : launch_tall_beta<1, 0>(nt, tb, grid, lds_bytes, a, s);
 }
 
 }  // namespace dnnopt_hip

@@ -698,7 +698,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
             }
             if (p.bias) {
 #pragma unroll
-                for (int k = 0; k < 4; ++k) out[k] = __fadd_rn(out[k], p.bias[n + k]);
+                for (int k = 0; k < 4; ++k) out[k] = add_rn(out[k], p.bias[n + k]);
             }
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, out), rc, off, 0, 0);
         } else {

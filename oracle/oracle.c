@@ -398,7 +398,23 @@ static void row_major(int ta, int tb, int M, int N, int K, float alpha, const fl
         B = bt;
         ldb = N;
     }
-    orc_gemm_naive_f32(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+    if (beta != 0.0f) {
+        orc_gemm_naive_f32(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+    } else {
+        /* beta == 0: the production kernels store alpha*acc and never read C
+         * (gemm_tiny_fp32.cpp:200-207, gemm_smallm_wide_fp32.cpp:47-59), so
+         * C may hold NaN or, for the oneDNN hook's small-ldc temporary,
+         * uninitialised memory.  Same k order as the naive loops. */
+        for (int i = 0; i < M; ++i)
+            for (int j = 0; j < N; ++j) {
+                float acc = 0.0f;
+                for (int k = 0; k < K; ++k) {
+                    const float p = A[(size_t)i * lda + k] * B[(size_t)k * ldb + j];
+                    acc = acc + p;
+                }
+                C[(size_t)i * ldc + j] = alpha * acc;
+            }
+    }
     free(at);
     free(bt);
 }

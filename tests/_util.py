@@ -170,6 +170,16 @@ def fp32_tol(K, scale):
     return (2 * K + 4) * U * scale + 1e-30
 
 
+def assert_bits_equal(got, want, what=""):
+    """Exact equality (NaNs compared by bit pattern); on failure name the
+    mismatching positions so a wrong address pattern is visible."""
+    g, w = np.asarray(got, np.float32).reshape(-1), np.asarray(want, np.float32).reshape(-1)
+    bad = np.nonzero(g.view(np.uint32) != w.view(np.uint32))[0]
+    if bad.size:
+        show = ", ".join(f"[{i}] got {g[i]!r} want {w[i]!r}" for i in bad[:12])
+        raise AssertionError(f"{what}: {bad.size} of {g.size} differ: {show}")
+
+
 def assert_fp32_close(got, want, scale, K, what=""):
     got = np.asarray(got, np.float64)
     tol = fp32_tol(K, scale)

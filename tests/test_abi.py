@@ -128,13 +128,14 @@ def test_plans_for_tall_skinny(lib):
     """Large M with N <= 64 and B small enough for LDS: the B-resident kernel;
     B too large for LDS or transposed A: the MFMA tiles."""
     b = u.binding()
-    for M, N, K in ((65536, 17, 256), (65536, 64, 256), (4096, 20, 512), (100000, 33, 300), (8192, 48, 333)):
+    for M, N, K in ((65536, 17, 256), (65536, 64, 256), (49153, 20, 512), (100000, 33, 300), (262144, 48, 333)):
         p = lib.plan_sgemm(M, N, K)
         assert p["kernel"] == b.K_TALL_F32 and p["cols"] >= N, p
         assert p["grid_x"] * 4 * 32 >= min(M, p["grid_x"] * 4 * 32)
     assert lib.plan_sgemm(65536, 64, 257)["kernel"] == b.K_TILE_F32   # 272 x 64 x 4 bytes > 64 KiB
     assert lib.plan_sgemm(65536, 64, 256, transA=1)["kernel"] == b.K_TILE_F32
     assert lib.plan_sgemm(1000, 64, 256)["kernel"] == b.K_TILE_F32    # too few rows
+    assert lib.plan_sgemm(32768, 64, 256)["kernel"] == b.K_TILE_F32   # fewer row tiles than waves
     assert lib.plan_sgemm(65536, 65, 64)["kernel"] == b.K_TILE_F32
     assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TILE_F32   # N <= 16: register tiles
 

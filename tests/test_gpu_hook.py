@@ -178,6 +178,36 @@ def test_hook_device(lib, orc, dev, M, N, K, ta, tb, bf16):
         assert (got.reshape(N, ldc)[:, M:] == -777.0).all(), "padding rows of C written"
 
 
+# (hook M, N, K, transa): the library's row-major problem is N x M, so these
+# reach, in order, the skinny kernel, the row-dot kernel, a tile, the tall
+# kernel (K % 16 == 0 and not), a tile with k-splits and the skinny kernel
+# with k-splits.
+BIAS_ROUNDING = [(1009, 3, 70, "N"), (1009, 5, 70, "T"), (300, 100, 64, "N"), (48, 8192, 64, "N"),
+                 (40, 5000, 70, "N"), (64, 16, 65536, "N"), (7, 2, 200000, "N")]
+
+
+@pytest.mark.parametrize("M,N,K,ta", BIAS_ROUNDING)
+def test_hook_bias_rounds_separately(lib, orc, dev, M, N, K, ta):
+    """beta == 0 with a bias: C = round(round(alpha * acc) + bias), the bias
+    added to the finished product as its own rounding (the reference adds it
+    after the GEMM).  Integer operands keep acc exact, alpha = 1/3 makes
+    alpha * acc inexact, so a fused alpha * acc + bias differs in some
+    elements and the comparison is bit for bit."""
+    opA = u.small_ints(orc, M * K, 1).reshape(M, K)
+    opB = u.small_ints(orc, K * N, 2).reshape(K, N)
+    A, lda, B, ldb = u.hook_operands(opA, opB, ta, "N")
+    bias = u.uniform(orc, M, 4, -100.0, 100.0)
+    alpha = np.float32(1.0 / 3.0)
+    acc = (opA.astype(np.int64) @ opB.astype(np.int64)).astype(np.float32)  # |acc| < 2^24: exact
+    want = (alpha * acc) + bias[:, None]  # float32 ops, each rounded
+    fused = ((np.float64(alpha) * acc.astype(np.float64)) + bias[:, None].astype(np.float64)).astype(np.float32)
+    assert (fused != want).any(), "inputs do not separate fused from unfused rounding"
+    dC = dev_copy(np.full(M * N, np.nan, np.float32), dev)
+    lib.ext_sgemm(ta, "N", M, N, K, float(alpha), dev_copy(A, dev), lda, dev_copy(B, dev), ldb, 0.0, dC, M,
+                  bias=dev_copy(bias, dev), stream=stream())
+    u.assert_bits_equal(u.cm_load(host(dC), M, N, M), want, f"bias rounding {M}x{N}x{K} {ta}")
+
+
 @pytest.mark.parametrize("ldc_delta", [2, 0, -3])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_hook_k_zero_bitwise(lib, orc, dev, ldc_delta, with_bias):
@@ -234,7 +264,7 @@ def test_hook_overlapping_columns(lib, orc, dev, ta, tb, beta, with_bias, bf16):
     else:
         lib.ext_sgemm(ta, tb, M, N, K, 1.0, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, beta, dC, ldc,
                       bias=None if bias is None else dev_copy(bias, dev), stream=stream())
-    assert np.array_equal(host(dC), want)
+    u.assert_bits_equal(host(dC), want, f"overlap ldc={ldc} bf16={bf16} beta={beta} bias={with_bias} {ta}{tb}")
 
 
 # ---------------------------------------------------------------- the hook's own argument list (host memory)

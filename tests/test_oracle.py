@@ -296,6 +296,33 @@ def test_cblas_oracle_semantics(orc, order, ta, tb):
     u.assert_fp32_close(got, want, scale, K, f"cblas {order} {ta} {tb}")
 
 
+def test_beta_zero_leaves_c_unread(orc):
+    """beta == 0: the reference's kernels store alpha*acc without reading C, so
+    NaN/Inf in C must not reach the result, and alpha*0 keeps its sign (-0.0),
+    which a zero-fill-then-add restatement would turn into +0.0."""
+    M, N, K = 5, 6, 9
+    opA = u.small_ints(orc, M * K, 1).reshape(M, K)
+    opA[2, :] = 0.0  # row 2 of the product is exactly zero
+    opB = u.small_ints(orc, K * N, 2).reshape(K, N)
+    want = (-1.0 * (opA.astype(np.float64) @ opB)).astype(np.float32)
+    assert np.signbit(want[2]).all()
+    poison = np.tile(np.array([np.nan, np.inf, -np.inf], np.float32), M * N)[: M * N]
+    # row-major cblas
+    C = poison.reshape(M, N).copy()
+    orc.orc_cblas_sgemm(101, 111, 111, M, N, K, -1.0, u.ptr(_f(opA)), K, u.ptr(_f(opB)), N, 0.0, u.ptr(C), N)
+    u.assert_bits_equal(C, want, "cblas beta=0")
+    # oneDNN hook, column-major, ldc >= M and ldc < M (the small-ldc temporary)
+    A, lda, B, ldb = u.hook_operands(opA, opB, "N", "N")
+    C = poison.copy()
+    assert _hook(orc, "N", "N", M, N, K, -1.0, A, lda, B, ldb, 0.0, C, M, None) == 0
+    u.assert_bits_equal(u.cm_load(C, M, N, M), want, "hook beta=0")
+    ldc = 3
+    C = np.full((N - 1) * ldc + M, np.nan, np.float32)
+    assert _hook(orc, "N", "N", M, N, K, -1.0, A, lda, B, ldb, 0.0, C, ldc, None) == 0
+    C0 = np.zeros_like(C)
+    u.assert_bits_equal(C, _overlap_closed_form(opA, opB, C0, M, N, ldc, -1.0, 0.0, None), "hook beta=0 ldc<M")
+
+
 def test_cblas_early_exits(orc):
     C = _f([1, 2, 3, 4])
     A = B = np.full(4, np.nan, np.float32)
@@ -379,7 +406,9 @@ def _overlap_closed_form(opA, opB, C0flat, M, N, ldc, alpha, beta, bias):
     order, then bias added column by column in order."""
     flat = C0flat.astype(np.float64).copy()
     G = np.stack([flat[r * ldc: r * ldc + M] for r in range(N)])
-    R = alpha * (opB.T.astype(np.float64) @ opA.T) + (beta * G if beta != 0.0 else 0.0)
+    R = alpha * (opB.T.astype(np.float64) @ opA.T)
+    if beta != 0.0:  # beta == 0: C unread, and alpha * 0 keeps its sign
+        R = R + beta * G
     for r in range(N):
         flat[r * ldc: r * ldc + M] = R[r]
     if bias is not None:
