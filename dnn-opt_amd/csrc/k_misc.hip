@@ -126,24 +126,23 @@ __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restr
     const int s_lo = (int)((long long)splits * q / Q), s_hi = (int)((long long)splits * (q + 1) / Q);
     f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
     if (live && s_lo < s_hi) {
-        const f4* src = reinterpret_cast<const f4*>(part) + idx;
-        const size_t stride = (size_t)tiles * per_tile;
-        s = src[(size_t)s_lo * stride];
-        int sp = s_lo + 1;
-        for (; sp + 8 <= s_hi; sp += 8) {
-            f4 v[8];
+        // One batch of unconditional 16-byte loads per kSplitBatch splits
+        // (offsets past s_hi are out of range and read zero), then the adds
+        // in ascending split order, predicated on the range.
+        constexpr int kSplitBatch = 16;
+        const uint32_t stride = (uint32_t)tiles * (uint32_t)per_tile * 16u;
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, range31((size_t)splits * tiles * per_tile * 16));
+        const uint32_t base = (uint32_t)idx * 16u;
+        for (int sp0 = s_lo; sp0 < s_hi; sp0 += kSplitBatch) {
+            f4 v[kSplitBatch];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(sp + u) * stride];
+            for (int u = 0; u < kSplitBatch; ++u)
+                v[u] = __builtin_bit_cast(f4, buf_load_x4(rp, sp0 + u < s_hi ? base + (uint32_t)(sp0 + u) * stride : kOobOffset));
 #pragma unroll
-            for (int u = 0; u < 8; ++u) s += v[u];
+            for (int u = 0; u < kSplitBatch; ++u) {
+                if (sp0 + u < s_hi) s = sp0 + u == s_lo ? v[u] : s + v[u];
+            }
         }
-        f4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (sp + u < s_hi) v[u] = src[(size_t)(sp + u) * stride];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (sp + u < s_hi) s += v[u];
     }
     if constexpr (Q > 1) {
         red[q * OUTS + o] = s;
@@ -164,6 +163,8 @@ hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int 
                                 int N, float alpha, float beta, float* C, int ldc, const float* bias,
                                 hipStream_t s) {
     const long long quads = (long long)tiles_n * tiles_m * bm * bn / 4;
+    // The kernel addresses the partials with 32-bit buffer offsets.
+    if (splits < 1 || (long long)splits * quads * 16 > 0x7FFFFFFFll) return hipErrorInvalidValue;
     if (splits <= 16) {
         hipLaunchKernelGGL(dnnopt_splitk_reduce<1>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, part,
                            splits, tiles_n, tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc, bias);
@@ -176,8 +177,13 @@ hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int 
 
 // Sum the k-split partials of the skinny kernel, [split][M][ncols_pad], in
 // ascending split order and apply the reference epilogue.  Column tile t of T
-// (width tw) has splits_of_tile(t, G, T) partials.  All loads of an output
-// are issued before the first add.
+// (width tw, a multiple of the 256-thread block) has splits_of_tile(t, G, T)
+// partials.  The loads of a batch of kRedBatch partials (all of them for up
+// to kRedBatch splits) are issued unconditionally -- offsets past the tile's
+// splits are out of range and read zero -- before the first add, so the
+// reduction costs one memory round trip; the adds are predicated on the
+// split count, so the sum is exactly the ordered sum of the real partials.
+constexpr int kRedBatch = 32;
 __global__ __launch_bounds__(256) void dnnopt_skinny_reduce(const float* __restrict__ part, int G, int T, int tw,
                                                            int M, int N, int ncols_pad, float alpha, float beta,
                                                            float* C, int ldc, const float* bias) {
@@ -185,27 +191,24 @@ __global__ __launch_bounds__(256) void dnnopt_skinny_reduce(const float* __restr
     const int m = blockIdx.y;
     if (n >= N) return;
     const int splits = splits_of_tile(n / tw, G, T);
-    const float* src = part + (size_t)m * ncols_pad + n;
-    const size_t stride = (size_t)M * ncols_pad;
+    const int max_splits = G / T + (G % T ? 1 : 0);
+    const uint32_t stride = (uint32_t)M * (uint32_t)ncols_pad * 4u;  // bytes between splits
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, range31((size_t)max_splits * M * ncols_pad * 4));
+    const uint32_t base = ((uint32_t)m * (uint32_t)ncols_pad + (uint32_t)n) * 4u;
     float* c = C + (size_t)m * ldc + n;
     // C is requested together with the partials (one memory round trip).
     const float c_old = beta != 0.0f ? *c : 0.0f;
-    float s = src[0];
-    int sp = 1;
-    for (; sp + 16 <= splits; sp += 16) {
-        float v[16];
+    float s = 0.0f;
+    for (int sp0 = 0; sp0 < splits; sp0 += kRedBatch) {
+        float v[kRedBatch];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = src[(size_t)(sp + u) * stride];
+        for (int u = 0; u < kRedBatch; ++u)
+            v[u] = as_f32(buf_load_x1(rp, sp0 + u < splits ? base + (uint32_t)(sp0 + u) * stride : kOobOffset));
 #pragma unroll
-        for (int u = 0; u < 16; ++u) s += v[u];
+        for (int u = 0; u < kRedBatch; ++u) {
+            if (sp0 + u < splits) s = sp0 + u == 0 ? v[u] : s + v[u];
+        }
     }
-    float v[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-        if (sp + u < splits) v[u] = src[(size_t)(sp + u) * stride];
-#pragma unroll
-    for (int u = 0; u < 16; ++u)
-        if (sp + u < splits) s += v[u];
     *c = add_bias(beta == 0.0f ? alpha * s : __builtin_fmaf(alpha, s, beta * c_old), bias, n);
 }
 
@@ -235,6 +238,9 @@ __global__ __launch_bounds__(256) void dnnopt_s8_reduce(const int32_t* __restric
 
 hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, int N, int ncols_pad,
                                 float alpha, float beta, float* C, int ldc, const float* bias, hipStream_t s) {
+    // The kernel addresses the partials with 32-bit buffer offsets.
+    if (G < 1 || T < 1 || (long long)(G / T + (G % T ? 1 : 0)) * M * ncols_pad * 4 > 0x7FFFFFFFll)
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(dnnopt_skinny_reduce, dim3((N + 255) / 256, M), dim3(256), 0, s, part, G, T, tw, M, N,
                        ncols_pad, alpha, beta, C, ldc, bias);
     return hipGetLastError();
