@@ -30,7 +30,7 @@
 //     leave more than half of the CUs idle.
 // Tunables (environment, read once, for sweeps):
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
-//   DNNOPT_SKINNY_WGS_PER_CU (default 2), DNNOPT_SKINNY_WGS (force G),
+//   DNNOPT_SKINNY_WGS_PER_CU (default 1), DNNOPT_SKINNY_WGS (force G),
 //   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel),
 //   DNNOPT_TILE_SPLITS (force the k-splits of a tile launch), DNNOPT_TILE_CFG
 //   (force an LDS-staged bf16 tile configuration, index 5 and up),
@@ -67,7 +67,7 @@ int skinny_nw() {
     return v;
 }
 int skinny_wgs_per_cu() {
-    static int v = env_int("DNNOPT_SKINNY_WGS_PER_CU", 2);
+    static int v = env_int("DNNOPT_SKINNY_WGS_PER_CU", 1);
     return v;
 }
 int max_splits() {

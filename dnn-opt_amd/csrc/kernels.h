@@ -68,7 +68,7 @@ struct RowdotArgs {
     const float* bias;  // per-column bias added after the epilogue (or null)
 };
 constexpr int kRowdotWaves = 8;
-constexpr int rowdot_rows(int mr) { return mr <= 4 ? 4 : 2; }
+constexpr int rowdot_rows(int mr) { return mr <= 2 ? 8 : (mr <= 4 ? 4 : 2); }
 // mode 0 fp32, 1 bf16 storage; kw in {1, 2, 4, 8}; aligned: every row of A
 // and B starts on a 4-byte boundary (bf16).  grid.x = workgroups, each
 // covering (kRowdotWaves / kw) * rowdot_rows(M) rows of B.
