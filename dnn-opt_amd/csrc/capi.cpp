@@ -303,11 +303,26 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
     const int aligned = ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) == 0 &&
                         (lda & 3) == 0 && (ldb & 3) == 0;
     Launch L;
-    int st = plan_s8(epi, M, N, K, &L, aligned != 0);
+    int st = plan_s8(epi, M, N, K, &L, aligned != 0, lda, ldb);
     if (st != DNNOPT_OK) return st;
+    hipStream_t s = as_stream(stream);
+    if (L.family == DNNOPT_K_ROWDOT_S8) {
+        RowdotArgs r{};
+        r.A = A;
+        r.B = B;
+        r.C = epi ? static_cast<float*>(C) : nullptr;
+        r.Ci = epi ? nullptr : static_cast<int32_t*>(C);
+        r.scale = scale;
+        r.lda = lda;
+        r.ldb = ldb;
+        r.ldc = ldc;
+        r.M = M;
+        r.N = N;
+        r.K = K;
+        return finish_launch(launch_rowdot(L.mode, L.mr, L.nw, aligned, L.grid, r, s));
+    }
     if ((long long)L.bm * lda + K >= 0x7FFFFFFFll || (long long)L.bn * ldb + K >= 0x7FFFFFFFll)
         return DNNOPT_ERR_UNSUPPORTED;
-    hipStream_t s = as_stream(stream);
     S8Args a{};
     a.A = A;
     a.B = B;

@@ -239,9 +239,20 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     return DNNOPT_OK;
 }
 
-int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok) {
+int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int ldb) {
     *L = Launch{};
     static const int forced_cfg = env_int("DNNOPT_S8_CFG", -1);
+    // M <= 4 (B is stored N x K): the row-dot kernel streams every row of B
+    // once in 1 KiB steps with exact int32 dot products and needs no partial
+    // sums; DNNOPT_S8_ROWDOT=0 keeps the MFMA tiles.
+    static const bool rowdot_ok = [] {
+        const char* e = getenv("DNNOPT_S8_ROWDOT");
+        return !(e && *e && atoi(e) == 0);
+    }();
+    if (M <= kRowdotS8MaxM && rowdot_ok && forced_cfg < 0 &&
+        plan_rowdot(2 + (epi ? 1 : 0), M, N, K, lda > 0 ? lda : K, ldb > 0 ? ldb : K, L) == DNNOPT_OK)
+        return DNNOPT_OK;
+    *L = Launch{};
     static const int forced_splits = env_int("DNNOPT_S8_SPLITS", 0);
     // M <= 16: 16 x 16 tiles with k split over the 8 waves of a workgroup
     // (one launch, no partial sums); larger M: 32 x 32 tiles through LDS with
@@ -290,7 +301,7 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok) {
 int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
     if (M < 1 || M > 8) return DNNOPT_ERR_UNSUPPORTED;
     *L = Launch{};
-    const long long es = mode ? 2 : 4, R = rowdot_rows(M);
+    const long long es = mode >= 2 ? 1 : (mode ? 2 : 4), R = rowdot_rows(mode, M);
     // Buffer offsets are 32-bit from the first row of a wave (B) and of A.
     if ((R * ldb + K) * es >= 0x7FFFFFFFll || ((long long)(M - 1) * lda + K) * es >= 0x7FFFFFFFll)
         return DNNOPT_ERR_UNSUPPORTED;
@@ -308,8 +319,8 @@ int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
     L->mr = M;
     L->nw = kw;
     L->grid = dim3((unsigned)G, 1, 1);
-    fill_pub(L, mode ? DNNOPT_K_ROWDOT_BF16 : DNNOPT_K_ROWDOT_F32, "dnnopt_rowdot", M, (int)rows_per_wg, 1,
-             kRowdotWaves * 64);
+    fill_pub(L, mode >= 2 ? DNNOPT_K_ROWDOT_S8 : (mode ? DNNOPT_K_ROWDOT_BF16 : DNNOPT_K_ROWDOT_F32), "dnnopt_rowdot", M,
+             (int)rows_per_wg, 1, kRowdotWaves * 64);
     return DNNOPT_OK;
 }
 

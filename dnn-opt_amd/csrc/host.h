@@ -55,7 +55,8 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
               bool lds_ok = true);
 // lds_ok = false keeps int8 GEMMs off the LDS-staged kernel (rows of A or B
 // not on 4-byte boundaries).
-int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok = true);
+// lda, ldb: row strides of A and B (0 = packed, K).
+int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok = true, int lda = 0, int ldb = 0);
 
 // fp32 GEMM of dnnopt_hip_sgemm with an optional per-column bias added to
 // each finished output (one more rounding): C = epilogue + bias[n].

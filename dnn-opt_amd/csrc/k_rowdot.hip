@@ -22,6 +22,15 @@
 // Tails: elements past the end of a row (of A and of B) are masked in the
 // only loop step that can hold them (the last); rows past N read as zero
 // (out-of-range buffer offsets) and are not stored.
+//
+// int8 (MODE 2: int32 C, MODE 3: fp32 C = (float)acc * scale[n], the
+// reference's s8s8s32 and column-scaled paths for M <= 4 with B stored
+// N x K, src/gemm/gemm_int8_native.cpp): 16 int8 per chunk, exact int32
+// accumulation with v_dot4_i32_i8 (four products per instruction, wrapping
+// like the int32 accumulators of the MFMA path), the lanes and waves combined
+// with integer adds.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -38,6 +47,13 @@ __device__ __forceinline__ uint32_t rec_bytes(size_t bytes) {
     bytes = (bytes + 3) & ~(size_t)3;
     return bytes > 0x7FFFFFFFull ? 0x7FFFFFFFu : (uint32_t)bytes;
 }
+
+// Element size and accumulator type per mode: 0 fp32, 1 bf16, 2 / 3 int8.
+template <int MODE>
+struct RowdotMode {
+    static constexpr int ES = MODE >= 2 ? 1 : (MODE ? 2 : 4);
+    using Acc = std::conditional_t<(MODE >= 2), int32_t, float>;
+};
 
 // Values of one 16-byte chunk as fp32: 4 floats, or 8 bf16 (MODE 1).
 template <int MODE>
@@ -58,7 +74,13 @@ __device__ __forceinline__ void widen(const u32x4& v, float (&out)[MODE ? 8 : 4]
 template <int MODE>
 __device__ __forceinline__ u32x4 keep_elems(u32x4 v, int valid) {
     u32x4 r;
-    if constexpr (MODE == 0) {
+    if constexpr (MODE >= 2) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const int keep = valid - 4 * d;
+            r[d] = keep >= 4 ? v[d] : (keep <= 0 ? 0u : (v[d] & ((1u << (8 * keep)) - 1u)));
+        }
+    } else if constexpr (MODE == 0) {
 #pragma unroll
         for (int d = 0; d < 4; ++d) r[d] = d < valid ? v[d] : 0u;
     } else {
@@ -82,10 +104,11 @@ __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) 
 // 4-byte boundaries.
 template <int MR, int R, int KW, int MODE, int AL>
 __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
-    constexpr int ES = MODE ? 2 : 4;
+    constexpr int ES = RowdotMode<MODE>::ES;
+    using Acc = typename RowdotMode<MODE>::Acc;
     constexpr int VEC = 16 / ES;  // elements per chunk
     constexpr int RG = kWaves / KW;
-    __shared__ float red[kWaves][MR * R];
+    __shared__ Acc red[kWaves][MR * R];
 
     const int lane = lane_id(), w = wave_id();
     const int wr = w / KW, kw = w % KW;
@@ -116,24 +139,34 @@ __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) a_row[m] = (uint32_t)m * p.lda * ES + alo;
 
-    float acc[MR][R];
+    Acc acc[MR][R];
 #pragma unroll
     for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+        for (int r = 0; r < R; ++r) acc[m][r] = Acc(0);
 
     auto step = [&](const u32x4 (&bv)[R], const u32x4 (&av)[MR]) {
-        float b[R][VEC];
+        if constexpr (MODE >= 2) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) widen<MODE>(bv[r], b[r]);
+            for (int m = 0; m < MR; ++m)
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            float a[VEC];
-            widen<MODE>(av[m], a);
+                for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int r = 0; r < R; ++r)
+                    for (int d = 0; d < 4; ++d)
+                        acc[m][r] = __builtin_amdgcn_sdot4((int)av[m][d], (int)bv[r][d], acc[m][r], false);
+        } else {
+            float b[R][VEC];
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) acc[m][r] = __builtin_fmaf(a[e], b[r][e], acc[m][r]);
+            for (int r = 0; r < R; ++r) widen<MODE>(bv[r], b[r]);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                float a[VEC];
+                widen<MODE>(av[m], a);
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) acc[m][r] = __builtin_fmaf(a[e], b[r][e], acc[m][r]);
+            }
         }
     };
 
@@ -178,7 +211,7 @@ __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
     for (int m = 0; m < MR; ++m)
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            float v = acc[m][r];
+            Acc v = acc[m][r];
 #pragma unroll
             for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s, 64);
             acc[m][r] = v;
@@ -197,7 +230,7 @@ __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
     if (lane >= MR * R) return;
     const int m = lane / R, r = lane % R;
     if (r >= nrows) return;
-    float v = 0.0f;
+    Acc v = Acc(0);
     if constexpr (KW > 1) {
 #pragma unroll
         for (int q = 0; q < KW; ++q) v += red[w + q][lane];
@@ -208,8 +241,14 @@ __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
             for (int rr = 0; rr < R; ++rr)
                 if (mm * R + rr == lane) v = acc[mm][rr];
     }
-    float* c = p.C + (size_t)m * p.ldc + n0 + r;
-    *c = add_bias(epilogue(v, p.alpha, p.beta, c), p.bias, n0 + r);
+    if constexpr (MODE == 2) {
+        p.Ci[(size_t)m * p.ldc + n0 + r] = v;
+    } else if constexpr (MODE == 3) {
+        p.C[(size_t)m * p.ldc + n0 + r] = mul_rn((float)v, p.scale[n0 + r]);
+    } else {
+        float* c = p.C + (size_t)m * p.ldc + n0 + r;
+        *c = add_bias(epilogue(v, p.alpha, p.beta, c), p.bias, n0 + r);
+    }
 }
 
 }  // namespace
@@ -225,24 +264,42 @@ __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
 
 template <int MODE, int AL>
 static hipError_t launch_rowdot_mode(int mr, int kw, dim3 grid, const RowdotArgs& a, hipStream_t s) {
+    // int8 modes are built for M <= kRowdotS8MaxM only.
+    if (MODE >= 2 && mr > kRowdotS8MaxM) return hipErrorInvalidValue;
     switch (mr) {
-        case 1: DNNOPT_ROWDOT_KW(1, rowdot_rows(1), MODE, AL) break;
-        case 2: DNNOPT_ROWDOT_KW(2, rowdot_rows(2), MODE, AL) break;
-        case 3: DNNOPT_ROWDOT_KW(3, rowdot_rows(3), MODE, AL) break;
-        case 4: DNNOPT_ROWDOT_KW(4, rowdot_rows(4), MODE, AL) break;
-        case 5: DNNOPT_ROWDOT_KW(5, rowdot_rows(5), MODE, AL) break;
-        case 6: DNNOPT_ROWDOT_KW(6, rowdot_rows(6), MODE, AL) break;
-        case 7: DNNOPT_ROWDOT_KW(7, rowdot_rows(7), MODE, AL) break;
-        case 8: DNNOPT_ROWDOT_KW(8, rowdot_rows(8), MODE, AL) break;
-        default: return hipErrorInvalidValue;
+        case 1: DNNOPT_ROWDOT_KW(1, rowdot_rows(MODE, 1), MODE, AL) break;
+        case 2: DNNOPT_ROWDOT_KW(2, rowdot_rows(MODE, 2), MODE, AL) break;
+        case 3: DNNOPT_ROWDOT_KW(3, rowdot_rows(MODE, 3), MODE, AL) break;
+        case 4: DNNOPT_ROWDOT_KW(4, rowdot_rows(MODE, 4), MODE, AL) break;
+        default:
+            if constexpr (MODE < 2) {
+                switch (mr) {
+                    case 5: DNNOPT_ROWDOT_KW(5, rowdot_rows(MODE, 5), MODE, AL) break;
+                    case 6: DNNOPT_ROWDOT_KW(6, rowdot_rows(MODE, 6), MODE, AL) break;
+                    case 7: DNNOPT_ROWDOT_KW(7, rowdot_rows(MODE, 7), MODE, AL) break;
+                    case 8: DNNOPT_ROWDOT_KW(8, rowdot_rows(MODE, 8), MODE, AL) break;
+                    default: return hipErrorInvalidValue;
+                }
+            } else {
+                return hipErrorInvalidValue;
+            }
     }
     return hipGetLastError();
 }
 
 hipError_t launch_rowdot(int mode, int mr, int kw, int aligned, dim3 grid, const RowdotArgs& a, hipStream_t s) {
     if (mr < 1 || mr > 8 || mr != a.M) return hipErrorInvalidValue;
-    if (mode == 0) return launch_rowdot_mode<0, 1>(mr, kw, grid, a, s);
-    return aligned ? launch_rowdot_mode<1, 1>(mr, kw, grid, a, s) : launch_rowdot_mode<1, 0>(mr, kw, grid, a, s);
+    switch (mode) {
+        case 0: return launch_rowdot_mode<0, 1>(mr, kw, grid, a, s);
+        case 1: return aligned ? launch_rowdot_mode<1, 1>(mr, kw, grid, a, s) : launch_rowdot_mode<1, 0>(mr, kw, grid, a, s);
+        case 2:
+            if (!a.Ci) return hipErrorInvalidValue;
+            return aligned ? launch_rowdot_mode<2, 1>(mr, kw, grid, a, s) : launch_rowdot_mode<2, 0>(mr, kw, grid, a, s);
+        case 3:
+            if (!a.C || !a.scale) return hipErrorInvalidValue;
+            return aligned ? launch_rowdot_mode<3, 1>(mr, kw, grid, a, s) : launch_rowdot_mode<3, 0>(mr, kw, grid, a, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace dnnopt_hip

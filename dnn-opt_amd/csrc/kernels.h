@@ -61,16 +61,27 @@ hipError_t launch_skinny(int mode, int mr, int nw, int b_aligned, int a_layout, 
 struct RowdotArgs {
     const void* A;
     const void* B;
-    float* C;
+    float* C;           // fp32 output (modes 0, 1, 3)
     int lda, ldb, ldc;
     int M, N, K;
     float alpha, beta;
     const float* bias;  // per-column bias added after the epilogue (or null)
+    int32_t* Ci;        // int32 output (mode 2)
+    const float* scale; // per-column scale of mode 3
 };
 constexpr int kRowdotWaves = 8;
 constexpr int rowdot_rows(int mr) { return mr <= 2 ? 8 : (mr <= 4 ? 4 : 2); }
-// mode 0 fp32, 1 bf16 storage; kw in {1, 2, 4, 8}; aligned: every row of A
-// and B starts on a 4-byte boundary (bf16).  grid.x = workgroups, each
+// Rows of B per wave for a mode (0 fp32, 1 bf16, 2 / 3 int8).  An int8 row
+// of B is a quarter of an fp32 one, so more waves with 2 rows each keep more
+// of it in flight (measured at K = 4096: 1 / 2 / 4 rows per wave 5.9 / 5.5
+// / 6.3 us at M = 1).
+constexpr int rowdot_rows(int mode, int mr) { return mode >= 2 ? 2 : rowdot_rows(mr); }
+// The int8 modes serve M <= kRowdotS8MaxM (beyond it the MFMA tiles are
+// faster: M = 5 ties, M = 8 is 1.2 us slower on the row-dot kernel).
+constexpr int kRowdotS8MaxM = 4;
+// mode 0 fp32, 1 bf16 storage, 2 int8 -> int32 C, 3 int8 -> fp32 C scaled
+// per column; kw in {1, 2, 4, 8}; aligned: every row of A and B starts on a
+// 4-byte boundary (bf16, int8).  grid.x = workgroups, each
 // covering (kRowdotWaves / kw) * rowdot_rows(M) rows of B.
 hipError_t launch_rowdot(int mode, int mr, int kw, int aligned, dim3 grid, const RowdotArgs& a, hipStream_t s);
 

@@ -185,6 +185,7 @@ int dnnopt_onednn_gemm_bf16bf16f32(const char* transa, const char* transb,
 #define DNNOPT_K_ROWDOT_F32  8  /* M <= 8, fp32 B stored N x K, rows once   */
 #define DNNOPT_K_ROWDOT_BF16 9  /* M <= 8, bf16 B stored N x K, rows once   */
 #define DNNOPT_K_TALL_F32   10  /* large M, N <= 64, fp32 B resident in LDS  */
+#define DNNOPT_K_ROWDOT_S8  11  /* M <= 8, int8 B stored N x K, rows once   */
 
 typedef struct dnnopt_plan {
     int kernel;             /* DNNOPT_K_* */

@@ -95,7 +95,14 @@ def test_plans_for_the_configs(lib):
     for M in (1, 8, 128):
         for N in (4096, 4093):
             p = lib.plan_s8(M, N, 4096)
-            assert p["kernel"] == b.K_MFMA_S8 and p["rows"] >= min(M, 16)
+            if M <= 4:  # B stored N x K: every row streamed once by the row-dot kernel
+                assert p["kernel"] == b.K_ROWDOT_S8 and p["rows"] == M and p["name"] == "dnnopt_rowdot"
+            else:
+                assert p["kernel"] == b.K_MFMA_S8 and p["rows"] >= min(M, 16)
+    for M in (1, 4):
+        assert lib.plan_s8(M, 4096, 4096)["kernel"] == b.K_ROWDOT_S8
+    for M in (5, 9):
+        assert lib.plan_s8(M, 4096, 4096)["kernel"] == b.K_MFMA_S8
 
 
 def test_plan_split_never_exceeds_k(lib):

@@ -292,6 +292,46 @@ def test_int8_padded_strides_and_extremes(lib, orc, dev):
     assert got[0, 0] == K * 128 * 128
 
 
+# M <= 4: the int8 row-dot kernel (v_dot4 on 16-byte row chunks); M = 5..8:
+# the MFMA tiles, same checks.  K values around the 16-byte chunk and the
+# 1 KiB step, rows off 4-byte boundaries.
+S8_ROWDOT = [(M, N, K) for M in range(1, 9) for (N, K) in ((7, 1), (33, 15), (100, 17), (65, 1024), (129, 4097))]
+
+
+@pytest.mark.parametrize("M,N,K", S8_ROWDOT)
+def test_int8_rowdot_bit_exact(lib, orc, dev, M, N, K):
+    b = u.binding()
+    assert lib.plan_s8(M, N, K)["kernel"] == (b.K_ROWDOT_S8 if M <= 4 else b.K_MFMA_S8)
+    for pad in (0, 1, 3):  # 1, 3: rows start off 4-byte boundaries (funnel-shifted loads)
+        lda, ldb, ldc = K + pad, K + 2 * pad, N + 1
+        A = u.ints8(orc, M * lda, 1, -128, 127).reshape(M, lda)
+        B = u.ints8(orc, N * ldb, 2, -128, 127).reshape(N, ldb)
+        A[:, K:] = 127  # row padding must never reach a product
+        B[:, K:] = 127
+        dC = torch.full((M, ldc), -7, dtype=torch.int32, device=dev)
+        lib.gemm_s8s8s32(M, N, K, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, dC, ldc, stream=stream())
+        got = host(dC)
+        want = A[:, :K].astype(np.int64) @ B[:, :K].astype(np.int64).T
+        assert np.array_equal(got[:, :N].astype(np.int64), want), (M, N, K, pad)
+        assert (got[:, N] == -7).all()
+        s = u.uniform(orc, N, 4, 0.001, 0.01)
+        dF = torch.zeros((M, ldc), dtype=torch.float32, device=dev)
+        lib.gemm_s8s8f32_colscale(M, N, K, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, dev_copy(s, dev), dF, ldc,
+                                  stream=stream())
+        assert np.array_equal(host(dF)[:, :N], want.astype(np.float32) * s[None, :]), (M, N, K, pad)
+
+
+def test_int8_rowdot_extremes(lib, orc, dev):
+    # -128 * -128 summed over K = 4097 (67,125,248): exact in int32
+    for M in (1, 4, 8):
+        N, K = 70, 4097
+        A = np.full((M, K), -128, np.int8)
+        B = np.full((N, K), -128, np.int8)
+        dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
+        lib.gemm_s8s8s32(M, N, K, dev_copy(A, dev), K, dev_copy(B, dev), K, dC, N, stream=stream())
+        assert (host(dC) == K * 128 * 128).all()
+
+
 @pytest.mark.parametrize("M,N", [(1, 4096), (8, 4093), (128, 4093)])
 def test_int8_colscale(lib, orc, dev, M, N):
     K = 4096
