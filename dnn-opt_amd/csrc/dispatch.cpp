@@ -19,15 +19,17 @@
 //     with 8 waves above M = 128; 64 x 128, 64 x 64 and 32 x 64 tiles with
 //     128-k blocks below), split-k only when the tiles leave more than half
 //     of the CUs idle.
-//   * fp32 with M >= 4096, 16 < N <= 64 and B small enough for LDS: B
-//     resident in LDS, persistent workgroups stream A (k_tall.hip).
+//   * fp32 with 16 < N <= 64, B small enough for LDS and at least a row
+//     tile for most waves of one workgroup per CU (M >~ 48K): B resident in
+//     LDS, persistent workgroups stream A (k_tall.hip).
 //   * other M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for
 //     N <= 16, 64 x 64 otherwise); split-k when the tile count cannot occupy
 //     the CUs, with a separate reduce kernel once the split count is large.
-//   * int8 (B as N x K): 16 x 16 MFMA tiles with k split over the waves of a
-//     workgroup for M <= 16; 32 x 32 tiles staged through LDS (256-byte
-//     k-blocks) above that (4-byte aligned rows), split-k only when the tiles
-//     leave more than half of the CUs idle.
+//   * int8 (B as N x K): the row-dot kernel (v_dot4) for M <= 4; 16 x 16
+//     MFMA tiles with k split over the waves of a workgroup for M <= 16;
+//     32 x 32 tiles staged through LDS (256-byte k-blocks) above that (4-byte
+//     aligned rows), split-k only when the tiles leave more than half of the
+//     CUs idle.
 // Tunables (environment, read once, for sweeps):
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
 //   DNNOPT_SKINNY_WGS_PER_CU (default 1), DNNOPT_SKINNY_WGS (force G),
@@ -35,7 +37,9 @@
 //   DNNOPT_TILE_SPLITS (force the k-splits of a tile launch), DNNOPT_TILE_CFG
 //   (force an LDS-staged bf16 tile configuration, index 5 and up),
 //   DNNOPT_S8_CFG / DNNOPT_S8_SPLITS (force the int8 configuration / splits),
-//   DNNOPT_TALL=0 (keep tall-skinny fp32 GEMMs on the register-only tiles).
+//   DNNOPT_TALL=0 (keep tall-skinny fp32 GEMMs on the register-only tiles),
+//   DNNOPT_TALL_WGS_PER_CU (default 1), DNNOPT_S8_ROWDOT=0 (int8 M <= 4 on
+//   the MFMA tiles).
 #include <stdlib.h>
 #include <string.h>
 
