@@ -324,15 +324,6 @@ int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
     L->mr = M;
     L->nw = kw;
     L->grid = dim3((unsigned)G, 1, 1);
-    // M >= 3 (fp32, bf16): every wave would re-read all of A for R rows of
-    // B; a copy of A in LDS (at most 64 KiB, two workgroups per CU) serves
-    // those re-reads instead.  DNNOPT_ROWDOT_ALDS=0 reads A through the caches.
-    static const bool alds_ok = [] {
-        const char* e = getenv("DNNOPT_ROWDOT_ALDS");
-        return !(e && *e && atoi(e) == 0);
-    }();
-    const size_t a_image = (size_t)M * (size_t)ceil_div(K, rowdot_chunk_elems(mode)) * 16;
-    L->lds = (alds_ok && mode < 2 && M >= 3 && a_image <= 65536) ? a_image : 0;
     fill_pub(L, mode >= 2 ? DNNOPT_K_ROWDOT_S8 : (mode ? DNNOPT_K_ROWDOT_BF16 : DNNOPT_K_ROWDOT_F32), "dnnopt_rowdot", M,
              (int)rows_per_wg, 1, kRowdotWaves * 64);
     return DNNOPT_OK;
