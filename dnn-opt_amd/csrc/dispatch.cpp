@@ -20,7 +20,7 @@
 //     with 8 waves above M = 128; 64 x 128, 64 x 64 and 32 x 64 tiles with
 //     128-k blocks below), split-k only when the tiles leave more than half
 //     of the CUs idle.
-//   * fp32 with 16 < N <= 64, B small enough for LDS and at least a row
+//   * fp32 with 12 < N <= 64 (K >= 128 for N <= 16), B small enough for LDS and at least a row
 //     tile for most waves of one workgroup per CU (M >~ 48K): B resident in
 //     LDS, persistent workgroups stream A (k_tall.hip).
 //   * other M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for
@@ -331,9 +331,12 @@ int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
 
 int plan_tall(int transB, int M, int N, int K, int lda, Launch* L) {
     *L = Launch{};
-    // N <= 16 streams faster through the register tiles (64 x 16), whose
-    // per-k re-reads of B are small at that width.
-    if (N <= 16 || N > 64 || M < 4096) return DNNOPT_ERR_UNSUPPORTED;
+    // N <= 12 (a quarter or more of the padded 16-column MFMA tile wasted)
+    // and N <= 16 with short K stream faster through the register tiles
+    // (64 x 16), whose per-k re-reads of B are small at that width; measured
+    // at 65536 x 16 x 256: 18.5 (here) vs 19.3 us, 65536 x 12 x 256: 20.4 vs
+    // 19.5, 262144 x 16 x 64: 20.9 vs 19.9.
+    if (N <= 12 || (N <= 16 && K < 128) || N > 64 || M < 4096) return DNNOPT_ERR_UNSUPPORTED;
     const int nt = (N + 15) / 16;
     const size_t lds = tall_lds_bytes(nt, K);
     if (lds > 65536) return DNNOPT_ERR_UNSUPPORTED;

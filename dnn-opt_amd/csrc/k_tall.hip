@@ -1,6 +1,6 @@
 // k_tall.hip -- fp32 tall-skinny GEMM with B resident in LDS (gfx950).
 //
-// Shapes: M large, N <= 64 (the dispatcher sends 16 < N <= 64), K small
+// Shapes: M large, N <= 64 (the dispatcher sends 12 < N <= 64), K small
 // enough that all of B (K x N, fp32) fits
 // in 64 KiB of LDS -- the tall-skinny case of the reference's packed BLIS
 // path (src/gemm/gemm_driver_generic.cpp:27-248), where every row block of A

@@ -83,7 +83,7 @@ def test_plans_for_the_configs(lib):
             # more than one CU's worth of work: a whole number of workgroups per CU
             if p["grid_x"] >= 256:
                 assert p["grid_x"] % 256 == 0 or p["grid_x"] == tiles
-    assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TILE_F32
+    assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TALL_F32  # C3 N=16: B resident in LDS
     assert lib.plan_sgemm(65536, 64, 256)["kernel"] == b.K_TALL_F32
     p = lib.plan_sgemm(64, 64, 262144, transA=1)
     assert p["kernel"] == b.K_TILE_F32 and p["splits"] > 16
@@ -144,7 +144,9 @@ def test_plans_for_tall_skinny(lib):
     assert lib.plan_sgemm(1000, 64, 256)["kernel"] == b.K_TILE_F32    # too few rows
     assert lib.plan_sgemm(32768, 64, 256)["kernel"] == b.K_TILE_F32   # fewer row tiles than waves
     assert lib.plan_sgemm(65536, 65, 64)["kernel"] == b.K_TILE_F32
-    assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TILE_F32   # N <= 16: register tiles
+    assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TALL_F32   # N = 16 with K >= 128: B in LDS
+    assert lib.plan_sgemm(65536, 16, 64)["kernel"] == b.K_TILE_F32    # short K: register tiles
+    assert lib.plan_sgemm(65536, 12, 256)["kernel"] == b.K_TILE_F32   # N <= 12: register tiles
 
 
 def test_plan_rejects_bad_args(lib):

@@ -140,19 +140,21 @@ def test_sgemm_configs_c3(lib, orc, dev, M, N, K, ta):
 # padded rows; the small-M rows and N <= 16 go to the register tiles.
 TALL = [(65536, 64, 256, 0, 0), (65536, 16, 256, 1, 0), (65537, 33, 300, 0, 3), (70001, 64, 17, 2, 1),
         (4096, 1, 1024, 0, 0), (100003, 7, 64, 1, 2), (50000, 48, 333, 0, 0), (49999, 17, 5, 3, 0),
-        (60000, 60, 250, 1, 1), (70000, 32, 128, 0, 0), (8192, 33, 300, 0, 3), (4097, 17, 5, 3, 0)]
+        (60000, 60, 250, 1, 1), (70000, 32, 128, 0, 0), (8192, 33, 300, 0, 3), (4097, 17, 5, 3, 0),
+        (65536, 13, 130, 1, 2), (50001, 16, 64, 0, 0), (65536, 12, 256, 0, 0)]
 
 
-def _routes_tall(M, N):
-    # one 32-row tile for at least 3/4 of the waves of one 8-wave workgroup per CU (256 CUs)
-    return N > 16 and -(-M // 32) * 4 >= 3 * 256 * 8
+def _routes_tall(M, N, K):
+    # one 32-row tile for at least 3/4 of the waves of one 8-wave workgroup per CU (256 CUs);
+    # N <= 12, and N <= 16 with K < 128, stay on the register tiles
+    return N > 12 and (N > 16 or K >= 128) and N <= 64 and -(-M // 32) * 4 >= 3 * 256 * 8
 
 
 @pytest.mark.parametrize("M,N,K,pa,pb", TALL)
 @pytest.mark.parametrize("tb", [0, 1])
 def test_sgemm_tall_skinny(lib, orc, dev, M, N, K, pa, pb, tb):
     p = lib.plan_sgemm(M, N, K, transB=tb)
-    assert p["name"] == ("dnnopt_tall_f32" if _routes_tall(M, N) else "dnnopt_tile_f32"), p
+    assert p["name"] == ("dnnopt_tall_f32" if _routes_tall(M, N, K) else "dnnopt_tile_f32"), p
     lda = K + pa
     opA = np.zeros((M, lda), np.float32)
     opA[:, :K] = u.uniform(orc, M * K, 1).reshape(M, K)
