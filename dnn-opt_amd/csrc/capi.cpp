@@ -166,7 +166,7 @@ int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const f
 
 extern "C" {
 
-int dnnopt_hip_abi_version(void) { return 2; }
+int dnnopt_hip_abi_version(void) { return DNNOPT_HIP_ABI_VERSION; }
 
 int dnnopt_hip_device_count(void) { return visible_devices(); }
 

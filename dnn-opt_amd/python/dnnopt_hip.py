@@ -36,6 +36,9 @@ OK, ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_OUT_OF_MEMORY 
 (K_NONE, K_SKINNY_F32, K_SKINNY_BF16, K_SKINNY_F2B, K_MFMA_S8, K_TILE_F32, K_TILE_BF16, K_NAIVE_F32, K_ROWDOT_F32,
  K_ROWDOT_BF16, K_TALL_F32, K_ROWDOT_S8) = range(12)
 
+# DNNOPT_HIP_ABI_VERSION of include/dnnopt_hip.h that these bindings follow.
+ABI_VERSION = 2
+
 CblasRowMajor, CblasColMajor = 101, 102
 CblasNoTrans, CblasTrans, CblasConjTrans = 111, 112, 113
 

@@ -223,7 +223,8 @@ const char* dnnopt_hip_status_string(int status);
 int dnnopt_hip_last_status(void);     /* last failure of the C++/cblas API on
                                          this thread, DNNOPT_OK if none      */
 int dnnopt_hip_device_count(void);    /* 0 when no device is visible        */
-int dnnopt_hip_abi_version(void);     /* bumped on any signature change     */
+#define DNNOPT_HIP_ABI_VERSION 2
+int dnnopt_hip_abi_version(void);     /* DNNOPT_HIP_ABI_VERSION; bumped on any signature change */
 
 #ifdef __cplusplus
 }

@@ -29,7 +29,10 @@ def _exports(path):
 
 
 def test_library_loads(lib):
-    assert lib.so.dnnopt_hip_abi_version() == 2
+    assert lib.so.dnnopt_hip_abi_version() == u.binding().ABI_VERSION
+    hdr = open(os.path.join(u.ROOT, "include", "dnnopt_hip.h")).read()
+    m = re.search(r"#define DNNOPT_HIP_ABI_VERSION (\d+)", hdr)
+    assert m and int(m.group(1)) == lib.so.dnnopt_hip_abi_version()
 
 
 def test_every_c_declaration_is_exported(lib):
