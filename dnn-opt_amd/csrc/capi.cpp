@@ -157,7 +157,7 @@ int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const f
         return run_rowdot(L, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
     if (L.family == DNNOPT_K_TALL_F32) {
         TallArgs a{A, B, C, lda, ldb, ldc, M, N, K, alpha, beta, bias};
-        return finish_launch(launch_tall_f32(L.cfg, L.mode, L.grid, L.lds, a, s));
+        return finish_launch(launch_tall_f32(L.cfg, L.mode, L.mr, L.grid, L.lds, a, s));
     }
     return run_tile(L, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
 }

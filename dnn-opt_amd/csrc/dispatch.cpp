@@ -21,8 +21,9 @@
 //     128-k blocks below), split-k only when the tiles leave more than half
 //     of the CUs idle.
 //   * fp32 with 12 < N <= 64 (K >= 128 for N <= 16), B small enough for LDS and at least a row
-//     tile for most waves of one workgroup per CU (M >~ 48K): B resident in
-//     LDS, persistent workgroups stream A (k_tall.hip).
+//     tile for most waves of one workgroup per CU (32-row tiles from ~48K
+//     rows, 16-row tiles from ~16K rows with K >= 256): B resident in LDS,
+//     persistent workgroups stream A (k_tall.hip).
 //   * other M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for
 //     N <= 16, 64 x 64 otherwise); split-k when the tile count cannot occupy
 //     the CUs, with a separate reduce kernel once the split count is large.
@@ -342,11 +343,19 @@ int plan_tall(int transB, int M, int N, int K, int lda, Launch* L) {
     if (lds > 65536) return DNNOPT_ERR_UNSUPPORTED;
     if (((long long)(M - 1) * lda + K) * 4 >= 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
     // Each wave runs its row tiles as one serial chain of MFMAs, so the kernel
-    // needs about one tile for every wave of one workgroup per CU; with fewer
-    // (M below ~48K rows on 256 CUs) the register tiles, which spread the same
-    // work over more waves, are faster.
-    const long long tiles = ceil_div(M, tall_tile_rows());
-    if (tiles * 4 < 3LL * num_cus() * tall_waves()) return DNNOPT_ERR_UNSUPPORTED;
+    // needs about one tile for every wave of one workgroup per CU: 32-row
+    // tiles from ~48K rows (on 256 CUs); 16-row tiles (half the chain) from
+    // ~16K rows when K >= 256; below that the register tiles, which spread
+    // the same work over more waves, are faster.  Measured at N = 64, K = 256:
+    // 16K rows 15.0 (16-row tiles) vs 17.8 us, 32K rows 17.2 vs 23.0, 64K rows
+    // 29.6 (32-row tiles) vs 31.6 (16-row tiles).
+    const long long waves = num_cus() * tall_waves();
+    int rt = 2;
+    if (ceil_div(M, 32) * 4 < 3 * waves) {
+        if (K < 256 || ceil_div(M, 16) * 2 < waves) return DNNOPT_ERR_UNSUPPORTED;
+        rt = 1;
+    }
+    const long long tiles = ceil_div(M, 16 * rt);
     // Persistent: one workgroup per CU by default, no more than there are row
     // tiles for their waves.  More row tiles per wave keep loads, MFMAs and
     // stores of different tiles overlapped; a second workgroup per CU (more
@@ -356,10 +365,11 @@ int plan_tall(int transB, int M, int N, int K, int lda, Launch* L) {
     const long long want = num_cus() * std::min<long long>(std::max(wgs_per_cu, 1), per_cu);
     const long long G = std::max<long long>(1, std::min<long long>(want, ceil_div(tiles, tall_waves())));
     L->cfg = nt;
+    L->mr = rt;
     L->lds = lds;
     L->mode = transB;
     L->grid = dim3((unsigned)G, 1, 1);
-    fill_pub(L, DNNOPT_K_TALL_F32, "dnnopt_tall_f32", tall_tile_rows(), 16 * nt, 1, tall_waves() * 64);
+    fill_pub(L, DNNOPT_K_TALL_F32, "dnnopt_tall_f32", 16 * rt, 16 * nt, 1, tall_waves() * 64);
     return DNNOPT_OK;
 }
 

@@ -43,12 +43,8 @@ namespace {
 #ifndef DNNOPT_TALL_D
 #define DNNOPT_TALL_D 2
 #endif
-#ifndef DNNOPT_TALL_RT
-#define DNNOPT_TALL_RT 2
-#endif
 constexpr int kTallWaves = DNNOPT_TALL_WAVES;
 constexpr int kTallD = DNNOPT_TALL_D;
-constexpr int kTallRT = DNNOPT_TALL_RT;
 
 __device__ __forceinline__ u32x4 keep_first(u32x4 v, int valid) {
     u32x4 r;
@@ -265,14 +261,13 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
 }
 
 int tall_waves() { return kTallWaves; }
-int tall_tile_rows() { return 16 * kTallRT; }
 
-template <int BETA, int KFULL>
+template <int RT, int BETA, int KFULL>
 static hipError_t launch_tall_beta(int nt, int tb, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s) {
     const dim3 blk(kTallWaves * 64);
-#define DNNOPT_TALL_CASE(NT, TB)                                                                               \
-    case NT * 2 + TB:                                                                                          \
-        hipLaunchKernelGGL((dnnopt_tall_f32<NT, kTallRT, kTallD, TB, BETA, KFULL>), grid, blk, lds_bytes, s, a); \
+#define DNNOPT_TALL_CASE(NT, TB)                                                                           \
+    case NT * 2 + TB:                                                                                      \
+        hipLaunchKernelGGL((dnnopt_tall_f32<NT, RT, kTallD, TB, BETA, KFULL>), grid, blk, lds_bytes, s, a); \
         break;
     switch (nt * 2 + (tb ? 1 : 0)) {
         DNNOPT_TALL_CASE(1, 0)
@@ -289,15 +284,24 @@ static hipError_t launch_tall_beta(int nt, int tb, dim3 grid, size_t lds_bytes, 
     return hipGetLastError();
 }
 
-hipError_t launch_tall_f32(int nt, int tb, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s) {
+template <int RT>
+static hipError_t launch_tall_rt(int nt, int tb, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s) {
+    const bool kfull = a.K % 16 == 0;
+    if (a.beta == 0.0f)
+        return kfull ? launch_tall_beta<RT, 0, 1>(nt, tb, grid, lds_bytes, a, s)
+                     : launch_tall_beta<RT, 0, 0>(nt, tb, grid, lds_bytes, a, s);
+    return kfull ? launch_tall_beta<RT, 1, 1>(nt, tb, grid, lds_bytes, a, s)
+                 : launch_tall_beta<RT, 1, 0>(nt, tb, grid, lds_bytes, a, s);
+}
+
+hipError_t launch_tall_f32(int nt, int tb, int rt, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s) {
     // The kernel stages all of B: the image must fit the 64 KiB its staging
     // loop is sized for, and the launch must provide it.
     const size_t need = tall_lds_bytes(nt, a.K);
     if (need > 65536 || lds_bytes < need) return hipErrorInvalidValue;
-    const bool kfull = a.K % 16 == 0;
-    if (a.beta == 0.0f)
-        return kfull ? launch_tall_beta<0, 1>(nt, tb, grid, lds_bytes, a, s) : launch_tall_beta<0, 0>(nt, tb, grid, lds_bytes, a, s);
-    return kfull ? launch_tall_beta<1, 1>(nt, tb, grid, lds_bytes, a, s) : launch_tall_beta<1, 0>(nt, tb, grid, lds_bytes, a, s);
+    if (rt == 1) return launch_tall_rt<1>(nt, tb, grid, lds_bytes, a, s);
+    if (rt == 2) return launch_tall_rt<2>(nt, tb, grid, lds_bytes, a, s);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace dnnopt_hip

@@ -100,9 +100,9 @@ struct TallArgs {
     const float* bias;  // per-column bias added after the epilogue (or null)
 };
 inline size_t tall_lds_bytes(int nt, int K) { return (size_t)((K + 15) / 16) * 16 * 16 * nt * 4; }
-int tall_waves();      // waves per workgroup of the tall kernel
-int tall_tile_rows();  // rows of A one wave takes at a time
-hipError_t launch_tall_f32(int nt, int tb, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s);
+int tall_waves();  // waves per workgroup of the tall kernel
+// rt: row tiles of 16 a wave takes at a time (1 or 2).
+hipError_t launch_tall_f32(int nt, int tb, int rt, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s);
 
 // ---------------------------------------------------------------- int8 MFMA
 // Exact s8 x s8 -> s32 with B stored N x K.  Each wave owns MT x NT tiles of

@@ -145,7 +145,11 @@ def test_plans_for_tall_skinny(lib):
     assert lib.plan_sgemm(65536, 64, 257)["kernel"] == b.K_TILE_F32   # 272 x 64 x 4 bytes > 64 KiB
     assert lib.plan_sgemm(65536, 64, 256, transA=1)["kernel"] == b.K_TILE_F32
     assert lib.plan_sgemm(1000, 64, 256)["kernel"] == b.K_TILE_F32    # too few rows
-    assert lib.plan_sgemm(32768, 64, 256)["kernel"] == b.K_TILE_F32   # fewer row tiles than waves
+    assert lib.plan_sgemm(8192, 64, 256)["kernel"] == b.K_TILE_F32    # fewer row tiles than waves
+    p = lib.plan_sgemm(32768, 64, 256)
+    assert p["kernel"] == b.K_TALL_F32 and p["rows"] == 16            # 16-row tiles at mid M (K >= 256)
+    assert lib.plan_sgemm(32768, 64, 128)["kernel"] == b.K_TILE_F32   # ... but not for short K
+    assert lib.plan_sgemm(65536, 64, 256)["rows"] == 32
     assert lib.plan_sgemm(65536, 65, 64)["kernel"] == b.K_TILE_F32
     assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TALL_F32   # N = 16 with K >= 128: B in LDS
     assert lib.plan_sgemm(65536, 16, 64)["kernel"] == b.K_TILE_F32    # short K: register tiles

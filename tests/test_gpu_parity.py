@@ -141,13 +141,17 @@ def test_sgemm_configs_c3(lib, orc, dev, M, N, K, ta):
 TALL = [(65536, 64, 256, 0, 0), (65536, 16, 256, 1, 0), (65537, 33, 300, 0, 3), (70001, 64, 17, 2, 1),
         (4096, 1, 1024, 0, 0), (100003, 7, 64, 1, 2), (50000, 48, 333, 0, 0), (49999, 17, 5, 3, 0),
         (60000, 60, 250, 1, 1), (70000, 32, 128, 0, 0), (8192, 33, 300, 0, 3), (4097, 17, 5, 3, 0),
-        (65536, 13, 130, 1, 2), (50001, 16, 64, 0, 0), (65536, 12, 256, 0, 0)]
+        (65536, 13, 130, 1, 2), (50001, 16, 64, 0, 0), (65536, 12, 256, 0, 0), (16384, 64, 256, 0, 0),
+        (20001, 40, 300, 1, 0), (16383, 64, 256, 0, 0), (30000, 33, 255, 0, 1)]
 
 
 def _routes_tall(M, N, K):
-    # one 32-row tile for at least 3/4 of the waves of one 8-wave workgroup per CU (256 CUs);
-    # N <= 12, and N <= 16 with K < 128, stay on the register tiles
-    return N > 12 and (N > 16 or K >= 128) and N <= 64 and -(-M // 32) * 4 >= 3 * 256 * 8
+    # one 32-row tile for at least 3/4 of the waves of one 8-wave workgroup per CU (256 CUs),
+    # or (K >= 256) one 16-row tile for every other wave; N <= 12, and N <= 16 with K < 128,
+    # stay on the register tiles
+    waves = 256 * 8
+    rows_ok = -(-M // 32) * 4 >= 3 * waves or (K >= 256 and -(-M // 16) * 2 >= waves)
+    return N > 12 and (N > 16 or K >= 128) and N <= 64 and rows_ok
 
 
 @pytest.mark.parametrize("M,N,K,pa,pb", TALL)
