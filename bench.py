@@ -19,8 +19,9 @@ touched once per step and a step's working set exceeds the 256 MB Infinity
 Cache (extra copies are rotated when it would not), so nothing is served from
 the cache between two launches of the same shape.
 
-Timing uses HIP graphs replayed on one stream (a step = one graph replay), so
-host-side launch cost does not enter.  `roofline` is for the kernel with the
+Timing uses HIP graphs on one stream: the K timed steps are recorded as one
+graph and replayed once between the two events, so host-side launch cost
+does not enter (a step of one small GEMM is shorter than a graph launch).  `roofline` is for the kernel with the
 largest share of the step time: achieved = its algorithmic bytes (or flops)
 per launch / its mean launch time, from HIP events around replays of a graph
 of 16 back-to-back launches of each shape (inter-kernel gaps included).  `traffic` is filled from
@@ -635,7 +636,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
-              "sharding across GPUs is not built.", file=sys.stderr)
+              "(sharding across GPUs is not built).", file=sys.stderr)
         sys.exit(2)
 
     names = ["c1", "c2", "c3", "c4", "c5", "hook"] if args.workload == "all" else [args.workload]
