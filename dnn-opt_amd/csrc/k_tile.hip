@@ -389,15 +389,17 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
 
 // ---------------------------------------------------------------- bf16, LDS-staged
 // Row-major A (M x K) and B (K x N) through LDS, double-buffered in k-blocks
-// of 64.  Per block a workgroup stages A as BM rows x 64 k and B transposed
-// as BN columns x 64 k, both k-contiguous, so that every MFMA operand is one
-// 16-byte LDS read.  The transpose happens on the way into LDS: a thread
-// loads 4 consecutive rows x 8 columns of B (four 16-byte global loads),
-// regroups them into 8 column runs of 4 k (v_perm_b32) and writes those with
-// 8-byte LDS stores.  16-byte chunks of an LDS row are XOR-swizzled by the
-// row index so that the 16 rows read by one MFMA operand, and the columns
-// written by one store, fall in different banks.  The next block's global
-// loads are issued before the current block's MFMAs.
+// of 64.  Per block a workgroup stages A as BM rows x 64 k (k-contiguous, so
+// an A operand is one 16-byte LDS read) and B as it lies in memory, BK rows
+// of k x BN columns, written with 16-byte stores.  A B operand (8 k of one
+// column per lane) is gathered by two ds_read_b64_tr_b16: in each group of
+// 16 lanes, lane p points at row k0 + p / 4, columns 4 (p % 4) .. + 3 of the
+// 16-column tile, and lane r receives B[k0 + 0..3][column r] -- four
+// consecutive k of its column.  B rows are padded by 32 bytes so that the
+// four rows of one read fall in different banks.  16-byte chunks of an A row
+// are XOR-swizzled by the row index so that the 16 rows read by one MFMA
+// operand fall in different banks.  The next block's global loads are issued
+// before the current block's MFMAs.
 //
 // TB = 1 (bf16 storage only): B is stored N x K.  Its rows are then staged
 // exactly like A's -- 16-byte chunks of 8 k, no transpose.
@@ -421,7 +423,6 @@ __device__ __forceinline__ u32x4 pack_bf16x8(const u32x4& lo, const u32x4& hi) {
 
 // Physical 16-byte chunk of logical chunk c (0..7) in LDS row `row`.
 __device__ __forceinline__ int swz_a(int row, int c) { return c ^ (row & 7); }
-__device__ __forceinline__ int swz_b(int n, int c) { return c ^ ((n ^ (n >> 3)) & 7); }
 
 }  // namespace
 
@@ -436,12 +437,15 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     constexpr int ROWB = BK * 2;  // bytes of one LDS row (BK bf16)
     constexpr int CPR = ROWB / 16;  // 16-byte chunks per LDS row
     constexpr int KK = BK / 32;     // MFMA k-steps per block
-    constexpr int A_BYTES = BM * ROWB, B_BYTES = BN * ROWB, STAGE = A_BYTES + B_BYTES;
+    // B in LDS: stored N x K, BN rows of BK k (like A); stored K x N, BK rows
+    // of BN columns padded by 32 bytes.
+    constexpr int BROW = TB ? ROWB : BN * 2 + 32;
+    constexpr int A_BYTES = BM * ROWB, B_BYTES = TB ? BN * ROWB : BK * BROW, STAGE = A_BYTES + B_BYTES;
     constexpr int ACH = BM * CPR;              // A chunks (8 k) per block
-    // B units per block: 4 k x 8 n (stored K x N, 4 loads and 8 LDS stores
-    // each), or one 16-byte chunk of 8 k (stored N x K).
+    // B units per block: 4 k x 8 n (stored K x N, 4 loads and 4 LDS stores
+    // of 16 bytes each), or one 16-byte chunk of 8 k (stored N x K).
     constexpr int BUN = TB ? BN * CPR : (BN / 8) * (BK / 4);
-    constexpr int BQ = TB ? 1 : 4, BL = TB ? 1 : 8;
+    constexpr int BQ = TB ? 1 : 4, BL = TB ? 1 : 4;
     constexpr int AU = (ACH + NTH - 1) / NTH;  // per thread
     constexpr int BU = (BUN + NTH - 1) / NTH;
     // The two k-block stages, reused after the main loop to stage C rows.
@@ -502,13 +506,9 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
             const bool ok = BUN % NTH == 0 || u < BUN;
             b_c[i] = 0;
 #pragma unroll
-            for (int q = 0; q < BQ; ++q)
+            for (int q = 0; q < BQ; ++q) {
                 b_off[i][q] = ok ? ((uint32_t)(4 * kg + q) * p.ldb + 8 * cg) * ES : kOobOffset;
-            const int c = kg >> 1, half = kg & 1;
-#pragma unroll
-            for (int j = 0; j < BL; ++j) {
-                const int n = 8 * cg + j;
-                b_lds[i][j] = ok ? n * ROWB + swz_b(n, c) * 16 + half * 8 : -1;
+                b_lds[i][q] = ok ? (4 * kg + q) * BROW + cg * 16 : -1;
             }
         }
     }
@@ -575,15 +575,9 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
                 if (tail) v = keep_k(v, p.K - (blk * BK + b_c[i]));
                 *reinterpret_cast<u32x4*>(Bs + b_lds[i][0]) = v;
             } else {
+                // Rows of a K x N B past K read as zero (out of range).
 #pragma unroll
-                for (int j = 0; j < BL; ++j) {
-                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-                    u32x2 v;
-                    v[0] = __builtin_amdgcn_perm(sb[slot][i][1][j >> 1], sb[slot][i][0][j >> 1], sel);
-                    v[1] = __builtin_amdgcn_perm(sb[slot][i][3][j >> 1], sb[slot][i][2][j >> 1], sel);
-                    *reinterpret_cast<u32x2*>(Bs + b_lds[i][j]) = v;
-                }
+                for (int q = 0; q < BQ; ++q) *reinterpret_cast<u32x4*>(Bs + b_lds[i][q]) = sb[slot][i][q];
             }
         }
     };
@@ -605,8 +599,13 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
-            const int n = (wn * NT + nt) * 16 + r;
-            b_rd[kk][nt] = A_BYTES + n * ROWB + (TB ? swz_a(n, c) : swz_b(n, c)) * 16;
+            if constexpr (TB) {
+                const int n = (wn * NT + nt) * 16 + r;
+                b_rd[kk][nt] = A_BYTES + n * ROWB + swz_a(n, c) * 16;
+            } else {
+                // first transposing read: row kk * 32 + 8 g + r / 4, columns 4 (r % 4) of the tile
+                b_rd[kk][nt] = A_BYTES + (kk * 32 + 8 * g + (r >> 2)) * BROW + ((wn * NT + nt) * 16 + 4 * (r & 3)) * 2;
+            }
         }
     }
     auto compute = [&](int buf) {
@@ -617,7 +616,19 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const u32x4*>(St + a_rd[kk][mt]);
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt) bfr[nt] = *reinterpret_cast<const u32x4*>(St + b_rd[kk][nt]);
+            for (int nt = 0; nt < NT; ++nt) {
+                if constexpr (TB) {
+                    bfr[nt] = *reinterpret_cast<const u32x4*>(St + b_rd[kk][nt]);
+                } else {
+                    typedef short s16x4 __attribute__((ext_vector_type(4)));
+                    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(St + b_rd[kk][nt]));
+                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(St + b_rd[kk][nt] + 4 * BROW));
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+                    bfr[nt] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+                }
+            }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
