@@ -584,6 +584,20 @@ def rocprof_summary(kernel, workload, trace_csv, pmc=None):
         lines.append("")
         lines.append(f"rocprof mean duration of {kernel}* launches: "
                      + ", ".join(f"{x:.2f} us" for x in dom))
+        # A split-K launch is followed by its reduce kernel; the bench times both
+        # (one GEMM call), so also give the pair: summed durations, and the span
+        # from the kernel's start to the reduce kernel's end.
+        pairs = []
+        for i, r in enumerate(tr[:-1]):
+            nxt = tr[i + 1]
+            if _short_kernel_name(r["Kernel_Name"]).startswith(kernel) and "reduce" in nxt["Kernel_Name"]:
+                d0 = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+                d1 = int(nxt["End_Timestamp"]) - int(nxt["Start_Timestamp"])
+                pairs.append(((d0 + d1) / 1000.0, (int(nxt["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0))
+        if pairs:
+            lines.append(f"with its reduce kernel ({len(pairs)} pairs): durations summed "
+                         f"{sum(p[0] for p in pairs) / len(pairs):.2f} us, start to end "
+                         f"{sum(p[1] for p in pairs) / len(pairs):.2f} us")
     return "\n".join(lines) + "\n", traffic
 
 

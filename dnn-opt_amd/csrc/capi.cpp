@@ -70,8 +70,11 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
     Launch L = L0;
     // The LDS-staged bf16 kernel reads whole dwords: bf16 operands must start
     // on 4-byte boundaries, else the register-only kernel serves the call.
-    if (L.cfg >= kTileFirstLds && L.mode == kTileBF16 &&
-        ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) != 0) {
+    // The k-major outer-product kernel reads 16-byte chunks: its operands must
+    // start on 16-byte boundaries, else the register tiles serve the call.
+    if ((L.cfg >= kTileFirstLds && L.cfg != kTileKOuter && L.mode == kTileBF16 &&
+         ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) != 0) ||
+        (L.cfg == kTileKOuter && ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15u) != 0)) {
         const int st = plan_tile(L.mode, ta, tb, M, N, K, lda, ldb, &L, false);
         if (st != DNNOPT_OK) return st;
     }

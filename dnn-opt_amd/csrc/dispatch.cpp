@@ -24,6 +24,10 @@
 //     tile for most waves of one workgroup per CU (32-row tiles from ~48K
 //     rows, 16-row tiles from ~16K rows with K >= 256): B resident in LDS,
 //     persistent workgroups stream A (k_tall.hip).
+//   * fp32 with A stored K x M and B stored K x N (TransA, NoTrans), 32 < M,
+//     N <= 64, K >= 32768, row strides multiples of 4 floats: the k-major
+//     outer-product kernel (k_kouter.hip), one workgroup per CU, each a
+//     contiguous k-range, partials summed by the split-K reduce kernel.
 //   * other M > 8 (fp32, bf16): MFMA tiles sized to the shape (64 x 16 for
 //     N <= 16, 64 x 64 otherwise); split-k when the tile count cannot occupy
 //     the CUs, with a separate reduce kernel once the split count is large.
@@ -41,7 +45,8 @@
 //   DNNOPT_S8_CFG / DNNOPT_S8_SPLITS (force the int8 configuration / splits),
 //   DNNOPT_TALL=0 (keep tall-skinny fp32 GEMMs on the register-only tiles),
 //   DNNOPT_TALL_WGS_PER_CU (default 1), DNNOPT_S8_ROWDOT=0 (int8 M <= 4 on
-//   the MFMA tiles).
+//   the MFMA tiles), DNNOPT_KOUTER=0 (k-major fp32 operands on the register
+//   tiles), DNNOPT_KOUTER_WGS_PER_CU (default 1).
 #include <stdlib.h>
 #include <string.h>
 
@@ -59,6 +64,21 @@ int env_int(const char* name, int dflt) {
     if (!v || !*v) return dflt;
     int x = atoi(v);
     return x > 0 ? x : dflt;
+}
+
+// k-major outer-product kernel: k-extent from which it replaces the
+// register tiles, and workgroups per CU.
+constexpr int kKOuterMinK = 32768;
+bool kouter_enabled() {
+    static const bool v = [] {
+        const char* e = getenv("DNNOPT_KOUTER");
+        return !(e && e[0] == '0');
+    }();
+    return v;
+}
+int kouter_wgs_per_cu() {
+    static int v = env_int("DNNOPT_KOUTER_WGS_PER_CU", 1);
+    return v;
 }
 
 int waves_per_cu() {
@@ -165,7 +185,42 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
     return DNNOPT_OK;
 }
 
+// k-major fp32 operands (A stored K x M, B stored K x N) with 32 < M, N <= 64
+// and a long k: the outer-product kernel streams both panels with 16-byte
+// loads, one 4-wave workgroup per CU, each summing a contiguous k-range.
+int plan_kouter(int M, int N, int K, int lda, int ldb, Launch* L) {
+    const long long cus = num_cus();
+    const long long nsteps = ((long long)K + 3) / 4;
+    static const int forced_splits = env_int("DNNOPT_TILE_SPLITS", 0);
+    long long s = forced_splits > 0 ? forced_splits : cus * kouter_wgs_per_cu();
+    s = std::min<long long>(s, std::max<long long>(1, nsteps / 16));
+    // 32-bit offsets within one split's rows (plus one 16-row step).
+    const long long ld = std::max(lda, ldb);
+    while ((((nsteps + s - 1) / s) * 4 + 16) * ld * 4 >= 0x7FFFFFFFll && s < nsteps) s *= 2;
+    s = std::min(s, nsteps);
+    if ((((nsteps + s - 1) / s) * 4 + 16) * ld * 4 >= 0x7FFFFFFFll || s > 65535) return DNNOPT_ERR_UNSUPPORTED;
+    L->mode = kTileF32;
+    L->cfg = kTileKOuter;
+    L->bm = 64;
+    L->bn = 64;
+    L->tn = 1;
+    L->tm = 1;
+    L->grid = dim3(1, 1, (unsigned)s);
+    L->defer_reduce = 1;
+    L->part_bytes = (size_t)s * 64 * 64 * sizeof(float);
+    L->tickets = 0;
+    (void)M;
+    (void)N;
+    fill_pub(L, DNNOPT_K_TILE_F32, "dnnopt_kouter_f32", 64, 64, (int)s, 256);
+    return DNNOPT_OK;
+}
+
 int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, bool lds_ok) {
+    *L = Launch{};
+    if (mode == kTileF32 && transA && !transB && lds_ok && kouter_enabled() && M > 32 && M <= 64 && N > 32 &&
+        N <= 64 && K >= kKOuterMinK && (lda & 3) == 0 && (ldb & 3) == 0 &&
+        plan_kouter(M, N, K, lda, ldb, L) == DNNOPT_OK)
+        return DNNOPT_OK;
     *L = Launch{};
     const long long es = mode == kTileBF16 ? 2 : 4;
     // bf16 GEMMs with 4-byte aligned rows go through the LDS-staged kernel

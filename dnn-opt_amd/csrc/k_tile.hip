@@ -780,6 +780,7 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
 hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid, const TileArgs& a, hipStream_t s) {
     // Transposed operands: fp32 both, bf16 storage B only (stored N x K).
     if (mode != kTileF32 && (ta || (tb && mode != kTileBF16))) return hipErrorInvalidValue;
+    if (cfg_idx == kTileKOuter) return mode == kTileF32 && ta && !tb ? launch_kouter_f32(grid, a, s) : hipErrorInvalidValue;
     if (cfg_idx < 0 || cfg_idx >= tile_config_count()) return hipErrorInvalidValue;
     const TileConfig c = kTileConfigs[cfg_idx];
     const dim3 blk(c.wm * c.wn * c.kw * 64);

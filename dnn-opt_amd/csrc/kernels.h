@@ -201,6 +201,12 @@ constexpr int kTileFirstLds = 5;
 constexpr int tile_lds_bk(int bm, int bn, int kblk) {
     return (bm + bn) * (kblk > 0 ? kblk : DNNOPT_LDS_KB) * 2 * 2 <= 131072 ? (kblk > 0 ? kblk : DNNOPT_LDS_KB) : 64;
 }
+// Tile "configuration" of the k-major outer-product kernel (k_kouter.hip):
+// fp32, A stored K x M and B stored K x N, 32 < M, N <= 64, a long k; one
+// 64 x 64 partial tile per k-split (grid = (1, 1, splits), 256 threads),
+// always followed by the split-K reduce kernel.
+constexpr int kTileKOuter = 64;
+hipError_t launch_kouter_f32(dim3 grid, const TileArgs& a, hipStream_t s);
 // transA: fp32 only; transB: fp32, or bf16 storage with B stored N x K.
 // aligned: all k-contiguous rows (A; B stored N x K) start on 4-byte
 // boundaries (matters for bf16 storage).

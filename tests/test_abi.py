@@ -88,8 +88,13 @@ def test_plans_for_the_configs(lib):
                 assert p["grid_x"] % 256 == 0 or p["grid_x"] == tiles
     assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TALL_F32  # C3 N=16: B resident in LDS
     assert lib.plan_sgemm(65536, 64, 256)["kernel"] == b.K_TALL_F32
-    p = lib.plan_sgemm(64, 64, 262144, transA=1)
-    assert p["kernel"] == b.K_TILE_F32 and p["splits"] > 16
+    p = lib.plan_sgemm(64, 64, 262144, transA=1)  # C3 split-K: k-major outer-product kernel
+    assert p["kernel"] == b.K_TILE_F32 and p["name"] == "dnnopt_kouter_f32" and p["splits"] > 16
+    assert (p["rows"], p["cols"], p["block"]) == (64, 64, 256)
+    # rows of A not a multiple of 4 floats, M or N <= 32, or a short k: register tiles
+    for M, N, K in ((63, 64, 262144), (32, 64, 262144), (64, 32, 262144), (64, 64, 16384)):
+        assert lib.plan_sgemm(M, N, K, transA=1)["name"] == "dnnopt_tile_f32", (M, N, K)
+    assert lib.plan_sgemm(64, 64, 262144)["name"] == "dnnopt_tile_f32"
     for M in (1, 4):
         assert lib.plan_bf16(M, 11008, 4096)["kernel"] == b.K_SKINNY_BF16
         assert lib.plan_bf16(M, 11008, 4096, fp32_inputs=1)["kernel"] == b.K_SKINNY_F2B

@@ -132,6 +132,52 @@ def test_sgemm_configs_c3(lib, orc, dev, M, N, K, ta):
     u.assert_fp32_close(host(dC), want, scale, K, f"C3 {M}x{N}x{K} ta={ta}")
 
 
+# k-major outer-product kernel (A stored K x M, B stored K x N, 32 < M, N <= 64,
+# K >= 32768, row strides multiples of 4): K not a multiple of 4, ragged M and
+# N, padded strides whose padding holds NaN (it may only reach outputs outside
+# C), alpha / beta, a padded C whose padding must stay untouched.
+# (M, N, K, A row padding, B row padding)
+KOUTER = [(64, 64, 262144, 0, 0), (33, 61, 32771, 3, 7), (48, 40, 100003, 0, 4), (64, 33, 40000, 4, 3),
+          (61, 64, 65537, 3, 0), (36, 36, 32768, 0, 0)]
+
+
+@pytest.mark.parametrize("M,N,K,pa,pb", KOUTER)
+def test_sgemm_kouter(lib, orc, dev, M, N, K, pa, pb):
+    lda, ldb, ldc = M + pa, N + pb, N + 5
+    assert lda % 4 == 0 and ldb % 4 == 0
+    opA = u.uniform(orc, M * K, 1).reshape(M, K)
+    opB = u.uniform(orc, K * N, 2).reshape(K, N)
+    A = np.full((K, lda), np.nan, np.float32)
+    A[:, :M] = opA.T
+    B = np.full((K, ldb), np.nan, np.float32)
+    B[:, :N] = opB
+    C0 = u.uniform(orc, M * ldc, 3).reshape(M, ldc)
+    dC = dev_copy(C0, dev)
+    if lda == M and ldb == N:
+        p = lib.plan_sgemm(M, N, K, transA=1)
+        assert p["name"] == "dnnopt_kouter_f32", p
+    lib.sgemm(M, N, K, 1.5, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, -0.5, dC, ldc, transA=1,
+              stream=stream())
+    got = host(dC)
+    want, scale = u.exact(opA, opB, 1.5, -0.5, C0[:, :N])
+    u.assert_fp32_close(got[:, :N], want, scale, K, f"kouter {M}x{N}x{K} lda={lda} ldb={ldb}")
+    assert np.array_equal(got[:, N:], C0[:, N:]), "wrote outside the C block"
+
+
+def test_sgemm_kouter_misaligned_falls_back(lib, orc, dev):
+    # Operands that do not start on 16-byte boundaries go to the register tiles.
+    M = N = 64
+    K = 32768
+    opA = u.uniform(orc, M * K, 1).reshape(M, K)
+    opB = u.uniform(orc, K * N, 2).reshape(K, N)
+    bufA = dev_copy(np.concatenate([np.zeros(1, np.float32), np.ascontiguousarray(opA.T).ravel()]), dev)
+    dB = dev_copy(opB, dev)
+    dC = dev_copy(np.zeros((M, N), np.float32), dev)
+    lib.sgemm(M, N, K, 1.0, bufA[1:], M, dB, N, 0.0, dC, N, transA=1, stream=stream())
+    want, scale = u.exact(opA, opB)
+    u.assert_fp32_close(host(dC), want, scale, K, "kouter misaligned A")
+
+
 # Tall-skinny fp32 with B resident in LDS: every column-tile width, ragged N
 # and K (K tails inside a 16-k chunk, N not a multiple of 16), padded strides,
 # B stored K x N or N x K, more row tiles than waves and fewer.
