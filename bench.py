@@ -29,9 +29,9 @@ profiles/<kernel>_<workload>_traffic.json when a rocprofv3 --pmc summary has
 been committed for it.
 
 `cpu_baseline` times the oracle's restatement of the reference's CPU path
-(oracle/liboracle.so) on the host, on every shape of the workload once per
-run (2 warmup runs, 5 timed runs, median -- the reference's
-dnnopt::benchmark method).  `cpu_reference` times the reference's literal
+(oracle/liboracle.so) on the host, on the workload's shapes of at most 2^30
+multiply-adds, each once per run (2 warmup runs, 5 timed runs, median -- the
+reference's dnnopt::benchmark method -- fewer when a run is long).  `cpu_reference` times the reference's literal
 portable fallback (its naive loops, built from its own sources into
 oracle/_ref) on a bounded sample, when that build is present.
 """
@@ -425,6 +425,7 @@ def cpu_baseline(cases, budget_s=20.0):
     orc = u.load_oracle()
     nthreads = os.cpu_count() or 1
     os.environ.setdefault("OMP_NUM_THREADS", str(nthreads))
+    kMaxMacs = 1 << 30  # larger M > 8 shapes are left out of the sample
     prepared = []
     for c in cases:
         M, N, K = c.M, c.N, c.K
@@ -445,13 +446,22 @@ def cpu_baseline(cases, budget_s=20.0):
 
             def run(A=A, B=B, C=C, c=c):
                 orc.orc_gemm_s8s8s32(c.M, c.N, c.K, u.ptr(A), c.K, u.ptr(B), c.K, u.ptr(C), c.N)
-        elif c.kind == "bf16" and c.M <= 8:
+        elif c.kind == "bf16" and (c.M <= 8 or M * N * K <= kMaxMacs):
             A = u.bf16_bits(orc, u.normal(orc, M * K, 1))
             B = u.bf16_bits(orc, u.normal(orc, K * N, 2, 0, 0.02))
             C = np.zeros(M * N, np.float32)
 
             def run(A=A, B=B, C=C, c=c):
                 orc.orc_gemm_bf16(c.M, c.N, c.K, 1.0, u.ptr(A), c.K, u.ptr(B), c.N, 0.0, u.ptr(C), c.N)
+        elif c.kind == "f32" and M * N * K <= kMaxMacs:
+            # M > 8 fp32 (tall-skinny, TransA): the restated cblas row-major path
+            A = u.uniform(orc, M * K, 1)
+            B = u.uniform(orc, K * N, 2)
+            C = np.zeros(M * N, np.float32)
+
+            def run(A=A, B=B, C=C, c=c):
+                orc.orc_cblas_sgemm(101, 112 if c.ta else 111, 111, c.M, c.N, c.K, c.alpha, u.ptr(A),
+                                    c.M if c.ta else c.K, u.ptr(B), c.N, c.beta, u.ptr(C), c.N)
         else:
             continue
         prepared.append((c, run))
@@ -464,15 +474,20 @@ def cpu_baseline(cases, budget_s=20.0):
     one = time.perf_counter() - t
     runs = []
     total_bytes = sum(c.bytes_alg() for c, _ in prepared)
-    reps = 5 if one * 7 < budget_s else max(1, int(budget_s / max(one, 1e-9)) - 2)
-    for _ in range(min(2, reps)):
-        for _, run in prepared:
-            run()
-    for _ in range(reps):
-        t = time.perf_counter()
-        for _, run in prepared:
-            run()
-        runs.append(time.perf_counter() - t)
+    warm = one * 3 < budget_s
+    if not warm:
+        # a long pass (seconds of scalar loops) is its own sample
+        reps, runs = 1, [one]
+    else:
+        reps = 5 if one * 7 < budget_s else max(1, int(budget_s / max(one, 1e-9)) - 2)
+        for _ in range(min(2, reps)):
+            for _, run in prepared:
+                run()
+        for _ in range(reps):
+            t = time.perf_counter()
+            for _, run in prepared:
+                run()
+            runs.append(time.perf_counter() - t)
     med = statistics.median(runs)
     cpu_model = ""
     try:
@@ -487,9 +502,11 @@ def cpu_baseline(cases, budget_s=20.0):
     return {
         "value": round(total_bytes / med / 1e9, 3), "unit": "GB/s",
         "cores": nthreads if threaded else 1, "kind": "port",
-        "sample": (f"every shape of the workload once ({len(prepared)} GEMMs, {total_bytes / 1e6:.0f} MB "
-                   f"algorithmic), median of {reps} runs after warmup; oracle restatement of the reference CPU "
-                   f"path (GEMV / wide driver single-threaded, adaptive tiles on {nthreads} OpenMP threads); "
+        "sample": (f"{len(prepared)} of {len(cases)} shapes of the workload once ({total_bytes / 1e6:.0f} MB "
+                   f"algorithmic; shapes above 2^30 multiply-adds left out), median of {reps} runs"
+                   f"{' after warmup' if warm else ''}; "
+                   f"oracle restatement of the reference CPU path (GEMV / wide driver single-threaded, adaptive "
+                   f"tiles on {nthreads} OpenMP threads, other shapes its single-threaded row-major loops); "
                    f"host CPU: {cpu_model}"),
     }
 
