@@ -179,7 +179,8 @@ int dnnopt_onednn_gemm_bf16bf16f32(const char* transa, const char* transb,
 #define DNNOPT_K_SKINNY_BF16 2  /* M <= 8, bf16 B streamed once             */
 #define DNNOPT_K_SKINNY_F2B  3  /* M <= 8, fp32 B rounded to bf16 in regs   */
 #define DNNOPT_K_MFMA_S8     4  /* int8 MFMA tiles, B as N x K              */
-#define DNNOPT_K_TILE_F32    5  /* fp32 MFMA tiles (tall-skinny, split-K)   */
+#define DNNOPT_K_TILE_F32    5  /* fp32 MFMA tiles (tall-skinny, split-K;   */
+                                /* name dnnopt_kouter_f32: k-major TransA) */
 #define DNNOPT_K_TILE_BF16   6  /* bf16 MFMA tiles                          */
 #define DNNOPT_K_NAIVE_F32   7  /* scalar reference kernel                  */
 #define DNNOPT_K_ROWDOT_F32  8  /* M <= 8, fp32 B stored N x K, rows once   */
