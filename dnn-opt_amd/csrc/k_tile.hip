@@ -442,10 +442,9 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     constexpr int BROW = TB ? ROWB : BN * 2 + 32;
     constexpr int A_BYTES = BM * ROWB, B_BYTES = TB ? BN * ROWB : BK * BROW, STAGE = A_BYTES + B_BYTES;
     constexpr int ACH = BM * CPR;              // A chunks (8 k) per block
-    // B units per block: 4 k x 8 n (stored K x N, 4 loads and 4 LDS stores
-    // of 16 bytes each), or one 16-byte chunk of 8 k (stored N x K).
-    constexpr int BUN = TB ? BN * CPR : (BN / 8) * (BK / 4);
-    constexpr int BQ = TB ? 1 : 4, BL = TB ? 1 : 4;
+    // B units per block: one 16-byte chunk, 8 n of one k row (stored K x N)
+    // or 8 k of one column (stored N x K).
+    constexpr int BUN = TB ? BN * CPR : (BN / 8) * BK;
     constexpr int AU = (ACH + NTH - 1) / NTH;  // per thread
     constexpr int BU = (BUN + NTH - 1) / NTH;
     // The two k-block stages, reused after the main loop to stage C rows.
@@ -482,8 +481,8 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     // once: global element offsets of this thread's A chunks and B rows (an
     // out-of-range offset for rows past M), LDS byte offsets of its stores
     // and of the wave's operand reads.
-    uint32_t a_off[AU], b_off[BU][BQ];
-    int a_lds[AU], b_lds[BU][BL];
+    uint32_t a_off[AU], b_off[BU];
+    int a_lds[AU], b_lds[BU];
     int a_c[AU], b_c[BU];
 #pragma unroll
     for (int i = 0; i < AU; ++i) {
@@ -498,18 +497,15 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
         if constexpr (TB) {
             const int idx = t + i * NTH, row = idx / CPR, c = idx % CPR;
             const bool ok = (BUN % NTH == 0 || idx < BUN) && n0 + row < p.N;
-            b_off[i][0] = ok ? ((uint32_t)row * p.ldb + 8 * c) * ES : kOobOffset;
-            b_lds[i][0] = row * ROWB + swz_a(row, c) * 16;
+            b_off[i] = ok ? ((uint32_t)row * p.ldb + 8 * c) * ES : kOobOffset;
+            b_lds[i] = row * ROWB + swz_a(row, c) * 16;
             b_c[i] = 8 * c;
         } else {
-            const int u = t + i * NTH, cg = u % (BN / 8), kg = u / (BN / 8);
+            const int u = t + i * NTH, cg = u % (BN / 8), kr = u / (BN / 8);
             const bool ok = BUN % NTH == 0 || u < BUN;
             b_c[i] = 0;
-#pragma unroll
-            for (int q = 0; q < BQ; ++q) {
-                b_off[i][q] = ok ? ((uint32_t)(4 * kg + q) * p.ldb + 8 * cg) * ES : kOobOffset;
-                b_lds[i][q] = ok ? (4 * kg + q) * BROW + cg * 16 : -1;
-            }
+            b_off[i] = ok ? ((uint32_t)kr * p.ldb + 8 * cg) * ES : kOobOffset;
+            b_lds[i] = ok ? kr * BROW + cg * 16 : -1;
         }
     }
 
@@ -518,7 +514,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     // range by up to D - 1 blocks; those re-read the last block (never used),
     // so every load is unconditional and the compiler waits for exactly the
     // loads each LDS store needs.
-    u32x4 sa[D][AU], sb[D][BU][BQ];
+    u32x4 sa[D][AU], sb[D][BU];
     auto load_stage = [&](int blk, int slot) {
         const int bc = blk < b_hi ? blk : b_hi - 1;
         const uint32_t ka = (uint32_t)bc * BK * ES;
@@ -534,17 +530,15 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
             }
         }
 #pragma unroll
-        for (int i = 0; i < BU; ++i)
-#pragma unroll
-            for (int q = 0; q < BQ; ++q) {
-                if constexpr (MODE == kTileBF16) {
-                    sb[slot][i][q] = buf_load_x4(rb, b_off[i][q] + kb);
-                } else {
-                    const u32x4 lo = buf_load_x4(rb, b_off[i][q] + kb);
-                    const u32x4 hi = buf_load_x4(rb, b_off[i][q] + kb + 16u);
-                    sb[slot][i][q] = pack_bf16x8(lo, hi);
-                }
+        for (int i = 0; i < BU; ++i) {
+            if constexpr (MODE == kTileBF16) {
+                sb[slot][i] = buf_load_x4(rb, b_off[i] + kb);
+            } else {
+                const u32x4 lo = buf_load_x4(rb, b_off[i] + kb);
+                const u32x4 hi = buf_load_x4(rb, b_off[i] + kb + 16u);
+                sb[slot][i] = pack_bf16x8(lo, hi);
             }
+        }
     };
     auto write_stage = [&](int slot, int buf, int blk) {
         char* As = lds + buf * STAGE;
@@ -571,13 +565,12 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
         for (int i = 0; i < BU; ++i) {
             if (BUN % NTH != 0 && t + i * NTH >= BUN) continue;
             if constexpr (TB) {
-                u32x4 v = sb[slot][i][0];
+                u32x4 v = sb[slot][i];
                 if (tail) v = keep_k(v, p.K - (blk * BK + b_c[i]));
-                *reinterpret_cast<u32x4*>(Bs + b_lds[i][0]) = v;
+                *reinterpret_cast<u32x4*>(Bs + b_lds[i]) = v;
             } else {
                 // Rows of a K x N B past K read as zero (out of range).
-#pragma unroll
-                for (int q = 0; q < BQ; ++q) *reinterpret_cast<u32x4*>(Bs + b_lds[i][q]) = sb[slot][i][q];
+                *reinterpret_cast<u32x4*>(Bs + b_lds[i]) = sb[slot][i];
             }
         }
     };
