@@ -70,7 +70,10 @@ struct RowdotArgs {
     const float* scale; // per-column scale of mode 3
 };
 constexpr int kRowdotWaves = 8;
-constexpr int rowdot_rows(int mr) { return mr <= 2 ? 8 : (mr <= 4 ? 4 : 2); }
+#ifndef DNNOPT_ROWDOT_R58
+#define DNNOPT_ROWDOT_R58 2  // rows of B per wave for 4 < M <= 8
+#endif
+constexpr int rowdot_rows(int mr) { return mr <= 2 ? 8 : (mr <= 4 ? 4 : DNNOPT_ROWDOT_R58); }
 // Rows of B per wave for a mode (0 fp32, 1 bf16, 2 / 3 int8).  An int8 row
 // of B is a quarter of an fp32 one, so more waves with 2 rows each keep more
 // of it in flight (measured at K = 4096: 1 / 2 / 4 rows per wave 5.9 / 5.5
