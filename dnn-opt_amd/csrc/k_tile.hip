@@ -543,35 +543,42 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     auto write_stage = [&](int slot, int buf, int blk) {
         char* As = lds + buf * STAGE;
         char* Bs = As + A_BYTES;
-        // Only the block holding k = K - 1 has elements of k-contiguous rows
-        // past K (the next row's data): zero them.  Rows of a K x N B past K
-        // read as zero (out of range).
-        const bool tail = (blk + 1) * BK > p.K;
-        auto keep_k = [&](u32x4 v, int kvalid) {
+        if ((blk + 1) * BK > p.K) {
+            // Only the block holding k = K - 1 has elements of k-contiguous
+            // rows past K (the next row's data): zero them.  Rows of a K x N
+            // B past K read as zero (out of range).  A separate, rarely taken
+            // path: computed on every block, the masks cost ~50 vector
+            // instructions per block and wave.
+            const int kv = p.K - blk * BK;
+            auto keep_k = [&](u32x4 v, int kvalid) {
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                const int keep = kvalid - 2 * d;
-                v[d] = keep >= 2 ? v[d] : (keep == 1 ? (v[d] & 0xFFFFu) : 0u);
+                for (int d = 0; d < 4; ++d) {
+                    const int keep = kvalid - 2 * d;
+                    v[d] = keep >= 2 ? v[d] : (keep == 1 ? (v[d] & 0xFFFFu) : 0u);
+                }
+                return v;
+            };
+#pragma unroll
+            for (int i = 0; i < AU; ++i)
+                if (ACH % NTH == 0 || t + i * NTH < ACH)
+                    *reinterpret_cast<u32x4*>(As + a_lds[i]) = keep_k(sa[slot][i], kv - a_c[i]);
+#pragma unroll
+            for (int i = 0; i < BU; ++i) {
+                if (BUN % NTH != 0 && t + i * NTH >= BUN) continue;
+                *reinterpret_cast<u32x4*>(Bs + b_lds[i]) = TB ? keep_k(sb[slot][i], kv - b_c[i]) : sb[slot][i];
             }
-            return v;
-        };
-#pragma unroll
-        for (int i = 0; i < AU; ++i) {
-            u32x4 v = sa[slot][i];
-            if (tail) v = keep_k(v, p.K - (blk * BK + a_c[i]));
-            if (ACH % NTH == 0 || t + i * NTH < ACH) *reinterpret_cast<u32x4*>(As + a_lds[i]) = v;
+            // Keeps the masked stores in this branch: merged with the plain
+            // path they would become per-element selects on every block.
+            asm volatile("" ::: "memory");
+            return;
         }
+#pragma unroll
+        for (int i = 0; i < AU; ++i)
+            if (ACH % NTH == 0 || t + i * NTH < ACH) *reinterpret_cast<u32x4*>(As + a_lds[i]) = sa[slot][i];
 #pragma unroll
         for (int i = 0; i < BU; ++i) {
             if (BUN % NTH != 0 && t + i * NTH >= BUN) continue;
-            if constexpr (TB) {
-                u32x4 v = sb[slot][i];
-                if (tail) v = keep_k(v, p.K - (blk * BK + b_c[i]));
-                *reinterpret_cast<u32x4*>(Bs + b_lds[i]) = v;
-            } else {
-                // Rows of a K x N B past K read as zero (out of range).
-                *reinterpret_cast<u32x4*>(Bs + b_lds[i]) = sb[slot][i];
-            }
+            *reinterpret_cast<u32x4*>(Bs + b_lds[i]) = sb[slot][i];
         }
     };
 
