@@ -102,19 +102,23 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
 
     // Operands of one 256-byte k block, loaded one block ahead of the MFMAs
     // that consume them (two register sets, alternating).
+    // blk >= b_hi: a block past this wave's range, loaded only to keep the
+    // loop free of conditional loads -- every offset is out of range, so it
+    // reads nothing from memory.
     auto load_blk = [&](int blk, i32x4 (&a)[MT][4], i32x4 (&b)[NT][4]) {
+        const bool live = blk < b_hi;
         const int kbase = blk * 256 + 16 * g;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int kc = kbase + 64 * j;
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const uint32_t off = (kc < p.K && arow[mt] != kOobOffset) ? arow[mt] + kc : kOobOffset;
+                const uint32_t off = (live && kc < p.K && arow[mt] != kOobOffset) ? arow[mt] + kc : kOobOffset;
                 a[mt][j] = load16<AL>(ra, off);
             }
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                const uint32_t off = (brow[nt] != kOobOffset) ? brow[nt] + kc : kOobOffset;
+                const uint32_t off = (live && brow[nt] != kOobOffset) ? brow[nt] + kc : kOobOffset;
                 b[nt][j] = load16<AL>(rb, off);
             }
         }
@@ -141,9 +145,8 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
     for (; blk + 2 <= b_hi; blk += 2) {
         load_blk(blk + 1, a1, b1);
         compute_blk(blk, a0, b0);
-        // The block after this pair, or (at the end) the last block again,
-        // so that the load is unconditional.
-        load_blk(min(blk + 2, b_hi - 1), a0, b0);
+        // The block after this pair (out of range at the end: no traffic).
+        load_blk(blk + 2, a0, b0);
         compute_blk(blk + 1, a1, b1);
     }
     if (blk < b_hi) compute_blk(blk, a0, b0);
