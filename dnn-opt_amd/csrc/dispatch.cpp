@@ -44,7 +44,8 @@
 //   (force an LDS-staged bf16 tile configuration, index 5 and up),
 //   DNNOPT_S8_CFG / DNNOPT_S8_SPLITS (force the int8 configuration / splits),
 //   DNNOPT_TALL=0 (keep tall-skinny fp32 GEMMs on the register-only tiles),
-//   DNNOPT_TALL_WGS_PER_CU (default 1), DNNOPT_S8_ROWDOT=0 (int8 M <= 4 on
+//   DNNOPT_TALL_WGS_PER_CU (default 1), DNNOPT_TALL_RT (force 16- or 32-row
+//   tall tiles: 1 or 2), DNNOPT_S8_ROWDOT=0 (int8 M <= 4 on
 //   the MFMA tiles), DNNOPT_KOUTER=0 (k-major fp32 operands on the register
 //   tiles), DNNOPT_KOUTER_WGS_PER_CU (default 1).
 #include <stdlib.h>
@@ -410,6 +411,8 @@ int plan_tall(int transB, int M, int N, int K, int lda, Launch* L) {
         if (K < 256 || ceil_div(M, 16) * 2 < waves) return DNNOPT_ERR_UNSUPPORTED;
         rt = 1;
     }
+    static const int forced_rt = env_int("DNNOPT_TALL_RT", 0);
+    if (forced_rt == 1 || forced_rt == 2) rt = forced_rt;
     const long long tiles = ceil_div(M, 16 * rt);
     // Persistent: one workgroup per CU by default, no more than there are row
     // tiles for their waves.  More row tiles per wave keep loads, MFMAs and
