@@ -161,6 +161,11 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
         G = std::min<long long>(g_target, T * smax);
         if (G >= cus) G = std::max<long long>(T, G / cus * cus);
     }
+    // A last tile of at most a quarter width finishes its splits early: round
+    // G up to whole splits per tile so that the extra workgroups take over
+    // those CUs (N = 4099: 272 instead of 256 workgroups, 1-3% faster).
+    if (G > T && G % T != 0 && N - (T - 1) * tw <= tw / 4)
+        G = std::min<long long>(ceil_div(G, T) * T, T * smax);
     static const int forced = env_int("DNNOPT_SKINNY_WGS", 0);
     if (forced > 0) G = std::min<long long>(std::max<long long>(forced, T), T * smax);
     G = std::max<long long>(G, T);
