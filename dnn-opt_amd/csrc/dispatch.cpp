@@ -152,7 +152,8 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
     // G workgroups, about skinny_wgs_per_cu() per CU, shared by the T column
     // tiles as G/T or G/T + 1 k-splits each (balanced work per workgroup).
     // When there is more than one CU's worth of work, G is a whole multiple
-    // of the CU count so that no CU runs one workgroup more than the others.
+    // of the CU count so that no CU runs one workgroup more than the others
+    // (then adjusted to whole splits per tile, below).
     const long long g_target = cus * skinny_wgs_per_cu();
     long long G;
     if (T >= g_target) {
@@ -161,11 +162,19 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
         G = std::min<long long>(g_target, T * smax);
         if (G >= cus) G = std::max<long long>(T, G / cus * cus);
     }
-    // A last tile of at most a quarter width finishes its splits early: round
-    // G up to whole splits per tile so that the extra workgroups take over
-    // those CUs (N = 4099: 272 instead of 256 workgroups, 1-3% faster).
-    if (G > T && G % T != 0 && N - (T - 1) * tw <= tw / 4)
-        G = std::min<long long>(ceil_div(G, T) * T, T * smax);
+    // Whole splits per column tile: the workgroups of a tile with one split
+    // fewer run longer and set the kernel's time, so an uneven share is
+    // rounded -- up when the last tile is at most a quarter wide (its
+    // workgroups finish early and the extra ones take over their CUs; N = 4099:
+    // 272 instead of 256 workgroups, 1-3% faster), else down when that idles
+    // at most a fifth of the CUs (N = 11003: 215, 4% faster; bf16 N = 11008:
+    // 242, 4% faster).
+    if (G > T && G % T != 0) {
+        if (N - (T - 1) * tw <= tw / 4)
+            G = std::min<long long>(ceil_div(G, T) * T, T * smax);
+        else if (G % T * 5 <= G)
+            G = G / T * T;
+    }
     static const int forced = env_int("DNNOPT_SKINNY_WGS", 0);
     if (forced > 0) G = std::min<long long>(std::max<long long>(forced, T), T * smax);
     G = std::max<long long>(G, T);

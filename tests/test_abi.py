@@ -83,13 +83,13 @@ def test_plans_for_the_configs(lib):
             tiles = -(-N // 256)
             # G >= T workgroups, each tile split G/T or G/T + 1 ways
             assert p["grid_x"] >= tiles and p["splits"] == -(-p["grid_x"] // tiles)
-            # more than one CU's worth of work: a whole number of workgroups per CU,
-            # or whole splits per tile when the last tile is at most a quarter wide
-            if p["grid_x"] >= 256:
-                if N - (tiles - 1) * 256 <= 64:
-                    assert p["grid_x"] % tiles == 0 and p["grid_x"] >= 256, p
-                else:
-                    assert p["grid_x"] % 256 == 0 or p["grid_x"] == tiles
+            # whole splits per column tile: 256 workgroups rounded up when the last
+            # tile is at most a quarter wide, else down (at most a fifth of the CUs idle)
+            assert p["grid_x"] % tiles == 0, p
+            if N - (tiles - 1) * 256 <= 64:
+                assert p["grid_x"] >= 256, p
+            elif N > 4096:
+                assert 256 - 256 // 5 <= p["grid_x"] <= 256, p
     assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TALL_F32  # C3 N=16: B resident in LDS
     assert lib.plan_sgemm(65536, 64, 256)["kernel"] == b.K_TALL_F32
     p = lib.plan_sgemm(64, 64, 262144, transA=1)  # C3 split-K: k-major outer-product kernel
