@@ -45,7 +45,8 @@
 //   DNNOPT_S8_CFG / DNNOPT_S8_SPLITS (force the int8 configuration / splits),
 //   DNNOPT_TALL=0 (keep tall-skinny fp32 GEMMs on the register-only tiles),
 //   DNNOPT_TALL_WGS_PER_CU (default 1), DNNOPT_TALL_RT (force 16- or 32-row
-//   tall tiles: 1 or 2), DNNOPT_S8_ROWDOT=0 (int8 M <= 4 on
+//   tall tiles: 1 or 2), DNNOPT_ROWDOT_KW (force the row-dot k-split: 1, 2,
+//   4 or 8 waves), DNNOPT_S8_ROWDOT=0 (int8 M <= 4 on
 //   the MFMA tiles), DNNOPT_KOUTER=0 (k-major fp32 operands on the register
 //   tiles), DNNOPT_KOUTER_WGS_PER_CU (default 1).
 #include <stdlib.h>
@@ -388,6 +389,8 @@ int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
     // per CU, as long as each wave keeps whole multi-step k-ranges.
     int kw = 1;
     while (kw < 8 && ceil_div(N, (kRowdotWaves / kw) * R) < 2 * cus && steps / (2 * kw) >= kSteps) kw *= 2;
+    static const int forced_kw = env_int("DNNOPT_ROWDOT_KW", 0);
+    if (forced_kw == 1 || forced_kw == 2 || forced_kw == 4 || forced_kw == 8) kw = forced_kw;
     const long long rows_per_wg = (kRowdotWaves / kw) * R;
     const long long G = ceil_div(N, rows_per_wg);
     if (G > 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
