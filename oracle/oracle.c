@@ -21,8 +21,13 @@
  *                         built in oracle/_ref); closed-form tie cases.
  *   orc_saxpy             bit-exact vs the reference's cblas_saxpy.cpp built
  *                         in oracle/_ref for the scalar (x86) build.
+ *   orc_gemm_int8_dynq    closed forms with scales 1 and 2 whose quantized
+ *                         values include exact ties (0.5, 1.5, 2.5, -0.5,
+ *                         -2.5) and fractions (63.7): only round-to-nearest-
+ *                         even passes (copies built with truncf or roundf
+ *                         are compiled and rejected by the tests).
  *   orc_gemv_1xn_f32, orc_smallm_wide_f32, orc_adaptive_f32, orc_gemm_bf16,
- *   orc_gemm_int8_dynq, orc_cblas_sgemm, orc_onednn_sgemm,
+ *   orc_cblas_sgemm, orc_onednn_sgemm,
  *   orc_onednn_gemm_bf16bf16f32:
  *                         the reference's NEON kernels cannot run here (no
  *                         AArch64 toolchain or emulator); pinned by exact
@@ -345,8 +350,16 @@ void orc_gemm_bf16(int M, int N, int K, float alpha, const uint16_t* A, int lda,
  * ---------------------------------------------------------------------- */
 static float quant_scale(float amax) { return amax == 0.0f ? 1.0f : amax / 127.0f; }
 
+/* The reference rounds with lrintf (nearest, ties to even, in the default
+ * rounding mode).  ORC_QUANT_ROUND exists only so that tests can build
+ * deliberately wrong copies of this oracle (truncf, roundf) and show that the
+ * tie/fraction closed-form test rejects them. */
+#ifndef ORC_QUANT_ROUND
+#define ORC_QUANT_ROUND rintf
+#endif
+
 static int8_t quant_s8(float v, float inv) {
-    float q = rintf(v * inv);
+    float q = ORC_QUANT_ROUND(v * inv);
     if (q > 127.0f) q = 127.0f;
     if (q < -128.0f) q = -128.0f;
     return (int8_t)(int)q;

@@ -221,3 +221,48 @@ def hook_operands(opA: np.ndarray, opB: np.ndarray, ta: str, tb: str, pad=0, dty
 def small_ints(orc, n, tid, lim=3, seed=SEED):
     """Integers in [-lim, lim] as float32 (every product and short sum exact)."""
     return np.rint(uniform(orc, n, tid, -lim - 0.499, lim + 0.499, seed)).astype(np.float32)
+
+
+# ---------------------------------------------------------------- int8 quantization ties
+# The fp32-API int8 path quantizes with lrintf: nearest, ties to even
+# (reference: src/gemm/gemm_pack_int8.cpp:66-71).  These operands have
+# per-tensor scales 1 (max|A| = 127) and 2 (max|B| = 254, x * 0.5 exact), so
+# every quantized value is the rounding of the listed number itself: exact
+# ties (0.5, 1.5, 2.5, -0.5, -2.5, -63.5, 62.5) and fractions (63.7), where
+# truncation and rounding half away from zero both give other integers.
+DYNQ_TIE_A = [127.0, 0.5, 1.5, 2.5, -0.5, -2.5, 63.7, -63.5, 62.5]
+DYNQ_TIE_B = [254.0, 1.0, 3.0, 5.0, -1.0, -5.0, 127.4, -127.0, 125.0]
+DYNQ_TIE_Q = [127, 0, 2, 2, 0, -2, 64, -64, 62]
+
+
+def dynq_tie_cases():
+    """(name, M, N, K, A, B, expected C) with A row-major M x K and B K x N,
+    alpha = 1, beta = 0.  Every product and sum is an exact small integer, so
+    C must equal the expected values bit for bit."""
+    q = np.array(DYNQ_TIE_Q, np.float64)
+    k = len(DYNQ_TIE_A)
+    out = []
+    # A's quantization against B = 127 I (scale 1): C[0][j] = 127 q(A[j]).
+    A = np.array([DYNQ_TIE_A], np.float32)
+    B = (127.0 * np.eye(k)).astype(np.float32)
+    out.append(("A ties, scale 1, M=1", 1, k, k, A, B, (127.0 * q)[None, :].astype(np.float32)))
+    # 20 rows (past the 16-row MFMA tiles): row i is the tie row rotated by i.
+    A = np.stack([np.roll(DYNQ_TIE_A, i) for i in range(20)]).astype(np.float32)
+    want = np.stack([np.roll(q, i) for i in range(20)]) * 127.0
+    out.append(("A ties, scale 1, M=20", 20, k, k, A, B, want.astype(np.float32)))
+    # B's quantization (scale 2) against A = [127] (scale 1): C[0][j] = 2 * 127 q(B[j]).
+    A = np.array([[127.0]], np.float32)
+    B = np.array([DYNQ_TIE_B], np.float32)
+    out.append(("B ties, scale 2, K=1", 1, k, 1, A, B, (254.0 * q)[None, :].astype(np.float32)))
+    return out
+
+
+def check_dynq_ties(gemm_int8_f32):
+    """gemm_int8_f32(M, N, K, A, B) -> C (M x N float32).  Raises
+    AssertionError naming the first case whose C is not bit-exact."""
+    for name, M, N, K, A, B, want in dynq_tie_cases():
+        got = np.asarray(gemm_int8_f32(M, N, K, A, B), np.float32).reshape(M, N)
+        if not np.array_equal(got, want):
+            bad = np.argwhere(got != want)[0]
+            raise AssertionError(f"int8 quantization ties ({name}): C{tuple(bad)} = {got[tuple(bad)]}, "
+                                 f"want {want[tuple(bad)]}")

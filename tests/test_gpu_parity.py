@@ -407,6 +407,19 @@ def test_int8_dynamic_quant_matches_oracle(lib, orc, dev, M, N, K):
         assert np.array_equal(host(dC).view(np.uint32), Co.view(np.uint32))
 
 
+def test_int8_dynamic_quant_rounding_ties(lib, dev):
+    """Quantized values that are exact ties and fractions (scales 1 and 2):
+    the device quantizer must round to nearest even like the reference's
+    lrintf (src/gemm/gemm_pack_int8.cpp:66-71), independently of the oracle."""
+
+    def run(M, N, K, A, B):
+        dC = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+        lib.gemm_int8_f32(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, 0.0, dC, N, stream=stream())
+        return host(dC)
+
+    u.check_dynq_ties(run)
+
+
 # ---------------------------------------------------------------- saxpy, C++ and BLAS APIs on host memory
 def test_saxpy(lib, orc, dev):
     for n, incx, incy in [(1, 1, 1), (1000, 1, 1), (777, 3, 2)]:

@@ -249,6 +249,46 @@ def test_int8_dynq_closed_form(orc):
     assert C2.tolist() == [2.5, -3.5]
 
 
+def _oracle_dynq(so):
+    def run(M, N, K, A, B):
+        A = np.ascontiguousarray(A, np.float32)
+        B = np.ascontiguousarray(B, np.float32)
+        C = np.full(M * N, np.nan, np.float32)
+        so.orc_gemm_int8_dynq(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 0.0, u.ptr(C), N)
+        return C
+
+    return run
+
+
+def test_int8_dynq_rounding_ties(orc):
+    # Quantized values that are exact ties or fractions: only nearest-even
+    # rounding (lrintf, src/gemm/gemm_pack_int8.cpp:66-71) gives these C.
+    u.check_dynq_ties(_oracle_dynq(orc))
+
+
+@pytest.mark.parametrize("wrong", ["truncf", "roundf", "floorf"])
+def test_int8_dynq_ties_reject_other_roundings(tmp_path, wrong):
+    """Build copies of the oracle whose quantizer rounds the wrong way and
+    show that the tie test rejects each (a planted mistake, on the CPU)."""
+    import ctypes
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler on this host")
+    so_path = tmp_path / f"liboracle_{wrong}.so"
+    subprocess.run([cc, "-O1", "-fPIC", "-ffp-contract=off", "-fopenmp", "-std=c11", "-shared",
+                    f"-DORC_QUANT_ROUND={wrong}", "-o", str(so_path), os.path.join(u.ROOT, "oracle", "oracle.c"),
+                    "-lm"], check=True)
+    bad = ctypes.CDLL(str(so_path))
+    res, args = u.ORACLE_ABI["orc_gemm_int8_dynq"]
+    bad.orc_gemm_int8_dynq.restype = res
+    bad.orc_gemm_int8_dynq.argtypes = args
+    with pytest.raises(AssertionError, match="quantization ties"):
+        u.check_dynq_ties(_oracle_dynq(bad))
+
+
 def test_int8_dynq_reference_tolerance(orc):
     # tests/test_gemm_correctness.cpp:145 bounds the int8 path by K * 2e-2.
     for M, N, K in [(1, 128, 64), (7, 13, 5), (3, 3, 1000), (13, 17, 19)]:
