@@ -4,12 +4,16 @@
                     [--detail FILE] [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input.  The
-default workload is config C2 (the configuration the headline metric is
+headline workload is config C2 (the configuration the headline metric is
 quoted on): fp32 C = A B + C for M in {2,3,5,7} x N in {1009,4099,11003},
 K = 2048, alpha = beta = 1, A, B ~ N(0, 0.02), C ~ U[-1, 1).  One step runs
-all twelve shapes once.  Other workloads (c1, c3, c4, c5) are selectable for
-per-config measurements; `--workload all` writes one line per workload to
---detail and prints the default line.
+all twelve shapes once; its rate is `value`.  The default run also times the
+other configs -- C1, C3, C4 through the bf16-storage entry and through the
+fp32-input gemm_bf16 (c4f), C5 -- each as its own workload, and reports
+their step rates, dominant kernels and per-shape GB/s, TFLOP/s and roofline
+fractions under `configs`.  `--workload NAME` times one workload (its rate
+becomes `value`); `--workload all` adds the oneDNN-hook workload;
+`--detail FILE` appends the full per-workload records.
 
 `value` is the algorithmic bytes of a step (sA*M*K + sB*K*N + sC*M*N*(1 +
 [beta != 0]), each operand counted once) divided by the wall time of the
@@ -109,6 +113,13 @@ def workload(name):
         return ("C4: bf16 storage, fp32 accumulate/output, M in {1,4,32,256} x N=11008 x K=4096, "
                 "weights ~ N(0,0.02), activations ~ N(0,1)", [
                     Case(f"c4_m{M}", "bf16", M, 11008, 4096, init={"A": ("n", 0, 1), "B": ("n", 0, 0.02)},
+                         dtype="bf16") for M in (1, 4, 32, 256)])
+    if name == "c4f":
+        # the same shapes through the fp32-input gemm_bf16 (operands stored
+        # fp32, rounded to bf16 in registers; src/gemm/gemm.cpp:379-416)
+        return ("C4 via fp32-input gemm_bf16: fp32 storage rounded to bf16, fp32 accumulate/output, "
+                "M in {1,4,32,256} x N=11008 x K=4096, weights ~ N(0,0.02), activations ~ N(0,1)", [
+                    Case(f"c4f_m{M}", "f2b", M, 11008, 4096, init={"A": ("n", 0, 1), "B": ("n", 0, 0.02)},
                          dtype="bf16") for M in (1, 4, 32, 256)])
     if name == "c5":
         cs = []
@@ -300,10 +311,14 @@ def run_gpu(args, wl_name):
         d = [a.elapsed_time(bb) / reps[i] for a, bb in samples]
         med = statistics.median(d)
         launch_ms.append(sum(d) / len(d))
+        t_hbm = c.bytes_alg() / (HBM_PEAK_GBS * 1e9)
+        t_mfma = c.flops_alg() / (PEAKS_TFLOPS.get(c.dtype, 157.3) * 1e12)
         per_case.append({
             "case": c.name, "M": c.M, "N": c.N, "K": c.K, "kernel": keys[i][0], "plan": keys[i][1],
             "us_median": med * 1e3, "us_mean": launch_ms[-1] * 1e3,
             "GBps": c.bytes_alg() / (med * 1e-3) / 1e9, "TFLOPs": c.flops_alg() / (med * 1e-3) / 1e12,
+            "bound": "hbm" if t_hbm >= t_mfma else "mfma",
+            "roofline_frac": max(t_hbm, t_mfma) / (med * 1e-3),
         })
     # dominant kernel instance: largest share of the per-launch time
     groups = {}
@@ -634,13 +649,35 @@ def copy_calibration(mib):
     print(json.dumps({"copy_bytes_per_launch": n, "launches": 5}), flush=True)
 
 
+def config_summary(r):
+    """Per-config figures of the JSON line: the step's GB/s and TFLOP/s, the
+    dominant kernel's roofline, and each shape's time, GB/s, TFLOP/s and
+    roofline fraction t_roof / t (t_roof = max(bytes / HBM peak, flops / MFMA
+    peak))."""
+    ms = r["ms_per_step"]
+    rf = r["roofline"]
+    return {
+        "workload": r["desc"], "GBps_step": round(r["value"], 1),
+        "TFLOPs_step": round(r["step_flops"] / (ms * 1e-3) / 1e12, 3), "us_per_step": round(ms * 1e3, 2),
+        "dominant": {"kernel": rf["kernel"], "bound": rf["bound"], "achieved": rf["achieved"], "unit": rf["unit"],
+                     "frac": rf["frac"], "launch_us": rf["launch_us"], "traffic": rf["traffic"]},
+        "cases": [{"case": c["case"], "kernel": c["kernel"], "us": round(c["us_median"], 2),
+                   "GBps": round(c["GBps"], 1), "TFLOPs": round(c["TFLOPs"], 2), "bound": c["bound"],
+                   "roofline_frac": round(c["roofline_frac"], 4)} for c in r["per_case"]],
+    }
+
+
 # ---------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "hook", "all"])
+    ap.add_argument("--workload", default="default",
+                    choices=["default", "c1", "c2", "c3", "c4", "c4f", "c5", "hook", "all"],
+                    help="default: C2 is `value`, C1, C3, C4 (bf16 storage and fp32 inputs) and C5 are timed too "
+                         "and reported under `configs`; a single workload makes it `value`; all adds the "
+                         "oneDNN-hook workload")
     ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
@@ -670,8 +707,12 @@ def main():
               "(sharding across GPUs is not built).", file=sys.stderr)
         sys.exit(2)
 
-    names = ["c1", "c2", "c3", "c4", "c5", "hook"] if args.workload == "all" else [args.workload]
-    main_name = "c2" if args.workload == "all" else args.workload
+    if args.workload in ("default", "all"):
+        names = ["c2", "c1", "c3", "c4", "c4f", "c5"] + (["hook"] if args.workload == "all" else [])
+        main_name = "c2"
+    else:
+        names = [args.workload]
+        main_name = args.workload
     results = {}
     for wl in names:
         r = run_gpu(args, wl)
@@ -694,6 +735,7 @@ def main():
         "roofline_kernel": {k: r["roofline"][k] for k in ("kernel", "launch_us", "bytes_per_launch")},
         "cpu_baseline": cpu,
         "cpu_reference": cpu_ref,
+        "configs": {wl: config_summary(rr) for wl, rr in results.items() if wl != main_name},
     }
     if args.detail:
         os.makedirs(os.path.dirname(os.path.abspath(args.detail)), exist_ok=True)

@@ -8,15 +8,23 @@
 // There is no host compute path: if no device is visible or a launch fails,
 // C is left unmodified and the failure is recorded (dnnopt_hip_last_status)
 // and reported once on stderr.
+//
+// Threads: every host thread enqueues on its own stream (thread_stream) and
+// stages through its own buffers, so concurrent calls from several threads
+// share no device memory and run side by side, as the reference's calls are
+// reentrant.  The streams are ordered with the null stream, so device
+// operands written by earlier null-stream work are read after it.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
 #include <cstdio>
 #include <cstring>
+#include <map>
 
 #include "api_internal.h"
 #include "dnnopt/gemm/gemm.h"
 #include "dnnopt_hip.h"
+#include "host.h"
 
 namespace dnnopt_api {
 
@@ -49,9 +57,27 @@ struct StageBuf {
     }
 };
 
-thread_local StageBuf t_stage[4];
+// Staging buffers of this thread, per device.
+struct StageSet {
+    StageBuf slot[4];
+};
+thread_local std::map<int, StageSet> t_stage;
+
+StageBuf& stage_buf(int slot, int* st) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        *st = DNNOPT_ERR_NO_DEVICE;
+    }
+    return t_stage[dev].slot[slot];
+}
 
 }  // namespace
+
+void* api_stream(int* st) {
+    if (*st != DNNOPT_OK) return nullptr;
+    return dnnopt_hip::thread_stream(st);
+}
 
 void record(int status, const char* what) {
     t_last_status = status;
@@ -75,17 +101,21 @@ bool is_device_pointer(const void* p) {
     return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
 
-Operand stage_in(const void* host, size_t bytes, int slot, bool copy, int* st) {
+Operand stage_in(const void* host, size_t bytes, int slot, bool copy, void* stream, int* st) {
     Operand o;
     if (*st != DNNOPT_OK || bytes == 0) return o;
     if (is_device_pointer(host)) {
         o.dev = const_cast<void*>(host);
         return o;
     }
-    void* d = t_stage[slot].get(bytes, st);
+    StageBuf& buf = stage_buf(slot, st);
+    if (*st != DNNOPT_OK) return o;
+    void* d = buf.get(bytes, st);
     if (!d) return o;
     if (copy) {
-        hipError_t e = hipMemcpy(d, host, bytes, hipMemcpyHostToDevice);
+        // Ordered before the launch on the same stream; the host memory is
+        // pageable, so the copy has read it when the call returns.
+        hipError_t e = hipMemcpyAsync(d, host, bytes, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream));
         if (e != hipSuccess) {
             (void)hipGetLastError();
             *st = DNNOPT_ERR_HIP;
@@ -98,9 +128,10 @@ Operand stage_in(const void* host, size_t bytes, int slot, bool copy, int* st) {
     return o;
 }
 
-int stage_out(const Operand& o) {
+int stage_out(const Operand& o, void* stream) {
     if (!o.host) return DNNOPT_OK;
-    hipError_t e = hipMemcpy(o.host, o.dev, o.bytes, hipMemcpyDeviceToHost);
+    hipError_t e = hipMemcpyAsync(o.host, o.dev, o.bytes, hipMemcpyDeviceToHost, static_cast<hipStream_t>(stream));
+    if (e == hipSuccess) e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return DNNOPT_ERR_HIP;
@@ -108,8 +139,8 @@ int stage_out(const Operand& o) {
     return DNNOPT_OK;
 }
 
-int sync_default_stream() {
-    hipError_t e = hipStreamSynchronize(nullptr);
+int sync_stream(void* stream) {
+    hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
     if (e != hipSuccess) {
         (void)hipGetLastError();
         return DNNOPT_ERR_HIP;
@@ -133,20 +164,21 @@ int sgemm_any(int ta, int tb, int M, int N, int K, float alpha, const float* A, 
     if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
     if (dnnopt_hip_device_count() == 0) return DNNOPT_ERR_NO_DEVICE;
     int st = DNNOPT_OK;
-    Operand a = stage_in(A, ta ? extent(K, M, lda, 4) : extent(M, K, lda, 4), 0, true, &st);
-    Operand b = stage_in(B, tb ? extent(N, K, ldb, 4) : extent(K, N, ldb, 4), 1, true, &st);
-    Operand c = stage_in(C, extent(M, N, ldc, 4), 2, naive || c_read_or_kept(beta, ldc, N), &st);
+    void* s = api_stream(&st);
+    Operand a = stage_in(A, ta ? extent(K, M, lda, 4) : extent(M, K, lda, 4), 0, true, s, &st);
+    Operand b = stage_in(B, tb ? extent(N, K, ldb, 4) : extent(K, N, ldb, 4), 1, true, s, &st);
+    Operand c = stage_in(C, extent(M, N, ldc, 4), 2, naive || c_read_or_kept(beta, ldc, N), s, &st);
     if (st != DNNOPT_OK) return st;
     if (naive)
         st = dnnopt_hip_sgemm_naive(M, N, K, alpha, (const float*)a.dev, lda, (const float*)b.dev, ldb, beta,
-                                    (float*)c.dev, ldc, nullptr);
+                                    (float*)c.dev, ldc, s);
     else
         st = dnnopt_hip_sgemm(ta, tb, M, N, K, alpha, (const float*)a.dev, lda, (const float*)b.dev, ldb, beta,
-                              (float*)c.dev, ldc, nullptr);
+                              (float*)c.dev, ldc, s);
     if (st != DNNOPT_OK) return st;
-    st = sync_default_stream();
+    st = sync_stream(s);
     if (st != DNNOPT_OK) return st;
-    return stage_out(c);
+    return stage_out(c, s);
 }
 
 }  // namespace dnnopt_api
@@ -175,14 +207,15 @@ void gemm_bf16(int M, int N, int K, float alpha, const float* A, int lda, const 
         } else if (dnnopt_hip_device_count() == 0) {
             st = DNNOPT_ERR_NO_DEVICE;
         } else {
-            Operand a = stage_in(A, extent(M, K, lda, 4), 0, true, &st);
-            Operand b = stage_in(B, extent(K, N, ldb, 4), 1, true, &st);
-            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), &st);
+            void* s = api_stream(&st);
+            Operand a = stage_in(A, extent(M, K, lda, 4), 0, true, s, &st);
+            Operand b = stage_in(B, extent(K, N, ldb, 4), 1, true, s, &st);
+            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), s, &st);
             if (st == DNNOPT_OK)
                 st = dnnopt_hip_gemm_bf16_f32in(M, N, K, alpha, (const float*)a.dev, lda, (const float*)b.dev, ldb,
-                                                beta, (float*)c.dev, ldc, nullptr);
-            if (st == DNNOPT_OK) st = sync_default_stream();
-            if (st == DNNOPT_OK) st = stage_out(c);
+                                                beta, (float*)c.dev, ldc, s);
+            if (st == DNNOPT_OK) st = sync_stream(s);
+            if (st == DNNOPT_OK) st = stage_out(c, s);
         }
     }
     record(st, "gemm_bf16");
@@ -197,14 +230,15 @@ void gemm_bf16_bf16bf16f32(int M, int N, int K, float alpha, const bfloat16_t* A
         } else if (dnnopt_hip_device_count() == 0) {
             st = DNNOPT_ERR_NO_DEVICE;
         } else {
-            Operand a = stage_in(A, extent(M, K, lda, 2), 0, true, &st);
-            Operand b = stage_in(B, extent(K, N, ldb, 2), 1, true, &st);
-            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), &st);
+            void* s = api_stream(&st);
+            Operand a = stage_in(A, extent(M, K, lda, 2), 0, true, s, &st);
+            Operand b = stage_in(B, extent(K, N, ldb, 2), 1, true, s, &st);
+            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), s, &st);
             if (st == DNNOPT_OK)
                 st = dnnopt_hip_gemm_bf16(M, N, K, alpha, (const uint16_t*)a.dev, lda, (const uint16_t*)b.dev, ldb,
-                                          beta, (float*)c.dev, ldc, nullptr);
-            if (st == DNNOPT_OK) st = sync_default_stream();
-            if (st == DNNOPT_OK) st = stage_out(c);
+                                          beta, (float*)c.dev, ldc, s);
+            if (st == DNNOPT_OK) st = sync_stream(s);
+            if (st == DNNOPT_OK) st = stage_out(c, s);
         }
     }
     record(st, "gemm_bf16_bf16bf16f32");
@@ -219,14 +253,15 @@ void gemm_int8(int M, int N, int K, float alpha, const float* A, int lda, const 
         } else if (dnnopt_hip_device_count() == 0) {
             st = DNNOPT_ERR_NO_DEVICE;
         } else {
-            Operand a = stage_in(A, extent(M, K, lda, 4), 0, true, &st);
-            Operand b = stage_in(B, extent(K, N, ldb, 4), 1, true, &st);
-            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), &st);
+            void* s = api_stream(&st);
+            Operand a = stage_in(A, extent(M, K, lda, 4), 0, true, s, &st);
+            Operand b = stage_in(B, extent(K, N, ldb, 4), 1, true, s, &st);
+            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), s, &st);
             if (st == DNNOPT_OK)
                 st = dnnopt_hip_gemm_int8_f32(M, N, K, alpha, (const float*)a.dev, lda, (const float*)b.dev, ldb,
-                                              beta, (float*)c.dev, ldc, nullptr);
-            if (st == DNNOPT_OK) st = sync_default_stream();
-            if (st == DNNOPT_OK) st = stage_out(c);
+                                              beta, (float*)c.dev, ldc, s);
+            if (st == DNNOPT_OK) st = sync_stream(s);
+            if (st == DNNOPT_OK) st = stage_out(c, s);
         }
     }
     record(st, "gemm_int8");
@@ -241,14 +276,15 @@ void gemm_int8_int8int8int32(int M, int N, int K, const int8_t* A, int lda, cons
         } else if (dnnopt_hip_device_count() == 0) {
             st = DNNOPT_ERR_NO_DEVICE;
         } else {
-            Operand a = stage_in(A, extent(M, K, lda, 1), 0, true, &st);
-            Operand b = stage_in(B, extent(N, K, ldb, 1), 1, true, &st);
-            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, ldc != N, &st);
+            void* s = api_stream(&st);
+            Operand a = stage_in(A, extent(M, K, lda, 1), 0, true, s, &st);
+            Operand b = stage_in(B, extent(N, K, ldb, 1), 1, true, s, &st);
+            Operand c = stage_in(C, extent(M, N, ldc, 4), 2, ldc != N, s, &st);
             if (st == DNNOPT_OK)
                 st = dnnopt_hip_gemm_s8s8s32(M, N, K, (const int8_t*)a.dev, lda, (const int8_t*)b.dev, ldb,
-                                             (int32_t*)c.dev, ldc, nullptr);
-            if (st == DNNOPT_OK) st = sync_default_stream();
-            if (st == DNNOPT_OK) st = stage_out(c);
+                                             (int32_t*)c.dev, ldc, s);
+            if (st == DNNOPT_OK) st = sync_stream(s);
+            if (st == DNNOPT_OK) st = stage_out(c, s);
         }
     }
     record(st, "gemm_int8_int8int8int32");

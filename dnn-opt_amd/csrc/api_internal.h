@@ -19,11 +19,16 @@ void set_threads(int n);
 int get_threads();
 
 bool is_device_pointer(const void* p);
-// Stage `bytes` of `host` into staging slot `slot` (0..3) unless it already is
-// device memory; `copy` = false skips the upload (output-only operand).
-Operand stage_in(const void* host, size_t bytes, int slot, bool copy, int* status);
-int stage_out(const Operand& o);
-int sync_default_stream();
+// The calling thread's stream on the current device (a hipStream_t), or
+// nullptr with *status set; nothing is done when *status is already an error.
+void* api_stream(int* status);
+// Stage `bytes` of `host` into this thread's staging slot `slot` (0..3) unless
+// it already is device memory; `copy` = false skips the upload (output-only
+// operand).  The upload is enqueued on `stream`.
+Operand stage_in(const void* host, size_t bytes, int slot, bool copy, void* stream, int* status);
+// Copy a staged operand back to host memory and wait for `stream`.
+int stage_out(const Operand& o, void* stream);
+int sync_stream(void* stream);
 // Bytes spanned by a rows x cols row-major block with row stride ld.
 size_t extent(int rows, int cols, int ld, size_t esize);
 

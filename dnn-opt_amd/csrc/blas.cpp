@@ -55,11 +55,12 @@ void cblas_saxpy(int N, float alpha, const float* X, int incX, float* Y, int inc
     } else if (dnnopt_hip_device_count() == 0) {
         st = DNNOPT_ERR_NO_DEVICE;
     } else {
-        Operand x = stage_in(X, ((size_t)(N - 1) * incX + 1) * 4, 0, true, &st);
-        Operand y = stage_in(Y, ((size_t)(N - 1) * incY + 1) * 4, 2, true, &st);
-        if (st == DNNOPT_OK) st = dnnopt_hip_saxpy(N, alpha, (const float*)x.dev, incX, (float*)y.dev, incY, nullptr);
-        if (st == DNNOPT_OK) st = sync_default_stream();
-        if (st == DNNOPT_OK) st = stage_out(y);
+        void* s = api_stream(&st);
+        Operand x = stage_in(X, ((size_t)(N - 1) * incX + 1) * 4, 0, true, s, &st);
+        Operand y = stage_in(Y, ((size_t)(N - 1) * incY + 1) * 4, 2, true, s, &st);
+        if (st == DNNOPT_OK) st = dnnopt_hip_saxpy(N, alpha, (const float*)x.dev, incX, (float*)y.dev, incY, s);
+        if (st == DNNOPT_OK) st = sync_stream(s);
+        if (st == DNNOPT_OK) st = stage_out(y, s);
     }
     record(st, "cblas_saxpy");
 }

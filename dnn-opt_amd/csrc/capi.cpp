@@ -75,7 +75,7 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
     if ((L.cfg >= kTileFirstLds && L.cfg != kTileKOuter && L.mode == kTileBF16 &&
          ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) != 0) ||
         (L.cfg == kTileKOuter && ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15u) != 0)) {
-        const int st = plan_tile(L.mode, ta, tb, M, N, K, lda, ldb, &L, false);
+        const int st = plan_tile(L.mode, ta, tb, M, N, K, lda, ldb, &L, false, ldc);
         if (st != DNNOPT_OK) return st;
     }
     TileArgs a{};
@@ -151,8 +151,9 @@ int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const f
     if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
     if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    StreamLock lock(s);
     Launch L;
-    int st = plan_sgemm(transA, transB, M, N, K, lda, ldb, &L);
+    int st = plan_sgemm(transA, transB, M, N, K, lda, ldb, &L, ldc);
     if (st != DNNOPT_OK) return st;
     if (L.family == DNNOPT_K_SKINNY_F32)
         return run_skinny(L, A, transA ? 1 : lda, transA ? lda : 1, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
@@ -190,6 +191,17 @@ int dnnopt_hip_plan_sgemm(int transA, int transB, int M, int N, int K, dnnopt_pl
     if (!dims_ok(M, N, K)) return DNNOPT_ERR_INVALID_ARG;
     Launch L;
     int st = plan_sgemm(transA, transB, M, N, K, transA ? M : K, transB ? K : N, &L);
+    if (st == DNNOPT_OK) *out = L.pub;
+    return st;
+}
+
+int dnnopt_hip_plan_sgemm_ex(int transA, int transB, int M, int N, int K, int lda, int ldb, int ldc,
+                             dnnopt_plan* out) {
+    if (!out || (transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return DNNOPT_ERR_INVALID_ARG;
+    if (!dims_ok(M, N, K)) return DNNOPT_ERR_INVALID_ARG;
+    if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N) return DNNOPT_ERR_INVALID_ARG;
+    Launch L;
+    int st = plan_sgemm(transA, transB, M, N, K, lda, ldb, &L, ldc);
     if (st == DNNOPT_OK) *out = L.pub;
     return st;
 }
@@ -243,10 +255,11 @@ static int gemm_bf16_common(int fp32_inputs, int M, int N, int K, float alpha, c
     if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
     if (lda < K || ldb < N || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
-    Launch L;
-    int st = plan_bf16(fp32_inputs, M, N, K, lda, ldb, &L);
-    if (st != DNNOPT_OK) return st;
     hipStream_t s = as_stream(stream);
+    StreamLock lock(s);
+    Launch L;
+    int st = plan_bf16(fp32_inputs, M, N, K, lda, ldb, &L, 0, ldc);
+    if (st != DNNOPT_OK) return st;
     if (L.family == DNNOPT_K_SKINNY_BF16 || L.family == DNNOPT_K_SKINNY_F2B)
         return run_skinny(L, A, lda, 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     return run_tile(L, 0, 0, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
@@ -265,10 +278,11 @@ int dnnopt_hip_gemm_bf16_ex(int transA, int transB, int M, int N, int K, float a
     if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
     hipStream_t s = as_stream(stream);
+    StreamLock lock(s);
     Launch L;
     if (transA && !transB && M <= 8) {
         // The skinny kernel reads a K x M A in place (A is M*K elements).
-        int st = plan_bf16(0, M, N, K, lda, ldb, &L);
+        int st = plan_bf16(0, M, N, K, lda, ldb, &L, 0, ldc);
         if (st != DNNOPT_OK) return st;
         return run_skinny(L, A, 1, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     }
@@ -285,7 +299,7 @@ int dnnopt_hip_gemm_bf16_ex(int transA, int transB, int M, int N, int K, float a
         A = static_cast<const uint16_t*>(ws);
         lda = ldt;
     }
-    int st = plan_bf16(0, M, N, K, lda, ldb, &L, transB);
+    int st = plan_bf16(0, M, N, K, lda, ldb, &L, transB, ldc);
     if (st != DNNOPT_OK) return st;
     if (L.family == DNNOPT_K_SKINNY_BF16) return run_skinny(L, A, lda, 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     if (L.family == DNNOPT_K_ROWDOT_BF16) return run_rowdot(L, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
@@ -305,10 +319,11 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
     const int aligned = ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) == 0 &&
                         (lda & 3) == 0 && (ldb & 3) == 0;
-    Launch L;
-    int st = plan_s8(epi, M, N, K, &L, aligned != 0, lda, ldb);
-    if (st != DNNOPT_OK) return st;
     hipStream_t s = as_stream(stream);
+    StreamLock lock(s);
+    Launch L;
+    int st = plan_s8(epi, M, N, K, &L, aligned != 0, lda, ldb, ldc);
+    if (st != DNNOPT_OK) return st;
     if (L.family == DNNOPT_K_ROWDOT_S8) {
         RowdotArgs r{};
         r.A = A;
@@ -371,6 +386,7 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
     if (lda < K || ldb < N || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
     hipStream_t s = as_stream(stream);
+    StreamLock lock(s);
     // Staging (slot 1): [int32 acc M*N][qA M x ldq][qB N x ldq][2 absmax words];
     // ldq pads K to 16 bytes so every quantized row is 16-byte aligned.
     const int ldq = (K + 15) & ~15;

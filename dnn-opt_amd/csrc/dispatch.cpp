@@ -231,8 +231,10 @@ int plan_kouter(int M, int N, int K, int lda, int ldb, Launch* L) {
     return DNNOPT_OK;
 }
 
-int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, bool lds_ok) {
+int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, bool lds_ok,
+              int ldc) {
     *L = Launch{};
+    if (ldc <= 0) ldc = N;
     if (mode == kTileF32 && transA && !transB && lds_ok && kouter_enabled() && M > 32 && M <= 64 && N > 32 &&
         N <= 64 && K >= kKOuterMinK && (lda & 3) == 0 && (ldb & 3) == 0 &&
         plan_kouter(M, N, K, lda, ldb, L) == DNNOPT_OK)
@@ -244,7 +246,8 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     const bool lds = mode != kTileF32 && lds_ok && !transA && (!transB || mode == kTileBF16) &&
                      (mode == kTileF2B || ((lda & 1) == 0 && (ldb & 1) == 0)) &&
                      ((long long)(M + 128) * lda + K) * es < 0x7FFFFFFFll &&
-                     (transB ? ((long long)(N + 128) * ldb + K) : ((long long)K * ldb + N)) * es < 0x7FFFFFFFll;
+                     (transB ? ((long long)(N + 128) * ldb + K) : ((long long)K * ldb + N)) * es < 0x7FFFFFFFll &&
+                     (long long)128 * ldc * 4 < 0x7FFFFFFFll;
     int cfg;
     static const int forced_cfg = env_int("DNNOPT_TILE_CFG", 0);
     if (lds) {
@@ -316,8 +319,11 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     return DNNOPT_OK;
 }
 
-int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int ldb) {
+int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int ldb, int ldc) {
     *L = Launch{};
+    if (ldc <= 0) ldc = N;
+    // The LDS-staged kernel addresses a C tile with 32-bit offsets.
+    if ((long long)128 * ldc * 4 >= 0x7FFFFFFFll) lds_ok = false;
     static const int forced_cfg = env_int("DNNOPT_S8_CFG", -1);
     // M <= 4 (B is stored N x K): the row-dot kernel streams every row of B
     // once in 1 KiB steps with exact int32 dot products and needs no partial
@@ -403,8 +409,9 @@ int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
     return DNNOPT_OK;
 }
 
-int plan_tall(int transB, int M, int N, int K, int lda, Launch* L) {
+int plan_tall(int transB, int M, int N, int K, int lda, Launch* L, int ldc) {
     *L = Launch{};
+    if (ldc <= 0) ldc = N;
     // N <= 12 (a quarter or more of the padded 16-column MFMA tile wasted)
     // and N <= 16 with short K stream faster through the register tiles
     // (64 x 16), whose per-k re-reads of B are small at that width; measured
@@ -415,6 +422,8 @@ int plan_tall(int transB, int M, int N, int K, int lda, Launch* L) {
     const size_t lds = tall_lds_bytes(nt, K);
     if (lds > 65536) return DNNOPT_ERR_UNSUPPORTED;
     if (((long long)(M - 1) * lda + K) * 4 >= 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
+    // C is stored through one descriptor from its first element.
+    if (((long long)(M - 1) * ldc + N) * 4 >= 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
     // Each wave runs its row tiles as one serial chain of MFMAs, so the kernel
     // needs about one tile for every wave of one workgroup per CU: 32-row
     // tiles from ~48K rows (on 256 CUs); 16-row tiles (half the chain) from
@@ -448,24 +457,24 @@ int plan_tall(int transB, int M, int N, int K, int lda, Launch* L) {
     return DNNOPT_OK;
 }
 
-int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L) {
+int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc) {
     if (M <= 8 && !transB) return plan_skinny(kSkinnyF32, M, N, K, ldb, L);
     if (M <= 8 && !transA && plan_rowdot(0, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
     static const bool tall_ok = [] {
         const char* e = getenv("DNNOPT_TALL");
         return !(e && *e && atoi(e) == 0);
     }();
-    if (tall_ok && !transA && plan_tall(transB, M, N, K, lda, L) == DNNOPT_OK) return DNNOPT_OK;
-    return plan_tile(kTileF32, transA, transB, M, N, K, lda, ldb, L);
+    if (tall_ok && !transA && plan_tall(transB, M, N, K, lda, L, ldc) == DNNOPT_OK) return DNNOPT_OK;
+    return plan_tile(kTileF32, transA, transB, M, N, K, lda, ldb, L, true, ldc);
 }
 
-int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB) {
+int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB, int ldc) {
     // B stored N x K has k-contiguous columns: MFMA tiles read it in place
     // for every M (the skinny kernel streams rows of a K x N B).
     if (M <= 8 && !transB) return plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L);
     if (transB && fp32_inputs) return DNNOPT_ERR_UNSUPPORTED;
     if (M <= 8 && plan_rowdot(1, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
-    return plan_tile(fp32_inputs ? kTileF2B : kTileBF16, 0, transB, M, N, K, lda, ldb, L);
+    return plan_tile(fp32_inputs ? kTileF2B : kTileBF16, 0, transB, M, N, K, lda, ldb, L, true, ldc);
 }
 
 }  // namespace dnnopt_hip

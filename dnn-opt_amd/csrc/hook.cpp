@@ -62,6 +62,7 @@ int ext_common(bool bf16, char transa, char transb, int64_t M, int64_t N, int64_
     if (K > 0 && (!A || !B || lda < (tA ? K : M) || ldb < (tB ? N : K))) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    StreamLock lock(s);
     const int m = (int)M, n = (int)N, k = (int)K;
     if (k == 0) {
         const int op = beta == 0.0f ? kCmZero : (beta != 1.0f ? kCmScale : kCmNone);
@@ -126,22 +127,23 @@ int onednn_common(bool bf16, const char* transa, const char* transb, const int64
     if (dnnopt_hip_device_count() == 0) return DNNOPT_ERR_NO_DEVICE;
     const size_t es = bf16 ? 2 : 4;
     int st = DNNOPT_OK;
+    void* s = api_stream(&st);
     Operand a, b;
     if (*K > 0) {
-        a = stage_in(A, (tA ? cm_extent(*K, *M, *lda) : cm_extent(*M, *K, *lda)) * es, 0, true, &st);
-        b = stage_in(B, (tB ? cm_extent(*N, *K, *ldb) : cm_extent(*K, *N, *ldb)) * es, 1, true, &st);
+        a = stage_in(A, (tA ? cm_extent(*K, *M, *lda) : cm_extent(*M, *K, *lda)) * es, 0, true, s, &st);
+        b = stage_in(B, (tB ? cm_extent(*N, *K, *ldb) : cm_extent(*K, *N, *ldb)) * es, 1, true, s, &st);
     }
     // C is uploaded unless every element of its extent is overwritten
     // without being read (beta == 0 and no gaps between columns).
-    Operand c = stage_in(C, cm_extent(*M, *N, *ldc) * 4, 2, *beta != 0.0f || *ldc > *M, &st);
-    Operand bs = bias ? stage_in(bias, (size_t)*M * 4, 3, true, &st) : Operand{};
+    Operand c = stage_in(C, cm_extent(*M, *N, *ldc) * 4, 2, *beta != 0.0f || *ldc > *M, s, &st);
+    Operand bs = bias ? stage_in(bias, (size_t)*M * 4, 3, true, s, &st) : Operand{};
     if (st != DNNOPT_OK) return st;
     st = ext_common(bf16, *transa, *transb, *M, *N, *K, *alpha, a.dev, *lda, b.dev, *ldb, *beta,
-                    static_cast<float*>(c.dev), *ldc, static_cast<const float*>(bs.dev), nullptr);
+                    static_cast<float*>(c.dev), *ldc, static_cast<const float*>(bs.dev), s);
     if (st != DNNOPT_OK) return st;
-    st = sync_default_stream();
+    st = sync_stream(s);
     if (st != DNNOPT_OK) return st;
-    return stage_out(c);
+    return stage_out(c, s);
 }
 
 }  // namespace

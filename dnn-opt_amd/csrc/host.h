@@ -20,8 +20,41 @@ int to_status(hipError_t e);
 // between launches) followed by `part_bytes` of partial-sum space.  Launches
 // on one stream are ordered, so they can share it; the buffer only grows.
 // Slot 0 serves the GEMM kernels, slot 1 the int8 quantization staging.
+// The caller must hold a StreamLock for `s` from this call until its last
+// launch that uses the buffer is enqueued.
 constexpr int kMaxTickets = 16384;
 int get_workspace(hipStream_t s, size_t part_bytes, void** part, unsigned** tickets, int slot = 0);
+
+// Serialises the calls that enqueue work on one stream of one device (the
+// current device).  Every entry point that may take workspace holds it from
+// planning until its last launch is enqueued, so that
+//   * the launches of two calls sharing a stream never interleave (a split-k
+//     kernel and its reduce kernel communicate through the stream's
+//     workspace, which the other call would overwrite), and
+//   * a workspace buffer is only freed (when it grows) by the holder of the
+//     lock, after synchronising the stream: no other call can still hold a
+//     pointer into it.
+// Recursive: entry points call one another on the same thread.
+class StreamLock {
+public:
+    explicit StreamLock(hipStream_t s);
+    ~StreamLock();
+    StreamLock(const StreamLock&) = delete;
+    StreamLock& operator=(const StreamLock&) = delete;
+
+private:
+    void* mu_;
+};
+
+// The calling thread's own stream on the current device, for the synchronous
+// host APIs (gemm.h, cblas.h, the oneDNN hook): each host thread gets a
+// distinct stream, hence distinct workspace, so that concurrent synchronous
+// calls from several threads neither share buffers nor wait on each other.
+// Streams are created with default flags and priority (ordered with the null
+// stream, like the null-stream launches they replace), taken from a pool of
+// the process and returned to it when the thread ends; they are never
+// destroyed.  nullptr (with *status set) if no stream could be created.
+hipStream_t thread_stream(int* status);
 
 // ---------------------------------------------------------------- dispatch
 struct Launch {
@@ -46,17 +79,21 @@ int split_reduce_mode();
 
 int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L);
 // fp32, large M, N <= 64, B small enough to stay in LDS (no transposed A).
-int plan_tall(int transB, int M, int N, int K, int lda, Launch* L);
+// ldc: row stride of C (0 = N); C is addressed with 32-bit offsets from its
+// first element, so ((M - 1) * ldc + N) * 4 must stay below 2^31.
+int plan_tall(int transB, int M, int N, int K, int lda, Launch* L, int ldc = 0);
 // M <= 8 against B stored N x K; mode 0 fp32, 1 bf16 storage.
 int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L);
 // lds_ok = false keeps bf16 GEMMs off the LDS-staged kernel (operands whose
 // rows do not start on 4-byte boundaries).
+// ldc: row stride of C (0 = N); the LDS-staged kernels address a C tile with
+// 32-bit offsets from its first element.
 int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L,
-              bool lds_ok = true);
+              bool lds_ok = true, int ldc = 0);
 // lds_ok = false keeps int8 GEMMs off the LDS-staged kernel (rows of A or B
 // not on 4-byte boundaries).
 // lda, ldb: row strides of A and B (0 = packed, K).
-int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok = true, int lda = 0, int ldb = 0);
+int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok = true, int lda = 0, int ldb = 0, int ldc = 0);
 
 // fp32 GEMM of dnnopt_hip_sgemm with an optional per-column bias added to
 // each finished output (one more rounding): C = epilogue + bias[n].
@@ -64,10 +101,10 @@ int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const f
                int ldb, float beta, float* C, int ldc, const float* bias, hipStream_t s);
 
 // Route an fp32 GEMM to a kernel family (skinny or tile).
-int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L);
+int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc = 0);
 // Route a bf16 GEMM (fp32_inputs: operands are fp32 and rounded in registers;
 // transB: B stored N x K, bf16 storage only).
-int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB = 0);
+int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB = 0, int ldc = 0);
 
 // Workspace slots (get_workspace): 0 GEMM partials and tickets, 1 int8
 // quantization staging, 2 the column-major hook's temporary C, 3 transposed

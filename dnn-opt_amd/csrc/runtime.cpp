@@ -4,6 +4,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "host.h"
 
@@ -55,7 +56,90 @@ std::map<std::pair<std::pair<int, int>, hipStream_t>, Scratch> g_ws;
 
 constexpr size_t kTicketBytes = (size_t)kMaxTickets * sizeof(unsigned);
 
+// Locks of StreamLock, per (device, stream).  Never destroyed: calls may
+// still run while the process's static objects are being torn down.
+std::mutex& lock_table_mu() {
+    static std::mutex* m = new std::mutex;
+    return *m;
+}
+std::map<std::pair<int, hipStream_t>, std::recursive_mutex*>& lock_table() {
+    static auto* t = new std::map<std::pair<int, hipStream_t>, std::recursive_mutex*>;
+    return *t;
+}
+
+// Streams of finished threads, per device, for reuse by new threads.
+struct StreamPool {
+    std::mutex mu;
+    std::map<int, std::vector<hipStream_t>> idle;
+};
+StreamPool& stream_pool() {
+    static StreamPool* p = new StreamPool;
+    return *p;
+}
+
+// A thread's streams; returned to the pool (no HIP call) when it ends.
+struct ThreadStreams {
+    std::map<int, hipStream_t> by_dev;
+    ~ThreadStreams() {
+        StreamPool& p = stream_pool();
+        std::lock_guard<std::mutex> g(p.mu);
+        for (auto& kv : by_dev) p.idle[kv.first].push_back(kv.second);
+    }
+};
+thread_local ThreadStreams t_streams;
+
 }  // namespace
+
+StreamLock::StreamLock(hipStream_t s) : mu_(nullptr) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        dev = -1;
+    }
+    std::recursive_mutex* m;
+    {
+        std::lock_guard<std::mutex> g(lock_table_mu());
+        std::recursive_mutex*& slot = lock_table()[{dev, s}];
+        if (!slot) slot = new std::recursive_mutex;
+        m = slot;
+    }
+    m->lock();
+    mu_ = m;
+}
+
+StreamLock::~StreamLock() { static_cast<std::recursive_mutex*>(mu_)->unlock(); }
+
+hipStream_t thread_stream(int* status) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *status = to_status(e);
+        return nullptr;
+    }
+    auto it = t_streams.by_dev.find(dev);
+    if (it != t_streams.by_dev.end()) return it->second;
+    hipStream_t s = nullptr;
+    {
+        StreamPool& p = stream_pool();
+        std::lock_guard<std::mutex> g(p.mu);
+        std::vector<hipStream_t>& v = p.idle[dev];
+        if (!v.empty()) {
+            s = v.back();
+            v.pop_back();
+        }
+    }
+    if (!s) {
+        e = hipStreamCreate(&s);  // default flags and priority
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            *status = to_status(e);
+            return nullptr;
+        }
+    }
+    t_streams.by_dev[dev] = s;
+    return s;
+}
 
 int get_workspace(hipStream_t s, size_t part_bytes, void** part, unsigned** tickets, int slot) {
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;

@@ -37,7 +37,7 @@ OK, ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_OUT_OF_MEMORY 
  K_ROWDOT_BF16, K_TALL_F32, K_ROWDOT_S8) = range(12)
 
 # DNNOPT_HIP_ABI_VERSION of include/dnnopt_hip.h that these bindings follow.
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 CblasRowMajor, CblasColMajor = 101, 102
 CblasNoTrans, CblasTrans, CblasConjTrans = 111, 112, 113
@@ -90,6 +90,7 @@ C_ABI = {
     "dnnopt_onednn_sgemm": (_I, [_P] * 14),
     "dnnopt_onednn_gemm_bf16bf16f32": (_I, [_P] * 13),
     "dnnopt_hip_plan_sgemm": (_I, [_I, _I, _I, _I, _I, POINTER(Plan)]),
+    "dnnopt_hip_plan_sgemm_ex": (_I, [_I, _I, _I, _I, _I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_plan_gemm_bf16": (_I, [_I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_plan_gemm_bf16_ex": (_I, [_I, _I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_plan_gemm_s8": (_I, [_I, _I, _I, _I, POINTER(Plan)]),
@@ -212,6 +213,12 @@ class Lib:
     def plan_sgemm(self, M, N, K, transA=0, transB=0) -> dict:
         p = Plan()
         self._check(self.so.dnnopt_hip_plan_sgemm(transA, transB, M, N, K, ctypes.byref(p)), "plan_sgemm")
+        return p.as_dict()
+
+    def plan_sgemm_ex(self, M, N, K, lda, ldb, ldc, transA=0, transB=0) -> dict:
+        p = Plan()
+        self._check(self.so.dnnopt_hip_plan_sgemm_ex(transA, transB, M, N, K, lda, ldb, ldc, ctypes.byref(p)),
+                    "plan_sgemm_ex")
         return p.as_dict()
 
     def plan_bf16(self, M, N, K, fp32_inputs=0) -> dict:

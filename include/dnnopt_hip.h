@@ -201,6 +201,11 @@ typedef struct dnnopt_plan {
 
 int dnnopt_hip_plan_sgemm(int transA, int transB, int M, int N, int K,
                           dnnopt_plan* out);
+/* As dnnopt_hip_plan_sgemm for the given row strides (the plan of
+ * dnnopt_hip_sgemm with these lda, ldb, ldc): kernels that address an
+ * operand with 32-bit offsets are only chosen when its strides allow. */
+int dnnopt_hip_plan_sgemm_ex(int transA, int transB, int M, int N, int K,
+                             int lda, int ldb, int ldc, dnnopt_plan* out);
 int dnnopt_hip_plan_gemm_bf16(int fp32_inputs, int M, int N, int K,
                               dnnopt_plan* out);
 int dnnopt_hip_plan_gemm_bf16_ex(int transA, int transB, int M, int N, int K,
@@ -224,7 +229,7 @@ const char* dnnopt_hip_status_string(int status);
 int dnnopt_hip_last_status(void);     /* last failure of the C++/cblas API on
                                          this thread, DNNOPT_OK if none      */
 int dnnopt_hip_device_count(void);    /* 0 when no device is visible        */
-#define DNNOPT_HIP_ABI_VERSION 2
+#define DNNOPT_HIP_ABI_VERSION 3
 int dnnopt_hip_abi_version(void);     /* DNNOPT_HIP_ABI_VERSION; bumped on any signature change */
 
 #ifdef __cplusplus

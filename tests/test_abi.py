@@ -165,6 +165,22 @@ def test_plans_for_tall_skinny(lib):
     assert lib.plan_sgemm(65536, 12, 256)["kernel"] == b.K_TILE_F32   # N <= 12: register tiles
 
 
+def test_plan_respects_c_row_stride(lib):
+    """The B-in-LDS tall kernel stores C through 32-bit offsets from C's first
+    element: a row stride that puts ((M - 1) * ldc + N) * 4 at or past 2^31
+    routes the GEMM to the tiles, which address C with 64-bit pointers."""
+    b = u.binding()
+    M, N, K = 65536, 64, 256
+    assert lib.plan_sgemm_ex(M, N, K, K, N, N)["kernel"] == b.K_TALL_F32
+    assert lib.plan_sgemm_ex(M, N, K, K, N, 8192)["kernel"] == b.K_TALL_F32   # (65535 * 8192 + 64) * 4 < 2^31
+    assert lib.plan_sgemm_ex(M, N, K, K, N, 8193)["kernel"] == b.K_TILE_F32   # ... and past it
+    assert lib.plan_sgemm_ex(M, N, K, K, N, 16384)["kernel"] == b.K_TILE_F32
+    # the stride-free plan is the packed case
+    assert lib.plan_sgemm(M, N, K) == lib.plan_sgemm_ex(M, N, K, K, N, N)
+    with pytest.raises(b.DnnoptError):
+        lib.plan_sgemm_ex(M, N, K, K, N, N - 1)
+
+
 def test_plan_rejects_bad_args(lib):
     b = u.binding()
     with pytest.raises(b.DnnoptError):

@@ -16,7 +16,7 @@ sys.path.insert(0, u.ROOT)
 import bench  # noqa: E402
 
 # C1..C5 and the oneDNN-hook workload.
-WORKLOADS = ["c1", "c2", "c3", "c4", "c5", "hook"]
+WORKLOADS = ["c1", "c2", "c3", "c4", "c4f", "c5", "hook"]
 
 
 def test_more_than_one_gpu_is_refused():
@@ -47,6 +47,8 @@ def test_config_shapes_match_the_baseline():
     assert shapes["c2"] == {(m, n, 2048) for m in (2, 3, 5, 7) for n in (1009, 4099, 11003)}
     assert shapes["c3"] == {(65536, 16, 256), (65536, 64, 256), (64, 64, 262144)}
     assert shapes["c4"] == {(m, 11008, 4096) for m in (1, 4, 32, 256)}
+    assert shapes["c4f"] == shapes["c4"]
+    assert {c.kind for c in bench.workload("c4f")[1]} == {"f2b"}
     assert shapes["c5"] == {(m, n, 4096) for m in (1, 8, 128) for n in (4096, 4093)}
 
 

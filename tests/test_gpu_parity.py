@@ -132,6 +132,25 @@ def test_sgemm_configs_c3(lib, orc, dev, M, N, K, ta):
     u.assert_fp32_close(host(dC), want, scale, K, f"C3 {M}x{N}x{K} ta={ta}")
 
 
+def test_sgemm_tall_large_c_stride(lib, orc, dev):
+    """65536 x 64 x 256 with ldc = 16384: C spans 4 GiB, beyond the tall
+    kernel's 32-bit C offsets, so the planner takes the tiles.  C's padding
+    holds NaN and must stay untouched."""
+    M, N, K, ldc = 65536, 64, 256, 16384
+    assert lib.plan_sgemm_ex(M, N, K, K, N, ldc)["name"] != "dnnopt_tall_f32"
+    A, B = u.uniform(orc, M * K, 1).reshape(M, K), u.uniform(orc, K * N, 2).reshape(K, N)
+    dC = torch.full((M, ldc), float("nan"), dtype=torch.float32, device=dev)
+    lib.sgemm(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, 0.0, dC, ldc, stream=stream())
+    got = host(dC[:, :N].contiguous())
+    want, scale = u.exact(A, B)
+    u.assert_fp32_close(got, want, scale, K, "65536x64x256 ldc=16384")
+    rows = torch.tensor([0, 1, 4095, 32768, M - 1], device=dev)
+    pad = host(dC[rows, N:N + 4096].contiguous())
+    assert np.isnan(pad).all(), "wrote outside the C block"
+    del dC
+    torch.cuda.empty_cache()
+
+
 # k-major outer-product kernel (A stored K x M, B stored K x N, 32 < M, N <= 64,
 # K >= 32768, row strides multiples of 4): K not a multiple of 4, ragged M and
 # N, padded strides whose padding holds NaN (it may only reach outputs outside
