@@ -317,8 +317,10 @@ def test_bf16_lds_misaligned_falls_back(lib, orc, dev):
         u.assert_fp32_close(host(dC), want, scale, K, f"misaligned a+{a_off} b+{b_off}")
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 11008, 4096), (4, 1000, 512), (7, 33, 65), (32, 300, 260), (256, 1024, 512)])
+@pytest.mark.parametrize("M,N,K", [(1, 11008, 4096), (4, 11008, 4096), (32, 11008, 4096), (256, 11008, 4096),
+                                   (4, 1000, 512), (7, 33, 65), (32, 300, 260), (256, 1024, 512)])
 def test_bf16_fp32_inputs(lib, orc, dev, M, N, K):
+    """fp32-input gemm_bf16, including every C4 shape at full size."""
     A = u.normal(orc, M * K, 1).reshape(M, K)
     B = u.normal(orc, K * N, 2, 0, 0.02).reshape(K, N)
     dC = torch.zeros(M * N, dtype=torch.float32, device=dev)
