@@ -23,8 +23,21 @@ int finish_launch(hipError_t e) {
     return DNNOPT_OK;
 }
 
+constexpr size_t kTicketBytes = (size_t)kMaxTickets * sizeof(unsigned);
+
+// Partial-sum space and tickets of a split-k launch: the stream's workspace,
+// or the caller's scratch when one is given.
+int take_workspace(hipStream_t s, size_t part_bytes, const ExtScratch* ext, void** part, unsigned** tickets) {
+    if (!ext) return get_workspace(s, part_bytes, part, tickets);
+    if (ext->bytes < kTicketBytes || part_bytes > ext->bytes - kTicketBytes) return DNNOPT_ERR_SCRATCH_LIMIT;
+    *tickets = static_cast<unsigned*>(ext->base);
+    *part = static_cast<char*>(ext->base) + kTicketBytes;
+    return DNNOPT_OK;
+}
+
 int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B, int ldb, float* C, int ldc,
-               int M, int N, int K, float alpha, float beta, hipStream_t s, const float* bias = nullptr) {
+               int M, int N, int K, float alpha, float beta, hipStream_t s, const float* bias = nullptr,
+               const ExtScratch* ext = nullptr) {
     SkinnyArgs a{};
     a.bias = bias;
     a.A = A;
@@ -48,7 +61,7 @@ int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B
     if (a.splits > 1) {
         void* part = nullptr;
         unsigned* tickets = nullptr;
-        int st = get_workspace(s, L.part_bytes, &part, &tickets);
+        int st = take_workspace(s, L.part_bytes, ext, &part, &tickets);
         if (st != DNNOPT_OK) return st;
         a.part = static_cast<float*>(part);
         a.tickets = tickets;
@@ -66,7 +79,8 @@ int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B
 }
 
 int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const void* B, int ldb, float* C, int ldc,
-             int M, int N, int K, float alpha, float beta, hipStream_t s, const float* bias = nullptr) {
+             int M, int N, int K, float alpha, float beta, hipStream_t s, const float* bias = nullptr,
+             const ExtScratch* ext = nullptr) {
     Launch L = L0;
     // The LDS-staged bf16 kernel reads whole dwords: bf16 operands must start
     // on 4-byte boundaries, else the register-only kernel serves the call.
@@ -100,7 +114,7 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
     if (a.splits > 1) {
         void* part = nullptr;
         unsigned* tickets = nullptr;
-        int st = get_workspace(s, L.part_bytes, &part, &tickets);
+        int st = take_workspace(s, L.part_bytes, ext, &part, &tickets);
         if (st != DNNOPT_OK) return st;
         a.part = static_cast<float*>(part);
         a.tickets = tickets;
@@ -144,26 +158,34 @@ bool dims_ok(int M, int N, int K) { return M > 0 && N > 0 && K > 0; }
 
 namespace dnnopt_hip {
 
-int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda, const float* B,
-               int ldb, float beta, float* C, int ldc, const float* bias, hipStream_t s) {
-    if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return DNNOPT_ERR_INVALID_ARG;
-    if (!dims_ok(M, N, K)) return DNNOPT_OK;
-    if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
-    if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N) return DNNOPT_ERR_INVALID_ARG;
-    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
-    StreamLock lock(s);
+static int sgemm_planned(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
+                         const float* B, int ldb, float beta, float* C, int ldc, const float* bias, hipStream_t s,
+                         const ExtScratch* ext) {
     Launch L;
     int st = plan_sgemm(transA, transB, M, N, K, lda, ldb, &L, ldc);
     if (st != DNNOPT_OK) return st;
     if (L.family == DNNOPT_K_SKINNY_F32)
-        return run_skinny(L, A, transA ? 1 : lda, transA ? lda : 1, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
+        return run_skinny(L, A, transA ? 1 : lda, transA ? lda : 1, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias,
+                          ext);
     if (L.family == DNNOPT_K_ROWDOT_F32)
         return run_rowdot(L, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
     if (L.family == DNNOPT_K_TALL_F32) {
         TallArgs a{A, B, C, lda, ldb, ldc, M, N, K, alpha, beta, bias};
         return finish_launch(launch_tall_f32(L.cfg, L.mode, L.mr, L.grid, L.lds, a, s));
     }
-    return run_tile(L, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
+    return run_tile(L, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias, ext);
+}
+
+int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda, const float* B,
+               int ldb, float beta, float* C, int ldc, const float* bias, hipStream_t s, const ExtScratch* ext) {
+    if ((transA != 0 && transA != 1) || (transB != 0 && transB != 1)) return DNNOPT_ERR_INVALID_ARG;
+    if (!dims_ok(M, N, K)) return DNNOPT_OK;
+    if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
+    if (lda < (transA ? M : K) || ldb < (transB ? K : N) || ldc < N) return DNNOPT_ERR_INVALID_ARG;
+    if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    if (ext) return sgemm_planned(transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, s, ext);
+    StreamLock lock(s);
+    return sgemm_planned(transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, s, nullptr);
 }
 
 }  // namespace dnnopt_hip
@@ -182,6 +204,8 @@ const char* dnnopt_hip_status_string(int status) {
         case DNNOPT_ERR_HIP: return "HIP runtime error";
         case DNNOPT_ERR_UNSUPPORTED: return "unsupported shape or option";
         case DNNOPT_ERR_OUT_OF_MEMORY: return "device memory allocation failed";
+        case DNNOPT_ERR_SCRATCH_LIMIT:
+            return "the call needs more device scratch than the no-allocation entry point holds";
         default: return "unknown status";
     }
 }

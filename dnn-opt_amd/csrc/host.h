@@ -95,10 +95,22 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
 // lda, ldb: row strides of A and B (0 = packed, K).
 int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok = true, int lda = 0, int ldb = 0, int ldc = 0);
 
+// Caller-provided device scratch in place of the stream's workspace: the
+// first kMaxTickets * 4 bytes are the ticket counters (zero between
+// launches), the rest holds partial sums.  A launch that needs more than
+// `bytes` fails with DNNOPT_ERR_SCRATCH_LIMIT; nothing is allocated.
+struct ExtScratch {
+    void* base;
+    size_t bytes;
+};
+
 // fp32 GEMM of dnnopt_hip_sgemm with an optional per-column bias added to
-// each finished output (one more rounding): C = epilogue + bias[n].
+// each finished output (one more rounding): C = epilogue + bias[n].  With
+// `ext`, split-k partials and tickets live in that scratch (no workspace is
+// taken and no stream lock is held).
 int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda, const float* B,
-               int ldb, float beta, float* C, int ldc, const float* bias, hipStream_t s);
+               int ldb, float beta, float* C, int ldc, const float* bias, hipStream_t s,
+               const ExtScratch* ext = nullptr);
 
 // Route an fp32 GEMM to a kernel family (skinny or tile).
 int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc = 0);

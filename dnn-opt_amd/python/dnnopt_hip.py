@@ -31,7 +31,8 @@ PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 # with different compile-time tunables); the default is this package's lib/.
 LIB_PATH = os.environ.get("DNNOPT_HIP_LIB") or os.path.join(PKG_DIR, "lib", "libdnnopt_blas.so")
 
-OK, ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_OUT_OF_MEMORY = range(6)
+OK, ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_OUT_OF_MEMORY, ERR_SCRATCH_LIMIT = range(7)
+NOALLOC_SCRATCH_BYTES = 16 << 20  # DNNOPT_NOALLOC_SCRATCH_BYTES
 
 (K_NONE, K_SKINNY_F32, K_SKINNY_BF16, K_SKINNY_F2B, K_MFMA_S8, K_TILE_F32, K_TILE_BF16, K_NAIVE_F32, K_ROWDOT_F32,
  K_ROWDOT_BF16, K_TALL_F32, K_ROWDOT_S8) = range(12)
@@ -77,6 +78,7 @@ _C = c_char
 # and the BLAS header, so a test can check the export list against this.
 C_ABI = {
     "dnnopt_hip_sgemm": (_I, [_I, _I, _I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
+    "dnnopt_hip_sgemm_noalloc": (_I, [_I, _I, _I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
     "dnnopt_hip_sgemm_naive": (_I, [_I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
     "dnnopt_hip_gemm_bf16": (_I, [_I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
     "dnnopt_hip_gemm_bf16_ex": (_I, [_I, _I, _I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I, _P]),
@@ -243,6 +245,12 @@ class Lib:
                                      stream),
             "dnnopt_hip_sgemm",
         )
+
+    def sgemm_noalloc(self, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, transA=0, transB=0, stream=None) -> int:
+        """dnnopt_hip_sgemm_noalloc; returns the status (the caller checks it:
+        ERR_SCRATCH_LIMIT is an expected outcome for large split-k plans)."""
+        return self.so.dnnopt_hip_sgemm_noalloc(transA, transB, M, N, K, alpha, _ptr(A), lda, _ptr(B), ldb, beta,
+                                                _ptr(C), ldc, stream)
 
     def sgemm_naive(self, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream=None):
         self._check(

@@ -38,6 +38,8 @@ extern "C" {
 #define DNNOPT_ERR_HIP           3  /* a HIP runtime call failed               */
 #define DNNOPT_ERR_UNSUPPORTED   4  /* shape/option outside what is built      */
 #define DNNOPT_ERR_OUT_OF_MEMORY 5  /* workspace or staging allocation failed  */
+#define DNNOPT_ERR_SCRATCH_LIMIT 6  /* needs more scratch than the no-allocation */
+                                    /* entry point holds (DNNOPT_NOALLOC_SCRATCH_BYTES) */
 
 /* operand transpose flags for dnnopt_hip_sgemm */
 #define DNNOPT_OP_N 0
@@ -56,6 +58,27 @@ int dnnopt_hip_sgemm(int transA, int transB, int M, int N, int K,
                      float alpha, const float* A, int lda,
                      const float* B, int ldb,
                      float beta, float* C, int ldc, void* stream);
+
+/* fp32 GEMM exactly as dnnopt_hip_sgemm (same plan, same kernels, same
+ * bits), for callers that cannot allocate device memory: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  It
+ * calls no hipMalloc/hipFree or other allocating routine: split-k partial
+ * sums and tickets live in a fixed device array of the library,
+ * DNNOPT_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load until
+ * the process ends.  A call whose plan needs more scratch than that returns
+ * DNNOPT_ERR_SCRATCH_LIMIT before any of its GEMM work is enqueued and
+ * leaves C untouched.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (concurrent
+ * streams, or host threads) race and must be serialised by the caller.  The
+ * first call on each device also enqueues one small kernel that clears the
+ * array's ticket counters.
+ * No counterpart in the reference (whose calls allocate per call); it exists
+ * for the callers that cannot allocate. */
+#define DNNOPT_NOALLOC_SCRATCH_BYTES (16u << 20)
+int dnnopt_hip_sgemm_noalloc(int transA, int transB, int M, int N, int K,
+                             float alpha, const float* A, int lda,
+                             const float* B, int ldb,
+                             float beta, float* C, int ldc, void* stream);
 
 /* fp32 scalar reference: one output per thread, k ascending, separate
  * multiply and add roundings, then alpha*acc + beta*C -- bit-identical to
