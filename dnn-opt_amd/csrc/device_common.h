@@ -55,6 +55,10 @@ __device__ __forceinline__ f32x4 buf_load_x4_coherent(__amdgpu_buffer_rsrc_t r, 
     return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kAuxCoherent));
 }
 
+__device__ __forceinline__ void buf_store_x4(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 0);
+}
+
 __device__ __forceinline__ void buf_store_x4_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kAuxCoherent);
 }

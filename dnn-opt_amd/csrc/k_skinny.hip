@@ -12,9 +12,9 @@
 // the grid.y workgroups of a column tile each take a contiguous slice of k;
 // within a lane the k of its slice are accumulated in ascending order with
 // fused multiply-adds.  Slices are combined in ascending order: waves through
-// LDS, workgroups through a workspace by the last workgroup to arrive.  The
-// summation order is therefore fixed for a given launch shape and the result
-// is bit-reproducible.
+// LDS, workgroups through a workspace (by a separate reduce kernel, or by the
+// last workgroup to arrive).  The summation order is therefore fixed for a
+// given launch shape and the result is bit-reproducible.
 //
 // Ragged tails: B is read through a buffer descriptor whose range ends at the
 // last element of B, so the loads of the last row past column N return zero;
@@ -67,14 +67,25 @@ __device__ __forceinline__ u32x4 load_row(__amdgpu_buffer_rsrc_t r, uint32_t off
     return buf_load_x4_unaligned(r, off);
 }
 
+// A is only read by these kernels.  Its loads go through the constant
+// address space, which tells the compiler that nothing the kernel stores
+// can change them: wave-uniform A loads then stay scalar loads (s_load)
+// however many stores the kernel makes elsewhere.
+template <typename T>
+using const_ptr = const __attribute__((address_space(4))) T*;
+template <typename T>
+__device__ __forceinline__ const_ptr<T> as_const(const void* p) {
+    return reinterpret_cast<const_ptr<T>>(reinterpret_cast<uintptr_t>(p));
+}
+
 template <int MODE>
 __device__ __forceinline__ float load_a(const void* A, size_t idx) {
     if constexpr (MODE == kSkinnyBF16) {
-        return bf16_to_f32(static_cast<const uint16_t*>(A)[idx]);
+        return bf16_to_f32(as_const<uint16_t>(A)[idx]);
     } else if constexpr (MODE == kSkinnyF2B) {
-        return round_bf16(static_cast<const float*>(A)[idx]);
+        return round_bf16(as_const<float>(A)[idx]);
     } else {
-        return static_cast<const float*>(A)[idx];
+        return as_const<float>(A)[idx];
     }
 }
 
@@ -91,8 +102,7 @@ __device__ __forceinline__ void load_a_block(const SkinnyArgs& p, int k, float (
         static_assert(UG % 2 == 0, "bf16 A groups load whole dwords");
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            const uint32_t* ap = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.A) +
-                                                                   (size_t)m * p.a_sm + k);
+            const_ptr<uint32_t> ap = as_const<uint32_t>(static_cast<const uint16_t*>(p.A) + (size_t)m * p.a_sm + k);
 #pragma unroll
             for (int d = 0; d < UG / 2; ++d) {
                 const uint32_t w2 = ap[d];
@@ -103,14 +113,14 @@ __device__ __forceinline__ void load_a_block(const SkinnyArgs& p, int k, float (
     } else if constexpr (AK == 0) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            const float* ap = static_cast<const float*>(p.A) + (size_t)m * p.a_sm + k;
+            const_ptr<float> ap = as_const<float>(static_cast<const float*>(p.A) + (size_t)m * p.a_sm + k);
 #pragma unroll
             for (int u = 0; u < UG; ++u) av[m][u] = MODE == kSkinnyF2B ? round_bf16(ap[u]) : ap[u];
         }
     } else if constexpr (AK == 1) {
 #pragma unroll
         for (int u = 0; u < UG; ++u) {
-            const float* ap = static_cast<const float*>(p.A) + (size_t)(k + u) * p.a_sk;
+            const_ptr<float> ap = as_const<float>(static_cast<const float*>(p.A) + (size_t)(k + u) * p.a_sk);
 #pragma unroll
             for (int m = 0; m < MR; ++m) av[m][u] = MODE == kSkinnyF2B ? round_bf16(ap[m]) : ap[m];
         }
@@ -173,9 +183,13 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     const uint32_t lane_off = col0 + lane * VEC < p.N ? (uint32_t)lane * VEC * ES + base_lo : kOobOffset;
 
     // Unsplit tiles store C directly: fetch the C values of this thread's
-    // outputs now so that the read overlaps the main loop.
+    // outputs now so that the read overlaps the main loop.  Output group gi
+    // of a reduction pass is (row gi / QG, float4 group gi % QG).
     constexpr int QG = TW / 4;                  // float4 groups per row of the tile
-    constexpr int I4 = (G * QG + NT - 1) / NT;  // groups per thread per reduction pass
+    constexpr int OG = G * QG;                  // output groups per reduction pass
+    constexpr int I4 = (OG + NT - 1) / NT;      // groups per thread per reduction pass
+    auto group_row = [](int gi) { return gi / QG; };
+    auto group_col = [](int gi) { return (gi % QG) * 4; };
     float c_pre[P][I4][4];
 #pragma unroll
     for (int pass = 0; pass < P; ++pass)
@@ -185,9 +199,9 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
             for (int e = 0; e < 4; ++e) {
                 c_pre[pass][i][e] = 0.0f;
                 const int gi = (int)threadIdx.x + i * NT;
-                const int m = pass * G + gi / QG;
-                const int n = col0 + (gi % QG) * 4 + e;
-                if (nsplit == 1 && p.beta != 0.0f && gi < G * QG && m < MR && n < p.N)
+                const int m = pass * G + group_row(gi);
+                const int n = col0 + group_col(gi) + e;
+                if (nsplit == 1 && p.beta != 0.0f && gi < OG && m < MR && n < p.N)
                     c_pre[pass][i][e] = p.C[(size_t)m * p.ldc + n];
             }
 
@@ -261,7 +275,6 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     // Reduce the NW waves of this workgroup, waves in ascending order.  Each
     // thread owns float4 groups of 4 consecutive columns of one row; LDS is
     // used in passes of G rows.
-    constexpr int Q = QG;
     f32x4 out[P][I4];
 #pragma unroll
     for (int pass = 0; pass < P; ++pass) {
@@ -281,9 +294,9 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
 #pragma unroll
         for (int i = 0; i < I4; ++i) {
             const int gi = (int)threadIdx.x + i * NT;
-            const int g = gi / Q, c4 = gi % Q;
+            const int g = group_row(gi), c4 = gi % QG;
             f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-            if (gi < G * Q && pass * G + g < MR) {
+            if (gi < OG && pass * G + g < MR) {
                 sum = *reinterpret_cast<const f32x4*>(&red[g * TW + c4 * 4]);
 #pragma unroll
                 for (int w2 = 1; w2 < NW; ++w2) sum += *reinterpret_cast<const f32x4*>(&red[(w2 * G + g) * TW + c4 * 4]);
@@ -298,11 +311,11 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
 #pragma unroll
             for (int i = 0; i < I4; ++i) {
                 const int gi = (int)threadIdx.x + i * NT;
-                const int m = pass * G + gi / Q;
-                if (gi < G * Q && m < MR) {
+                const int m = pass * G + group_row(gi);
+                if (gi < OG && m < MR) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const int n = col0 + (gi % Q) * 4 + e;
+                        const int n = col0 + group_col(gi) + e;
                         if (n < p.N)
                             p.C[(size_t)m * p.ldc + n] =
                                 add_bias(p.beta == 0.0f ? p.alpha * out[pass][i][e]
@@ -316,9 +329,9 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     }
 
     // Split-k: publish this workgroup's partial sums [split][MR][ncols_pad].
-    // They are written through to memory (sc0 sc1) so that the workgroup that
-    // reduces them -- here or in a separate kernel -- reads them without any
-    // cache maintenance.
+    // For the reduce kernel that follows, plain stores (the launch boundary
+    // makes them visible); for the last-arriving workgroup, stores written
+    // through to memory (sc0 sc1), which it reads without cache maintenance.
     const __amdgpu_buffer_rsrc_t rp =
         make_rsrc(p.part, range31((size_t)p.splits * MR * p.ncols_pad * 4));
 #pragma unroll
@@ -326,10 +339,12 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
 #pragma unroll
         for (int i = 0; i < I4; ++i) {
             const int gi = (int)threadIdx.x + i * NT;
-            const int m = pass * G + gi / Q;
-            if (gi < G * Q && m < MR) {
-                const uint32_t off = (uint32_t)((((size_t)split * MR + m) * p.ncols_pad + col0 + (gi % Q) * 4) * 4);
-                buf_store_x4_coherent(rp, off, out[pass][i]);
+            const int m = pass * G + group_row(gi);
+            if (gi < OG && m < MR) {
+                const uint32_t off =
+                    (uint32_t)((((size_t)split * MR + m) * p.ncols_pad + col0 + group_col(gi)) * 4);
+                if (p.defer_reduce) buf_store_x4(rp, off, out[pass][i]);
+                else buf_store_x4_coherent(rp, off, out[pass][i]);
             }
         }
     if (p.defer_reduce) return;
@@ -339,7 +354,8 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     // thread owns float4 outputs of the whole tile; C (for beta != 0) and a
     // chunk of CH partials per output are requested before any is used, so
     // the tail costs one memory round trip per CH splits.
-    constexpr int OUTS = MR * QG;
+    constexpr int QT = QG;
+    constexpr int OUTS = MR * QT;
     constexpr int OPT = (OUTS + NT - 1) / NT;
     constexpr int CH = OPT == 1 ? 16 : 8;
     const uint32_t stride = (uint32_t)((size_t)MR * p.ncols_pad * 4);
@@ -348,7 +364,7 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
 #pragma unroll
     for (int o = 0; o < OPT; ++o) {
         const int idx = (int)threadIdx.x + o * NT;
-        const int m = idx / QG, n0 = col0 + (idx % QG) * 4;
+        const int m = idx / QT, n0 = col0 + (idx % QT) * 4;
         off0[o] = idx < OUTS ? (uint32_t)(((size_t)m * p.ncols_pad + n0) * 4) : kOobOffset;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
@@ -387,7 +403,7 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
 #pragma unroll
     for (int o = 0; o < OPT; ++o) {
         const int idx = (int)threadIdx.x + o * NT;
-        const int m = idx / QG, n0 = col0 + (idx % QG) * 4;
+        const int m = idx / QT, n0 = col0 + (idx % QT) * 4;
         if (idx < OUTS) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)

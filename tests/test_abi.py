@@ -82,14 +82,15 @@ def test_plans_for_the_configs(lib):
             assert p["kernel"] == b.K_SKINNY_F32 and p["rows"] == M
             tiles = -(-N // 256)
             # G >= T workgroups, each tile split G/T or G/T + 1 ways
-            assert p["grid_x"] >= tiles and p["splits"] == -(-p["grid_x"] // tiles)
+            G = p["grid_x"]
+            assert G >= tiles and p["splits"] == -(-G // tiles) and p["splits"] > 1
             # whole splits per column tile: 256 workgroups rounded up when the last
             # tile is at most a quarter wide, else down (at most a fifth of the CUs idle)
-            assert p["grid_x"] % tiles == 0, p
+            assert G % tiles == 0, p
             if N - (tiles - 1) * 256 <= 64:
-                assert p["grid_x"] >= 256, p
+                assert G >= 256, p
             elif N > 4096:
-                assert 256 - 256 // 5 <= p["grid_x"] <= 256, p
+                assert 256 - 256 // 5 <= G <= 256, p
     assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TALL_F32  # C3 N=16: B resident in LDS
     assert lib.plan_sgemm(65536, 64, 256)["kernel"] == b.K_TALL_F32
     p = lib.plan_sgemm(64, 64, 262144, transA=1)  # C3 split-K: k-major outer-product kernel
