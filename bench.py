@@ -9,7 +9,8 @@ quoted on): fp32 C = A B + C for M in {2,3,5,7} x N in {1009,4099,11003},
 K = 2048, alpha = beta = 1, A, B ~ N(0, 0.02), C ~ U[-1, 1).  One step runs
 all twelve shapes once; its rate is `value`.  The default run also times the
 other configs -- C1, C3, C4 through the bf16-storage entry and through the
-fp32-input gemm_bf16 (c4f), C5 -- each as its own workload, and reports
+fp32-input gemm_bf16 (c4f), C5, and C5's shapes through the fp32-API
+gemm_int8 (c5f) -- each as its own workload, and reports
 their step rates, dominant kernels and per-shape GB/s, TFLOP/s and roofline
 fractions under `configs`.  `--workload NAME` times one workload (its rate
 becomes `value`); `--workload all` adds the oneDNN-hook workload;
@@ -77,7 +78,7 @@ class Case:
 
     def sizes(self):
         sa, sb = {"f32": (4, 4), "bf16": (2, 2), "f2b": (4, 4), "s8": (1, 1), "s8s": (1, 1), "hf32": (4, 4),
-                  "hbf16": (2, 2)}[self.kind]
+                  "hbf16": (2, 2), "i8f": (4, 4)}[self.kind]
         sc = 4
         # per-column scale (int8) or bias (hook) vector
         extra = 4 * self.N if self.kind == "s8s" or (self.kind == "hf32" and self.init.get("bias")) else 0
@@ -129,6 +130,14 @@ def workload(name):
         cs.append(Case("c5_m128_n4093_scale", "s8s", 128, 4093, 4096, init={"A": ("i",), "B": ("i",)}, dtype="s8"))
         return ("C5: int8 s8 x s8 -> s32 (B as N x K), M in {1,8,128} x N in {4096,4093} x K=4096; "
                 "+ per-column fp32 scale", cs)
+    if name == "c5f":
+        # fp32-API gemm_int8 at C5's shapes: dynamic per-tensor quantization
+        # of both fp32 operands, exact int8 GEMM, dequantized fp32 C
+        # (src/gemm/gemm.cpp:418-455)
+        cs = [Case(f"c5f_m{M}_n4096", "i8f", M, 4096, 4096, init={"A": ("u", -1, 1), "B": ("n", 0, 0.02)},
+                   dtype="s8") for M in (1, 8, 128)]
+        return ("C5 via the fp32-API gemm_int8: fp32 A, B quantized per tensor to int8, exact int32 "
+                "accumulation, fp32 C, M in {1,8,128} x N=4096 x K=4096", cs)
     if name == "hook":
         # oneDNN inner product through the column-major hook: extended_sgemm
         # ('T', 'N', OC, MB, IC, W, IC, X, IC, dst, OC, bias).  The case's
@@ -150,7 +159,7 @@ class Buffers:
         self.case = case
         M, N, K = case.M, case.N, case.K
         tA = {"f32": torch.float32, "f2b": torch.float32, "bf16": torch.int16, "s8": torch.int8,
-              "s8s": torch.int8, "hf32": torch.float32, "hbf16": torch.int16}[case.kind]
+              "s8s": torch.int8, "hf32": torch.float32, "hbf16": torch.int16, "i8f": torch.float32}[case.kind]
         dt_code = {torch.float32: 0, torch.int16: 1, torch.int8: 2}[tA]
         a_elems = M * K
         b_elems = K * N
@@ -191,6 +200,8 @@ class Buffers:
             lib.gemm_bf16_f32in(M, N, K, c.alpha, A, K, B, N, c.beta, C, N, stream=stream)
         elif c.kind == "s8":
             lib.gemm_s8s8s32(M, N, K, A, K, B, K, C, N, stream=stream)
+        elif c.kind == "i8f":
+            lib.gemm_int8_f32(M, N, K, c.alpha, A, K, B, N, c.beta, C, N, stream=stream)
         elif c.kind == "hf32":
             lib.ext_sgemm("T", "N", N, M, K, c.alpha, B, K, A, K, c.beta, C, N,
                           bias=self.S[r] if self.S else None, stream=stream)
@@ -210,6 +221,8 @@ def kernel_key(lib, case):
         p = lib.plan_bf16_ex(case.M, case.N, case.K, transB=1)
     elif case.kind in ("bf16", "f2b"):
         p = lib.plan_bf16(case.M, case.N, case.K, fp32_inputs=int(case.kind == "f2b"))
+    elif case.kind == "i8f":
+        p = lib.plan_s8(case.M, case.N, case.K, with_scale=1)
     else:
         p = lib.plan_s8(case.M, case.N, case.K, with_scale=int(case.kind == "s8s"))
     if p["name"] == "dnnopt_skinny":
@@ -674,7 +687,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="default",
-                    choices=["default", "c1", "c2", "c3", "c4", "c4f", "c5", "hook", "all"],
+                    choices=["default", "c1", "c2", "c3", "c4", "c4f", "c5", "c5f", "hook", "all"],
                     help="default: C2 is `value`, C1, C3, C4 (bf16 storage and fp32 inputs) and C5 are timed too "
                          "and reported under `configs`; a single workload makes it `value`; all adds the "
                          "oneDNN-hook workload")
@@ -708,7 +721,7 @@ def main():
         sys.exit(2)
 
     if args.workload in ("default", "all"):
-        names = ["c2", "c1", "c3", "c4", "c4f", "c5"] + (["hook"] if args.workload == "all" else [])
+        names = ["c2", "c1", "c3", "c4", "c4f", "c5", "c5f"] + (["hook"] if args.workload == "all" else [])
         main_name = "c2"
     else:
         names = [args.workload]

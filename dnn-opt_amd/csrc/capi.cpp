@@ -335,10 +335,17 @@ int dnnopt_hip_gemm_bf16_f32in(int M, int N, int K, float alpha, const float* A,
     return gemm_bf16_common(1, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream);
 }
 
+// Dynamic dequantization of the fp32-API gemm_int8 (EPI 1 with amax): C =
+// (sA sB alpha) acc (+ beta C), sA, sB from the bits of max|A|, max|B|.
+struct DynDequant {
+    const unsigned* amax;
+    float alpha, beta;
+};
+
 static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda, const int8_t* B, int ldb,
-                          const float* scale, void* C, int ldc, void* stream) {
+                          const float* scale, void* C, int ldc, void* stream, const DynDequant* dyn = nullptr) {
     if (!dims_ok(M, N, K)) return DNNOPT_OK;
-    if (!A || !B || !C || (epi && !scale)) return DNNOPT_ERR_INVALID_ARG;
+    if (!A || !B || !C || (epi && !scale && !dyn)) return DNNOPT_ERR_INVALID_ARG;
     if (lda < K || ldb < K || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
     const int aligned = ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) == 0 &&
@@ -355,6 +362,9 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
         r.C = epi ? static_cast<float*>(C) : nullptr;
         r.Ci = epi ? nullptr : static_cast<int32_t*>(C);
         r.scale = scale;
+        r.amax = dyn ? dyn->amax : nullptr;
+        r.alpha = dyn ? dyn->alpha : 1.0f;
+        r.beta = dyn ? dyn->beta : 0.0f;
         r.lda = lda;
         r.ldb = ldb;
         r.ldc = ldc;
@@ -370,6 +380,9 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
     a.B = B;
     a.C = C;
     a.scale = scale;
+    a.amax = dyn ? dyn->amax : nullptr;
+    a.alpha = dyn ? dyn->alpha : 1.0f;
+    a.beta = dyn ? dyn->beta : 0.0f;
     a.lda = lda;
     a.ldb = ldb;
     a.ldc = ldc;
@@ -390,7 +403,8 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
     }
     st = finish_launch(launch_mfma_s8(L.cfg, epi, aligned, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
-    return finish_launch(launch_s8_reduce(a.part, a.splits, L.tn, L.tm, L.bm, L.bn, M, N, epi, scale, C, ldc, s));
+    return finish_launch(launch_s8_reduce(a.part, a.splits, L.tn, L.tm, L.bm, L.bn, M, N, epi, scale, a.amax, a.alpha,
+                                          a.beta, C, ldc, s));
 }
 
 int dnnopt_hip_gemm_s8s8s32(int M, int N, int K, const int8_t* A, int lda, const int8_t* B, int ldb, int32_t* C,
@@ -409,28 +423,32 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
     if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
     if (lda < K || ldb < N || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
+    if (N > 0x7FFFFFFF / 2 || (long long)N * ((K + 15) & ~15) > 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
     hipStream_t s = as_stream(stream);
     StreamLock lock(s);
-    // Staging (slot 1): [int32 acc M*N][qA M x ldq][qB N x ldq][2 absmax words];
+    // Staging (slot 1): [qA M x ldq][qB N x ldq][absmax partials][max|A|, max|B|];
     // ldq pads K to 16 bytes so every quantized row is 16-byte aligned.
+    // Three launches: maxima, quantization, and the int8 GEMM whose epilogue
+    // dequantizes straight into C.
     const int ldq = (K + 15) & ~15;
-    const size_t acc_bytes = ((size_t)M * N * 4 + 255) & ~(size_t)255;
+    int ga = 1, gb = 1;
+    absmax_blocks(M, N, K, &ga, &gb);
     const size_t qa_bytes = ((size_t)M * ldq + 255) & ~(size_t)255;
     const size_t qb_bytes = ((size_t)N * ldq + 255) & ~(size_t)255;
+    const size_t part_bytes = ((size_t)(ga + gb) * 4 + 255) & ~(size_t)255;
     void* stage = nullptr;
     unsigned* unused = nullptr;
-    int st = get_workspace(s, acc_bytes + qa_bytes + qb_bytes + 256, &stage, &unused, kSlotQuant);
+    int st = get_workspace(s, qa_bytes + qb_bytes + part_bytes + 256, &stage, &unused, kSlotQuant);
     if (st != DNNOPT_OK) return st;
     char* base = static_cast<char*>(stage);
-    int32_t* acc = reinterpret_cast<int32_t*>(base);
-    int8_t* qa = reinterpret_cast<int8_t*>(base + acc_bytes);
-    int8_t* qb = reinterpret_cast<int8_t*>(base + acc_bytes + qa_bytes);
-    unsigned* amax = reinterpret_cast<unsigned*>(base + acc_bytes + qa_bytes + qb_bytes);
-    st = finish_launch(launch_quant_prepare(A, lda, B, ldb, M, N, K, ldq, amax, qa, qb, s));
+    int8_t* qa = reinterpret_cast<int8_t*>(base);
+    int8_t* qb = reinterpret_cast<int8_t*>(base + qa_bytes);
+    unsigned* part = reinterpret_cast<unsigned*>(base + qa_bytes + qb_bytes);
+    unsigned* amax = reinterpret_cast<unsigned*>(base + qa_bytes + qb_bytes + part_bytes);
+    st = finish_launch(launch_quant_pair(A, lda, B, ldb, M, N, K, ldq, part, amax, qa, qb, s));
     if (st != DNNOPT_OK) return st;
-    st = gemm_s8_common(0, M, N, K, qa, ldq, qb, ldq, nullptr, acc, N, stream);
-    if (st != DNNOPT_OK) return st;
-    return finish_launch(launch_dequant(acc, M, N, amax, alpha, beta, C, ldc, s));
+    const DynDequant dyn{amax, alpha, beta};
+    return gemm_s8_common(1, M, N, K, qa, ldq, qb, ldq, nullptr, C, ldc, stream, &dyn);
 }
 
 int dnnopt_hip_saxpy(int N, float alpha, const float* X, int incX, float* Y, int incY, void* stream) {

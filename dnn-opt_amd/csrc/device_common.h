@@ -187,6 +187,31 @@ __device__ __forceinline__ float add_bias(float y, const float* bias, int n) {
     return bias ? add_rn(y, bias[n]) : y;
 }
 
+// Per-tensor int8 quantization scale of the fp32-API gemm_int8: max|X| / 127,
+// or 1 when the tensor is all zero (src/gemm/gemm_driver_generic.cpp:49-67).
+// `amax_bits` is the bit pattern of max|X|.
+__device__ __forceinline__ float quant_scale_bits(uint32_t amax_bits) {
+    const float amax = as_f32(amax_bits);
+    return amax == 0.0f ? 1.0f : amax / 127.0f;
+}
+
+// fp32 output of an exact int32 accumulator (EPI 1 of the int8 kernels):
+//   amax == nullptr: per-column dequantization, (float)acc * scale[n];
+//   amax != nullptr: the dynamic per-tensor dequantization of the fp32-API
+//     gemm_int8, with dq = (sA * sB) * alpha from dyn_dequant_scale():
+//     beta == 0 ? dq * acc : fma(dq, acc, beta * C)
+//     (src/gemm/gemm_ukernel_int8_neon.cpp:87-131).
+// Every product and the conversion round once, as in the reference.
+__device__ __forceinline__ float dyn_dequant_scale(const unsigned* amax, float alpha) {
+    return mul_rn(mul_rn(quant_scale_bits(amax[0]), quant_scale_bits(amax[1])), alpha);
+}
+__device__ __forceinline__ float s8_out(int32_t acc, int n, const float* scale, const unsigned* amax, float dq,
+                                        float beta, const float* c) {
+    if (!amax) return mul_rn((float)acc, scale[n]);
+    if (beta == 0.0f) return mul_rn(dq, (float)acc);
+    return __builtin_fmaf(dq, (float)acc, mul_rn(beta, *c));
+}
+
 // Cross-workgroup ticket: every workgroup of a split-k group calls this after
 // storing its partial sums with coherent (sc0 sc1, write-through) stores.
 // Returns true in exactly one workgroup -- the last to arrive -- which then

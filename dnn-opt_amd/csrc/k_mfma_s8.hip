@@ -221,6 +221,7 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
         return;
     }
 
+    const float dq = EPI == 1 && p.amax ? dyn_dequant_scale(p.amax, p.alpha) : 0.0f;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -233,7 +234,8 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
                     if constexpr (EPI == 0) {
                         static_cast<int32_t*>(p.C)[(size_t)m * p.ldc + n] = acc[mt][nt][i];
                     } else {
-                        static_cast<float*>(p.C)[(size_t)m * p.ldc + n] = (float)acc[mt][nt][i] * p.scale[n];
+                        float* c = static_cast<float*>(p.C) + (size_t)m * p.ldc + n;
+                        *c = s8_out(acc[mt][nt][i], n, p.scale, p.amax, dq, p.beta, c);
                     }
                 }
             }
@@ -417,6 +419,7 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
         return;
     }
     const size_t esz = EPI == 0 ? 4 : 4;
+    const float dq = EPI == 1 && p.amax ? dyn_dequant_scale(p.amax, p.alpha) : 0.0f;
     const __amdgpu_buffer_rsrc_t rc =
         make_rsrc(static_cast<char*>(p.C) + ((size_t)m0 * p.ldc + n0) * esz,
                   range31(((size_t)(p.M - 1 - m0) * p.ldc + (p.N - n0)) * esz));
@@ -431,14 +434,19 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
             if constexpr (EPI == 0) {
                 out = __builtin_bit_cast(u32x4, v);
             } else {
+                float* c = static_cast<float*>(p.C) + (size_t)m * p.ldc + n;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) out[k] = as_u32((float)v[k] * p.scale[n + k]);
+                for (int k = 0; k < 4; ++k) out[k] = as_u32(s8_out(v[k], n + k, p.scale, p.amax, dq, p.beta, c + k));
             }
             __builtin_amdgcn_raw_buffer_store_b128(out, rc, off, 0, 0);
         } else {
             for (int k = 0; k < p.N - n; ++k) {
-                if constexpr (EPI == 0) static_cast<int32_t*>(p.C)[(size_t)m * p.ldc + n + k] = v[k];
-                else static_cast<float*>(p.C)[(size_t)m * p.ldc + n + k] = (float)v[k] * p.scale[n + k];
+                if constexpr (EPI == 0) {
+                    static_cast<int32_t*>(p.C)[(size_t)m * p.ldc + n + k] = v[k];
+                } else {
+                    float* c = static_cast<float*>(p.C) + (size_t)m * p.ldc + n + k;
+                    *c = s8_out(v[k], n + k, p.scale, p.amax, dq, p.beta, c);
+                }
             }
         }
     }

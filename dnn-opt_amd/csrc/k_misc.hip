@@ -215,7 +215,8 @@ __global__ __launch_bounds__(256) void dnnopt_skinny_reduce(const float* __restr
 // Sum exact int32 partial tiles [split][tile][bm*bn] and store C.
 __global__ __launch_bounds__(256) void dnnopt_s8_reduce(const int32_t* __restrict__ part, int splits, int tiles_n,
                                                        int tiles, int bm, int bn, int M, int N, int epi,
-                                                       const float* scale, void* C, int ldc) {
+                                                       const float* scale, const unsigned* amax, float alpha,
+                                                       float beta, void* C, int ldc) {
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     if (idx >= (long long)M * N) return;
     const int m = (int)(idx / N), n = (int)(idx % N);
@@ -232,8 +233,12 @@ __global__ __launch_bounds__(256) void dnnopt_s8_reduce(const int32_t* __restric
         for (int u = 0; u < 8; ++u) s += v[u];
     }
     for (; sp < splits; ++sp) s += src[sp * stride];
-    if (epi) static_cast<float*>(C)[(size_t)m * ldc + n] = (float)s * scale[n];
-    else static_cast<int32_t*>(C)[(size_t)m * ldc + n] = s;
+    if (epi) {
+        float* c = static_cast<float*>(C) + (size_t)m * ldc + n;
+        *c = s8_out(s, n, scale, amax, amax ? dyn_dequant_scale(amax, alpha) : 0.0f, beta, c);
+    } else {
+        static_cast<int32_t*>(C)[(size_t)m * ldc + n] = s;
+    }
 }
 
 hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, int N, int ncols_pad,
@@ -247,10 +252,11 @@ hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, 
 }
 
 hipError_t launch_s8_reduce(const int32_t* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
-                            int N, int epi, const float* scale, void* C, int ldc, hipStream_t s) {
+                            int N, int epi, const float* scale, const unsigned* amax, float alpha, float beta,
+                            void* C, int ldc, hipStream_t s) {
     const long long outs = (long long)M * N;
     hipLaunchKernelGGL(dnnopt_s8_reduce, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, part, splits,
-                       tiles_n, tiles_n * tiles_m, bm, bn, M, N, epi, scale, C, ldc);
+                       tiles_n, tiles_n * tiles_m, bm, bn, M, N, epi, scale, amax, alpha, beta, C, ldc);
     return hipGetLastError();
 }
 

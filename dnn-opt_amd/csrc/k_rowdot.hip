@@ -244,7 +244,9 @@ __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
     if constexpr (MODE == 2) {
         p.Ci[(size_t)m * p.ldc + n0 + r] = v;
     } else if constexpr (MODE == 3) {
-        p.C[(size_t)m * p.ldc + n0 + r] = mul_rn((float)v, p.scale[n0 + r]);
+        float* c = p.C + (size_t)m * p.ldc + n0 + r;
+        const float dq = p.amax ? dyn_dequant_scale(p.amax, p.alpha) : 0.0f;
+        *c = s8_out(v, n0 + r, p.scale, p.amax, dq, p.beta, c);
     } else {
         float* c = p.C + (size_t)m * p.ldc + n0 + r;
         *c = add_bias(epilogue(v, p.alpha, p.beta, c), p.bias, n0 + r);
@@ -296,7 +298,7 @@ hipError_t launch_rowdot(int mode, int mr, int kw, int aligned, dim3 grid, const
             if (!a.Ci) return hipErrorInvalidValue;
             return aligned ? launch_rowdot_mode<2, 1>(mr, kw, grid, a, s) : launch_rowdot_mode<2, 0>(mr, kw, grid, a, s);
         case 3:
-            if (!a.C || !a.scale) return hipErrorInvalidValue;
+            if (!a.C || (!a.scale && !a.amax)) return hipErrorInvalidValue;
             return aligned ? launch_rowdot_mode<3, 1>(mr, kw, grid, a, s) : launch_rowdot_mode<3, 0>(mr, kw, grid, a, s);
         default: return hipErrorInvalidValue;
     }

@@ -68,6 +68,10 @@ struct RowdotArgs {
     const float* bias;  // per-column bias added after the epilogue (or null)
     int32_t* Ci;        // int32 output (mode 2)
     const float* scale; // per-column scale of mode 3
+    // Mode 3 with amax != nullptr: the fp32-API gemm_int8's dynamic
+    // dequantization instead of the column scale (s8_out in device_common.h;
+    // amax[0..1] = bits of max|A|, max|B|; alpha, beta as above).
+    const unsigned* amax;
 };
 constexpr int kRowdotWaves = 8;
 #ifndef DNNOPT_ROWDOT_R58
@@ -124,6 +128,10 @@ struct S8Args {
     int splits;
     int defer_reduce;    // splits > 1: 1 = only store partials (a reduce kernel follows)
     int tiles_n, tiles_m;  // LDS-staged kernel: tile grid (blockIdx.x is XCD-ordered, see xcd_tile)
+    // EPI 1 with amax != nullptr: the fp32-API gemm_int8's dynamic
+    // dequantization instead of the column scale (s8_out in device_common.h).
+    const unsigned* amax;
+    float alpha, beta;
 };
 
 struct S8Config {
@@ -224,21 +232,24 @@ hipError_t launch_saxpy(int n, float alpha, const float* x, int incx, float* y, 
                         hipStream_t s);
 hipError_t launch_fill(void* dst, size_t n, int dtype, int dist, uint64_t seed,
                        uint32_t tensor_id, double p0, double p1, hipStream_t s);
-// fp32-API int8: zero the two absmax words, reduce max|A| and max|B|, quantize
-// A (M x K) and B (K x N, written transposed as N x K), then after the int8
-// GEMM dequantize the int32 accumulators into C.
-hipError_t launch_quant_prepare(const float* A, int lda, const float* B, int ldb, int M, int N, int K,
-                                int ldq, unsigned* amax, int8_t* qA, int8_t* qB, hipStream_t s);
-hipError_t launch_dequant(const int32_t* acc, int M, int N, const unsigned* amax, float alpha,
-                          float beta, float* C, int ldc, hipStream_t s);
+// fp32-API int8, before the GEMM: two launches.  The first stores per-block
+// maxima of |A| and |B| in part (absmax_blocks() words); the second reduces
+// them, stores the bits of max|A| and max|B| in amax[0..1], and quantizes
+// A (M x K) into qA (M x ldq) and B (K x N) into qB transposed (N x ldq).
+// The GEMM then dequantizes in its epilogue (EPI 1 / mode 3 with amax).
+void absmax_blocks(int M, int N, int K, int* ga, int* gb);
+hipError_t launch_quant_pair(const float* A, int lda, const float* B, int ldb, int M, int N, int K, int ldq,
+                             unsigned* part, unsigned* amax, int8_t* qA, int8_t* qB, hipStream_t s);
 // Reduce skinny partials [split][M][ncols_pad] into C (epilogue applied);
 // tile t (of T, tile width tw) has splits_of_tile(t, G, T) partials.
 hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, int N, int ncols_pad,
                                 float alpha, float beta, float* C, int ldc, const float* bias, hipStream_t s);
 // Reduce int8 partial tiles [splits][tiles][bm*bn] (exact int32) into C:
-// epi 0 stores int32, epi 1 stores (float)acc * scale[n].
+// epi 0 stores int32, epi 1 stores s8_out(acc) (column scale, or the dynamic
+// dequantization when amax != nullptr).
 hipError_t launch_s8_reduce(const int32_t* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
-                            int N, int epi, const float* scale, void* C, int ldc, hipStream_t s);
+                            int N, int epi, const float* scale, const unsigned* amax, float alpha, float beta,
+                            void* C, int ldc, hipStream_t s);
 // Reduce partial tiles [splits][tiles_m*tiles_n][bm*bn] into C (epilogue applied).
 hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm,
                                 int bn, int M, int N, float alpha, float beta, float* C, int ldc,

@@ -16,7 +16,7 @@ sys.path.insert(0, u.ROOT)
 import bench  # noqa: E402
 
 # C1..C5 and the oneDNN-hook workload.
-WORKLOADS = ["c1", "c2", "c3", "c4", "c4f", "c5", "hook"]
+WORKLOADS = ["c1", "c2", "c3", "c4", "c4f", "c5", "c5f", "hook"]
 
 
 def test_more_than_one_gpu_is_refused():
@@ -30,7 +30,8 @@ def test_more_than_one_gpu_is_refused():
 def test_algorithmic_counts(wl):
     """bytes = sA*M*K + sB*K*N + 4*M*N*(1 + [beta != 0]) (+ 4*N for a column
     scale or bias), flops = 2*M*N*K, with the element sizes of each kind."""
-    size = {"f32": (4, 4), "bf16": (2, 2), "f2b": (4, 4), "s8": (1, 1), "s8s": (1, 1), "hf32": (4, 4), "hbf16": (2, 2)}
+    size = {"f32": (4, 4), "bf16": (2, 2), "f2b": (4, 4), "s8": (1, 1), "s8s": (1, 1), "hf32": (4, 4), "hbf16": (2, 2),
+            "i8f": (4, 4)}
     _, cases = bench.workload(wl)
     assert cases
     for c in cases:

@@ -417,7 +417,8 @@ def test_int8_colscale(lib, orc, dev, M, N):
     assert np.array_equal(host(dC), acc * s[None, :])
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (7, 13, 5), (3, 3, 1000), (13, 17, 19), (64, 300, 257)])
+@pytest.mark.parametrize("M,N,K", [(1, 128, 64), (7, 13, 5), (3, 3, 1000), (13, 17, 19), (64, 300, 257),
+                                   (8, 4093, 4096), (1, 4096, 4096), (128, 1024, 512), (40, 70, 2000)])
 def test_int8_dynamic_quant_matches_oracle(lib, orc, dev, M, N, K):
     A, B, C0 = u.uniform(orc, M * K, 1), u.uniform(orc, K * N, 2), u.uniform(orc, M * N, 3)
     for beta in (0.0, 0.5):
