@@ -426,17 +426,23 @@ __device__ __forceinline__ int swz_a(int row, int c) { return c ^ (row & 7); }
 
 }  // namespace
 
-template <int MT, int NT, int WM, int WN, int D, int MODE, int TB = 0, int KB0 = 0>
-__global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) {
+// KW: waves that split each k-block's MFMA k-steps for the same output
+// sub-tile (the WM x WN output waves are replicated KW times); their sums
+// are added in ascending order through LDS after the loop.  Fewer, larger
+// per-wave sub-tiles read fewer operand bytes from LDS per MFMA.
+template <int MT, int NT, int WM, int WN, int D, int MODE, int TB = 0, int KB0 = 0, int KW = 1>
+__global__ __launch_bounds__(WM* WN * KW * 64) void dnnopt_tile_bf16_lds(TileArgs p) {
     static_assert(!TB || MODE == kTileBF16, "B stored N x K needs bf16 storage");
     using S = TileShape<MT, NT, WM, WN, 1>;
     constexpr int BM = S::BM, BN = S::BN;
     // k per block: DNNOPT_LDS_KB when both stages fit in 128 KiB of LDS.
     constexpr int BK = tile_lds_bk(BM, BN, KB0);
-    constexpr int NTH = WM * WN * 64;
+    constexpr int NTH = WM * WN * KW * 64;
     constexpr int ROWB = BK * 2;  // bytes of one LDS row (BK bf16)
     constexpr int CPR = ROWB / 16;  // 16-byte chunks per LDS row
     constexpr int KK = BK / 32;     // MFMA k-steps per block
+    static_assert(KK % KW == 0, "the k-steps of a block split evenly over the KW waves");
+    constexpr int KKW = KK / KW;    // k-steps per wave per block
     // B in LDS: stored N x K, BN rows of BK k (like A); stored K x N, BK rows
     // of BN columns padded by 32 bytes.
     constexpr int BROW = TB ? ROWB : BN * 2 + 32;
@@ -447,16 +453,19 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
     constexpr int BUN = TB ? BN * CPR : (BN / 8) * BK;
     constexpr int AU = (ACH + NTH - 1) / NTH;  // per thread
     constexpr int BU = (BUN + NTH - 1) / NTH;
-    // The two k-block stages, reused after the main loop to stage C rows.
+    // The two k-block stages, reused after the main loop to add the KW waves'
+    // sums and to stage C rows.
     constexpr int CROW = BN + 4;  // floats per staged C row (padding spreads the banks)
-    constexpr int LDS_BYTES = 2 * STAGE > BM * CROW * 4 ? 2 * STAGE : BM * CROW * 4;
+    constexpr int RED_BYTES = (KW - 1) * WM * WN * S::SUB * 64 * 4;
+    constexpr int LDS_0 = 2 * STAGE > BM * CROW * 4 ? 2 * STAGE : BM * CROW * 4;
+    constexpr int LDS_BYTES = LDS_0 > RED_BYTES ? LDS_0 : RED_BYTES;
     __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
     __shared__ float red_unused[1];
     __shared__ int last_flag;
 
     const int lane = lane_id(), r = lane & 15, g = lane >> 4;
     const int w = wave_id();
-    const int wn = w % WN, wm = w / WN;
+    const int wn = w % WN, wm = (w / WN) % WM, wk = w / (WN * WM);
     const int t = (int)threadIdx.x;
     const TileXY tile = xcd_tile((int)blockIdx.x, p.tiles_n, p.tiles_m);
     if (!tile.ok) return;
@@ -588,30 +597,32 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    int a_rd[KK][MT], b_rd[KK][NT];
+    // LDS offsets of this wave's operand reads for its k-steps kk = j * KW + wk.
+    int a_rd[KKW][MT], b_rd[KKW][NT];
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
+    for (int j = 0; j < KKW; ++j) {
+        const int kk = j * KW + wk;
         const int c = kk * 4 + g;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
             const int row = (wm * MT + mt) * 16 + r;
-            a_rd[kk][mt] = row * ROWB + swz_a(row, c) * 16;
+            a_rd[j][mt] = row * ROWB + swz_a(row, c) * 16;
         }
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
             if constexpr (TB) {
                 const int n = (wn * NT + nt) * 16 + r;
-                b_rd[kk][nt] = A_BYTES + n * ROWB + swz_a(n, c) * 16;
+                b_rd[j][nt] = A_BYTES + n * ROWB + swz_a(n, c) * 16;
             } else {
                 // first transposing read: row kk * 32 + 8 g + r / 4, columns 4 (r % 4) of the tile
-                b_rd[kk][nt] = A_BYTES + (kk * 32 + 8 * g + (r >> 2)) * BROW + ((wn * NT + nt) * 16 + 4 * (r & 3)) * 2;
+                b_rd[j][nt] = A_BYTES + (kk * 32 + 8 * g + (r >> 2)) * BROW + ((wn * NT + nt) * 16 + 4 * (r & 3)) * 2;
             }
         }
     }
     auto compute = [&](int buf) {
         const char* St = lds + buf * STAGE;
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
+        for (int kk = 0; kk < KKW; ++kk) {
             u32x4 af[MT], bfr[NT];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const u32x4*>(St + a_rd[kk][mt]);
@@ -671,23 +682,54 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_lds(TileArgs p) 
         }
     }
 
+    if constexpr (KW > 1) {
+        // Add the KW waves of each output sub-tile in ascending k order (the
+        // main loop ended with a barrier, so the stages are free).
+        float* red = reinterpret_cast<float*>(lds);
+        const int slot = wm * WN + wn;
+        if (wk > 0) {
+            float* dst = &red[(((wk - 1) * WM * WN + slot) * S::SUB) * 64];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dst[((mt * NT + nt) * 4 + i) * 64 + lane] = acc[mt][nt][i];
+        }
+        __syncthreads();
+        if (wk == 0) {
+#pragma unroll
+            for (int q = 1; q < KW; ++q) {
+                const float* src = &red[(((q - 1) * WM * WN + slot) * S::SUB) * 64];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[mt][nt][i] += src[((mt * NT + nt) * 4 + i) * 64 + lane];
+            }
+        }
+        __syncthreads();
+    }
     if (p.splits > 1) {
+        // Waves of k-slot wk > 0 store nothing (tile_finish keys on it).
         tile_finish<MT, NT, WM, WN, 1>(p, acc, red_unused, &last_flag, w, lane, tile.n, tile.m, p.tiles_n,
                                        p.tiles_n * p.tiles_m);
         return;
     }
-    // Unsplit tile: stage the BM x BN accumulators in LDS (the main loop
-    // ended with a barrier, so the stages are free), then write C row by row
-    // with 16-byte accesses -- the MFMA layout would store 4 rows x 16
-    // columns per instruction.
+    // Unsplit tile: stage the BM x BN accumulators in LDS (the stages are
+    // free), then write C row by row with 16-byte accesses -- the MFMA layout
+    // would store 4 rows x 16 columns per instruction.
     float* Cs = reinterpret_cast<float*>(lds);
+    if (wk == 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
+            for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                Cs[((wm * MT + mt) * 16 + 4 * g + i) * CROW + (wn * NT + nt) * 16 + r] = acc[mt][nt][i];
+                for (int i = 0; i < 4; ++i)
+                    Cs[((wm * MT + mt) * 16 + 4 * g + i) * CROW + (wn * NT + nt) * 16 + r] = acc[mt][nt][i];
+    }
     __syncthreads();
     constexpr int Q4 = BN / 4;  // float4 groups per row
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(
@@ -746,6 +788,8 @@ static const TileConfig kTileConfigs[] = {
     {2, 2, 2, 2, 1, 3, 128},  // 21: 64 x 64  bf16 through LDS, 128 k per block, 3 ahead
     {2, 4, 2, 2, 1, 2, 128},  // 22: 64 x 128 bf16 through LDS, 128 k per block
     {2, 2, 2, 4, 1, 2, 128},  // 23: 64 x 128 bf16 through LDS, 8 waves, 128 k per block
+    {4, 3, 2, 2, 2, 3},       // 24: 128 x 96  bf16 through LDS, 4 x 2 waves (k-steps split), 3 ahead
+    {4, 3, 2, 2, 2, 6},       // 25: 128 x 96  bf16 through LDS, 4 x 2 waves, 6 ahead
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -769,11 +813,11 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
         }                                                                                                \
         break;
 
-#define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN, D, KB)                                                  \
+#define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN, D, KB, KW)                                              \
     case IDX:                                                                                              \
-        if (mode == kTileBF16 && tb) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16, 1, KB>), grid, blk, 0, s, a); \
-        else if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16, 0, KB>), grid, blk, 0, s, a); \
-        else if (mode == kTileF2B) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileF2B, 0, KB>), grid, blk, 0, s, a); \
+        if (mode == kTileBF16 && tb) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16, 1, KB, KW>), grid, blk, 0, s, a); \
+        else if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileBF16, 0, KB, KW>), grid, blk, 0, s, a); \
+        else if (mode == kTileF2B) hipLaunchKernelGGL((dnnopt_tile_bf16_lds<MT, NT, WM, WN, D, kTileF2B, 0, KB, KW>), grid, blk, 0, s, a); \
         else return hipErrorInvalidValue;                                                                  \
         break;
 
@@ -791,25 +835,27 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_CASE(2, 2, 2, 2, 2, 1)
         DNNOPT_TILE_CASE(3, 2, 2, 2, 2, 2)
         DNNOPT_TILE_CASE(4, 2, 4, 2, 2, 1)
-        DNNOPT_TILE_LDS_CASE(5, 4, 4, 2, 2, 2, 0)
-        DNNOPT_TILE_LDS_CASE(6, 2, 2, 1, 4, 2, 0)
-        DNNOPT_TILE_LDS_CASE(7, 2, 4, 2, 2, 2, 0)
-        DNNOPT_TILE_LDS_CASE(8, 4, 4, 2, 2, 3, 0)
-        DNNOPT_TILE_LDS_CASE(9, 4, 4, 2, 2, 4, 0)
-        DNNOPT_TILE_LDS_CASE(10, 2, 2, 1, 4, 4, 0)
-        DNNOPT_TILE_LDS_CASE(11, 2, 4, 2, 2, 4, 0)
-        DNNOPT_TILE_LDS_CASE(12, 4, 2, 2, 4, 3, 0)
-        DNNOPT_TILE_LDS_CASE(13, 2, 3, 4, 2, 3, 0)
-        DNNOPT_TILE_LDS_CASE(14, 2, 3, 4, 2, 2, 0)
-        DNNOPT_TILE_LDS_CASE(15, 4, 2, 2, 4, 2, 0)
-        DNNOPT_TILE_LDS_CASE(16, 2, 1, 1, 4, 2, 256)
-        DNNOPT_TILE_LDS_CASE(17, 2, 2, 1, 2, 2, 256)
-        DNNOPT_TILE_LDS_CASE(18, 2, 2, 1, 4, 2, 128)
-        DNNOPT_TILE_LDS_CASE(19, 2, 1, 1, 4, 3, 128)
-        DNNOPT_TILE_LDS_CASE(20, 2, 3, 4, 2, 2, 128)
-        DNNOPT_TILE_LDS_CASE(21, 2, 2, 2, 2, 3, 128)
-        DNNOPT_TILE_LDS_CASE(22, 2, 4, 2, 2, 2, 128)
-        DNNOPT_TILE_LDS_CASE(23, 2, 2, 2, 4, 2, 128)
+        DNNOPT_TILE_LDS_CASE(5, 4, 4, 2, 2, 2, 0, 1)
+        DNNOPT_TILE_LDS_CASE(6, 2, 2, 1, 4, 2, 0, 1)
+        DNNOPT_TILE_LDS_CASE(7, 2, 4, 2, 2, 2, 0, 1)
+        DNNOPT_TILE_LDS_CASE(8, 4, 4, 2, 2, 3, 0, 1)
+        DNNOPT_TILE_LDS_CASE(9, 4, 4, 2, 2, 4, 0, 1)
+        DNNOPT_TILE_LDS_CASE(10, 2, 2, 1, 4, 4, 0, 1)
+        DNNOPT_TILE_LDS_CASE(11, 2, 4, 2, 2, 4, 0, 1)
+        DNNOPT_TILE_LDS_CASE(12, 4, 2, 2, 4, 3, 0, 1)
+        DNNOPT_TILE_LDS_CASE(13, 2, 3, 4, 2, 3, 0, 1)
+        DNNOPT_TILE_LDS_CASE(14, 2, 3, 4, 2, 2, 0, 1)
+        DNNOPT_TILE_LDS_CASE(15, 4, 2, 2, 4, 2, 0, 1)
+        DNNOPT_TILE_LDS_CASE(16, 2, 1, 1, 4, 2, 256, 1)
+        DNNOPT_TILE_LDS_CASE(17, 2, 2, 1, 2, 2, 256, 1)
+        DNNOPT_TILE_LDS_CASE(18, 2, 2, 1, 4, 2, 128, 1)
+        DNNOPT_TILE_LDS_CASE(19, 2, 1, 1, 4, 3, 128, 1)
+        DNNOPT_TILE_LDS_CASE(20, 2, 3, 4, 2, 2, 128, 1)
+        DNNOPT_TILE_LDS_CASE(21, 2, 2, 2, 2, 3, 128, 1)
+        DNNOPT_TILE_LDS_CASE(22, 2, 4, 2, 2, 2, 128, 1)
+        DNNOPT_TILE_LDS_CASE(23, 2, 2, 2, 4, 2, 128, 1)
+        DNNOPT_TILE_LDS_CASE(24, 4, 3, 2, 2, 3, 0, 2)
+        DNNOPT_TILE_LDS_CASE(25, 4, 3, 2, 2, 6, 0, 2)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
