@@ -646,6 +646,118 @@ def rocprof_summary(kernel, workload, trace_csv, pmc=None):
     return "\n".join(lines) + "\n", traffic
 
 
+def _graph_time_us(torch, stream, launches, reps=5):
+    """Median time of one launch: a graph of the launches (back to back on
+    one stream) is replayed between HIP events, `reps` times."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for fn in launches:
+            fn()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        g.replay()
+    torch.cuda.synchronize()
+    out = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) * 1e3 / len(launches))
+    return statistics.median(out)
+
+
+def probe(which):
+    """Floors the routing decisions are judged against (one JSON line each):
+      launch   the cost of one empty kernel launch in a graph;
+      read     contiguous streaming reads of the byte counts of B at C1 / C2
+               (and 1 GiB): the HBM read ceiling per size;
+      tiles    the skinny kernel's access pattern without its arithmetic at
+               the C1 / C2 shapes, with the planner's workgroup count;
+      combine  the C1 and C2 workloads with the k-split partials combined by
+               the separate reduce kernel (default) and by the last-arriving
+               workgroup (DNNOPT_SPLIT_REDUCE=0), each in its own process.
+    Buffers rotate over more than 600 MB so nothing is served from the
+    Infinity Cache between launches."""
+    import ctypes
+    import subprocess
+    import tempfile
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    b = _binding()
+    lib = b.load()
+    so = ctypes.CDLL(os.path.join(ROOT, "dnn-opt_amd", "lib", "libdnnopt_probe.so"))
+    so.dnnopt_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
+    so.dnnopt_probe_tiles.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                      ctypes.c_void_p]
+    so.dnnopt_probe_empty.argtypes = [ctypes.c_void_p]
+    for fn in (so.dnnopt_probe_read, so.dnnopt_probe_tiles, so.dnnopt_probe_empty):
+        fn.restype = ctypes.c_int
+    stream = torch.cuda.Stream(device=dev)
+    sp = stream.cuda_stream
+    out = torch.zeros(1, dtype=torch.float32, device=dev)
+    lines = []
+
+    def emit(d):
+        lines.append(d)
+        print(json.dumps(d), flush=True)
+
+    def check(rc):
+        if rc != 0:
+            raise RuntimeError(f"probe launch failed (status {rc})")
+
+    if which in ("launch", "all"):
+        us = _graph_time_us(torch, stream, [lambda: check(so.dnnopt_probe_empty(sp))] * 64)
+        emit({"probe": "launch", "us_per_launch": round(us, 3)})
+    shapes = [(1, 4096, 4096)] + [(M, N, 2048) for M in (2, 7) for N in (1009, 4099, 11003)]
+    if which in ("read", "all"):
+        for nbytes in sorted({4 * K * N for _, N, K in shapes} | {1 << 30}):
+            nbytes = nbytes // 16 * 16
+            copies = max(2, -(-(600 << 20) // nbytes))
+            bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(copies)]
+            launches = [lambda x=x: check(so.dnnopt_probe_read(x.data_ptr(), nbytes, out.data_ptr(), sp))
+                        for x in bufs] * max(1, 32 // copies)
+            us = _graph_time_us(torch, stream, launches)
+            emit({"probe": "read", "bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1)})
+            del bufs
+    if which in ("tiles", "all"):
+        for M, N, K in shapes:
+            if N % 4:
+                N4 = N + 4 - N % 4  # the probe reads whole 16-byte chunks: next multiple of 4 columns
+            else:
+                N4 = N
+            G = lib.plan_sgemm(M, N, K)["grid_x"]
+            nbytes = 4 * K * N4
+            copies = max(2, -(-(600 << 20) // nbytes))
+            bufs = [torch.ones(K * N4, dtype=torch.float32, device=dev) for _ in range(copies)]
+            launches = [lambda x=x: check(so.dnnopt_probe_tiles(x.data_ptr(), N4, K, G, out.data_ptr(), sp))
+                        for x in bufs] * max(1, 32 // copies)
+            us = _graph_time_us(torch, stream, launches)
+            emit({"probe": "tiles", "M": M, "N": N4, "K": K, "workgroups": G, "bytes": nbytes, "us": round(us, 3),
+                  "GBps": round(nbytes / us / 1e3, 1)})
+            del bufs
+    if which in ("combine", "all"):
+        for wl in ("c1", "c2"):
+            for mode, env in (("reduce kernel", "1"), ("last workgroup", "0")):
+                with tempfile.TemporaryDirectory() as td:
+                    detail = os.path.join(td, "d.jsonl")
+                    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--workload", wl, "--no-cpu",
+                                        "--detail", detail], env=dict(os.environ, DNNOPT_SPLIT_REDUCE=env),
+                                       capture_output=True, text=True, timeout=300)
+                    if r.returncode != 0:
+                        raise RuntimeError(f"bench.py --workload {wl} failed: {r.stderr[-2000:]}")
+                    d = json.loads(open(detail).read().splitlines()[-1])
+                emit({"probe": "combine", "workload": wl, "mode": mode, "us_per_step": round(d["ms_per_step"] * 1e3, 2),
+                      "GBps_step": round(d["GBps_step"], 1),
+                      "cases_us": {c["case"]: round(c["us_median"], 2) for c in d["per_case"]}})
+    return lines
+
+
 def copy_calibration(mib):
     """Plain copies of a known size: what FETCH_SIZE / WRITE_SIZE read for
     them scales the counters of the GEMM kernels to bytes."""
@@ -694,6 +806,9 @@ def main():
     ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
+    ap.add_argument("--probe", choices=["launch", "read", "tiles", "combine", "all"], default=None,
+                    help="only run the measurement probes (launch cost, read ceilings, the skinny access pattern, "
+                         "split-k combine variants); one JSON line each")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (scale for HBM byte counters)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="ARG",
@@ -703,6 +818,9 @@ def main():
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.probe:
+        probe(args.probe)
         return
     if args.rocprof_summary:
         a = args.rocprof_summary
