@@ -409,7 +409,7 @@ int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
     return DNNOPT_OK;
 }
 
-int plan_tall(int transB, int M, int N, int K, int lda, Launch* L, int ldc) {
+int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc) {
     *L = Launch{};
     if (ldc <= 0) ldc = N;
     // N <= 12 (a quarter or more of the padded 16-column MFMA tile wasted)
@@ -422,21 +422,23 @@ int plan_tall(int transB, int M, int N, int K, int lda, Launch* L, int ldc) {
     const size_t lds = tall_lds_bytes(nt, K);
     if (lds > 65536) return DNNOPT_ERR_UNSUPPORTED;
     if (((long long)(M - 1) * lda + K) * 4 >= 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
+    // B is read through one descriptor with 32-bit offsets.
+    if ((transB ? (long long)(N - 1) * ldb + K : (long long)(K - 1) * ldb + N) * 4 >= 0x7FFFFFFFll)
+        return DNNOPT_ERR_UNSUPPORTED;
     // C is stored through one descriptor from its first element.
     if (((long long)(M - 1) * ldc + N) * 4 >= 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
     // Each wave runs its row tiles as one serial chain of MFMAs, so the kernel
-    // needs about one tile for every wave of one workgroup per CU: 32-row
-    // tiles from ~48K rows (on 256 CUs); 16-row tiles (half the chain) from
-    // ~16K rows when K >= 256; below that the register tiles, which spread
-    // the same work over more waves, are faster.  Measured at N = 64, K = 256:
-    // 16K rows 15.0 (16-row tiles) vs 17.8 us, 32K rows 17.2 vs 23.0, 64K rows
-    // 29.6 (32-row tiles) vs 31.6 (16-row tiles).
+    // needs about one tile for every wave of one workgroup per CU: 16-row
+    // tiles from ~48K rows, and from ~16K rows when K >= 256; below that the
+    // register tiles, which spread the same work over more waves, are faster.
+    // Measured at N = 64, K = 256: 16K rows 15.0 vs 17.8 us (register tiles),
+    // 32K rows 17.2 vs 23.0.  16-row tiles beat 32-row tiles from 48K rows
+    // too (two tiles per wave, so one tile's C stores overlap the next
+    // tile's loads): 65536 x 16 x 256 17.6 vs 19.0 us, 131072 x 16 x 256 32.1
+    // vs 33.6, 65536 x 64 x 256 27.4 vs 28.6, 65536 x 48 x 128 14.3 vs 15.1.
     const long long waves = num_cus() * tall_waves();
-    int rt = 2;
-    if (ceil_div(M, 32) * 4 < 3 * waves) {
-        if (K < 256 || ceil_div(M, 16) * 2 < waves) return DNNOPT_ERR_UNSUPPORTED;
-        rt = 1;
-    }
+    int rt = 1;
+    if (ceil_div(M, 32) * 4 < 3 * waves && (K < 256 || ceil_div(M, 16) * 2 < waves)) return DNNOPT_ERR_UNSUPPORTED;
     static const int forced_rt = env_int("DNNOPT_TALL_RT", 0);
     if (forced_rt == 1 || forced_rt == 2) rt = forced_rt;
     const long long tiles = ceil_div(M, 16 * rt);
@@ -464,7 +466,7 @@ int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, La
         const char* e = getenv("DNNOPT_TALL");
         return !(e && *e && atoi(e) == 0);
     }();
-    if (tall_ok && !transA && plan_tall(transB, M, N, K, lda, L, ldc) == DNNOPT_OK) return DNNOPT_OK;
+    if (tall_ok && !transA && plan_tall(transB, M, N, K, lda, ldb, L, ldc) == DNNOPT_OK) return DNNOPT_OK;
     return plan_tile(kTileF32, transA, transB, M, N, K, lda, ldb, L, true, ldc);
 }
 

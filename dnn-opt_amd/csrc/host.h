@@ -81,7 +81,7 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L);
 // fp32, large M, N <= 64, B small enough to stay in LDS (no transposed A).
 // ldc: row stride of C (0 = N); C is addressed with 32-bit offsets from its
 // first element, so ((M - 1) * ldc + N) * 4 must stay below 2^31.
-int plan_tall(int transB, int M, int N, int K, int lda, Launch* L, int ldc = 0);
+int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc = 0);
 // M <= 8 against B stored N x K; mode 0 fp32, 1 bf16 storage.
 int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L);
 // lds_ok = false keeps bf16 GEMMs off the LDS-staged kernel (operands whose

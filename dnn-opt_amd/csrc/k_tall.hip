@@ -87,7 +87,10 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
     uint32_t l_off = (uint32_t)gw * (uint32_t)(16 * RT) * (uint32_t)p.lda * 4u;
     int l_kc = 0;
 
-    u32x4 ring[D][RT];
+    // D chunks in flight need D + 1 slots: chunk i + D is loaded into the
+    // slot chunk i - 1 left before chunk i's MFMAs are issued.
+    constexpr int S = D + 1;
+    u32x4 ring[S][RT];
     auto load = [&](int slot) {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) ring[slot][rt] = buf_load_x4(ra, lane_a[rt] + l_off);
@@ -103,8 +106,10 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
         for (int d = 0; d < D; ++d) load(d);
     }
 
-    // Stage B.  Both layouts have KC * 16 * NP / 4 16-byte units, at most
-    // kStageU per thread (the host caps the LDS image at 64 KiB); every
+    // Stage B.  Unit u = (k quad kq = u / NP, column n = u % NP) is the
+    // 16-byte chunk at bsm[u * 4], so consecutive threads write consecutive
+    // chunks (no LDS bank conflicts).  There are KC * 4 * NP units, at
+    // most kStageU per thread (the host caps B's image at 64 KiB); every
     // thread issues all its loads before its first LDS write, so staging
     // costs one L2 round trip rather than one per unit.
     {
@@ -113,49 +118,32 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
         constexpr int kStageU = 65536 / 16 / (kTallWaves * 64);
         const int units = KC * 4 * NP;
         u32x4 v[kStageU];
-        if constexpr (TB) {
-            // unit u = (k quad kq, column n) -> 4 floats at bsm[(kq * NP + n) * 4]
 #pragma unroll
-            for (int j = 0; j < kStageU; ++j) {
-                const int u = (int)threadIdx.x + j * kTallWaves * 64;
-                const int kq = u / NP, n = u % NP, k0 = 4 * kq;
-                const uint32_t off = (u < units && n < p.N && k0 < p.K) ? ((uint32_t)n * p.ldb + k0) * 4u : kOobOffset;
-                v[j] = buf_load_x4(rb, off);
+        for (int j = 0; j < kStageU; ++j) {
+            const int u = (int)threadIdx.x + j * kTallWaves * 64;
+            const int kq = u / NP, n = u % NP, k0 = 4 * kq;
+            const bool ok = u < units && n < p.N;
+            if constexpr (TB) {
+                // B stored N x K: the chunk is one 16-byte load from row n
+                // (its elements past K, in the row's padding or the next
+                // row, are masked when written).
+                v[j] = buf_load_x4(rb, ok && k0 < p.K ? ((uint32_t)n * p.ldb + k0) * 4u : kOobOffset);
+            } else {
+                // B stored K x N: four loads from rows k0..k0+3, column n;
+                // a wave's loads of one row are contiguous.  Rows past K
+                // read zero.
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    v[j][c] = buf_load_x1(rb, ok && k0 + c < p.K ? ((uint32_t)(k0 + c) * p.ldb + n) * 4u : kOobOffset);
             }
+        }
 #pragma unroll
-            for (int j = 0; j < kStageU; ++j) {
-                const int u = (int)threadIdx.x + j * kTallWaves * 64;
-                if (u < units) *reinterpret_cast<u32x4*>(&bsm[(size_t)u * 4]) = keep_first(v[j], p.K - 4 * (u / NP));
-            }
-        } else {
-            // B stored K x N: unit u = (k, 4 columns from n0), one 16-byte
-            // load spread over the 4 column slots of quad k / 4.  Columns past
-            // N (in the last partial group, or past the padded width) and rows
-            // past K are zero (out-of-range offsets read 0).
-            const int NQ = NP / 4;
-            const bool vec = (p.ldb & 3) == 0;
-#pragma unroll
-            for (int j = 0; j < kStageU; ++j) {
-                const int u = (int)threadIdx.x + j * kTallWaves * 64;
-                const int k = u / NQ, n0 = (u % NQ) * 4;
-                const bool row_ok = u < units && k < p.K;
-                if (vec && n0 + 4 <= p.N) {
-                    v[j] = buf_load_x4(rb, row_ok ? ((uint32_t)k * p.ldb + n0) * 4u : kOobOffset);
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        v[j][c] = buf_load_x1(rb, (row_ok && n0 + c < p.N) ? ((uint32_t)k * p.ldb + n0 + c) * 4u
-                                                                            : kOobOffset);
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < kStageU; ++j) {
-                const int u = (int)threadIdx.x + j * kTallWaves * 64;
-                const int k = u / NQ, n0 = (u % NQ) * 4;
-                if (u < units) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) bsm[((size_t)(k >> 2) * NP + n0 + c) * 4 + (k & 3)] = as_f32(v[j][c]);
-                }
+        for (int j = 0; j < kStageU; ++j) {
+            const int u = (int)threadIdx.x + j * kTallWaves * 64;
+            if (u < units) {
+                u32x4 w = v[j];
+                if constexpr (TB) w = keep_first(w, p.K - 4 * (u / NP));
+                *reinterpret_cast<u32x4*>(&bsm[(size_t)u * 4]) = w;
             }
         }
     }
@@ -236,28 +224,24 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
         }
     };
 
-    // Chunk i lives in slot i % D from its load until its MFMAs; full groups
-    // of D run without conditionals so the waits stay exact.
+    // Chunk i lives in slot i % S from its load until its MFMAs.  Unrolled
+    // over the S slots, every slot keeps its registers around the loop (no
+    // copy at the back edge, whose wait would drain every load in flight),
+    // and the wait for chunk i leaves the D later chunks' loads in flight.
     int i0 = 0;
-    for (; i0 + D <= total; i0 += D) {
+    for (; i0 + S <= total; i0 += S) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            u32x4 a[RT];
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) a[rt] = ring[d][rt];
-            load(d);
-            step(a);
+        for (int s = 0; s < S; ++s) {
+            load((s + D) % S);
+            // Keep the loads ahead of this chunk's wait and MFMAs.
+            __builtin_amdgcn_sched_barrier(0);
+            step(ring[s]);
         }
     }
+    // The last total - i0 < S chunks are in slots 0, 1, ... already.
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-        if (i0 + d < total) {
-            u32x4 a[RT];
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) a[rt] = ring[d][rt];
-            step(a);
-        }
-    }
+    for (int s = 0; s < S - 1; ++s)
+        if (i0 + s < total) step(ring[s]);
 }
 
 int tall_waves() { return kTallWaves; }

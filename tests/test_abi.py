@@ -159,7 +159,7 @@ def test_plans_for_tall_skinny(lib):
     p = lib.plan_sgemm(32768, 64, 256)
     assert p["kernel"] == b.K_TALL_F32 and p["rows"] == 16            # 16-row tiles at mid M (K >= 256)
     assert lib.plan_sgemm(32768, 64, 128)["kernel"] == b.K_TILE_F32   # ... but not for short K
-    assert lib.plan_sgemm(65536, 64, 256)["rows"] == 32
+    assert lib.plan_sgemm(65536, 64, 256)["rows"] == 16
     assert lib.plan_sgemm(65536, 65, 64)["kernel"] == b.K_TILE_F32
     assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TALL_F32   # N = 16 with K >= 128: B in LDS
     assert lib.plan_sgemm(65536, 16, 64)["kernel"] == b.K_TILE_F32    # short K: register tiles
@@ -180,6 +180,15 @@ def test_plan_respects_c_row_stride(lib):
     assert lib.plan_sgemm(M, N, K) == lib.plan_sgemm_ex(M, N, K, K, N, N)
     with pytest.raises(b.DnnoptError):
         lib.plan_sgemm_ex(M, N, K, K, N, N - 1)
+
+
+def test_plan_respects_b_row_stride(lib):
+    """The tall kernel stages B through one descriptor with 32-bit offsets:
+    ((K - 1) * ldb + N) * 4 at or past 2^31 routes the GEMM to the tiles."""
+    b = u.binding()
+    M, N, K = 65536, 64, 256
+    assert lib.plan_sgemm_ex(M, N, K, K, 2105375, N)["kernel"] == b.K_TALL_F32   # (255 * 2105375 + 64) * 4 < 2^31
+    assert lib.plan_sgemm_ex(M, N, K, K, 2105376, N)["kernel"] == b.K_TILE_F32   # ... and past it
 
 
 def test_plan_rejects_bad_args(lib):
