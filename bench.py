@@ -10,9 +10,9 @@ K = 2048, alpha = beta = 1, A, B ~ N(0, 0.02), C ~ U[-1, 1).  One step runs
 all twelve shapes once; its rate is `value`.  The default run also times the
 other configs -- C1, C3, C4 through the bf16-storage entry and through the
 fp32-input gemm_bf16 (c4f), C5, and C5's shapes through the fp32-API
-gemm_int8 (c5f) -- each as its own workload, and reports
-their step rates, dominant kernels and per-shape GB/s, TFLOP/s and roofline
-fractions under `configs`.  `--workload NAME` times one workload (its rate
+gemm_int8 (c5f) -- each as its own workload, and reports every timed
+workload's step rate, dominant kernel and per-shape GB/s, TFLOP/s and
+roofline fractions under `configs` (C2's own per-shape figures included).  `--workload NAME` times one workload (its rate
 becomes `value`); `--workload all` adds the oneDNN-hook workload;
 `--detail FILE` appends the full per-workload records.
 
@@ -866,7 +866,9 @@ def main():
         "roofline_kernel": {k: r["roofline"][k] for k in ("kernel", "launch_us", "bytes_per_launch")},
         "cpu_baseline": cpu,
         "cpu_reference": cpu_ref,
-        "configs": {wl: config_summary(rr) for wl, rr in results.items() if wl != main_name},
+        # every workload timed in this run, the `value` workload included
+        # (its per-case figures)
+        "configs": {wl: config_summary(rr) for wl, rr in results.items()},
     }
     if args.detail:
         os.makedirs(os.path.dirname(os.path.abspath(args.detail)), exist_ok=True)
