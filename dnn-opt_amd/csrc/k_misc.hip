@@ -183,7 +183,10 @@ hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int 
 // splits are out of range and read zero -- before the first add, so the
 // reduction costs one memory round trip; the adds are predicated on the
 // split count, so the sum is exactly the ordered sum of the real partials.
-constexpr int kRedBatch = 32;
+// The batch is the smallest of 8, 16, 32, 64 that holds every split of a
+// tile (at most 64), so a tile of 5 splits issues 8 loads per output, not
+// 32, and one of 64 splits needs one round trip, not two.
+template <int kRedBatch>
 __global__ __launch_bounds__(256) void dnnopt_skinny_reduce(const float* __restrict__ part, int G, int T, int tw,
                                                            int M, int N, int ncols_pad, float alpha, float beta,
                                                            float* C, int ldc, const float* bias) {
@@ -246,8 +249,20 @@ hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, 
     // The kernel addresses the partials with 32-bit buffer offsets.
     if (G < 1 || T < 1 || (long long)(G / T + (G % T ? 1 : 0)) * M * ncols_pad * 4 > 0x7FFFFFFFll)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(dnnopt_skinny_reduce, dim3((N + 255) / 256, M), dim3(256), 0, s, part, G, T, tw, M, N,
-                       ncols_pad, alpha, beta, C, ldc, bias);
+    const int max_splits = G / T + (G % T ? 1 : 0);
+    const dim3 grid((N + 255) / 256, M);
+    if (max_splits <= 8)
+        hipLaunchKernelGGL(dnnopt_skinny_reduce<8>, grid, dim3(256), 0, s, part, G, T, tw, M, N, ncols_pad, alpha, beta,
+                           C, ldc, bias);
+    else if (max_splits <= 16)
+        hipLaunchKernelGGL(dnnopt_skinny_reduce<16>, grid, dim3(256), 0, s, part, G, T, tw, M, N, ncols_pad, alpha,
+                           beta, C, ldc, bias);
+    else if (max_splits <= 32)
+        hipLaunchKernelGGL(dnnopt_skinny_reduce<32>, grid, dim3(256), 0, s, part, G, T, tw, M, N, ncols_pad, alpha,
+                           beta, C, ldc, bias);
+    else
+        hipLaunchKernelGGL(dnnopt_skinny_reduce<64>, grid, dim3(256), 0, s, part, G, T, tw, M, N, ncols_pad, alpha,
+                           beta, C, ldc, bias);
     return hipGetLastError();
 }
 
