@@ -67,3 +67,19 @@ def test_traffic_profiles_are_consistent():
     for f in glob.glob(os.path.join(u.ROOT, "profiles", "*_kernel_trace.txt")):
         text = open(f).read()
         assert "rocprofv3 --kernel-trace --stats" in text and "avg_us" in text, f
+
+
+def test_counter_files_name_a_traced_kernel():
+    """Every MFMA/LDS counter file names the kernel instance it read, and that
+    instance appears in a committed kernel trace of the same workload, so the
+    counters describe a kernel the bench launches."""
+    files = glob.glob(os.path.join(u.ROOT, "profiles", "*_mfma_counters.txt"))
+    assert files
+    for f in files:
+        wl = os.path.basename(f)[: -len("_mfma_counters.txt")].rsplit("_", 1)[1]
+        names = [l.split("kernel:", 1)[1].strip() for l in open(f) if l.startswith("# kernel:")]
+        assert names, f
+        inst = names[0].replace("void ", "").replace("dnnopt_hip::", "").replace("(anonymous namespace)::", "")
+        traces = glob.glob(os.path.join(u.ROOT, "profiles", f"*_{wl}_kernel_trace.txt"))
+        assert traces, f
+        assert any(inst in open(t).read() for t in traces), (f, inst)
