@@ -338,12 +338,24 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int l
     *L = Launch{};
     static const int forced_splits = env_int("DNNOPT_S8_SPLITS", 0);
     // M <= 16: 16 x 16 tiles with k split over the 8 waves of a workgroup
-    // (one launch, no partial sums); larger M: 32 x 32 tiles through LDS with
-    // 256-byte k-blocks.
-    int cfg = M <= 16 ? 5 : 20;
+    // (one launch, no partial sums).  Larger M: operands copied into LDS by
+    // the memory unit (LDS DMA), the largest of 64 x 64 (4 stages of
+    // 128-byte blocks), 64 x 32 (3 stages of 256 bytes) and 32 x 32 (4
+    // stages of 256 bytes) that still gives every CU a tile.  Measured (us,
+    // against the register-staged 32 x 32 LDS kernel): 128 x 4096 x 4096
+    // 11.2 vs 12.6, 128 x 2048 x 4096 7.9 vs 9.6, 64 x 4096 x 4096 8.8 vs
+    // 10.2, 256 x 4096 x 4096 13.9 vs 21.7, 128 x 8192 x 4096 16.1 vs 22.5.
+    int cfg = 5;
+    if (M > 16) {
+        const long long cus_ = num_cus();
+        if (ceil_div(M, 64) * ceil_div(N, 64) >= cus_) cfg = 29;
+        else if (ceil_div(M, 64) * ceil_div(N, 32) >= cus_) cfg = 23;
+        else cfg = 22;
+    }
     if (forced_cfg >= 0 && forced_cfg < s8_config_count()) cfg = forced_cfg;
     if (cfg >= kS8FirstLds && !lds_ok) cfg = M <= 16 ? 5 : (M >= 128 ? 3 : 2);
     const bool lds = cfg >= kS8FirstLds;
+    const bool dma = cfg >= kS8FirstDma;
     const S8Config c = s8_config(cfg);
     const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
     const long long tn = ceil_div(N, bn), tm = ceil_div(M, bm), tiles = tn * tm;
@@ -377,7 +389,8 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int l
     L->grid = lds ? dim3((unsigned)xcd_grid((int)tn, (int)tm), 1, (unsigned)s) : dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(int32_t) : 0;
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
-    fill_pub(L, DNNOPT_K_MFMA_S8, lds ? "dnnopt_s8_lds" : "dnnopt_mfma_s8", bm, bn, (int)s, waves_per_wg * 64);
+    fill_pub(L, DNNOPT_K_MFMA_S8, dma ? "dnnopt_s8_dma" : (lds ? "dnnopt_s8_lds" : "dnnopt_mfma_s8"), bm, bn, (int)s,
+             waves_per_wg * 64);
     return DNNOPT_OK;
 }
 

@@ -15,6 +15,8 @@
 // Tails: rows of A past M and rows of B past N read as zero (out-of-range
 // buffer offset); bytes of A past K are masked to zero inside the last chunk,
 // which zeroes their products whatever B holds there.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -452,6 +454,216 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     }
 }
 
+// ---------------------------------------------------------------- LDS DMA
+// The LDS-staged tile of above with both operands copied into LDS by the
+// vector memory unit itself (buffer_load_dwordx4 ... lds: lane l of a wave
+// load writes its 16 bytes at the wave's LDS address + 16 l), so no block
+// passes through registers and no LDS store waits on them.  S stages, one
+// __shared__ array each, blocks S - 1 ahead; per block one wait for this
+// wave's own copies of the next block, one barrier, the copy of block
+// i + S - 1 into the stage block i - 1 left, then block i's fragments.
+// LDS rows are BK bytes, chunk c of row r at slot c ^ (r mod 16) (mod 8 for
+// 8-chunk rows): the wave load that fills a 1 KB span of a stage reads, for
+// its lane at slot s of row r, global chunk s ^ swz(r) of that row, so its
+// lanes still read whole rows of 128 / 256 bytes, and the 16 rows an MFMA
+// operand reads fall in 16 different bank groups.  Bytes of A past K are
+// zeroed in registers after the fragment read.
+template <int CPR>
+__device__ __forceinline__ int dma_swz(int row, int c) { return c ^ (row & (CPR >= 16 ? 15 : CPR - 1)); }
+
+// One 16-byte-per-lane buffer load into LDS: lane l's bytes land at
+// lds + 16 l (lds wave-uniform).  The builtin exists only for the device
+// pass; the host pass never runs the kernel body.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+#else
+    (void)r;
+    (void)lds;
+    (void)voffset;
+#endif
+}
+
+// s_waitcnt vmcnt(n) (n < 64), other counters not waited on.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+template <int MT, int NT, int WM, int WN, int NS, int EPI, int BK>
+__global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_dma(S8Args p) {
+    constexpr int BM = WM * MT * 16, BN = WN * NT * 16;
+    constexpr int NW = WM * WN;
+    constexpr int CPR = BK / 16;  // 16-byte chunks per LDS row
+    constexpr int KK = BK / 64;   // MFMA k-steps per block
+    constexpr int A_BYTES = BM * BK, STAGE = (BM + BN) * BK;
+    static_assert(NS >= 2 && NS <= 4, "2 to 4 stages");
+    static_assert(A_BYTES % 1024 == 0 && STAGE % (NW * 1024) == 0, "whole 1 KB wave loads, as many per wave");
+    constexpr int IPW = STAGE / 1024 / NW;  // wave loads per wave and block
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st2[NS > 2 ? STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) char st3[NS > 3 ? STAGE : 16];
+    auto stage = [&](int i) -> char* { return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3; };
+
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+    const int w = wave_id();
+    const int wn = w % WN, wm = w / WN;
+    const TileXY tile = xcd_tile((int)blockIdx.x, p.tiles_n, p.tiles_m);
+    if (!tile.ok) return;
+    const int tile_n = tile.n, tile_m = tile.m, split = blockIdx.z;
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const int nblk = (p.K + BK - 1) / BK;
+    const int b_lo = (int)(((long long)nblk * split) / p.splits);
+    const int b_hi = (int)(((long long)nblk * (split + 1)) / p.splits);
+    const int nb = b_hi - b_lo;
+
+    // Ranges end at the last byte of each operand, rounded up to a dword;
+    // rows past M / N start at kOobOffset and read zero.
+    const __amdgpu_buffer_rsrc_t ra =
+        make_rsrc(p.A + (size_t)m0 * p.lda, range31(((size_t)(p.M - 1 - m0) * p.lda + p.K + 3) & ~(size_t)3));
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(p.B + (size_t)n0 * p.ldb, range31(((size_t)(p.N - 1 - n0) * p.ldb + p.K + 3) & ~(size_t)3));
+    uint32_t goff[IPW];
+    bool gb[IPW];
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+        const int q = (w * IPW + j) * 1024 + 16 * lane;  // byte of the stage this lane fills
+        const bool isb = (w * IPW + j) * 1024 >= A_BYTES;
+        const int qq = isb ? q - A_BYTES : q;
+        const int row = qq / BK, c = dma_swz<CPR>(row, (qq % BK) / 16);
+        const bool ok = isb ? n0 + row < p.N : m0 + row < p.M;
+        goff[j] = ok ? (uint32_t)row * (uint32_t)(isb ? p.ldb : p.lda) + 16u * c : kOobOffset;
+        gb[j] = isb;
+    }
+    // Block `blk` of this split into stage `st`; blocks past the split read
+    // nothing (out-of-range offsets) but are issued, so every wave's count of
+    // outstanding loads per block is the same.
+    auto dma = [&](int st, int blk) {
+        const uint32_t k0 = blk < b_hi ? (uint32_t)blk * BK : kOobOffset;
+        char* base = stage(st) + w * IPW * 1024;
+#pragma unroll
+        for (int j = 0; j < IPW; ++j)
+            lds_dma16(gb[j] ? rb : ra, base + j * 1024, goff[j] + k0);
+    };
+
+    int a_rd[KK][MT], b_rd[KK][NT];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+        const int c = kk * 4 + g;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int row = (wm * MT + mt) * 16 + r;
+            a_rd[kk][mt] = row * BK + dma_swz<CPR>(row, c) * 16;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int row = (wn * NT + nt) * 16 + r;
+            b_rd[kk][nt] = A_BYTES + row * BK + dma_swz<CPR>(row, c) * 16;
+        }
+    }
+    // Two accumulator sets (even and odd k-steps) halve the dependent MFMA
+    // chain of a block; integer sums, so the split does not change C.
+    constexpr int AS = KK >= 2 ? 2 : 1;
+    i32x4 acc[AS][MT][NT];
+#pragma unroll
+    for (int a = 0; a < AS; ++a)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[a][mt][nt] = i32x4{0, 0, 0, 0};
+    // TAIL: the block holds k = K - 1 (compiled separately, so the common
+    // block has no branch between its fragment reads).
+    auto compute_blk = [&](int st, int blk, auto tail_tag) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        const char* St = stage(st);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            i32x4 af[MT], bfr[NT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const i32x4*>(St + a_rd[kk][mt]);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) bfr[nt] = *reinterpret_cast<const i32x4*>(St + b_rd[kk][nt]);
+            if constexpr (TAIL) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) af[mt] = mask_chunk(af[mt], p.K - (blk * BK + kk * 64 + 16 * g));
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[kk % AS][mt][nt] =
+                        __builtin_amdgcn_mfma_i32_16x16x64_i8(af[mt], bfr[nt], acc[kk % AS][mt][nt], 0, 0, 0);
+        }
+    };
+    auto compute = [&](int st, int blk) {
+        if ((blk + 1) * BK > p.K) compute_blk(st, blk, std::true_type{});
+        else compute_blk(st, blk, std::false_type{});
+    };
+    auto iter = [&](int i, int st) {
+        // This wave's copies of block i are done (the NS - 2 later blocks'
+        // may still be in flight); after the barrier every wave's are, and
+        // every wave has consumed block i - 1's fragments.
+        wait_vmcnt<(NS - 2) * IPW>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        dma((st + NS - 1) % NS, b_lo + i + NS - 1);
+        compute(st, b_lo + i);
+    };
+
+    if (nb > 0) {
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s) dma(s, b_lo + s);
+    }
+    int i0 = 0;
+    for (; i0 + NS <= nb; i0 += NS) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) iter(i0 + s, s);
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+        if (i0 + s < nb) iter(i0 + s, s);
+    // Every copy has landed before the workgroup ends (the last ones read
+    // nothing but still write their stage).
+    wait_vmcnt<0>();
+
+    i32x4 res[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            res[mt][nt] = acc[0][mt][nt];
+            if constexpr (AS > 1) res[mt][nt] += acc[1][mt][nt];
+        }
+    // Lane element i of sub-tile (mt, nt): row 4g + i, column r.
+    const int tiles = p.tiles_n * p.tiles_m;
+    const int tile_id = tile_m * p.tiles_n + tile_n;
+    const float dq = EPI == 1 && p.amax ? dyn_dequant_scale(p.amax, p.alpha) : 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const int nl = (wn * NT + nt) * 16 + r, n = n0 + nl;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int ml = (wm * MT + mt) * 16 + 4 * g + i, m = m0 + ml;
+                if (p.splits > 1) {
+                    // Exact int32 partial tile [split][tile][BM * BN], summed
+                    // by the reduce kernel that follows.
+                    p.part[((size_t)split * tiles + tile_id) * (BM * BN) + ml * BN + nl] = res[mt][nt][i];
+                } else if (m < p.M && n < p.N) {
+                    if constexpr (EPI == 0) {
+                        static_cast<int32_t*>(p.C)[(size_t)m * p.ldc + n] = res[mt][nt][i];
+                    } else {
+                        float* c = static_cast<float*>(p.C) + (size_t)m * p.ldc + n;
+                        *c = s8_out(res[mt][nt][i], n, p.scale, p.amax, dq, p.beta, c);
+                    }
+                }
+            }
+        }
+}
+
 // ---------------------------------------------------------------- launch table
 // {MT, NT, WM, WN, KW}
 static const S8Config kS8Configs[] = {
@@ -476,6 +688,16 @@ static const S8Config kS8Configs[] = {
     {2, 2, 2, 2, 1, 2, 512},  // 18: 64 x 64 through LDS, 512-byte k blocks
     {1, 1, 1, 4, 1, 2, 512},  // 19: 16 x 64 through LDS, 512-byte k blocks (M <= 16)
     {1, 1, 2, 2, 1, 2, 256},  // 20: 32 x 32 through LDS, 256-byte k blocks
+    // LDS DMA: {MT, NT, WM, WN, 1, stages, k bytes per block}
+    {1, 1, 2, 2, 1, 3, 256},  // 21: 32 x 32, 3 stages
+    {1, 1, 2, 2, 1, 4, 256},  // 22: 32 x 32, 4 stages
+    {2, 1, 2, 2, 1, 3, 256},  // 23: 64 x 32, 3 stages
+    {1, 1, 2, 2, 1, 4, 128},  // 24: 32 x 32, 4 stages of 128-byte blocks
+    {2, 2, 2, 2, 1, 3, 256},  // 25: 64 x 64, 3 stages
+    {1, 1, 1, 4, 1, 4, 256},  // 26: 16 x 64, 4 stages (M <= 16)
+    {2, 1, 2, 2, 1, 4, 256},  // 27: 64 x 32, 4 stages
+    {2, 1, 2, 2, 1, 4, 128},  // 28: 64 x 32, 4 stages of 128-byte blocks
+    {2, 2, 2, 2, 1, 4, 128},  // 29: 64 x 64, 4 stages of 128-byte blocks
 };
 
 int s8_config_count() { return (int)(sizeof(kS8Configs) / sizeof(kS8Configs[0])); }
@@ -505,6 +727,15 @@ static hipError_t launch_s8_cfg(int cfg, dim3 grid, const S8Args& a, hipStream_t
         case 18: hipLaunchKernelGGL((dnnopt_s8_lds<2, 2, 2, 2, 2, EPI, 512>), grid, dim3(256), 0, s, a); break;
         case 19: hipLaunchKernelGGL((dnnopt_s8_lds<1, 1, 1, 4, 2, EPI, 512>), grid, dim3(256), 0, s, a); break;
         case 20: hipLaunchKernelGGL((dnnopt_s8_lds<1, 1, 2, 2, 2, EPI, 256>), grid, dim3(256), 0, s, a); break;
+        case 21: hipLaunchKernelGGL((dnnopt_s8_dma<1, 1, 2, 2, 3, EPI, 256>), grid, dim3(256), 0, s, a); break;
+        case 22: hipLaunchKernelGGL((dnnopt_s8_dma<1, 1, 2, 2, 4, EPI, 256>), grid, dim3(256), 0, s, a); break;
+        case 23: hipLaunchKernelGGL((dnnopt_s8_dma<2, 1, 2, 2, 3, EPI, 256>), grid, dim3(256), 0, s, a); break;
+        case 24: hipLaunchKernelGGL((dnnopt_s8_dma<1, 1, 2, 2, 4, EPI, 128>), grid, dim3(256), 0, s, a); break;
+        case 25: hipLaunchKernelGGL((dnnopt_s8_dma<2, 2, 2, 2, 3, EPI, 256>), grid, dim3(256), 0, s, a); break;
+        case 26: hipLaunchKernelGGL((dnnopt_s8_dma<1, 1, 1, 4, 4, EPI, 256>), grid, dim3(256), 0, s, a); break;
+        case 27: hipLaunchKernelGGL((dnnopt_s8_dma<2, 1, 2, 2, 4, EPI, 256>), grid, dim3(256), 0, s, a); break;
+        case 28: hipLaunchKernelGGL((dnnopt_s8_dma<2, 1, 2, 2, 4, EPI, 128>), grid, dim3(256), 0, s, a); break;
+        case 29: hipLaunchKernelGGL((dnnopt_s8_dma<2, 2, 2, 2, 4, EPI, 128>), grid, dim3(256), 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -142,6 +142,10 @@ struct S8Config {
 // Configurations from this index on stage both operands through LDS; they
 // need 4-byte aligned rows and reduce k-splits with the reduce kernel only.
 constexpr int kS8FirstLds = 10;
+// Configurations from this index on copy both operands into LDS with the
+// vector memory unit's LDS path (no register staging); same requirements
+// and tile order as the LDS-staged ones, depth = stages.
+constexpr int kS8FirstDma = 21;
 // Index into the table of built int8 configurations.
 int s8_config_count();
 S8Config s8_config(int idx);
