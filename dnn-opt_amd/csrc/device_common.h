@@ -238,4 +238,24 @@ __device__ __forceinline__ bool split_ticket(unsigned* ticket, unsigned nsplits,
     return *lds_flag != 0;
 }
 
+// One 16-byte-per-lane buffer load into LDS: lane l's bytes land at
+// lds + 16 l (lds wave-uniform).  The builtin exists only for the device
+// pass; the host pass never runs the kernel body.
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+#else
+    (void)r;
+    (void)lds;
+    (void)voffset;
+#endif
+}
+
+// s_waitcnt vmcnt(n) (n < 64), other counters not waited on.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 }  // namespace dnnopt_dev

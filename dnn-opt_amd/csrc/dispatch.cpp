@@ -254,7 +254,13 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         // 128 k per LDS block below M = 128 (fewer barriers, more bytes per
         // block in flight); measured on MI355X at N = 11008, K = 4096.
         cfg = M > 128 ? 13 : (M > 64 ? 23 : (M > 32 ? 21 : 19));
-        if (forced_cfg >= kTileFirstLds && forced_cfg < tile_config_count()) cfg = forced_cfg;
+        // bf16 storage above M = 128: the same 128 x 96 tile with the
+        // operands copied into LDS by the memory unit (C4 M=256 43.1 vs 45.4
+        // us; no gain measured at M = 32).
+        if (M > 128 && mode == kTileBF16) cfg = 26;
+        if (forced_cfg >= kTileFirstLds && forced_cfg < tile_config_count() &&
+            (forced_cfg < kTileFirstDma || mode == kTileBF16))
+            cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
     } else if (mode == kTileF32 && N <= 64 && M >= 4096) {
@@ -314,8 +320,10 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(float) : 0;
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
     const int kernel = mode == kTileF32 ? DNNOPT_K_TILE_F32 : DNNOPT_K_TILE_BF16;
-    fill_pub(L, kernel, mode == kTileF32 ? "dnnopt_tile_f32" : (lds ? "dnnopt_tile_bf16_lds" : "dnnopt_tile_bf16"), bm,
-             bn, (int)s, waves_per_wg * 64);
+    fill_pub(L, kernel,
+             mode == kTileF32 ? "dnnopt_tile_f32"
+                              : (cfg >= kTileFirstDma ? "dnnopt_tile_bf16_dma" : (lds ? "dnnopt_tile_bf16_lds" : "dnnopt_tile_bf16")),
+             bm, bn, (int)s, waves_per_wg * 64);
     return DNNOPT_OK;
 }
 

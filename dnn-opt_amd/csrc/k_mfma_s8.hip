@@ -471,26 +471,6 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
 template <int CPR>
 __device__ __forceinline__ int dma_swz(int row, int c) { return c ^ (row & (CPR >= 16 ? 15 : CPR - 1)); }
 
-// One 16-byte-per-lane buffer load into LDS: lane l's bytes land at
-// lds + 16 l (lds wave-uniform).  The builtin exists only for the device
-// pass; the host pass never runs the kernel body.
-__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voffset) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
-#else
-    (void)r;
-    (void)lds;
-    (void)voffset;
-#endif
-}
-
-// s_waitcnt vmcnt(n) (n < 64), other counters not waited on.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
 template <int MT, int NT, int WM, int WN, int NS, int EPI, int BK>
 __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_dma(S8Args p) {
     constexpr int BM = WM * MT * 16, BN = WN * NT * 16;

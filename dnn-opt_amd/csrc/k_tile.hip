@@ -22,6 +22,8 @@
 // Tails: operand rows/columns outside M/N and k outside K read as zero
 // (out-of-range buffer offsets, and masking inside a partially valid 128-bit
 // chunk), so garbage past an edge never reaches an accumulator.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -424,6 +426,9 @@ __device__ __forceinline__ u32x4 pack_bf16x8(const u32x4& lo, const u32x4& hi) {
 // Physical 16-byte chunk of logical chunk c (0..7) in LDS row `row`.
 __device__ __forceinline__ int swz_a(int row, int c) { return c ^ (row & 7); }
 
+// 32-byte segment swizzle of LDS row k of a K x N B tile (LDS DMA kernel).
+__device__ __forceinline__ int bseg_swz(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+
 }  // namespace
 
 // KW: waves that split each k-block's MFMA k-steps for the same output
@@ -761,6 +766,220 @@ __global__ __launch_bounds__(WM* WN * KW * 64) void dnnopt_tile_bf16_lds(TileArg
     }
 }
 
+// ---------------------------------------------------------------- bf16, LDS DMA
+// bf16 storage: the tile above with both operands copied into LDS by the
+// vector memory unit (buffer_load_dwordx4 ... lds: a wave load fills 1 KB of
+// a stage, lane l's 16 bytes at +16 l), so no block passes through registers
+// and no LDS store waits on them.  The stage layout is the one the
+// register-staged kernel builds for A (rows of BK bf16 with XOR-swizzled
+// 16-byte chunks) and for B stored N x K (like A); B stored K x N is kept as
+// BK rows of 256 bytes (BN <= 128 columns) whose 32-byte segments are
+// XOR-swizzled by f(k) = (k mod 4) + 4 ((k / 8) mod 2), so that the 8 rows
+// {k0..k0+3, k0+8..k0+11} one half of a ds_read_b64_tr_b16 gathers from
+// land in 8 different bank groups (the register-staged kernel's 32-byte
+// padding leaves rows k and k + 8 on the same banks).  The lane that fills
+// stage byte q loads the global chunk that belongs there (a padding slot
+// loads nothing).
+// The stage's 1 KB units are dealt round robin over the waves; a wave with
+// one unit fewer issues one load into a spare 1 KB so that every wave waits
+// on the same count.  S stages (one __shared__ array each), blocks S - 1
+// ahead; per block one wait for this wave's own copies of the next block, one
+// barrier, the copy of block i + S - 1 into the stage block i - 1 left, then
+// block i's MFMAs.  Elements past K of k-contiguous rows (A, and B stored
+// N x K) are zeroed in registers after the fragment read, in a separately
+// compiled tail block; rows of a K x N B past K are out of range (zero).
+template <int MT, int NT, int WM, int WN, int NS, int TB, int BK>
+__global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_dma(TileArgs p) {
+    using SH = TileShape<MT, NT, WM, WN, 1>;
+    constexpr int BM = SH::BM, BN = SH::BN;
+    constexpr int NW = WM * WN;
+    constexpr int ROWB = BK * 2;  // bytes of one A row (BK bf16)
+    constexpr int KK = BK / 32;   // MFMA k-steps per block
+    constexpr int BROW = TB ? ROWB : 256;
+    static_assert(TB || BN <= 128, "a K x N B row of the tile fits 256 bytes");
+    constexpr int A_BYTES = BM * ROWB, B_BYTES = TB ? BN * ROWB : BK * BROW, STAGE = A_BYTES + B_BYTES;
+    static_assert(NS >= 2 && NS <= 4, "2 to 4 stages");
+    static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole 1 KB wave loads per operand");
+    constexpr int UNITS = STAGE / 1024;
+    constexpr int IPW = (UNITS + NW - 1) / NW;  // wave loads per wave and block
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st2[NS > 2 ? STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) char st3[NS > 3 ? STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) char spare[UNITS % NW ? 1024 : 16];
+    __shared__ float red_unused[1];
+    __shared__ int last_flag;
+    auto stage = [&](int i) -> char* { return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3; };
+
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+    const int w = wave_id();
+    const int wn = w % WN, wm = w / WN;
+    const TileXY tile = xcd_tile((int)blockIdx.x, p.tiles_n, p.tiles_m);
+    if (!tile.ok) return;
+    const int m0 = tile.m * BM, n0 = tile.n * BN;
+    const int nblk = (p.K + BK - 1) / BK;
+    const int b_lo = (int)(((long long)nblk * blockIdx.z) / p.splits);
+    const int b_hi = (int)(((long long)nblk * (blockIdx.z + 1)) / p.splits);
+    const int nb = b_hi - b_lo;
+
+    const char* abase = static_cast<const char*>(p.A) + (size_t)m0 * p.lda * 2;
+    const char* bbase = static_cast<const char*>(p.B) + (TB ? (size_t)n0 * p.ldb : (size_t)n0) * 2;
+    // Ranges end at the last element of each operand, rounded up to a dword.
+    const __amdgpu_buffer_rsrc_t ra =
+        make_rsrc(abase, clamp_rec((((size_t)(p.M - 1 - m0) * p.lda + p.K) * 2 + 3) & ~(size_t)3));
+    const size_t b_last = TB ? (size_t)(p.N - 1 - n0) * p.ldb + p.K : (size_t)(p.K - 1) * p.ldb + (p.N - n0);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase, clamp_rec((b_last * 2 + 3) & ~(size_t)3));
+
+    // This lane's global byte offset (block 0) for each of its wave's loads;
+    // rows past M / N and padding slots start at kOobOffset (read zero).
+    uint32_t goff[IPW];
+    bool gb[IPW];
+    int unit[IPW];
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+        const int u = j * NW + w;
+        unit[j] = u < UNITS ? u : -1;
+        gb[j] = u * 1024 >= A_BYTES;
+        goff[j] = kOobOffset;
+        if (u >= UNITS) continue;
+        const int q = u * 1024 + 16 * lane;
+        if (q < A_BYTES) {
+            const int row = q / ROWB, c = swz_a(row, (q % ROWB) / 16);
+            if (m0 + row < p.M) goff[j] = ((uint32_t)row * p.lda + 8 * c) * 2u;
+        } else if constexpr (TB) {
+            const int qq = q - A_BYTES, row = qq / ROWB, c = swz_a(row, (qq % ROWB) / 16);
+            if (n0 + row < p.N) goff[j] = ((uint32_t)row * p.ldb + 8 * c) * 2u;
+        } else {
+            const int qq = q - A_BYTES, kr = qq / BROW, b = qq % BROW;
+            const int cb = (((b >> 5) ^ bseg_swz(kr)) << 5) | (b & 31);  // column byte held by slot byte b
+            if (cb < 2 * BN) goff[j] = (uint32_t)kr * p.ldb * 2u + (uint32_t)cb;
+        }
+    }
+    // Block `blk` into stage `st`; blocks past the split read nothing
+    // (out-of-range offsets) but are issued, so every wave's count of
+    // outstanding loads per block is the same.
+    auto dma = [&](int st, int blk) {
+        const bool live = blk < b_hi;
+        const uint32_t ka = live ? (uint32_t)blk * BK * 2u : kOobOffset;
+        const uint32_t kb = TB ? ka : (live ? (uint32_t)blk * BK * (uint32_t)p.ldb * 2u : kOobOffset);
+        char* base = stage(st);
+#pragma unroll
+        for (int j = 0; j < IPW; ++j)
+            lds_dma16(gb[j] ? rb : ra, unit[j] >= 0 ? base + unit[j] * 1024 : spare, goff[j] + (gb[j] ? kb : ka));
+    };
+
+    int a_rd[KK][MT], b_rd[KK][NT], b_rd2[KK][NT];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+        const int c = kk * 4 + g;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int row = (wm * MT + mt) * 16 + r;
+            a_rd[kk][mt] = row * ROWB + swz_a(row, c) * 16;
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            if constexpr (TB) {
+                const int n = (wn * NT + nt) * 16 + r;
+                b_rd[kk][nt] = A_BYTES + n * ROWB + swz_a(n, c) * 16;
+                b_rd2[kk][nt] = 0;
+            } else {
+                // transposing reads: rows kk * 32 + 8 g + r / 4 and that + 4,
+                // columns 4 (r % 4) .. + 3 of the 16-column tile
+                const int cb = ((wn * NT + nt) * 16 + 4 * (r & 3)) * 2;
+                const int k1 = kk * 32 + 8 * g + (r >> 2), k2 = k1 + 4;
+                b_rd[kk][nt] = A_BYTES + k1 * BROW + ((((cb >> 5) ^ bseg_swz(k1)) << 5) | (cb & 31));
+                b_rd2[kk][nt] = A_BYTES + k2 * BROW + ((((cb >> 5) ^ bseg_swz(k2)) << 5) | (cb & 31));
+            }
+        }
+    }
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto keep_k = [](u32x4 v, int kvalid) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const int keep = kvalid - 2 * d;
+            v[d] = keep >= 2 ? v[d] : (keep == 1 ? (v[d] & 0xFFFFu) : 0u);
+        }
+        return v;
+    };
+    auto compute_blk = [&](int st, int blk, auto tail_tag) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        const char* St = stage(st);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            u32x4 af[MT], bfr[NT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const u32x4*>(St + a_rd[kk][mt]);
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                if constexpr (TB) {
+                    bfr[nt] = *reinterpret_cast<const u32x4*>(St + b_rd[kk][nt]);
+                } else {
+                    typedef short s16x4 __attribute__((ext_vector_type(4)));
+                    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+                    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(St + b_rd[kk][nt]));
+                    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(St + b_rd2[kk][nt]));
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+                    bfr[nt] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+                }
+            }
+            if constexpr (TAIL) {
+                const int kv = p.K - (blk * BK + kk * 32 + 8 * g);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) af[mt] = keep_k(af[mt], kv);
+                if constexpr (TB) {
+#pragma unroll
+                    for (int nt = 0; nt < NT; ++nt) bfr[nt] = keep_k(bfr[nt], kv);
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[mt]),
+                                                                         __builtin_bit_cast(bf16x8, bfr[nt]),
+                                                                         acc[mt][nt], 0, 0, 0);
+        }
+    };
+    auto compute = [&](int st, int blk) {
+        if ((blk + 1) * BK > p.K) compute_blk(st, blk, std::true_type{});
+        else compute_blk(st, blk, std::false_type{});
+    };
+    auto iter = [&](int i, int st) {
+        // This wave's copies of block i are done (the NS - 2 later blocks'
+        // may still be in flight); after the barrier every wave's are, and
+        // every wave has consumed block i - 1's fragments.
+        wait_vmcnt<(NS - 2) * IPW>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        dma((st + NS - 1) % NS, b_lo + i + NS - 1);
+        compute(st, b_lo + i);
+    };
+
+    if (nb > 0) {
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s) dma(s, b_lo + s);
+    }
+    int i0 = 0;
+    for (; i0 + NS <= nb; i0 += NS) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) iter(i0 + s, s);
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+        if (i0 + s < nb) iter(i0 + s, s);
+    // Every copy has landed before the workgroup ends (the run-on copies
+    // read nothing but still write their stage).
+    wait_vmcnt<0>();
+    tile_finish<MT, NT, WM, WN, 1>(p, acc, red_unused, &last_flag, w, lane, tile.n, tile.m, p.tiles_n,
+                                   p.tiles_n * p.tiles_m);
+}
+
 // ---------------------------------------------------------------- launch table
 // {MT, NT, WM, WN, KW}
 static const TileConfig kTileConfigs[] = {
@@ -790,6 +1009,14 @@ static const TileConfig kTileConfigs[] = {
     {2, 2, 2, 4, 1, 2, 128},  // 23: 64 x 128 bf16 through LDS, 8 waves, 128 k per block
     {4, 3, 2, 2, 2, 3},       // 24: 128 x 96  bf16 through LDS, 4 x 2 waves (k-steps split), 3 ahead
     {4, 3, 2, 2, 2, 6},       // 25: 128 x 96  bf16 through LDS, 4 x 2 waves, 6 ahead
+    // bf16 storage, LDS DMA: {MT, NT, WM, WN, 1, stages, k per block}
+    {2, 3, 4, 2, 1, 3, 64},   // 26: 128 x 96, 3 stages
+    {2, 3, 4, 2, 1, 4, 64},   // 27: 128 x 96, 4 stages
+    {2, 1, 1, 4, 1, 3, 128},  // 28: 32 x 64, 3 stages of 128 k
+    {2, 2, 2, 2, 1, 3, 128},  // 29: 64 x 64, 3 stages of 128 k
+    {2, 2, 2, 4, 1, 3, 128},  // 30: 64 x 128, 8 waves, 3 stages of 128 k
+    {4, 3, 2, 2, 1, 3, 64},   // 31: 128 x 96, 4 waves, 3 stages
+    {2, 4, 4, 2, 1, 3, 64},   // 32: 128 x 128, 8 waves, 3 stages
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -811,6 +1038,13 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
         } else {                                                                                         \
             hipLaunchKernelGGL((dnnopt_tile_bf16<MT, NT, WM, WN, KW, kTileF2B, 1>), grid, blk, 0, s, a);  \
         }                                                                                                \
+        break;
+
+#define DNNOPT_TILE_DMA_CASE(IDX, MT, NT, WM, WN, NS, BK)                                                  \
+    case IDX:                                                                                              \
+        if (mode == kTileBF16 && tb) hipLaunchKernelGGL((dnnopt_tile_bf16_dma<MT, NT, WM, WN, NS, 1, BK>), grid, blk, 0, s, a); \
+        else if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_dma<MT, NT, WM, WN, NS, 0, BK>), grid, blk, 0, s, a); \
+        else return hipErrorInvalidValue;                                                                  \
         break;
 
 #define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN, D, KB, KW)                                              \
@@ -856,6 +1090,13 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_LDS_CASE(23, 2, 2, 2, 4, 2, 128, 1)
         DNNOPT_TILE_LDS_CASE(24, 4, 3, 2, 2, 3, 0, 2)
         DNNOPT_TILE_LDS_CASE(25, 4, 3, 2, 2, 6, 0, 2)
+        DNNOPT_TILE_DMA_CASE(26, 2, 3, 4, 2, 3, 64)
+        DNNOPT_TILE_DMA_CASE(27, 2, 3, 4, 2, 4, 64)
+        DNNOPT_TILE_DMA_CASE(28, 2, 1, 1, 4, 3, 128)
+        DNNOPT_TILE_DMA_CASE(29, 2, 2, 2, 2, 3, 128)
+        DNNOPT_TILE_DMA_CASE(30, 2, 2, 2, 4, 3, 128)
+        DNNOPT_TILE_DMA_CASE(31, 4, 3, 2, 2, 3, 64)
+        DNNOPT_TILE_DMA_CASE(32, 2, 4, 4, 2, 3, 64)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -211,6 +211,10 @@ TileConfig tile_config(int idx);
 // fp32-rounded modes only, rows of A and B 4-byte aligned, no transposed A
 // (B stored N x K with bf16 storage).
 constexpr int kTileFirstLds = 5;
+// Configurations from this index on copy the operands into LDS with the
+// memory unit's LDS path (bf16 storage only; the fp32-input mode keeps the
+// register-staged kernel).
+constexpr int kTileFirstDma = 26;
 // k per LDS block of an LDS-staged configuration: its kblk (or
 // DNNOPT_LDS_KB) when both stages fit in 128 KiB of LDS, else 64.
 constexpr int tile_lds_bk(int bm, int bn, int kblk) {
