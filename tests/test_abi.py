@@ -296,3 +296,22 @@ def test_aligned_alloc(lib):
     q = lib.cxx["aligned_malloc_huge"](5 << 20, 64)
     assert q and q % 64 == 0
     lib.cxx["aligned_free_huge"](q, 5 << 20)
+
+
+def test_plans_route_lds_dma_kernels(lib):
+    """int8 above M = 16 and bf16 storage above M = 128 copy their operands
+    into LDS with the memory unit; the int8 tile is the largest of 64 x 64,
+    64 x 32 and 32 x 32 that gives every CU a tile; fp32-input bf16 and
+    unaligned operands keep the register-staged kernels."""
+    b = u.binding()
+    cases = {(128, 4096): (64, 32), (128, 4093): (64, 32), (256, 4096): (64, 64), (128, 8192): (64, 64),
+             (32, 4096): (32, 32), (17, 4096): (32, 32)}
+    for (M, N), (bm, bn) in cases.items():
+        p = lib.plan_s8(M, N, 4096)
+        assert p["name"] == "dnnopt_s8_dma" and (p["rows"], p["cols"]) == (bm, bn), (M, N, p)
+    assert lib.plan_s8(8, 4096, 4096)["name"] == "dnnopt_mfma_s8"   # M <= 16: register tiles, k over 8 waves
+    for M in (129, 256):
+        assert lib.plan_bf16(M, 11008, 4096)["name"] == "dnnopt_tile_bf16_dma"
+        assert lib.plan_bf16_ex(M, 11008, 4096, transB=1)["name"] == "dnnopt_tile_bf16_dma"
+        assert lib.plan_bf16(M, 11008, 4096, fp32_inputs=1)["name"] == "dnnopt_tile_bf16_lds"
+    assert lib.plan_bf16(128, 11008, 4096)["name"] == "dnnopt_tile_bf16_lds"
