@@ -256,8 +256,16 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         cfg = M > 128 ? 13 : (M > 64 ? 23 : (M > 32 ? 21 : 19));
         // bf16 storage above M = 128: the same 128 x 96 tile with the
         // operands copied into LDS by the memory unit (C4 M=256 43.1 vs 45.4
-        // us; no gain measured at M = 32).
-        if (M > 128 && mode == kTileBF16) cfg = 26;
+        // us; no gain measured at M = 32).  When 128-row tiles would take more
+        // than one round over the CUs, 256 x 96 tiles (64 x 48 per wave: 30%
+        // fewer LDS bytes read per MFMA) in fewer rounds: 512 x 11008 x 4096
+        // 67 vs 86 us, 1024 x 4096 x 4096 58 vs 77 us, 384 x 11008 x 4096 66
+        // vs 82 us; 512 x 4096 x 4096 (one round of 128-row tiles) keeps the
+        // 128-row tile, 42 vs 51 us.
+        if (M > 128 && mode == kTileBF16) {
+            cfg = 26;
+            if (ceil_div(M, 128) * ceil_div(N, 96) > num_cus()) cfg = 33;
+        }
         if (forced_cfg >= kTileFirstLds && forced_cfg < tile_config_count() &&
             (forced_cfg < kTileFirstDma || mode == kTileBF16))
             cfg = forced_cfg;
@@ -316,7 +324,13 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     L->tm = (int)tm;
     // LDS-staged tiles are launched as one XCD-ordered row of workgroups.
     L->grid = lds ? dim3((unsigned)xcd_grid((int)tn, (int)tm), 1, (unsigned)s) : dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
-    L->defer_reduce = (s > 1 && (split_reduce_mode() || s > kTicketSplitLimit || tiles > kMaxTickets || lds)) ? 1 : 0;
+    // k-splits of the LDS-staged kernels are summed by a reduce kernel, except
+    // for the LDS-DMA tiles (DNNOPT_TILE_TICKET=1): the last workgroup to
+    // finish a tile adds the others' partials.
+    static const bool dma_ticket = env_int("DNNOPT_TILE_TICKET", 0) == 1;
+    const bool ticket_ok = !lds || (dma_ticket && cfg >= kTileFirstDma);
+    L->defer_reduce =
+        (s > 1 && (split_reduce_mode() || s > kTicketSplitLimit || tiles > kMaxTickets || !ticket_ok)) ? 1 : 0;
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(float) : 0;
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
     const int kernel = mode == kTileF32 ? DNNOPT_K_TILE_F32 : DNNOPT_K_TILE_BF16;

@@ -98,8 +98,10 @@ namespace dnnopt_hip {
 // of the last-arriving-workgroup reduction, so both give the same bits.
 // Q > 1 (many splits): Q threads per output each add an ascending range of
 // splits, and the Q range sums are added in ascending order through LDS; the
-// order is fixed, so the result is still reproducible.
-template <int Q>
+// order is fixed, so the result is still reproducible.  SB loads (the
+// smallest of 2, 4, 8, 16 that covers a thread's splits) are issued per batch,
+// so a 2-way split issues 2 loads per output group, not 16.
+template <int Q, int SB = 16>
 __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restrict__ part, int splits,
                                                            int tiles_n, int tiles, int bm, int bn, int M, int N,
                                                            float alpha, float beta, float* C, int ldc,
@@ -129,7 +131,7 @@ __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restr
         // One batch of unconditional 16-byte loads per kSplitBatch splits
         // (offsets past s_hi are out of range and read zero), then the adds
         // in ascending split order, predicated on the range.
-        constexpr int kSplitBatch = 16;
+        constexpr int kSplitBatch = SB;
         const uint32_t stride = (uint32_t)tiles * (uint32_t)per_tile * 16u;
         const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, range31((size_t)splits * tiles * per_tile * 16));
         const uint32_t base = (uint32_t)idx * 16u;
@@ -153,10 +155,19 @@ __global__ __launch_bounds__(256) void dnnopt_splitk_reduce(const float* __restr
             if ((long long)splits * qq / Q < (long long)splits * (qq + 1) / Q) s += red[qq * OUTS + o];
     }
     if (!live) return;
+    f4 out;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        if (n + e < N)
-            c[e] = add_bias(beta == 0.0f ? alpha * s[e] : __builtin_fmaf(alpha, s[e], beta * c_old[e]), bias, n + e);
+        out[e] = n + e < N ? add_bias(beta == 0.0f ? alpha * s[e] : __builtin_fmaf(alpha, s[e], beta * c_old[e]), bias, n + e)
+                           : 0.0f;
+    // Four whole columns on a 16-byte boundary: one 16-byte store.
+    if (n + 4 <= N && (reinterpret_cast<uintptr_t>(c) & 15) == 0) {
+        *reinterpret_cast<f4*>(c) = out;
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (n + e < N) c[e] = out[e];
+    }
 }
 
 hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int tiles_m, int bm, int bn, int M,
@@ -166,8 +177,20 @@ hipError_t launch_splitk_reduce(const float* part, int splits, int tiles_n, int 
     // The kernel addresses the partials with 32-bit buffer offsets.
     if (splits < 1 || (long long)splits * quads * 16 > 0x7FFFFFFFll) return hipErrorInvalidValue;
     if (splits <= 16) {
-        hipLaunchKernelGGL(dnnopt_splitk_reduce<1>, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, part,
-                           splits, tiles_n, tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc, bias);
+        const dim3 grid((unsigned)((quads + 255) / 256));
+        const int tiles = tiles_n * tiles_m;
+        if (splits <= 2)
+            hipLaunchKernelGGL((dnnopt_splitk_reduce<1, 2>), grid, dim3(256), 0, s, part, splits, tiles_n, tiles, bm,
+                               bn, M, N, alpha, beta, C, ldc, bias);
+        else if (splits <= 4)
+            hipLaunchKernelGGL((dnnopt_splitk_reduce<1, 4>), grid, dim3(256), 0, s, part, splits, tiles_n, tiles, bm,
+                               bn, M, N, alpha, beta, C, ldc, bias);
+        else if (splits <= 8)
+            hipLaunchKernelGGL((dnnopt_splitk_reduce<1, 8>), grid, dim3(256), 0, s, part, splits, tiles_n, tiles, bm,
+                               bn, M, N, alpha, beta, C, ldc, bias);
+        else
+            hipLaunchKernelGGL((dnnopt_splitk_reduce<1, 16>), grid, dim3(256), 0, s, part, splits, tiles_n, tiles,
+                               bm, bn, M, N, alpha, beta, C, ldc, bias);
     } else {
         hipLaunchKernelGGL(dnnopt_splitk_reduce<16>, dim3((unsigned)((quads + 15) / 16)), dim3(256), 0, s, part,
                            splits, tiles_n, tiles_n * tiles_m, bm, bn, M, N, alpha, beta, C, ldc, bias);

@@ -132,9 +132,12 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
                     const int nl = (wn * NT + nt) * 16 + r;
                     const size_t off0 = (size_t)tile_id * (S::BM * S::BN) + ml * S::BN + nl;
                     const size_t stride = (size_t)tiles * (S::BM * S::BN);
-                    float s = as_f32(buf_load_x1_coherent(rp, (uint32_t)(off0 * 4)));
+                    // Ascending split order; this workgroup's own partial is
+                    // the value in its registers (the same bits it stored).
+                    const float mine = acc[mt][nt][i];
+                    float s = split == 0 ? mine : as_f32(buf_load_x1_coherent(rp, (uint32_t)(off0 * 4)));
                     for (int sp = 1; sp < p.splits; ++sp)
-                        s += as_f32(buf_load_x1_coherent(rp, (uint32_t)((off0 + sp * stride) * 4)));
+                        s += sp == split ? mine : as_f32(buf_load_x1_coherent(rp, (uint32_t)((off0 + sp * stride) * 4)));
                     acc[mt][nt][i] = s;
                 }
     } else if (wk != 0) {
@@ -1017,6 +1020,8 @@ static const TileConfig kTileConfigs[] = {
     {2, 2, 2, 4, 1, 3, 128},  // 30: 64 x 128, 8 waves, 3 stages of 128 k
     {4, 3, 2, 2, 1, 3, 64},   // 31: 128 x 96, 4 waves, 3 stages
     {2, 4, 4, 2, 1, 3, 64},   // 32: 128 x 128, 8 waves, 3 stages
+    {4, 3, 4, 2, 1, 3, 64},   // 33: 256 x 96, 8 waves (64 x 48 each), 3 stages
+    {4, 4, 4, 2, 1, 3, 64},   // 34: 256 x 128, 8 waves (64 x 64 each), 3 stages
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -1097,6 +1102,8 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_DMA_CASE(30, 2, 2, 2, 4, 3, 128)
         DNNOPT_TILE_DMA_CASE(31, 4, 3, 2, 2, 3, 64)
         DNNOPT_TILE_DMA_CASE(32, 2, 4, 4, 2, 3, 64)
+        DNNOPT_TILE_DMA_CASE(33, 4, 3, 4, 2, 3, 64)
+        DNNOPT_TILE_DMA_CASE(34, 4, 4, 4, 2, 3, 64)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -315,3 +315,9 @@ def test_plans_route_lds_dma_kernels(lib):
         assert lib.plan_bf16_ex(M, 11008, 4096, transB=1)["name"] == "dnnopt_tile_bf16_dma"
         assert lib.plan_bf16(M, 11008, 4096, fp32_inputs=1)["name"] == "dnnopt_tile_bf16_lds"
     assert lib.plan_bf16(128, 11008, 4096)["name"] == "dnnopt_tile_bf16_lds"
+    # 256 x 96 tiles once 128 x 96 tiles take more than one round over the CUs
+    cus = 256  # MI355X (and the planner's figure when no GPU is visible)
+    for (M, N), rows in {(256, 11008): 128, (384, 11008): 256, (1024, 4096): 256, (512, 4096): 128}.items():
+        want = 256 if -(-M // 128) * -(-N // 96) > cus else 128
+        for p in (lib.plan_bf16(M, N, 4096), lib.plan_bf16_ex(M, N, 4096, transB=1)):
+            assert p["name"] == "dnnopt_tile_bf16_dma" and (p["rows"], p["cols"]) == (want, 96), (M, N, p)

@@ -303,6 +303,26 @@ def test_bf16_lds_tiles(lib, orc, dev, M, N, K, pa, pb, mode):
     u.assert_fp32_close(host(dC), want, scale, K, f"lds {mode} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("tb", [0, 1])
+def test_bf16_dma_256_row_tiles(lib, orc, dev, tb):
+    """bf16 storage with more 128-row tiles than CUs takes 256 x 96 tiles:
+    ragged M and N, a K tail inside a 64-k block, padded strides, B stored
+    K x N and N x K."""
+    M, N, K = 1030, 4100, 200
+    lda, ldb = K + 8, (K + 4 if tb else N + 2)
+    p = lib.plan_bf16_ex(M, N, K, transB=tb)
+    assert p["name"] == "dnnopt_tile_bf16_dma" and p["rows"] == 256, p
+    A = u.bf16_bits(orc, u.normal(orc, M * lda, 1)).reshape(M, lda)
+    Bs = u.bf16_bits(orc, u.normal(orc, (N if tb else K) * ldb, 2, 0, 0.02)).reshape(N if tb else K, ldb)
+    Bkn = Bs[:, :K].T if tb else Bs[:, :N]
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    want, scale = u.exact(u.bf16_value(A)[:, :K], u.bf16_value(np.ascontiguousarray(Bkn)), 0.5, 1.0, C0)
+    dC = dev_copy(C0, dev)
+    lib.gemm_bf16_ex(M, N, K, 0.5, dev_copy(A.view(np.int16), dev), lda, dev_copy(Bs.view(np.int16), dev), ldb, 1.0,
+                     dC, N, transB=tb, stream=stream())
+    u.assert_fp32_close(host(dC), want, scale, K, f"dma 256-row tiles tb={tb}")
+
+
 def test_bf16_lds_misaligned_falls_back(lib, orc, dev):
     """bf16 operands 2 bytes off a 4-byte boundary take the register-only tiles."""
     M, N, K = 128, 512, 256
