@@ -678,9 +678,17 @@ def probe(which):
                the C1 / C2 shapes, with the planner's workgroup count;
       combine  the C1 and C2 workloads with the k-split partials combined by
                the separate reduce kernel (default) and by the last-arriving
-               workgroup (DNNOPT_SPLIT_REDUCE=0), each in its own process.
+               workgroup (DNNOPT_SPLIT_REDUCE=0), each in its own process;
+      overlap  LDS reads, loads into registers and bf16 MFMAs of the same
+               waves, alone and together (one workgroup of 8 waves per CU):
+               whether the LDS-staged tile kernels can hide one behind the
+               other;
+      dma      the LDS-DMA copy pattern of the int8 64 x 32 tile (384 KiB per
+               CU) from L2-resident and from HBM-resident sources;
+      narrow   C2's matrices read as narrow column strips, all of k in one
+               workgroup (no k-split across workgroups, no partial sums).
     Buffers rotate over more than 600 MB so nothing is served from the
-    Infinity Cache between launches."""
+    Infinity Cache between launches (except where a probe says L2)."""
     import ctypes
     import subprocess
     import tempfile
@@ -696,8 +704,15 @@ def probe(which):
     so.dnnopt_probe_tiles.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                       ctypes.c_void_p]
     so.dnnopt_probe_empty.argtypes = [ctypes.c_void_p]
-    for fn in (so.dnnopt_probe_read, so.dnnopt_probe_tiles, so.dnnopt_probe_empty):
+    so.dnnopt_probe_overlap.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                        ctypes.c_void_p]
+    so.dnnopt_probe_dma.argtypes = [ctypes.c_void_p, ctypes.c_uint, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    so.dnnopt_probe_narrow.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_void_p]
+    for fn in (so.dnnopt_probe_read, so.dnnopt_probe_tiles, so.dnnopt_probe_empty, so.dnnopt_probe_overlap,
+               so.dnnopt_probe_dma, so.dnnopt_probe_narrow):
         fn.restype = ctypes.c_int
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
     stream = torch.cuda.Stream(device=dev)
     sp = stream.cuda_stream
     out = torch.zeros(1, dtype=torch.float32, device=dev)
@@ -740,6 +755,39 @@ def probe(which):
             us = _graph_time_us(torch, stream, launches)
             emit({"probe": "tiles", "M": M, "N": N4, "K": K, "workgroups": G, "bytes": nbytes, "us": round(us, 3),
                   "GBps": round(nbytes / us / 1e3, 1)})
+            del bufs
+    if which in ("overlap", "all"):
+        src = torch.ones(1 << 21, dtype=torch.uint8, device=dev)
+        iters = 2000
+        for mode, name in ((1, "lds"), (2, "mfma"), (3, "lds+mfma"), (4, "vmem"), (6, "vmem+mfma")):
+            us = _graph_time_us(torch, stream, [lambda m=mode: check(so.dnnopt_probe_overlap(
+                m, src.data_ptr(), cus, iters, out.data_ptr(), sp))] * 4)
+            emit({"probe": "overlap", "mode": name, "ns_per_iter": round(us * 1e3 / iters, 1),
+                  "per_cu_iter": {"lds_read_KiB": 80 if mode & 1 else 0, "bf16_mfma_16x16x32": 96 if mode & 2 else 0,
+                                  "vmem_KiB": 32 if mode & 4 else 0}})
+        del src
+    if which in ("dma", "all"):
+        region = 96 * 4096
+        for name, nreg, copies in (("L2", 32, 1), ("HBM", cus, max(2, -(-(600 << 20) // (cus * region))))):
+            bufs = [torch.ones(nreg * region, dtype=torch.uint8, device=dev) for _ in range(copies)]
+            launches = [lambda x=x: check(so.dnnopt_probe_dma(x.data_ptr(), nreg, cus, out.data_ptr(), sp))
+                        for x in bufs] * max(1, 32 // copies)
+            us = _graph_time_us(torch, stream, launches)
+            emit({"probe": "dma", "source": name, "bytes_per_cu": region, "us": round(us, 3),
+                  "GBps_per_cu": round(region / us / 1e3, 1), "GBps_total": round(cus * region / us / 1e3, 1)})
+            del bufs
+    if which in ("narrow", "all"):
+        for N in (1012, 4100, 11004):
+            K = 2048
+            nbytes = 4 * K * N
+            copies = max(2, -(-(600 << 20) // nbytes))
+            bufs = [torch.ones(K * N, dtype=torch.float32, device=dev) for _ in range(copies)]
+            for cols in (16, 32, 64):
+                launches = [lambda x=x, c=cols: check(so.dnnopt_probe_narrow(x.data_ptr(), N, K, c, out.data_ptr(), sp))
+                            for x in bufs] * max(1, 32 // copies)
+                us = _graph_time_us(torch, stream, launches)
+                emit({"probe": "narrow", "N": N, "K": K, "cols": cols, "workgroups": -(-N // cols), "bytes": nbytes,
+                      "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1)})
             del bufs
     if which in ("combine", "all"):
         for wl in ("c1", "c2"):
@@ -806,9 +854,11 @@ def main():
     ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
-    ap.add_argument("--probe", choices=["launch", "read", "tiles", "combine", "all"], default=None,
+    ap.add_argument("--probe", choices=["launch", "read", "tiles", "combine", "overlap", "dma", "narrow", "all"],
+                    default=None,
                     help="only run the measurement probes (launch cost, read ceilings, the skinny access pattern, "
-                         "split-k combine variants); one JSON line each")
+                         "split-k combine variants, LDS / MFMA overlap, LDS-DMA copy rate, narrow strips); one JSON "
+                         "line each")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (scale for HBM byte counters)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="ARG",

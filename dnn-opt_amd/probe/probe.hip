@@ -10,9 +10,21 @@
 //                       of 256 floats (1 KiB per wave and row), k split over
 //                       the 8 waves of a workgroup and over G / T workgroups
 //                       per tile, 16 rows in flight per wave;
-//   dnnopt_probe_empty  an empty kernel: the fixed cost of one launch.
+//   dnnopt_probe_empty  an empty kernel: the fixed cost of one launch;
+//   dnnopt_probe_overlap  whether LDS reads, loads into registers and bf16
+//                       MFMAs of the same waves overlap in time (the
+//                       LDS-staged tile kernels' per-block budget);
+//   dnnopt_probe_dma    the memory unit's LDS path (buffer_load ... lds) at
+//                       the int8 64 x 32 tile's pattern: per-CU copy rate
+//                       from L2 and from HBM;
+//   dnnopt_probe_narrow narrow column strips of a K x N fp32 matrix, all of
+//                       k in one workgroup (no k-split across workgroups,
+//                       so no partial sums): the alternative to the skinny
+//                       kernel's split-k plan.
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+
+#include "device_common.h"
 
 namespace {
 
@@ -69,6 +81,146 @@ __global__ __launch_bounds__(512) void probe_tiles(const float* __restrict__ B, 
 
 __global__ void probe_empty() {}
 
+using dnnopt_dev::bf16x8;
+using dnnopt_dev::f32x4;
+using dnnopt_dev::u32x4;
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// MODE bits, per wave and iteration: 1 = LDS reads of a 128 x 96 bf16 tile's
+// wave share (4 ds_read_b128 + 12 ds_read_b64_tr_b16, 10 KB), 2 = 12 bf16
+// MFMAs (16x16x32) on the previous iteration's operands, 4 = four 1 KB loads
+// into registers from an L2-resident 2 MB buffer.  8 waves per workgroup, one
+// workgroup per CU; the operands of the MFMAs are what the reads / loads of
+// the previous iteration returned, so the two can run concurrently.
+template <int MODE>
+__global__ __launch_bounds__(512) void probe_overlap(const char* src, unsigned* out, int iters) {
+    __shared__ __attribute__((aligned(16))) char rd[65536];
+    const int lane = (int)threadIdx.x & 63, w = (int)threadIdx.x >> 6, r = lane & 15, g = lane >> 4;
+    for (int i = (int)threadIdx.x; i < 16384; i += 512) reinterpret_cast<unsigned*>(rd)[i] = (unsigned)i;
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t rs = dnnopt_dev::make_rsrc(src, 1u << 21);
+    u32x4 ca[4] = {}, cv[4] = {};
+    u32x2 cb[12] = {};
+    f32x4 acc[3] = {};
+    for (int it = 0; it < iters; ++it) {
+        // No read of an iteration may be moved out of the loop (the LDS and
+        // buffer addresses repeat with short periods).
+        asm volatile("" ::: "memory");
+        u32x4 na[4] = {}, nv[4] = {};
+        u32x2 nb[12] = {};
+        if (MODE & 1) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                na[j] = *reinterpret_cast<const u32x4*>(rd + ((w * 4 + j) * 1024 + lane * 16 + it * 64) % 65536);
+#pragma unroll
+                for (int q = 0; q < 3; ++q) {
+                    // rows 16 (w, j, q) + row of 256 bytes, 32-byte segment rotated by row: no bank conflicts
+                    const int row = g * 4 + (r >> 2);
+                    const int byte = (((w * 12 + j * 3 + q) * 16 + row) * 256 + ((((row & 7) + it) & 7) * 32) +
+                                      (r & 3) * 8) & 65535;
+                    nb[j * 3 + q] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(rd + byte)));
+                }
+            }
+        }
+        if (MODE & 4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                nv[j] = dnnopt_dev::buf_load_x4(rs, ((blockIdx.x * 8u + w) * 4096u + j * 1024u + it * 65536u + lane * 16u) & ((1u << 21) - 1));
+        }
+        if (MODE & 2) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int q = 0; q < 3; ++q) {
+                    const u32x4 a = (MODE & 4) ? cv[j] : ca[j];
+                    const u32x4 b = (MODE & 4) ? cv[(j + q) & 3]
+                                               : u32x4{cb[j * 3 + q][0], cb[j * 3 + q][1], cb[(j * 3 + q + 1) % 12][0],
+                                                       cb[(j * 3 + q + 1) % 12][1]};
+                    acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc[q], 0, 0, 0);
+                }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ca[j] ^= na[j];
+            cv[j] ^= nv[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 12; ++j) cb[j] ^= nb[j];
+    }
+    u32x4 t = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) t ^= ca[j] ^ cv[j];
+#pragma unroll
+    for (int j = 0; j < 12; ++j) t[j & 3] ^= cb[j][0] ^ cb[j][1];
+    const float f = acc[0][0] + acc[1][1] + acc[2][2];
+    if (t[0] + t[1] + t[2] + t[3] == 12345u || f == 12345.0f) out[0] = 1u;
+}
+
+// The int8 64 x 32 LDS-DMA tile's copy pattern: 4 waves, per 256-byte k-block
+// 96 rows x 256 bytes (rows 4 KiB apart, 24 one-KB wave copies), 3 stages,
+// one wait + barrier per block, 16 blocks (K = 4096).  Workgroup b reads
+// region b % nreg of 384 KiB: nreg = 32 keeps every XCD's regions in its L2.
+__global__ __launch_bounds__(256) void probe_dma(const char* S, unsigned nreg, unsigned* out) {
+    __shared__ __attribute__((aligned(1024))) char st[3][24 * 1024];
+    const int lane = (int)threadIdx.x & 63, w = (int)threadIdx.x >> 6;
+    const char* base = S + (size_t)(blockIdx.x % nreg) * (96u * 4096u);
+    const __amdgpu_buffer_rsrc_t rs = dnnopt_dev::make_rsrc(base, 96u * 4096u);
+    uint32_t goff[6];
+#pragma unroll
+    for (int j = 0; j < 6; ++j) {
+        const int q = (w * 6 + j) * 1024 + 16 * lane;
+        goff[j] = (uint32_t)(q / 256) * 4096u + (uint32_t)(q % 256);
+    }
+    auto dma = [&](int s, int blk) {
+        const uint32_t k0 = blk < 16 ? (uint32_t)blk * 256u : dnnopt_dev::kOobOffset;
+#pragma unroll
+        for (int j = 0; j < 6; ++j) dnnopt_dev::lds_dma16(rs, &st[s][(w * 6 + j) * 1024], goff[j] + k0);
+    };
+    dma(0, 0);
+    dma(1, 1);
+    for (int i = 0; i < 18; i += 3) {
+        dnnopt_dev::wait_vmcnt<6>();
+        __builtin_amdgcn_s_barrier();
+        dma(2, i + 2);
+        dnnopt_dev::wait_vmcnt<6>();
+        __builtin_amdgcn_s_barrier();
+        dma(0, i + 3);
+        dnnopt_dev::wait_vmcnt<6>();
+        __builtin_amdgcn_s_barrier();
+        dma(1, i + 4);
+    }
+    dnnopt_dev::wait_vmcnt<0>();
+    __syncthreads();
+    if (*reinterpret_cast<const unsigned*>(&st[0][threadIdx.x * 16]) == 12345u) out[0] = 1u;
+}
+
+// One workgroup (8 waves, k split over the waves) per COLS-column strip of a
+// K x N fp32 matrix; a wave load reads 64 / (COLS / 4) rows x COLS floats,
+// 16 loads in flight per wave.
+template <int COLS>
+__global__ __launch_bounds__(512) void probe_narrow(const float* B, int N, int K, float* out) {
+    constexpr int Q = COLS / 4, R = 64 / Q, U = 16;
+    const int w = (int)threadIdx.x >> 6, lane = (int)threadIdx.x & 63;
+    const int col = (int)blockIdx.x * COLS + (lane % Q) * 4, rr = lane / Q;
+    const int k0 = K * w / 8, k1 = K * (w + 1) / 8;
+    const __amdgpu_buffer_rsrc_t rs = dnnopt_dev::make_rsrc(B, dnnopt_dev::range31((size_t)K * N * 4));
+    const uint32_t lane_off = col < N ? (uint32_t)(rr * N + col) * 4u : dnnopt_dev::kOobOffset;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int kk = k0; kk < k1; kk += U * R) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int row = kk + u * R;
+            v[u] = dnnopt_dev::buf_load_x4(rs, row + rr < k1 ? (uint32_t)row * (uint32_t)N * 4u + lane_off : dnnopt_dev::kOobOffset);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc += __builtin_bit_cast(f4, v[u]);
+    }
+    if (acc[0] + acc[1] + acc[2] + acc[3] == 12345.0f) out[0] = 1.0f;
+}
+
 }  // namespace
 
 extern "C" {
@@ -87,6 +239,45 @@ int dnnopt_probe_tiles(const float* B, int N, int K, int G, float* out, void* st
     const int T = (N + 255) / 256;
     if (N % 4 != 0 || G < T) return 1;
     hipLaunchKernelGGL(probe_tiles, dim3(G), dim3(512), 0, static_cast<hipStream_t>(stream), B, N, K, T, out);
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// mode: 1 LDS reads, 2 MFMAs, 3 both, 4 loads into registers, 6 loads and
+// MFMAs; one workgroup of 8 waves per CU (`cus`), `iters` iterations.
+int dnnopt_probe_overlap(int mode, const void* src2mb, int cus, int iters, unsigned* out, void* stream) {
+    const dim3 grid((unsigned)cus), blk(512);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const char* src = static_cast<const char*>(src2mb);
+    switch (mode) {
+        case 1: hipLaunchKernelGGL(probe_overlap<1>, grid, blk, 0, s, src, out, iters); break;
+        case 2: hipLaunchKernelGGL(probe_overlap<2>, grid, blk, 0, s, src, out, iters); break;
+        case 3: hipLaunchKernelGGL(probe_overlap<3>, grid, blk, 0, s, src, out, iters); break;
+        case 4: hipLaunchKernelGGL(probe_overlap<4>, grid, blk, 0, s, src, out, iters); break;
+        case 6: hipLaunchKernelGGL(probe_overlap<6>, grid, blk, 0, s, src, out, iters); break;
+        default: return 1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// `wgs` workgroups copy 384 KiB each into LDS from S (nreg regions of 384 KiB).
+int dnnopt_probe_dma(const void* S, unsigned nreg, int wgs, unsigned* out, void* stream) {
+    if (nreg == 0) return 1;
+    hipLaunchKernelGGL(probe_dma, dim3((unsigned)wgs), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const char*>(S), nreg, out);
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// ceil(N / cols) workgroups over a K x N fp32 matrix (N a multiple of 4).
+int dnnopt_probe_narrow(const float* B, int N, int K, int cols, float* out, void* stream) {
+    if (N % 4 != 0) return 1;
+    const dim3 grid((unsigned)((N + cols - 1) / cols)), blk(512);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (cols) {
+        case 16: hipLaunchKernelGGL(probe_narrow<16>, grid, blk, 0, s, B, N, K, out); break;
+        case 32: hipLaunchKernelGGL(probe_narrow<32>, grid, blk, 0, s, B, N, K, out); break;
+        case 64: hipLaunchKernelGGL(probe_narrow<64>, grid, blk, 0, s, B, N, K, out); break;
+        default: return 1;
+    }
     return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 
