@@ -323,6 +323,48 @@ def test_bf16_dma_256_row_tiles(lib, orc, dev, tb):
     u.assert_fp32_close(host(dC), want, scale, K, f"dma 256-row tiles tb={tb}")
 
 
+def _bf16_storage_sweep_cases():
+    """Seeded shapes for bf16 storage above M = 128 (the LDS-DMA tiles, 128-
+    and 256-row): ragged M / N / K, even padded strides, both B layouts,
+    assorted alpha / beta.  Sizes keep the fp64 reference to about a second."""
+    rng = np.random.default_rng(20261202)
+    cases = []
+    while len(cases) < 12:
+        M = int(rng.integers(129, 1101))
+        N = int(rng.integers(90, 5001))
+        K = int(rng.integers(1, 301))
+        if M * N * K > 400_000_000:
+            continue
+        tb = int(rng.integers(0, 2))
+        pa, pb = 2 * int(rng.integers(0, 5)), 2 * int(rng.integers(0, 5))
+        alpha = float(rng.choice([1.0, 0.5, -2.0]))
+        beta = float(rng.choice([0.0, 1.0, 0.25]))
+        cases.append((M, N, K, tb, pa, pb, alpha, beta))
+    # two shapes that take the 256-row tiles for certain (more 128-row tiles than CUs)
+    cases += [(1100, 3000, 96, 0, 2, 0, 1.0, 0.0), (1024, 3100, 130, 1, 0, 4, -2.0, 0.25)]
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,tb,pa,pb,alpha,beta", _bf16_storage_sweep_cases())
+def test_bf16_storage_sweep(lib, orc, dev, M, N, K, tb, pa, pb, alpha, beta):
+    lda, ldb = K + pa, (K + pb if tb else N + pb)
+    p = lib.plan_bf16_ex(M, N, K, transB=tb)
+    # rows of A and B on 4-byte boundaries: the LDS-DMA tiles; else the register tiles
+    assert p["name"] == ("dnnopt_tile_bf16_dma" if lda % 2 == 0 and ldb % 2 == 0 else "dnnopt_tile_bf16"), p
+    if -(-M // 128) * -(-N // 96) > 256 and lda % 2 == 0 and ldb % 2 == 0:
+        assert p["rows"] == 256, p
+    A = u.bf16_bits(orc, u.normal(orc, M * lda, 11)).reshape(M, lda)
+    rows = N if tb else K
+    Bs = u.bf16_bits(orc, u.normal(orc, rows * ldb, 12, 0, 0.02)).reshape(rows, ldb)
+    Bkn = np.ascontiguousarray(Bs[:, :K].T if tb else Bs[:, :N])
+    C0 = u.uniform(orc, M * N, 13).reshape(M, N)
+    want, scale = u.exact(u.bf16_value(A)[:, :K], u.bf16_value(Bkn), alpha, beta, C0 if beta else None)
+    dC = dev_copy(C0 if beta else np.full_like(C0, np.nan), dev)
+    lib.gemm_bf16_ex(M, N, K, alpha, dev_copy(A.view(np.int16), dev), lda, dev_copy(Bs.view(np.int16), dev), ldb,
+                     beta, dC, N, transB=tb, stream=stream())
+    u.assert_fp32_close(host(dC), want, scale, K, f"bf16 sweep {M}x{N}x{K} tb={tb} a={alpha} b={beta}")
+
+
 _TICKET_CHILD = r"""
 import os, sys
 import numpy as np
