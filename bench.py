@@ -686,7 +686,10 @@ def probe(which):
       dma      the LDS-DMA copy pattern of the int8 64 x 32 tile (384 KiB per
                CU) from L2-resident and from HBM-resident sources;
       narrow   C2's matrices read as narrow column strips, all of k in one
-               workgroup (no k-split across workgroups, no partial sums).
+               workgroup (no k-split across workgroups, no partial sums);
+      hostapi  C1 / C2 through cblas_sgemm with host (pageable numpy)
+               buffers: the PCIe-inclusive rate of the drop-in CBLAS
+               boundary (staging copies included; never the bench value).
     Buffers rotate over more than 600 MB so nothing is served from the
     Infinity Cache between launches (except where a probe says L2)."""
     import ctypes
@@ -789,6 +792,23 @@ def probe(which):
                 emit({"probe": "narrow", "N": N, "K": K, "cols": cols, "workgroups": -(-N // cols), "bytes": nbytes,
                       "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1)})
             del bufs
+    if which in ("hostapi", "all"):
+        import numpy as np
+
+        for M, N, K in shapes:
+            rng = np.random.default_rng(SEED)
+            A = rng.standard_normal((M, K), dtype=np.float32)
+            B = rng.standard_normal((K, N), dtype=np.float32)
+            C = np.zeros((M, N), dtype=np.float32)
+            ts = []
+            for rep in range(8):
+                t0 = time.perf_counter()
+                lib.cblas_sgemm(101, 111, 111, M, N, K, 1.0, A, K, B, N, 0.0, C, N)
+                ts.append(time.perf_counter() - t0)
+            us = statistics.median(ts[2:]) * 1e6
+            nbytes = 4 * (M * K + K * N + M * N)
+            emit({"probe": "hostapi", "entry": "cblas_sgemm (host buffers)", "M": M, "N": N, "K": K, "us": round(us, 1),
+                  "GBps": round(nbytes / us / 1e3, 2)})
     if which in ("combine", "all"):
         for wl in ("c1", "c2"):
             for mode, env in (("reduce kernel", "1"), ("last workgroup", "0")):
@@ -854,7 +874,8 @@ def main():
     ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
-    ap.add_argument("--probe", choices=["launch", "read", "tiles", "combine", "overlap", "dma", "narrow", "all"],
+    ap.add_argument("--probe", choices=["launch", "read", "tiles", "combine", "overlap", "dma", "narrow", "hostapi",
+                                        "all"],
                     default=None,
                     help="only run the measurement probes (launch cost, read ceilings, the skinny access pattern, "
                          "split-k combine variants, LDS / MFMA overlap, LDS-DMA copy rate, narrow strips); one JSON "
