@@ -689,7 +689,12 @@ def probe(which):
                workgroup (no k-split across workgroups, no partial sums);
       hostapi  C1 / C2 through cblas_sgemm with host (pageable numpy)
                buffers: the PCIe-inclusive rate of the drop-in CBLAS
-               boundary (staging copies included; never the bench value).
+               boundary (staging copies included; never the bench value);
+      mfma     sustained fp32 16x16x4 and bf16 16x16x32 MFMA rates (one or
+               two waves per SIMD, independent accumulators, no memory);
+      l2read   every workgroup reading the same 1 / 4 MiB: the L2 -> CU rate;
+      pieces   a 65536 x 256 fp32 matrix (64 MiB) read in the MFMA operand
+               layout (16 rows x 64 bytes per wave load) and as whole rows.
     Buffers rotate over more than 600 MB so nothing is served from the
     Infinity Cache between launches (except where a probe says L2)."""
     import ctypes
@@ -712,8 +717,14 @@ def probe(which):
     so.dnnopt_probe_dma.argtypes = [ctypes.c_void_p, ctypes.c_uint, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     so.dnnopt_probe_narrow.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                        ctypes.c_void_p]
+    so.dnnopt_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                     ctypes.c_void_p]
+    so.dnnopt_probe_l2read.argtypes = [ctypes.c_void_p, ctypes.c_uint, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    so.dnnopt_probe_pieces.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_void_p]
     for fn in (so.dnnopt_probe_read, so.dnnopt_probe_tiles, so.dnnopt_probe_empty, so.dnnopt_probe_overlap,
-               so.dnnopt_probe_dma, so.dnnopt_probe_narrow):
+               so.dnnopt_probe_dma, so.dnnopt_probe_narrow, so.dnnopt_probe_mfma, so.dnnopt_probe_l2read,
+               so.dnnopt_probe_pieces):
         fn.restype = ctypes.c_int
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     stream = torch.cuda.Stream(device=dev)
@@ -792,6 +803,35 @@ def probe(which):
                 emit({"probe": "narrow", "N": N, "K": K, "cols": cols, "workgroups": -(-N // cols), "bytes": nbytes,
                       "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1)})
             del bufs
+    if which in ("mfma", "all"):
+        iters = 4000
+        for kind, name, macs in ((0, "fp32 16x16x4", 16 * 16 * 4), (1, "bf16 16x16x32", 16 * 16 * 32)):
+            for waves in (4, 8):
+                us = _graph_time_us(torch, stream, [lambda k=kind, wv=waves: check(so.dnnopt_probe_mfma(
+                    k, cus, wv, iters, out.data_ptr(), sp))] * 4)
+                flops = 2.0 * macs * 8 * iters * waves * cus
+                emit({"probe": "mfma", "kind": name, "waves_per_simd": waves // 4, "us": round(us, 2),
+                      "TFLOPs": round(flops / us / 1e6, 1)})
+    if which in ("l2read", "all"):
+        X = torch.ones(4 << 20, dtype=torch.uint8, device=dev)
+        for nbytes in (1 << 20, 4 << 20):
+            us = _graph_time_us(torch, stream, [lambda nb=nbytes: check(so.dnnopt_probe_l2read(
+                X.data_ptr(), nb, 2 * cus, out.data_ptr(), sp))] * 8)
+            emit({"probe": "l2read", "bytes_per_workgroup": nbytes, "workgroups": 2 * cus, "us": round(us, 2),
+                  "TBps": round(nbytes * 2 * cus / us / 1e6, 2)})
+        del X
+    if which in ("pieces", "all"):
+        M = 65536
+        nbytes = M * 1024
+        copies = max(2, -(-(600 << 20) // nbytes))
+        bufs = [torch.ones(M * 256, dtype=torch.float32, device=dev) for _ in range(copies)]
+        for pat, name in ((0, "16 rows x 64 B per wave load (MFMA operand layout)"), (1, "one 1 KiB row per wave load")):
+            launches = [lambda x=x, pt=pat: check(so.dnnopt_probe_pieces(x.data_ptr(), M, cus, pt, out.data_ptr(), sp))
+                        for x in bufs] * max(1, 32 // copies)
+            us = _graph_time_us(torch, stream, launches)
+            emit({"probe": "pieces", "pattern": name, "bytes": nbytes, "us": round(us, 2),
+                  "TBps": round(nbytes / us / 1e6, 2)})
+        del bufs
     if which in ("hostapi", "all"):
         import numpy as np
 
@@ -875,7 +915,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
     ap.add_argument("--probe", choices=["launch", "read", "tiles", "combine", "overlap", "dma", "narrow", "hostapi",
-                                        "all"],
+                                        "mfma", "l2read", "pieces", "all"],
                     default=None,
                     help="only run the measurement probes (launch cost, read ceilings, the skinny access pattern, "
                          "split-k combine variants, LDS / MFMA overlap, LDS-DMA copy rate, narrow strips); one JSON "

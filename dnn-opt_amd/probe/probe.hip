@@ -20,7 +20,14 @@
 //   dnnopt_probe_narrow narrow column strips of a K x N fp32 matrix, all of
 //                       k in one workgroup (no k-split across workgroups,
 //                       so no partial sums): the alternative to the skinny
-//                       kernel's split-k plan.
+//                       kernel's split-k plan;
+//   dnnopt_probe_mfma   sustained MFMA rate (independent accumulator chains,
+//                       no memory traffic): fp32 16x16x4 or bf16 16x16x32;
+//   dnnopt_probe_l2read every workgroup reads the same region (L2-resident):
+//                       the L2 -> CU read rate;
+//   dnnopt_probe_pieces an M x 256 fp32 matrix streamed as the tall kernel's
+//                       waves load it (16 rows x 64 bytes per wave load, the
+//                       MFMA operand layout) or as whole 1 KB rows.
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
@@ -221,6 +228,82 @@ __global__ __launch_bounds__(512) void probe_narrow(const float* B, int N, int K
     if (acc[0] + acc[1] + acc[2] + acc[3] == 12345.0f) out[0] = 1.0f;
 }
 
+// KIND 0: v_mfma_f32_16x16x4_f32, 1: v_mfma_f32_16x16x32_bf16; 8 independent
+// accumulators per wave, `iters` rounds of 8 MFMAs.
+template <int KIND>
+__global__ void probe_mfma(float* out, int iters) {
+    f32x4 acc[8] = {};
+    const float a = (float)(threadIdx.x & 7) * 0.125f;
+    const u32x4 av = {threadIdx.x, threadIdx.x + 1u, threadIdx.x + 2u, threadIdx.x + 3u};
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if constexpr (KIND == 0)
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, a + (float)j, acc[j], 0, 0, 0);
+            else
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                                 __builtin_bit_cast(bf16x8, av), acc[j], 0, 0, 0);
+        }
+    }
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t += acc[j][0];
+    if (t == 12345.0f) out[0] = t;
+}
+
+// Every workgroup reads the same `bytes` (a multiple of 8 KiB) with 16-byte
+// loads, 8 in flight per thread, starting at a workgroup-dependent chunk.
+__global__ __launch_bounds__(512) void probe_l2read(const char* X, uint32_t bytes, float* out) {
+    const __amdgpu_buffer_rsrc_t rx = dnnopt_dev::make_rsrc(X, bytes);
+    const uint32_t nchunk = bytes / 16;
+    const uint32_t start = (blockIdx.x * 4099u) % nchunk;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t c = threadIdx.x; c < nchunk; c += 512 * 8) {
+        u32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t idx = start + c + j * 512;
+            while (idx >= nchunk) idx -= nchunk;
+            v[j] = dnnopt_dev::buf_load_x4(rx, idx * 16u);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += __builtin_bit_cast(f4, v[j]);
+    }
+    if (acc[0] + acc[1] + acc[2] + acc[3] == 12345.0f) out[0] = 1.0f;
+}
+
+// An M x 256 fp32 matrix (rows of 1 KiB) read once by 8-wave workgroups, 8
+// wave loads in flight per wave.  PAT 0: a wave load is 16 rows x 64 bytes
+// (lane l: row l % 16, bytes 16 (l / 16) of a 64-byte column chunk; a wave
+// walks the 16 chunks of its 16-row tile), PAT 1: a wave load is one row.
+template <int PAT>
+__global__ __launch_bounds__(512) void probe_pieces(const float* A, int M, float* out) {
+    const int lane = (int)threadIdx.x & 63, w = (int)threadIdx.x >> 6;
+    const int gw = (int)blockIdx.x * 8 + w, GW = (int)gridDim.x * 8;
+    const __amdgpu_buffer_rsrc_t ra = dnnopt_dev::make_rsrc(A, dnnopt_dev::range31((size_t)M * 1024));
+    // loads per wave: the wave's share of M x 1 KiB in 1 KiB wave loads
+    const int loads = M / GW;  // M is a multiple of 16 * GW
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int l0 = 0; l0 < loads; l0 += 8) {
+        u32x4 v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int l = l0 + j;
+            uint32_t off;
+            if constexpr (PAT == 0) {
+                const int tile = gw + GW * (l / 16), chunk = l % 16;
+                off = ((uint32_t)(tile * 16 + (lane & 15)) * 256u + 4u * (lane >> 4)) * 4u + chunk * 64u;
+            } else {
+                off = ((uint32_t)(gw + GW * l) * 256u) * 4u + 16u * lane;
+            }
+            v[j] = dnnopt_dev::buf_load_x4(ra, l < loads ? off : dnnopt_dev::kOobOffset);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc += __builtin_bit_cast(f4, v[j]);
+    }
+    if (acc[0] + acc[1] + acc[2] + acc[3] == 12345.0f) out[0] = 1.0f;
+}
+
 }  // namespace
 
 extern "C" {
@@ -278,6 +361,34 @@ int dnnopt_probe_narrow(const float* B, int N, int K, int cols, float* out, void
         case 64: hipLaunchKernelGGL(probe_narrow<64>, grid, blk, 0, s, B, N, K, out); break;
         default: return 1;
     }
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// kind 0: fp32 16x16x4, 1: bf16 16x16x32; `cus` workgroups of `waves` waves.
+int dnnopt_probe_mfma(int kind, int cus, int waves, int iters, float* out, void* stream) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (waves < 1 || waves > 16) return 1;
+    if (kind == 0) hipLaunchKernelGGL(probe_mfma<0>, dim3((unsigned)cus), dim3(64 * waves), 0, s, out, iters);
+    else if (kind == 1) hipLaunchKernelGGL(probe_mfma<1>, dim3((unsigned)cus), dim3(64 * waves), 0, s, out, iters);
+    else return 1;
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// `wgs` workgroups each read the same `bytes` (a multiple of 8 KiB) of X.
+int dnnopt_probe_l2read(const void* X, unsigned bytes, int wgs, float* out, void* stream) {
+    if (bytes == 0 || bytes % 8192 != 0) return 1;
+    hipLaunchKernelGGL(probe_l2read, dim3((unsigned)wgs), dim3(512), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const char*>(X), bytes, out);
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// Read an M x 256 fp32 matrix with `wgs` 8-wave workgroups (M a multiple of
+// 16 * 8 * wgs); pat 0: MFMA-operand pieces, 1: whole rows.
+int dnnopt_probe_pieces(const float* A, int M, int wgs, int pat, float* out, void* stream) {
+    if (wgs < 1 || M % (16 * 8 * wgs) != 0) return 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (pat == 0) hipLaunchKernelGGL(probe_pieces<0>, dim3((unsigned)wgs), dim3(512), 0, s, A, M, out);
+    else hipLaunchKernelGGL(probe_pieces<1>, dim3((unsigned)wgs), dim3(512), 0, s, A, M, out);
     return hipGetLastError() == hipSuccess ? 0 : 3;
 }
 
