@@ -266,11 +266,19 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
             cfg = 26;
             if (ceil_div(M, 128) * ceil_div(N, 96) > num_cus()) cfg = 33;
         }
-        if (forced_cfg >= kTileFirstLds && forced_cfg < tile_config_count() &&
+        if (forced_cfg >= kTileFirstLds && forced_cfg < tile_config_count() && forced_cfg != kTileF32Few &&
             (forced_cfg < kTileFirstDma || mode == kTileBF16))
             cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
+    } else if (mode == kTileF32 && !transA && (M <= 16 || (transB && M <= 32))) {
+        // Few rows: 16-row tiles with k over 8 waves instead of 64-row tiles
+        // that are mostly padding (MI355X, us, 64x64 tiles -> 16x16: B stored
+        // N x K 12 x 11003 x 2048 71.1 -> 30.7, 16 x 4096 x 4096 46.7 -> 23.1,
+        // 32 x 4096 x 4096 47.3 -> 37.4; B stored K x N 12 x 11003 x 2048
+        // 60.4 -> 40.8, 16 x 4096 x 4096 36.5 -> 29.4, but 32 x 4096 x 4096
+        // 37.4 -> 46.1, so K x N stops at M = 16).
+        cfg = kTileF32Few;
     } else if (mode == kTileF32 && N <= 64 && M >= 4096) {
         cfg = 1;
     } else if (M >= 128 && N >= 128) {
@@ -496,7 +504,14 @@ int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int 
 
 int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc) {
     if (M <= 8 && !transB) return plan_skinny(kSkinnyF32, M, N, K, ldb, L);
-    if (M <= 8 && !transA && plan_rowdot(0, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
+    // B stored N x K: the row-dot kernel up to M = 4 and for narrow N; from
+    // M = 5 at N >= 2048 the 16-row MFMA tiles (us, row-dot -> tiles: M=5 / 6
+    // / 8 x 11003 x 2048 27.6 / 29.8 / 32.4 -> 26.1 / 26.5 / 28.1, x 4096 x
+    // 4096 21.5 / 21.2 / 25.5 -> 17.3 / 17.9 / 19.0, M=7 x 4099 x 2048 15.9
+    // -> 13.8; N = 1009 and M <= 4 favour the row-dot kernel).
+    const bool few_rows_tile = transB && M >= 5 && N >= 2048;
+    if (M <= 8 && !transA && !few_rows_tile && plan_rowdot(0, M, N, K, lda, ldb, L) == DNNOPT_OK)
+        return DNNOPT_OK;
     static const bool tall_ok = [] {
         const char* e = getenv("DNNOPT_TALL");
         return !(e && *e && atoi(e) == 0);

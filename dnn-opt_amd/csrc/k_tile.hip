@@ -1022,6 +1022,8 @@ static const TileConfig kTileConfigs[] = {
     {2, 4, 4, 2, 1, 3, 64},   // 32: 128 x 128, 8 waves, 3 stages
     {4, 3, 4, 2, 1, 3, 64},   // 33: 256 x 96, 8 waves (64 x 48 each), 3 stages
     {4, 4, 4, 2, 1, 3, 64},   // 34: 256 x 128, 8 waves (64 x 64 each), 3 stages
+    // fp32 register tiles for few rows
+    {1, 1, 1, 1, 8},          // 35: 16 x 16, k over the 8 waves of a workgroup
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -1104,6 +1106,7 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_DMA_CASE(32, 2, 4, 4, 2, 3, 64)
         DNNOPT_TILE_DMA_CASE(33, 4, 3, 4, 2, 3, 64)
         DNNOPT_TILE_DMA_CASE(34, 4, 4, 4, 2, 3, 64)
+        DNNOPT_TILE_CASE(35, 1, 1, 1, 1, 8)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

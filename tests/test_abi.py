@@ -129,14 +129,22 @@ def test_plan_split_never_exceeds_k(lib):
 
 def test_plans_for_weights_stored_n_by_k(lib):
     """M <= 8 with B stored N x K (an inner product's weights) streams the rows
-    of B with the row-dot kernel; enough workgroups for two per CU."""
+    of B with the row-dot kernel (enough workgroups for two per CU) up to
+    M = 4 and for narrow N; from M = 5 at N >= 2048, and for 8 < M <= 32,
+    16 x 16 MFMA tiles with k over the 8 waves of a workgroup."""
     b = u.binding()
-    for M, N, K in ((1, 4096, 4096), (7, 11003, 2048), (3, 1009, 2048), (8, 5, 7)):
+    for M, N, K in ((1, 4096, 4096), (4, 11003, 2048), (3, 1009, 2048), (8, 5, 7), (7, 1009, 2048)):
         p = lib.plan_sgemm(M, N, K, transB=1)
         assert p["kernel"] == b.K_ROWDOT_F32 and p["name"] == "dnnopt_rowdot", p
         assert p["grid_x"] * p["cols"] >= N
-    p = lib.plan_sgemm(7, 11003, 2048, transB=1)
+    p = lib.plan_sgemm(4, 11003, 2048, transB=1)
     assert p["grid_x"] >= 256
+    for M, N, K in ((5, 4096, 4096), (7, 11003, 2048), (12, 11003, 2048), (32, 4096, 4096)):
+        p = lib.plan_sgemm(M, N, K, transB=1)
+        assert p["kernel"] == b.K_TILE_F32 and (p["rows"], p["cols"], p["block"]) == (16, 16, 512), (M, N, p)
+    # B stored K x N: 16-row tiles up to M = 16, then the 64-row tiles
+    assert lib.plan_sgemm(16, 4096, 4096)["rows"] == 16
+    assert lib.plan_sgemm(32, 4096, 4096)["rows"] == 64
     assert lib.plan_bf16_ex(1, 11008, 4096, transB=1)["kernel"] == b.K_ROWDOT_BF16
     assert lib.plan_bf16_ex(8, 11008, 4096, transA=1, transB=1)["kernel"] == b.K_ROWDOT_BF16
     # transposed A (stored K x M) with B stored N x K stays on the MFMA tiles (fp32)

@@ -83,8 +83,9 @@ ROWDOT += [(1, 4096, 4096), (7, 11003, 2048), (4, 33, 65536)]
 
 @pytest.mark.parametrize("M,N,K", ROWDOT)
 def test_rowdot_fp32(lib, orc, dev, M, N, K):
-    """fp32 C = A B^T (+ beta C) with B stored N x K; the row padding past K
-    holds Inf and NaN, which must not reach any product."""
+    """fp32 C = A B^T (+ beta C) with B stored N x K (the row-dot kernel; from
+    M = 5 at N >= 2048 the 16-row MFMA tiles); the row padding past K holds
+    Inf and NaN, which must not reach any product."""
     lda, ldb = K + 3, K + 5
     A = np.full((M, lda), np.inf, np.float32)
     B = np.full((N, ldb), np.nan, np.float32)
@@ -92,7 +93,7 @@ def test_rowdot_fp32(lib, orc, dev, M, N, K):
     B[:, :K] = u.normal(orc, N * K, 2, 0, 0.02).reshape(N, K)
     C0 = u.uniform(orc, M * N, 3).reshape(M, N)
     p = lib.plan_sgemm(M, N, K, transB=1)
-    assert p["name"] == "dnnopt_rowdot", p
+    assert p["name"] == ("dnnopt_tile_f32" if M >= 5 and N >= 2048 else "dnnopt_rowdot"), p
     dA, dB = dev_copy(A, dev), dev_copy(B, dev)
     for beta in (0.0, 0.5):
         dC = dev_copy(C0 if beta else np.full_like(C0, np.nan), dev)

@@ -48,6 +48,31 @@ def test_sgemm_skinny(lib, orc, dev, M, N, K):
         u.assert_fp32_close(got, want, scale, K, f"skinny {M}x{N}x{K} a={alpha} b={beta}")
 
 
+# Few rows on the 16 x 16 MFMA tiles (k over 8 waves): B stored N x K from
+# M = 5 at N >= 2048 and up to M = 32, B stored K x N for 9 <= M <= 16;
+# ragged N / K, padded strides, k-splits across workgroups at small N.
+FEW = [(5, 2048, 1000, 1, 0), (7, 4099, 2048, 1, 4), (8, 2053, 77, 1, 0), (9, 1009, 300, 1, 2), (13, 300, 4096, 1, 0),
+       (16, 4096, 129, 1, 1), (17, 2000, 513, 1, 0), (32, 1001, 64, 1, 3), (9, 1000, 517, 0, 0), (13, 4099, 2048, 0, 4),
+       (16, 77, 8192, 0, 1)]
+
+
+@pytest.mark.parametrize("M,N,K,tb,pad", FEW)
+def test_sgemm_few_rows_tiles(lib, orc, dev, M, N, K, tb, pad):
+    p = lib.plan_sgemm(M, N, K, transB=tb)
+    assert p["name"] == "dnnopt_tile_f32" and p["rows"] == 16 and p["cols"] == 16, p
+    lda, ldb = K + pad, (K + pad if tb else N + pad)
+    A = u.normal(orc, M * lda, 1, 0, 0.02).reshape(M, lda)
+    Bs = u.normal(orc, (N if tb else K) * ldb, 2, 0, 0.02).reshape(N if tb else K, ldb)
+    Bkn = np.ascontiguousarray(Bs[:, :K].T if tb else Bs[:, :N])
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    dA, dB = dev_copy(A, dev), dev_copy(Bs, dev)
+    for alpha, beta in ((1.0, 1.0), (-0.75, 0.0)):
+        dC = dev_copy(C0 if beta != 0.0 else np.full_like(C0, np.nan), dev)
+        lib.sgemm(M, N, K, alpha, dA, lda, dB, ldb, beta, dC, N, transB=tb, stream=stream())
+        want, scale = u.exact(A[:, :K], Bkn, alpha, beta, C0)
+        u.assert_fp32_close(host(dC), want, scale, K, f"few rows {M}x{N}x{K} tb={tb} a={alpha} b={beta}")
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096)] + [(M, N, 2048) for M in (2, 3, 5, 7) for N in (1009, 4099, 11003)])
 def test_sgemm_configs_c1_c2(lib, orc, dev, M, N, K):
     """Full benchmark shapes: C1 (beta 0, C pre-filled NaN) and C2 (beta 1),
