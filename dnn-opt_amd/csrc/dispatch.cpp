@@ -266,19 +266,20 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
             cfg = 26;
             if (ceil_div(M, 128) * ceil_div(N, 96) > num_cus()) cfg = 33;
         }
-        if (forced_cfg >= kTileFirstLds && forced_cfg < tile_config_count() && forced_cfg != kTileF32Few &&
+        if (forced_cfg >= kTileFirstLds && forced_cfg < kTileF32Few &&
             (forced_cfg < kTileFirstDma || mode == kTileBF16))
             cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
-    } else if (mode == kTileF32 && !transA && (M <= 16 || (transB && M <= 32))) {
-        // Few rows: 16-row tiles with k over 8 waves instead of 64-row tiles
-        // that are mostly padding (MI355X, us, 64x64 tiles -> 16x16: B stored
-        // N x K 12 x 11003 x 2048 71.1 -> 30.7, 16 x 4096 x 4096 46.7 -> 23.1,
-        // 32 x 4096 x 4096 47.3 -> 37.4; B stored K x N 12 x 11003 x 2048
-        // 60.4 -> 40.8, 16 x 4096 x 4096 36.5 -> 29.4, but 32 x 4096 x 4096
-        // 37.4 -> 46.1, so K x N stops at M = 16).
-        cfg = kTileF32Few;
+    } else if (mode == kTileF32 && !transA && M <= 32) {
+        // Few rows: 16-row tiles instead of 64-row tiles that are mostly
+        // padding.  MI355X, us (64 x 64 tiles -> 16 x 16 with k over 8 waves
+        // / 16 x 128 with two k-groups): B stored N x K 12 x 11003 x 2048
+        // 71.1 -> 30.9 / 34.7, 16 x 4096 x 4096 46.7 -> 23.2 / 24.3, 24 x 4096
+        // x 4096 -> 34.6 / 32.3, 32 x 4096 x 4096 47.5 -> 37.1 / 32.8; B stored
+        // K x N 12 x 11003 x 2048 60.4 -> 40.4 / 37.0, 16 x 4096 x 4096 36.5 ->
+        // 29.6 / 21.5, 32 x 4096 x 4096 38.8 -> 46.5 / 28.9.
+        cfg = transB && M <= 16 ? kTileF32Few : kTileF32Few128;
     } else if (mode == kTileF32 && N <= 64 && M >= 4096) {
         cfg = 1;
     } else if (M >= 128 && N >= 128) {

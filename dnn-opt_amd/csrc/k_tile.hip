@@ -1024,6 +1024,7 @@ static const TileConfig kTileConfigs[] = {
     {4, 4, 4, 2, 1, 3, 64},   // 34: 256 x 128, 8 waves (64 x 64 each), 3 stages
     // fp32 register tiles for few rows
     {1, 1, 1, 1, 8},          // 35: 16 x 16, k over the 8 waves of a workgroup
+    {1, 4, 1, 2, 2},          // 36: 16 x 128, 2 column waves x 2 k-groups
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -1107,6 +1108,7 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_DMA_CASE(33, 4, 3, 4, 2, 3, 64)
         DNNOPT_TILE_DMA_CASE(34, 4, 4, 4, 2, 3, 64)
         DNNOPT_TILE_CASE(35, 1, 1, 1, 1, 8)
+        DNNOPT_TILE_CASE(36, 1, 4, 1, 2, 2)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

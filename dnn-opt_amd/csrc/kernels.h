@@ -215,9 +215,11 @@ constexpr int kTileFirstLds = 5;
 // memory unit's LDS path (bf16 storage only; the fp32-input mode keeps the
 // register-staged kernel).
 constexpr int kTileFirstDma = 26;
-// fp32 register tiles of 16 x 16 with k split over the 8 waves of a
-// workgroup (after the LDS-staged entries; fp32 only).
+// fp32 register tiles for few rows (after the LDS-staged entries; fp32
+// only): 16 x 16 with k split over the 8 waves of a workgroup, and 16 x 128
+// with two column waves and two k-groups.
 constexpr int kTileF32Few = 35;
+constexpr int kTileF32Few128 = 36;
 // k per LDS block of an LDS-staged configuration: its kblk (or
 // DNNOPT_LDS_KB) when both stages fit in 128 KiB of LDS, else 64.
 constexpr int tile_lds_bk(int bm, int bn, int kblk) {

@@ -139,12 +139,15 @@ def test_plans_for_weights_stored_n_by_k(lib):
         assert p["grid_x"] * p["cols"] >= N
     p = lib.plan_sgemm(4, 11003, 2048, transB=1)
     assert p["grid_x"] >= 256
-    for M, N, K in ((5, 4096, 4096), (7, 11003, 2048), (12, 11003, 2048), (32, 4096, 4096)):
+    for M, N, K in ((5, 4096, 4096), (7, 11003, 2048), (12, 11003, 2048), (16, 4096, 4096)):
         p = lib.plan_sgemm(M, N, K, transB=1)
         assert p["kernel"] == b.K_TILE_F32 and (p["rows"], p["cols"], p["block"]) == (16, 16, 512), (M, N, p)
-    # B stored K x N: 16-row tiles up to M = 16, then the 64-row tiles
-    assert lib.plan_sgemm(16, 4096, 4096)["rows"] == 16
-    assert lib.plan_sgemm(32, 4096, 4096)["rows"] == 64
+    # 16 x 128 tiles (two k-groups of two column waves) above M = 16 with B
+    # stored N x K and from M = 9 with B stored K x N, up to M = 32
+    for M, tb in ((17, 1), (32, 1), (9, 0), (16, 0), (32, 0)):
+        p = lib.plan_sgemm(M, 4096, 4096, transB=tb)
+        assert p["kernel"] == b.K_TILE_F32 and (p["rows"], p["cols"], p["block"]) == (16, 128, 256), (M, tb, p)
+    assert lib.plan_sgemm(33, 4096, 4096)["rows"] == 64
     assert lib.plan_bf16_ex(1, 11008, 4096, transB=1)["kernel"] == b.K_ROWDOT_BF16
     assert lib.plan_bf16_ex(8, 11008, 4096, transA=1, transB=1)["kernel"] == b.K_ROWDOT_BF16
     # transposed A (stored K x M) with B stored N x K stays on the MFMA tiles (fp32)

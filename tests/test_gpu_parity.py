@@ -48,9 +48,10 @@ def test_sgemm_skinny(lib, orc, dev, M, N, K):
         u.assert_fp32_close(got, want, scale, K, f"skinny {M}x{N}x{K} a={alpha} b={beta}")
 
 
-# Few rows on the 16 x 16 MFMA tiles (k over 8 waves): B stored N x K from
-# M = 5 at N >= 2048 and up to M = 32, B stored K x N for 9 <= M <= 16;
-# ragged N / K, padded strides, k-splits across workgroups at small N.
+# Few rows on 16-row MFMA tiles: 16 x 16 with k over 8 waves for B stored
+# N x K from M = 5 (N >= 2048) to M = 16, 16 x 128 with two k-groups above
+# that and for B stored K x N (9 <= M <= 32); ragged N / K, padded strides,
+# k-splits across workgroups at small N.
 FEW = [(5, 2048, 1000, 1, 0), (7, 4099, 2048, 1, 4), (8, 2053, 77, 1, 0), (9, 1009, 300, 1, 2), (13, 300, 4096, 1, 0),
        (16, 4096, 129, 1, 1), (17, 2000, 513, 1, 0), (32, 1001, 64, 1, 3), (9, 1000, 517, 0, 0), (13, 4099, 2048, 0, 4),
        (16, 77, 8192, 0, 1)]
@@ -59,7 +60,7 @@ FEW = [(5, 2048, 1000, 1, 0), (7, 4099, 2048, 1, 4), (8, 2053, 77, 1, 0), (9, 10
 @pytest.mark.parametrize("M,N,K,tb,pad", FEW)
 def test_sgemm_few_rows_tiles(lib, orc, dev, M, N, K, tb, pad):
     p = lib.plan_sgemm(M, N, K, transB=tb)
-    assert p["name"] == "dnnopt_tile_f32" and p["rows"] == 16 and p["cols"] == 16, p
+    assert p["name"] == "dnnopt_tile_f32" and p["rows"] == 16 and p["cols"] == (16 if tb and M <= 16 else 128), p
     lda, ldb = K + pad, (K + pad if tb else N + pad)
     A = u.normal(orc, M * lda, 1, 0, 0.02).reshape(M, lda)
     Bs = u.normal(orc, (N if tb else K) * ldb, 2, 0, 0.02).reshape(N if tb else K, ldb)
