@@ -526,7 +526,13 @@ int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L,
     // for every M (the skinny kernel streams rows of a K x N B).
     if (M <= 8 && !transB) return plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L);
     if (transB && fp32_inputs) return DNNOPT_ERR_UNSUPPORTED;
-    if (M <= 8 && plan_rowdot(1, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
+    // B stored N x K: the row-dot kernel up to M = 4 and for rows off 4-byte
+    // boundaries; from M = 5 the LDS-staged tiles (us, row-dot -> 32 x 64
+    // tiles, N = 11008, K = 4096: M=5 26.5 -> 23.3, M=7 31.6 -> 23.5, M=8 34.0
+    // -> 24.1; 8 x 4096 x 4096 15.7 -> 12.4; M=4 24.1 vs 23.8, M=1 19.1 vs
+    // 22.6).
+    const bool tile_tb = transB && M >= 5 && (lda & 1) == 0 && (ldb & 1) == 0;
+    if (M <= 8 && !tile_tb && plan_rowdot(1, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
     return plan_tile(fp32_inputs ? kTileF2B : kTileBF16, 0, transB, M, N, K, lda, ldb, L, true, ldc);
 }
 

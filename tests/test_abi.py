@@ -149,7 +149,11 @@ def test_plans_for_weights_stored_n_by_k(lib):
         assert p["kernel"] == b.K_TILE_F32 and (p["rows"], p["cols"], p["block"]) == (16, 128, 256), (M, tb, p)
     assert lib.plan_sgemm(33, 4096, 4096)["rows"] == 64
     assert lib.plan_bf16_ex(1, 11008, 4096, transB=1)["kernel"] == b.K_ROWDOT_BF16
-    assert lib.plan_bf16_ex(8, 11008, 4096, transA=1, transB=1)["kernel"] == b.K_ROWDOT_BF16
+    assert lib.plan_bf16_ex(4, 11008, 4096, transA=1, transB=1)["kernel"] == b.K_ROWDOT_BF16
+    # bf16, B stored N x K, M >= 5 (rows 4-byte aligned): the LDS-staged tiles
+    for M in (5, 8):
+        assert lib.plan_bf16_ex(M, 11008, 4096, transB=1)["name"] == "dnnopt_tile_bf16_lds"
+        assert lib.plan_bf16_ex(M, 11008, 4096, transA=1, transB=1)["name"] == "dnnopt_tile_bf16_lds"
     # transposed A (stored K x M) with B stored N x K stays on the MFMA tiles (fp32)
     assert lib.plan_sgemm(4, 300, 64, transA=1, transB=1)["kernel"] == b.K_TILE_F32
     assert lib.plan_bf16_ex(32, 11008, 4096, transB=1)["name"] == "dnnopt_tile_bf16_lds"
