@@ -64,9 +64,18 @@ struct TileShape {
     static constexpr int RED = KW > 1 ? (KW - 1) * WM * WN * SUB * 64 : 1;
 };
 
+// Column (within the tile) of lane column r of accumulator sub-tile nt of
+// wave column wn: 16 consecutive columns per sub-tile, or (ILV) sub-tiles in
+// groups of 4 whose columns interleave over 64: 4 r + nt mod 4.
+template <int NT, bool ILV>
+__device__ __forceinline__ int tile_col(int wn, int nt, int r) {
+    if constexpr (ILV) return ((wn * NT + nt) / 4) * 64 + 4 * r + (nt & 3);
+    return (wn * NT + nt) * 16 + r;
+}
+
 // Combine k-split waves (LDS) and k-split workgroups (ticket), then apply the
 // epilogue.  Shared by the fp32 and bf16 kernels.
-template <int MT, int NT, int WM, int WN, int KW>
+template <int MT, int NT, int WM, int WN, int KW, bool ILV = false>
 __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][NT], float* red,
                                             int* last_flag, int w, int lane, int tile_n, int tile_m, int tiles_n,
                                             int tiles) {
@@ -115,7 +124,7 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int ml = (wm * MT + mt) * 16 + 4 * g + i;
-                        const int nl = (wn * NT + nt) * 16 + r;
+                        const int nl = tile_col<NT, ILV>(wn, nt, r);
                         buf_store_x1_coherent(rp, (uint32_t)((base + ml * S::BN + nl) * 4), as_u32(acc[mt][nt][i]));
                     }
         }
@@ -129,7 +138,7 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int ml = (wm * MT + mt) * 16 + 4 * g + i;
-                    const int nl = (wn * NT + nt) * 16 + r;
+                    const int nl = tile_col<NT, ILV>(wn, nt, r);
                     const size_t off0 = (size_t)tile_id * (S::BM * S::BN) + ml * S::BN + nl;
                     const size_t stride = (size_t)tiles * (S::BM * S::BN);
                     // Ascending split order; this workgroup's own partial is
@@ -152,7 +161,7 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = m0 + (wm * MT + mt) * 16 + 4 * g + i;
-                const int n = n0 + (wn * NT + nt) * 16 + r;
+                const int n = n0 + tile_col<NT, ILV>(wn, nt, r);
                 if (m < p.M && n < p.N) {
                     float* c = p.C + (size_t)m * p.ldc + n;
                     *c = add_bias(epilogue(acc[mt][nt][i], p.alpha, p.beta, c), p.bias, n);
@@ -204,6 +213,22 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_f32(TileArgs p) {
         nloc[nt] = (wn * NT + nt) * 16 + r;
         nval[nt] = n0 + nloc[nt] < p.N;
     }
+    // B stored K x N, 16-row tiles with whole groups of 4 sub-tiles: one
+    // 16-byte load of columns 4 r .. 4 r + 3 of a 64-column group per k
+    // (instead of four 4-byte loads of one column); component e feeds
+    // sub-tile 4 q + e, whose lane column r is column 4 r + e of the group.
+    // (MI355X, us, 16 x 128 tiles: 32 x 4096 x 4096 29.3 -> 25.1, 32 x 11003
+    // x 2048 52.8 -> 45.7; the 64 x 128 tiles at M >= 128 were slower with it,
+    // 65.2 -> 79.8 at 128 x 4096 x 4096, and keep the column loads.)
+    constexpr bool ILV = TB == 0 && NT % 4 == 0 && WM == 1 && MT == 1;
+    constexpr int NG = ILV ? NT / 4 : 1;
+    int gloc[NG];
+    bool gval[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        gloc[q] = (wn * NG + q) * 64 + 4 * r;
+        gval[q] = n0 + gloc[q] < p.N;
+    }
 
     f32x4 acc[MT][NT];
 #pragma unroll
@@ -234,7 +259,18 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_f32(TileArgs p) {
             }
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
-                if constexpr (TB == 1) {
+                if constexpr (ILV) {
+                    // b[4 q + c][j] holds row kq + c, columns 4 r .. + 3 of group q;
+                    // sub-tile 4 q + e takes its component e below.
+                    if (nt % 4 == 0) {
+                        const int q = nt / 4;
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            const uint32_t off = (gval[q] && c < kvalid) ? ((uint32_t)(kq + c) * p.ldb + gloc[q]) * 4u : kOobOffset;
+                            b[nt + c][j] = buf_load_x4(rb, off);
+                        }
+                    }
+                } else if constexpr (TB == 1) {
                     const uint32_t off = (nval[nt] && kvalid > 0) ? ((uint32_t)nloc[nt] * p.ldb + kq) * 4u : kOobOffset;
                     b[nt][j] = buf_load_x4(rb, off);
                     if (kvalid < 4) b[nt][j] = keep_dwords(b[nt][j], kvalid);
@@ -254,13 +290,17 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_f32(TileArgs p) {
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                    for (int nt = 0; nt < NT; ++nt)
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(as_f32(a[mt][j][c]), as_f32(b[nt][j][c]),
+                    for (int nt = 0; nt < NT; ++nt) {
+                        // ILV: the B value of k = kq + c for sub-tile nt = 4 q + e is
+                        // component e of the load of row kq + c of group q.
+                        const uint32_t bv = ILV ? b[(nt & ~3) + c][j][nt & 3] : b[nt][j][c];
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(as_f32(a[mt][j][c]), as_f32(bv),
                                                                           acc[mt][nt], 0, 0, 0);
+                    }
     }
 
-    tile_finish<MT, NT, WM, WN, KW>(p, acc, red, &last_flag, w, lane, blockIdx.x, blockIdx.y, gridDim.x,
-                                    gridDim.x * gridDim.y);
+    tile_finish<MT, NT, WM, WN, KW, ILV>(p, acc, red, &last_flag, w, lane, blockIdx.x, blockIdx.y, gridDim.x,
+                                         gridDim.x * gridDim.y);
 }
 
 // ---------------------------------------------------------------- bf16
@@ -312,6 +352,22 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_bf16(TileArgs p) 
     for (int nt = 0; nt < NT; ++nt) {
         nloc[nt] = (wn * NT + nt) * 16 + r;
         nval[nt] = n0 + nloc[nt] < p.N;
+    }
+    // B stored K x N, 16-row tiles with whole groups of 4 sub-tiles: one
+    // 16-byte load of columns 4 r .. 4 r + 3 of a 64-column group per k
+    // (instead of four 4-byte loads of one column); component e feeds
+    // sub-tile 4 q + e, whose lane column r is column 4 r + e of the group.
+    // (MI355X, us, 16 x 128 tiles: 32 x 4096 x 4096 29.3 -> 25.1, 32 x 11003
+    // x 2048 52.8 -> 45.7; the 64 x 128 tiles at M >= 128 were slower with it,
+    // 65.2 -> 79.8 at 128 x 4096 x 4096, and keep the column loads.)
+    constexpr bool ILV = TB == 0 && NT % 4 == 0 && WM == 1 && MT == 1;
+    constexpr int NG = ILV ? NT / 4 : 1;
+    int gloc[NG];
+    bool gval[NG];
+#pragma unroll
+    for (int q = 0; q < NG; ++q) {
+        gloc[q] = (wn * NG + q) * 64 + 4 * r;
+        gval[q] = n0 + gloc[q] < p.N;
     }
 
     f32x4 acc[MT][NT];
