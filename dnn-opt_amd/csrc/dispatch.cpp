@@ -271,14 +271,18 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
             cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
-    } else if (mode == kTileF32 && !transA && M <= 32) {
+    } else if (mode == kTileF32 && !transA && (M <= 32 || (!transB && M <= 64))) {
         // Few rows: 16-row tiles instead of 64-row tiles that are mostly
         // padding.  MI355X, us (64 x 64 tiles -> 16 x 16 with k over 8 waves
         // / 16 x 128 with two k-groups): B stored N x K 12 x 11003 x 2048
         // 71.1 -> 30.9 / 34.7, 16 x 4096 x 4096 46.7 -> 23.2 / 24.3, 24 x 4096
         // x 4096 -> 34.6 / 32.3, 32 x 4096 x 4096 47.5 -> 37.1 / 32.8; B stored
         // K x N 12 x 11003 x 2048 60.4 -> 40.4 / 37.0, 16 x 4096 x 4096 36.5 ->
-        // 29.6 / 21.5, 32 x 4096 x 4096 38.8 -> 46.5 / 28.9.
+        // 29.6 / 21.5, 32 x 4096 x 4096 38.8 -> 46.5 / 28.9.  With B stored
+        // K x N the 16 x 128 tile (its 16-byte column loads) also wins up to M =
+        // 64: 48 / 64 x 4096 x 4096 40.4 / 42.8 -> 32.5 / 34.6, 64 x 11003 x
+        // 2048 76.1 -> 73.6; at M = 128 it loses where B is large (128 x 11003
+        // x 2048: 106 -> 122).
         cfg = transB && M <= 16 ? kTileF32Few : kTileF32Few128;
     } else if (mode == kTileF32 && N <= 64 && M >= 4096) {
         cfg = 1;
