@@ -271,7 +271,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
             cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
-    } else if (mode == kTileF32 && !transA && (M <= 32 || (!transB && M <= 64))) {
+    } else if (mode == kTileF32 && !transA && (M <= 32 || (!transB && M <= 512))) {
         // Few rows: 16-row tiles instead of 64-row tiles that are mostly
         // padding.  MI355X, us (64 x 64 tiles -> 16 x 16 with k over 8 waves
         // / 16 x 128 with two k-groups): B stored N x K 12 x 11003 x 2048
@@ -279,10 +279,12 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         // x 4096 -> 34.6 / 32.3, 32 x 4096 x 4096 47.5 -> 37.1 / 32.8; B stored
         // K x N 12 x 11003 x 2048 60.4 -> 40.4 / 37.0, 16 x 4096 x 4096 36.5 ->
         // 29.6 / 21.5, 32 x 4096 x 4096 38.8 -> 46.5 / 28.9.  With B stored
-        // K x N the 16 x 128 tile (its 16-byte column loads) also wins up to M =
-        // 64: 48 / 64 x 4096 x 4096 40.4 / 42.8 -> 32.5 / 34.6, 64 x 11003 x
-        // 2048 76.1 -> 73.6; at M = 128 it loses where B is large (128 x 11003
-        // x 2048: 106 -> 122).
+        // K x N the 16 x 128 tile (its 16-byte column loads, and the row tiles
+        // of a column strip sharing one XCD's L2) also wins up to M = 512
+        // (measured): 48 / 64 x 4096 x 4096 40.4 / 42.8 -> 32.5 / 34.6, 128 /
+        // 256 / 512 x 4096 x 4096 67.0 / 109.6 / 189.0 -> 61.8 / 96.8 / 175.6,
+        // 128 x 11003 x 2048 108.9 -> 89.2.  With B stored N x K it loses above
+        // M = 32 (128 x 4096 x 4096 77.7 -> 90.0).
         cfg = transB && M <= 16 ? kTileF32Few : kTileF32Few128;
     } else if (mode == kTileF32 && N <= 64 && M >= 4096) {
         cfg = 1;
@@ -336,7 +338,10 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     L->tn = (int)tn;
     L->tm = (int)tm;
     // LDS-staged tiles are launched as one XCD-ordered row of workgroups.
-    L->grid = lds ? dim3((unsigned)xcd_grid((int)tn, (int)tm), 1, (unsigned)s) : dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
+    // LDS-staged tiles and the 16-row fp32 tiles are launched as one
+    // XCD-ordered row of workgroups.
+    const bool xcd = lds || (mode == kTileF32 && c.mt == 1 && c.wm == 1);
+    L->grid = xcd ? dim3((unsigned)xcd_grid((int)tn, (int)tm), 1, (unsigned)s) : dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
     // k-splits of the LDS-staged kernels are summed by a reduce kernel, except
     // for the LDS-DMA tiles (DNNOPT_TILE_TICKET=1): the last workgroup to
     // finish a tile adds the others' partials.

@@ -182,7 +182,19 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_f32(TileArgs p) {
     const int lane = lane_id(), r = lane & 15, g = lane >> 4;
     const int w = wave_id();
     const int wn = w % WN, wm = (w / WN) % WM, wk = w / (WN * WM);
-    const int m0 = blockIdx.y * S::BM, n0 = blockIdx.x * S::BN;
+    // 16-row tiles (one row of waves) are launched as one XCD-ordered row of
+    // workgroups: the row tiles of a column strip run on one XCD, close in
+    // time, and share B in its L2.
+    constexpr bool XCD = MT == 1 && WM == 1;
+    int tn_ = (int)blockIdx.x, tm_ = (int)blockIdx.y, tiles_n = (int)gridDim.x;
+    if constexpr (XCD) {
+        const TileXY t = xcd_tile((int)blockIdx.x, p.tiles_n, p.tiles_m);
+        if (!t.ok) return;
+        tn_ = t.n;
+        tm_ = t.m;
+        tiles_n = p.tiles_n;
+    }
+    const int m0 = tm_ * S::BM, n0 = tn_ * S::BN;
 
     const int nblk = (p.K + KB - 1) / KB;
     const long long chunks = (long long)p.splits * KW;
@@ -299,8 +311,8 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_tile_f32(TileArgs p) {
                     }
     }
 
-    tile_finish<MT, NT, WM, WN, KW, ILV>(p, acc, red, &last_flag, w, lane, blockIdx.x, blockIdx.y, gridDim.x,
-                                         gridDim.x * gridDim.y);
+    tile_finish<MT, NT, WM, WN, KW, ILV>(p, acc, red, &last_flag, w, lane, tn_, tm_, tiles_n,
+                                         XCD ? p.tiles_n * p.tiles_m : (int)(gridDim.x * gridDim.y));
 }
 
 // ---------------------------------------------------------------- bf16

@@ -147,8 +147,8 @@ def test_plans_for_weights_stored_n_by_k(lib):
     for M, tb in ((17, 1), (32, 1), (9, 0), (16, 0), (32, 0)):
         p = lib.plan_sgemm(M, 4096, 4096, transB=tb)
         assert p["kernel"] == b.K_TILE_F32 and (p["rows"], p["cols"], p["block"]) == (16, 128, 256), (M, tb, p)
-    assert lib.plan_sgemm(64, 4096, 4096)["rows"] == 16             # B stored K x N: up to M = 64
-    assert lib.plan_sgemm(65, 4096, 4096)["rows"] == 64
+    assert lib.plan_sgemm(512, 4096, 4096)["rows"] == 16            # B stored K x N: up to M = 512
+    assert lib.plan_sgemm(513, 4096, 4096)["rows"] == 64
     assert lib.plan_sgemm(33, 4096, 4096, transB=1)["rows"] == 64
     assert lib.plan_bf16_ex(1, 11008, 4096, transB=1)["kernel"] == b.K_ROWDOT_BF16
     assert lib.plan_bf16_ex(4, 11008, 4096, transA=1, transB=1)["kernel"] == b.K_ROWDOT_BF16

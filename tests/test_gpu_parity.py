@@ -54,7 +54,7 @@ def test_sgemm_skinny(lib, orc, dev, M, N, K):
 # k-splits across workgroups at small N.
 FEW = [(5, 2048, 1000, 1, 0), (7, 4099, 2048, 1, 4), (8, 2053, 77, 1, 0), (9, 1009, 300, 1, 2), (13, 300, 4096, 1, 0),
        (16, 4096, 129, 1, 1), (17, 2000, 513, 1, 0), (32, 1001, 64, 1, 3), (9, 1000, 517, 0, 0), (13, 4099, 2048, 0, 4),
-       (16, 77, 8192, 0, 1), (48, 1500, 700, 0, 2), (64, 4099, 129, 0, 0)]
+       (16, 77, 8192, 0, 1), (48, 1500, 700, 0, 2), (64, 4099, 129, 0, 0), (300, 1001, 257, 0, 1), (512, 515, 64, 0, 0)]
 
 
 @pytest.mark.parametrize("M,N,K,tb,pad", FEW)

@@ -72,7 +72,7 @@ def test_noalloc_refuses_large_scratch(lib, orc, dev):
     """A split-k plan needing more partial-sum space than the array holds is
     refused before anything is enqueued; a following small call still works."""
     b = u.binding()
-    M, N, K = 300, 300, 300000
+    M, N, K = 600, 600, 300000
     assert lib.plan_sgemm(M, N, K)["workspace_bytes"] > b.NOALLOC_SCRATCH_BYTES - 4 * 16384
     dA = torch.zeros(M * K, dtype=torch.float32, device=dev)
     dB = torch.zeros(K * N, dtype=torch.float32, device=dev)
