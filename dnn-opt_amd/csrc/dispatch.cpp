@@ -271,7 +271,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
             cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
-    } else if (mode == kTileF32 && !transA && (M <= 32 || (!transB && M <= 512))) {
+    } else if (mode == kTileF32 && (transA ? M <= (transB ? 16 : 32) : (M <= 32 || (!transB && M <= 512)))) {
         // Few rows: 16-row tiles instead of 64-row tiles that are mostly
         // padding.  MI355X, us (64 x 64 tiles -> 16 x 16 with k over 8 waves
         // / 16 x 128 with two k-groups): B stored N x K 12 x 11003 x 2048
@@ -284,7 +284,11 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         // (measured): 48 / 64 x 4096 x 4096 40.4 / 42.8 -> 32.5 / 34.6, 128 /
         // 256 / 512 x 4096 x 4096 67.0 / 109.6 / 189.0 -> 61.8 / 96.8 / 175.6,
         // 128 x 11003 x 2048 108.9 -> 89.2.  With B stored N x K it loses above
-        // M = 32 (128 x 4096 x 4096 77.7 -> 90.0).
+        // M = 32 (128 x 4096 x 4096 77.7 -> 90.0).  A stored K x M (64 x 64
+        // tiles -> 16-row tiles): B stored K x N 16 / 32 x 4096 x 4096 35.6 /
+        // 35.8 -> 23.3 / 31.2, but 64 / 128 x 4096 x 4096 39.8 / 61.0 -> 48.2 /
+        // 82.9; B stored N x K 8 / 16 x 4096 x 4096 39.1 / 39.5 -> 22.8 / 24.5,
+        // 7 x 11003 x 2048 62.4 -> 32.5, but 32 x 4096 x 4096 40.2 -> 43.4.
         cfg = transB && M <= 16 ? kTileF32Few : kTileF32Few128;
     } else if (mode == kTileF32 && N <= 64 && M >= 4096) {
         cfg = 1;

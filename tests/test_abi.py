@@ -150,6 +150,9 @@ def test_plans_for_weights_stored_n_by_k(lib):
     assert lib.plan_sgemm(512, 4096, 4096)["rows"] == 16            # B stored K x N: up to M = 512
     assert lib.plan_sgemm(513, 4096, 4096)["rows"] == 64
     assert lib.plan_sgemm(33, 4096, 4096, transB=1)["rows"] == 64
+    # A stored K x M: 16-row tiles up to M = 16 (B stored N x K) / 32 (K x N)
+    for M, tb, rows in ((7, 1, 16), (16, 1, 16), (17, 1, 64), (9, 0, 16), (32, 0, 16), (33, 0, 64)):
+        assert lib.plan_sgemm(M, 4096, 4096, transA=1, transB=tb)["rows"] == rows, (M, tb)
     assert lib.plan_bf16_ex(1, 11008, 4096, transB=1)["kernel"] == b.K_ROWDOT_BF16
     assert lib.plan_bf16_ex(4, 11008, 4096, transA=1, transB=1)["kernel"] == b.K_ROWDOT_BF16
     # bf16, B stored N x K, M >= 5 (rows 4-byte aligned): the LDS-staged tiles

@@ -57,21 +57,28 @@ FEW = [(5, 2048, 1000, 1, 0), (7, 4099, 2048, 1, 4), (8, 2053, 77, 1, 0), (9, 10
        (16, 77, 8192, 0, 1), (48, 1500, 700, 0, 2), (64, 4099, 129, 0, 0), (300, 1001, 257, 0, 1), (512, 515, 64, 0, 0)]
 
 
-@pytest.mark.parametrize("M,N,K,tb,pad", FEW)
-def test_sgemm_few_rows_tiles(lib, orc, dev, M, N, K, tb, pad):
-    p = lib.plan_sgemm(M, N, K, transB=tb)
+# A stored K x M (transA): 16-row tiles up to M = 16 with B stored N x K, up
+# to M = 32 with B stored K x N.
+FEW_TA = [(7, 11003, 300, 1, 0), (8, 4096, 129, 1, 3), (13, 2053, 517, 1, 1), (16, 1001, 64, 1, 0),
+          (11, 2048, 1000, 0, 2), (16, 4099, 129, 0, 0), (24, 300, 2048, 0, 1), (32, 1001, 77, 0, 4)]
+
+
+@pytest.mark.parametrize("M,N,K,tb,pad,ta", [f + (0,) for f in FEW] + [f + (1,) for f in FEW_TA])
+def test_sgemm_few_rows_tiles(lib, orc, dev, M, N, K, tb, pad, ta):
+    p = lib.plan_sgemm(M, N, K, transA=ta, transB=tb)
     assert p["name"] == "dnnopt_tile_f32" and p["rows"] == 16 and p["cols"] == (16 if tb and M <= 16 else 128), p
-    lda, ldb = K + pad, (K + pad if tb else N + pad)
-    A = u.normal(orc, M * lda, 1, 0, 0.02).reshape(M, lda)
+    lda, ldb = (M + pad if ta else K + pad), (K + pad if tb else N + pad)
+    As = u.normal(orc, (K if ta else M) * lda, 1, 0, 0.02).reshape(K if ta else M, lda)
+    Amk = np.ascontiguousarray(As[:, :M].T if ta else As[:, :K])
     Bs = u.normal(orc, (N if tb else K) * ldb, 2, 0, 0.02).reshape(N if tb else K, ldb)
     Bkn = np.ascontiguousarray(Bs[:, :K].T if tb else Bs[:, :N])
     C0 = u.uniform(orc, M * N, 3).reshape(M, N)
-    dA, dB = dev_copy(A, dev), dev_copy(Bs, dev)
+    dA, dB = dev_copy(As, dev), dev_copy(Bs, dev)
     for alpha, beta in ((1.0, 1.0), (-0.75, 0.0)):
         dC = dev_copy(C0 if beta != 0.0 else np.full_like(C0, np.nan), dev)
-        lib.sgemm(M, N, K, alpha, dA, lda, dB, ldb, beta, dC, N, transB=tb, stream=stream())
-        want, scale = u.exact(A[:, :K], Bkn, alpha, beta, C0)
-        u.assert_fp32_close(host(dC), want, scale, K, f"few rows {M}x{N}x{K} tb={tb} a={alpha} b={beta}")
+        lib.sgemm(M, N, K, alpha, dA, lda, dB, ldb, beta, dC, N, transA=ta, transB=tb, stream=stream())
+        want, scale = u.exact(Amk, Bkn, alpha, beta, C0)
+        u.assert_fp32_close(host(dC), want, scale, K, f"few rows {M}x{N}x{K} ta={ta} tb={tb} a={alpha} b={beta}")
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096)] + [(M, N, 2048) for M in (2, 3, 5, 7) for N in (1009, 4099, 11003)])
