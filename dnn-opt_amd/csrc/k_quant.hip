@@ -8,12 +8,14 @@
 //       fma(alpha*scale_A*scale_B, acc, beta*C)   (ukernel_int8_neon.cpp:87-131).
 //
 // The pipeline is three launches: dnnopt_absmax_part (per-workgroup maxima of
-// both operands), dnnopt_quantize_pair (every workgroup reduces those maxima,
-// then quantizes its share of A, or of B straight into the N x K layout the
-// int8 kernels read), and the int8 GEMM, whose epilogue dequantizes into the
-// fp32 C (s8_out in device_common.h) -- no int32 copy of C exists.
+// both operands), dnnopt_quantize_pair (every wave reduces those maxima, then
+// quantizes its share of A, or of B straight into the N x K layout the int8
+// kernels read), and the int8 GEMM, whose epilogue dequantizes into the fp32
+// C (s8_out in device_common.h) -- no int32 copy of C exists.
 #include "device_common.h"
 #include "kernels.h"
+
+#include <algorithm>
 
 using namespace dnnopt_dev;
 
@@ -41,14 +43,21 @@ __device__ __forceinline__ unsigned block_max(unsigned m, unsigned* lds) {
     return m;
 }
 
-__device__ __forceinline__ int8_t quantize(float x, float inv) {
-    float v = __builtin_rintf(x * inv);
-    v = v > 127.0f ? 127.0f : (v < -128.0f ? -128.0f : v);
-    return (int8_t)(int)v;
+// q = clamp(rint(x * inv), -128, 127) as an int.  The conversion of NaN gives
+// 0 and large values saturate before the clamp, so the result equals the
+// clamp-then-convert form for every input.
+__device__ __forceinline__ int quantize(float x, float inv) {
+    const int v = (int)__builtin_rintf(x * inv);
+    return v > 127 ? 127 : (v < -128 ? -128 : v);
 }
 
-constexpr int kTK = 128;  // B tile (k rows) quantized and transposed through LDS
-constexpr int kTN = 64;   // B tile (n columns)
+// Four quantized values as the bytes of one dword, the first in the low byte.
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | (uint32_t)(b & 0xFF) << 8 | (uint32_t)(c & 0xFF) << 16 | (uint32_t)d << 24;
+}
+
+constexpr int kQK = 64;   // k rows of a B block (16 per lane, 4 lanes)
+constexpr int kQN = 256;  // n columns of a B block (64 per wave, 4 per lane)
 
 // Four consecutive floats of a row starting at column c (VEC: one 16-byte
 // load; else element loads), zero past `cols`.
@@ -61,6 +70,36 @@ __device__ __forceinline__ f32x4 load4(const float* row, int c, int cols) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = c + e < cols ? row[c + e] : 0.0f;
     return v;
+}
+
+// The maxima of A (part[0, ga)) and B (part[ga, ga + gb)), ga + gb <= 1024,
+// reduced by one wave on its own (no barrier): 16 consecutive partials per
+// lane, read as four 16-byte loads.  The buffer range is rounded up to whole
+// 16-byte loads (the partials' allocation is padded to 256 bytes); values
+// past ga + gb are masked.
+__device__ __forceinline__ void wave_maxima(const unsigned* part, int ga, int gb, unsigned* ma, unsigned* mb) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(part, ((uint32_t)(ga + gb) * 4u + 15u) & ~15u);
+    const int lane = lane_id();
+    u32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = buf_load_x4(r, (uint32_t)(lane * 16 + 4 * j) * 4u);
+    unsigned a = 0, b = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = lane * 16 + 4 * j + e;
+            if (i < ga) a = v[j][e] > a ? v[j][e] : a;
+            else if (i < ga + gb) b = v[j][e] > b ? v[j][e] : b;
+        }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned oa = (unsigned)__shfl_xor((int)a, off, 64), ob = (unsigned)__shfl_xor((int)b, off, 64);
+        a = oa > a ? oa : a;
+        b = ob > b ? ob : b;
+    }
+    *ma = a;
+    *mb = b;
 }
 
 }  // namespace
@@ -102,76 +141,72 @@ __global__ __launch_bounds__(256) void dnnopt_absmax_part(const float* __restric
     if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
-// Every block first reduces the partial maxima (ga of A, gb of B); block 0
-// also stores them to amax[0..1] for the GEMM's epilogue.  Blocks [0, qa)
-// quantize rows of A into qA (M x ldq); the others quantize 128 x 64 (k x n)
-// tiles of B into qB (N x ldq, i.e. transposed) through LDS: a wave reads 4
-// rows of 64 floats per instruction, and each row of the tile is written as
-// 128 contiguous bytes of k.  Bytes of a row between K and ldq are zero.
+// Blocks [0, qa) quantize rows of A into qA (M x ldq); blocks [qa, grid)
+// quantize 64 (k) x 256 (n) tiles of B into qB (N x ldq, i.e. transposed)
+// without LDS: lane (kq, ng) of wave w loads rows k0 + 16 kq .. + 15 of
+// columns n0 + 64 w + 4 ng .. + 3 (per load, 4 rows x 256 contiguous bytes
+// per wave), quantizes them and stores each column's 16 k as one 16-byte
+// store (64 contiguous bytes of a qB row per 4 lanes).  B's loads are issued
+// before the maxima are read, and every wave reduces the block maxima itself,
+// so the loads stay in flight through the reduction.  Wave 0 of block 0
+// stores max|A|, max|B| to amax[0..1] for the GEMM's epilogue.  Bytes of a
+// row between K and ldq are zero.
 template <int VEC>
 __global__ __launch_bounds__(256) void dnnopt_quantize_pair(const float* __restrict__ A, int M, int K, int lda,
                                                            const float* __restrict__ B, int N, int ldb,
                                                            const unsigned* part, int ga, int gb, unsigned* amax,
                                                            int qa, int8_t* qA, int8_t* qB, int ldq) {
-    __shared__ unsigned red[4];
-    __shared__ __attribute__((aligned(16))) int8_t tile[kTN][kTK + 16];
-    unsigned ma = 0, mb = 0;
-    for (int i = (int)threadIdx.x; i < ga; i += 256) ma = part[i] > ma ? part[i] : ma;
-    for (int i = (int)threadIdx.x; i < gb; i += 256) mb = part[ga + i] > mb ? part[ga + i] : mb;
-    ma = block_max(ma, red);
-    __syncthreads();
-    mb = block_max(mb, red);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
-        amax[0] = ma;
-        amax[1] = mb;
-    }
     if ((int)blockIdx.x < qa) {
+        unsigned ma, mb;
+        wave_maxima(part, ga, gb, &ma, &mb);
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            amax[0] = ma;
+            amax[1] = mb;
+        }
         const float inv = 1.0f / quant_scale_bits(ma);
         for (int r = (int)blockIdx.x; r < M; r += qa) {
             const float* row = A + (size_t)r * lda;
             int8_t* q = qA + (size_t)r * ldq;
             for (int c = (int)threadIdx.x * 4; c < ldq; c += 256 * 4) {
                 const f32x4 v = c < K ? load4<VEC>(row, c, K) : f32x4{0.f, 0.f, 0.f, 0.f};
-                char4 o;
-                o.x = quantize(v[0], inv);
-                o.y = quantize(v[1], inv);
-                o.z = quantize(v[2], inv);
-                o.w = quantize(v[3], inv);
-                *reinterpret_cast<char4*>(q + c) = o;  // ldq is a multiple of 16, so c + 4 <= ldq
+                // ldq is a multiple of 16, so c + 4 <= ldq
+                *reinterpret_cast<uint32_t*>(q + c) =
+                    pack4(quantize(v[0], inv), quantize(v[1], inv), quantize(v[2], inv), quantize(v[3], inv));
             }
         }
         return;
     }
-    const float inv = 1.0f / quant_scale_bits(mb);
-    const int tiles_k = (ldq + kTK - 1) / kTK;
-    const int tb = (int)blockIdx.x - qa;
-    const int k0 = (tb % tiles_k) * kTK, n0 = (tb / tiles_k) * kTN;
-    // Load: lanes 16 apart take rows 4 apart; 16 lanes cover 64 floats of a row.
-    {
-        const int nc = ((int)threadIdx.x & 15) * 4;
-        const int kr0 = (int)threadIdx.x >> 4;  // 0..15
-        f32x4 v[kTK / 16];
+    // The B blocks stride over the tiles (two per block at 4096 x 4096), so
+    // one tile's stores overlap the next tile's loads.
+    const int tiles_n = (N + kQN - 1) / kQN;
+    const int ntiles = tiles_n * ((ldq + kQK - 1) / kQK);
+    const int lane = lane_id();
+    const int kq = lane & 3, ng = lane >> 2;
+    float inv = 0.0f;
+    bool first = true;
+    for (int tb = (int)blockIdx.x - qa; tb < ntiles; tb += (int)gridDim.x - qa) {
+        const int kr = (tb / tiles_n) * kQK + 16 * kq;                   // first of this lane's 16 rows
+        const int n = (tb % tiles_n) * kQN + 64 * wave_id() + 4 * ng;  // first of its 4 columns
+        f32x4 v[16];
 #pragma unroll
-        for (int j = 0; j < kTK / 16; ++j) {
-            const int k = k0 + kr0 + 16 * j;
-            v[j] = (k < K && n0 + nc < N) ? load4<VEC>(B + (size_t)k * ldb + n0, nc, N - n0)
-                                          : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < 16; ++r)
+            v[r] = (kr + r < K && n < N) ? load4<VEC>(B + (size_t)(kr + r) * ldb, n, N) : f32x4{0.f, 0.f, 0.f, 0.f};
+        if (first) {
+            unsigned ma, mb;
+            wave_maxima(part, ga, gb, &ma, &mb);
+            inv = 1.0f / quant_scale_bits(mb);
+            first = false;
         }
+        if (kr >= ldq) continue;  // ldq is a multiple of 16: a lane's 16 rows are all below it or all past it
 #pragma unroll
-        for (int j = 0; j < kTK / 16; ++j)
+        for (int e = 0; e < 4; ++e) {
+            if (n + e >= N) break;
+            u32x4 o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) tile[nc + e][kr0 + 16 * j] = quantize(v[j][e], inv);
-    }
-    __syncthreads();
-    // Store: 8 threads per row of the tile, 16 bytes of k each.
-    {
-        const int kc = ((int)threadIdx.x & 7) * 16;
-#pragma unroll
-        for (int j = 0; j < kTN / 32; ++j) {
-            const int nr = ((int)threadIdx.x >> 3) + 32 * j;
-            const int n = n0 + nr, k = k0 + kc;
-            if (n < N && k < ldq) *reinterpret_cast<int4*>(qB + (size_t)n * ldq + k) =
-                *reinterpret_cast<const int4*>(&tile[nr][kc]);
+            for (int j = 0; j < 4; ++j)
+                o[j] = pack4(quantize(v[4 * j][e], inv), quantize(v[4 * j + 1][e], inv),
+                             quantize(v[4 * j + 2][e], inv), quantize(v[4 * j + 3][e], inv));
+            *reinterpret_cast<u32x4*>(qB + (size_t)(n + e) * ldq + kr) = o;
         }
     }
 }
@@ -207,7 +242,12 @@ hipError_t launch_quant_pair(const float* A, int lda, const float* B, int ldb, i
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int qa = M < 256 ? M : 256;
-    const long long qb = (long long)((ldq + kTK - 1) / kTK) * ((N + kTN - 1) / kTN);
+    if (ga + gb > 1024) return hipErrorInvalidValue;  // one wave reduces the maxima
+    // Tiles of B; above 1024 of them each block takes two, else at most 512
+    // blocks (MI355X, 4096 x 4096: 1024 blocks of one tile 16.5 us, 512 of
+    // two 15 us).
+    const long long tiles = (long long)((ldq + kQK - 1) / kQK) * ((N + kQN - 1) / kQN);
+    const long long qb = tiles > 1024 ? (tiles + 1) / 2 : std::min<long long>(tiles, 512);
     if (qa + qb > 0x7FFFFFFFll) return hipErrorInvalidValue;
     if (vec)
         hipLaunchKernelGGL(dnnopt_quantize_pair<1>, dim3((unsigned)(qa + qb)), dim3(256), 0, s, A, M, K, lda, B, N,

@@ -581,6 +581,24 @@ def test_int8_dynamic_quant_matches_oracle(lib, orc, dev, M, N, K):
         assert np.array_equal(host(dC).view(np.uint32), Co.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N,K,pa,pb", [(9, 300, 130, 3, 5), (2, 1000, 77, 1, 4), (130, 257, 600, 0, 1),
+                                        (16, 515, 256, 4, 9), (24, 1030, 200, 4, 2)])
+def test_int8_dynamic_quant_padded_strides(lib, orc, dev, M, N, K, pa, pb):
+    # Rows of A and B that do not start on 16-byte boundaries, padding between
+    # rows (NaN, never read) and a C block inside a wider matrix.
+    lda, ldb, ldc = K + pa, N + pb, N + 2
+    A = np.full((M, lda), np.nan, np.float32)
+    A[:, :K] = u.uniform(orc, M * K, 1).reshape(M, K)
+    B = np.full((K, ldb), np.nan, np.float32)
+    B[:, :N] = u.normal(orc, K * N, 2, 0, 0.02).reshape(K, N)
+    C0 = u.uniform(orc, M * ldc, 3).reshape(M, ldc)
+    Co, Ak, Bn = C0.copy(), np.ascontiguousarray(A[:, :K]), np.ascontiguousarray(B[:, :N])
+    orc.orc_gemm_int8_dynq(M, N, K, 0.75, u.ptr(Ak), K, u.ptr(Bn), N, 0.5, u.ptr(Co), ldc)
+    dC = dev_copy(C0, dev)
+    lib.gemm_int8_f32(M, N, K, 0.75, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, 0.5, dC, ldc, stream=stream())
+    assert np.array_equal(host(dC).view(np.uint32), Co.view(np.uint32))
+
+
 def test_int8_dynamic_quant_rounding_ties(lib, dev):
     """Quantized values that are exact ties and fractions (scales 1 and 2):
     the device quantizer must round to nearest even like the reference's
