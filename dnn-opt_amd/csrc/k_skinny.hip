@@ -328,10 +328,11 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
         return;
     }
 
-    // Split-k: publish this workgroup's partial sums [split][MR][ncols_pad].
-    // For the reduce kernel that follows, plain stores (the launch boundary
-    // makes them visible); for the last-arriving workgroup, stores written
-    // through to memory (sc0 sc1), which it reads without cache maintenance.
+    // Split-k: publish this workgroup's partial sums [split][MR][ncols_pad],
+    // written through to memory (sc0 sc1).  The last-arriving workgroup reads
+    // them without cache maintenance; for the reduce kernel that follows they
+    // leave no dirty L2 lines to write back at the end of the launch (MI355X,
+    // C2 step 3243 -> 3267 GB/s against plain stores).
     const __amdgpu_buffer_rsrc_t rp =
         make_rsrc(p.part, range31((size_t)p.splits * MR * p.ncols_pad * 4));
 #pragma unroll
@@ -343,8 +344,7 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
             if (gi < OG && m < MR) {
                 const uint32_t off =
                     (uint32_t)((((size_t)split * MR + m) * p.ncols_pad + col0 + group_col(gi)) * 4);
-                if (p.defer_reduce) buf_store_x4(rp, off, out[pass][i]);
-                else buf_store_x4_coherent(rp, off, out[pass][i]);
+                buf_store_x4_coherent(rp, off, out[pass][i]);
             }
         }
     if (p.defer_reduce) return;
