@@ -242,10 +242,12 @@ int dnnopt_hip_plan_gemm_bf16_ex(int transA, int transB, int M, int N, int K, dn
     if (!out || !dims_ok(M, N, K) || (transA != 0 && transA != 1) || (transB != 0 && transB != 1))
         return DNNOPT_ERR_INVALID_ARG;
     // As dnnopt_hip_gemm_bf16_ex with unpadded strides (a transposed A is
+    // read in place by the skinny kernel up to M = 8 with B stored K x N, else
     // first copied to an even row stride).
-    const int lda = transA ? (M <= 8 && !transB ? M : (K + 1) & ~1) : K;
+    const int lda = transA ? (K + 1) & ~1 : K;
     Launch L;
-    int st = plan_bf16(0, M, N, K, lda, transB ? K : N, &L, transB);
+    int st = transA && !transB && M <= 8 ? plan_skinny(kSkinnyBF16, M, N, K, N, &L)
+                                         : plan_bf16(0, M, N, K, lda, transB ? K : N, &L, transB);
     if (st == DNNOPT_OK) *out = L.pub;
     return st;
 }
@@ -306,7 +308,7 @@ int dnnopt_hip_gemm_bf16_ex(int transA, int transB, int M, int N, int K, float a
     Launch L;
     if (transA && !transB && M <= 8) {
         // The skinny kernel reads a K x M A in place (A is M*K elements).
-        int st = plan_bf16(0, M, N, K, lda, ldb, &L, 0, ldc);
+        int st = plan_skinny(kSkinnyBF16, M, N, K, ldb, &L);
         if (st != DNNOPT_OK) return st;
         return run_skinny(L, A, 1, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     }

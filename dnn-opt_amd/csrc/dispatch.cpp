@@ -524,7 +524,8 @@ int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, La
     // 4096 21.5 / 21.2 / 25.5 -> 17.3 / 17.9 / 19.0, M=7 x 4099 x 2048 15.9
     // -> 13.8; N = 1009 and M <= 4 favour the row-dot kernel).
     const bool few_rows_tile = transB && M >= 5 && N >= 2048;
-    if (M <= 8 && !transA && !few_rows_tile && plan_rowdot(0, M, N, K, lda, ldb, L) == DNNOPT_OK)
+    // (The row-dot kernel reads B as N x K rows: never for a K x N B.)
+    if (transB && M <= 8 && !transA && !few_rows_tile && plan_rowdot(0, M, N, K, lda, ldb, L) == DNNOPT_OK)
         return DNNOPT_OK;
     static const bool tall_ok = [] {
         const char* e = getenv("DNNOPT_TALL");
@@ -536,8 +537,14 @@ int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, La
 
 int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB, int ldc) {
     // B stored N x K has k-contiguous columns: MFMA tiles read it in place
-    // for every M (the skinny kernel streams rows of a K x N B).
-    if (M <= 8 && !transB) return plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L);
+    // for every M (the skinny kernel streams rows of a K x N B).  bf16
+    // storage with a K x N B and 4-byte aligned rows: the skinny kernel up to
+    // M = 5, the LDS-staged 32 x 64 tiles from M = 6 (MI355X, us, skinny ->
+    // tiles, N = 11008, K = 4096: M=6 24.8 -> 22.6, M=7 27.9 -> 22.6, M=8
+    // 31.0 -> 22.4; 8 x 4096 x 4096 16.2 -> 13.5; M=5 22.6 vs 22.4, M=4 21.0
+    // vs 22.2, 5 x 4096 x 4096 13.6 vs 13.8).
+    const bool tile_kn = !transB && !fp32_inputs && M >= 6 && (lda & 1) == 0 && (ldb & 1) == 0;
+    if (M <= 8 && !transB && !tile_kn) return plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L);
     if (transB && fp32_inputs) return DNNOPT_ERR_UNSUPPORTED;
     // B stored N x K: the row-dot kernel up to M = 4 and for rows off 4-byte
     // boundaries; from M = 5 the LDS-staged tiles (us, row-dot -> 32 x 64
@@ -545,7 +552,7 @@ int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L,
     // -> 24.1; 8 x 4096 x 4096 15.7 -> 12.4; M=4 24.1 vs 23.8, M=1 19.1 vs
     // 22.6).
     const bool tile_tb = transB && M >= 5 && (lda & 1) == 0 && (ldb & 1) == 0;
-    if (M <= 8 && !tile_tb && plan_rowdot(1, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
+    if (transB && M <= 8 && !tile_tb && plan_rowdot(1, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
     return plan_tile(fp32_inputs ? kTileF2B : kTileBF16, 0, transB, M, N, K, lda, ldb, L, true, ldc);
 }
 

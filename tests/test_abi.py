@@ -155,6 +155,14 @@ def test_plans_for_weights_stored_n_by_k(lib):
         assert lib.plan_sgemm(M, 4096, 4096, transA=1, transB=tb)["rows"] == rows, (M, tb)
     assert lib.plan_bf16_ex(1, 11008, 4096, transB=1)["kernel"] == b.K_ROWDOT_BF16
     assert lib.plan_bf16_ex(4, 11008, 4096, transA=1, transB=1)["kernel"] == b.K_ROWDOT_BF16
+    # bf16 storage, B stored K x N: the skinny kernel up to M = 5, the
+    # LDS-staged tiles from M = 6 when rows are 4-byte aligned; fp32 inputs and
+    # A stored K x M keep the skinny kernel
+    for M, name in ((5, "dnnopt_skinny"), (6, "dnnopt_tile_bf16_lds"), (8, "dnnopt_tile_bf16_lds")):
+        assert lib.plan_bf16(M, 11008, 4096)["name"] == name, M
+        assert lib.plan_bf16_ex(M, 11008, 4096)["name"] == name, M
+        assert lib.plan_bf16_ex(M, 11008, 4096, transA=1)["name"] == "dnnopt_skinny", M
+        assert lib.plan_bf16(M, 11008, 4096, fp32_inputs=1)["name"] == "dnnopt_skinny", M
     # bf16, B stored N x K, M >= 5 (rows 4-byte aligned): the LDS-staged tiles
     for M in (5, 8):
         assert lib.plan_bf16_ex(M, 11008, 4096, transB=1)["name"] == "dnnopt_tile_bf16_lds"

@@ -336,6 +336,32 @@ def test_bf16_lds_tiles(lib, orc, dev, M, N, K, pa, pb, mode):
     u.assert_fp32_close(host(dC), want, scale, K, f"lds {mode} {M}x{N}x{K}")
 
 
+# bf16 storage, B stored K x N, 6 <= M <= 8: LDS-staged 32 x 64 tiles when
+# both row strides are even, the skinny kernel otherwise; A stored K x M stays
+# on the skinny kernel.
+@pytest.mark.parametrize("M,N,K,pa,pb,ta", [(6, 1001, 130, 2, 1, 0), (7, 11008, 4096, 0, 0, 0), (8, 4099, 300, 0, 1, 0),
+                                            (6, 77, 1000, 4, 3, 0), (7, 300, 129, 0, 0, 0), (8, 515, 64, 0, 1, 1)])
+def test_bf16_small_m_kn_tiles(lib, orc, dev, M, N, K, pa, pb, ta):
+    lda, ldb = (M if ta else K) + pa, N + pb
+    p = lib.plan_bf16_ex(M, N, K, transA=ta)
+    tiled = not ta and lda % 2 == 0 and ldb % 2 == 0
+    if lda == (M if ta else K) and ldb == N:
+        assert p["name"] == ("dnnopt_tile_bf16_lds" if tiled else "dnnopt_skinny"), p
+    Amk = u.bf16_bits(orc, u.normal(orc, M * K, 1)).reshape(M, K)
+    As = np.zeros((K, lda) if ta else (M, lda), np.uint16)
+    if ta:
+        As[:, :M] = Amk.T
+    else:
+        As[:, :K] = Amk
+    Bs = u.bf16_bits(orc, u.normal(orc, K * ldb, 2, 0, 0.02)).reshape(K, ldb)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    want, scale = u.exact(u.bf16_value(Amk), u.bf16_value(Bs)[:, :N], -0.5, 0.75, C0)
+    dC = dev_copy(C0, dev)
+    lib.gemm_bf16_ex(M, N, K, -0.5, dev_copy(As.view(np.int16), dev), lda, dev_copy(Bs.view(np.int16), dev), ldb, 0.75,
+                     dC, N, transA=ta, stream=stream())
+    u.assert_fp32_close(host(dC), want, scale, K, f"bf16 small-M K x N {M}x{N}x{K} ta={ta}")
+
+
 @pytest.mark.parametrize("tb", [0, 1])
 def test_bf16_dma_256_row_tiles(lib, orc, dev, tb):
     """bf16 storage with more 128-row tiles than CUs takes 256 x 96 tiles:
