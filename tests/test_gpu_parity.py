@@ -824,3 +824,91 @@ def test_edge_shapes_every_entry_point(lib, orc, dev, M, N, K):
     dC = torch.zeros((M, N), dtype=torch.int32, device=dev)
     lib.gemm_s8s8s32(M, N, K, dev_copy(A8, dev), K, dev_copy(B8, dev), K, dC, N, stream=stream())
     assert np.array_equal(host(dC).astype(np.int64), A8.astype(np.int64) @ B8.T.astype(np.int64))
+
+
+# ---------------------------------------------------------------- seeded sweeps over every route
+def _sgemm_sweep_cases():
+    """Seeded fp32 shapes spread over the dispatcher's routes (skinny, row-dot,
+    16-row tiles, 64-row tiles, tall-skinny, k-outer), both operand layouts,
+    padded strides, assorted alpha / beta.  Sizes keep the fp64 reference
+    under a second each."""
+    rng = np.random.default_rng(20261203)
+    cases = []
+    while len(cases) < 28:
+        kind = len(cases) % 7
+        if kind == 0:
+            M, N, K = int(rng.integers(1, 9)), int(rng.integers(1, 6000)), int(rng.integers(1, 3000))
+        elif kind == 1:
+            M, N, K = int(rng.integers(9, 33)), int(rng.integers(16, 5000)), int(rng.integers(1, 2000))
+        elif kind == 2:
+            M, N, K = int(rng.integers(33, 600)), int(rng.integers(16, 3000)), int(rng.integers(1, 700))
+        elif kind == 3:
+            M, N, K = int(rng.integers(20000, 70000)), int(rng.integers(17, 65)), 256
+        elif kind == 4:
+            M, N, K = int(rng.integers(1, 5)), int(rng.integers(1, 9000)), int(rng.integers(1, 2100))
+        elif kind == 5:
+            M, N, K = 4 * int(rng.integers(9, 17)), 4 * int(rng.integers(9, 17)), int(rng.integers(32768, 70000))
+        else:
+            M, N, K = int(rng.integers(1, 400)), int(rng.integers(1, 400)), int(rng.integers(1, 400))
+        if M * N * K > 250_000_000:
+            continue
+        ta = int(rng.integers(0, 2)) if kind not in (3, 5) else int(kind == 5)
+        tb = int(rng.integers(0, 2)) if kind not in (3, 5) else 0
+        if kind == 4:
+            tb = 1
+        pa, pb = int(rng.integers(0, 4)) * (kind != 5), int(rng.integers(0, 4)) * (kind != 5)
+        alpha = float(rng.choice([1.0, 0.5, -1.25]))
+        beta = float(rng.choice([0.0, 1.0, -0.5]))
+        cases.append((M, N, K, ta, tb, pa, pb, alpha, beta))
+    return cases
+
+
+_SGEMM_SWEEP = _sgemm_sweep_cases()
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb,pa,pb,alpha,beta", _SGEMM_SWEEP)
+def test_sgemm_route_sweep(lib, orc, dev, M, N, K, ta, tb, pa, pb, alpha, beta):
+    lda = (M if ta else K) + pa
+    ldb = (K if tb else N) + pb
+    As = u.normal(orc, (K if ta else M) * lda, 1, 0, 0.5).reshape(K if ta else M, lda)
+    Bs = u.normal(orc, (N if tb else K) * ldb, 2, 0, 0.5).reshape(N if tb else K, ldb)
+    Amk = np.ascontiguousarray(As[:, :M].T if ta else As[:, :K])
+    Bkn = np.ascontiguousarray(Bs[:, :K].T if tb else Bs[:, :N])
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    dC = dev_copy(C0 if beta != 0.0 else np.full_like(C0, np.nan), dev)
+    lib.sgemm(M, N, K, alpha, dev_copy(As, dev), lda, dev_copy(Bs, dev), ldb, beta, dC, N, transA=ta, transB=tb,
+              stream=stream())
+    want, scale = u.exact(Amk, Bkn, alpha, beta, C0 if beta != 0.0 else None)
+    u.assert_fp32_close(host(dC), want, scale, K, f"sweep {M}x{N}x{K} ta={ta} tb={tb} a={alpha} b={beta}")
+
+
+def test_sgemm_route_sweep_covers_every_route(lib):
+    names = {lib.plan_sgemm(M, N, K, transA=ta, transB=tb)["name"] for M, N, K, ta, tb, *_ in _SGEMM_SWEEP}
+    assert names >= {"dnnopt_skinny", "dnnopt_rowdot", "dnnopt_tile_f32", "dnnopt_tall_f32", "dnnopt_kouter_f32"}, names
+
+
+def _s8_sweep_cases():
+    rng = np.random.default_rng(20261204)
+    cases = []
+    while len(cases) < 16:
+        band = len(cases) % 4
+        M = int(rng.integers(*((1, 5), (5, 17), (17, 300), (1, 300))[band]))
+        N, K = int(rng.integers(1, 3000)), int(rng.integers(1, 3000))
+        if M * N * K > 400_000_000:
+            continue
+        pa, pb = int(rng.integers(0, 5)), int(rng.integers(0, 5))
+        cases.append((M, N, K, pa, pb))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,pa,pb", _s8_sweep_cases())
+def test_int8_route_sweep(lib, orc, dev, M, N, K, pa, pb):
+    lda, ldb, ldc = K + pa, K + pb, N + 1
+    A = u.ints8(orc, M * lda, 1, -128, 127).reshape(M, lda)
+    B = u.ints8(orc, N * ldb, 2, -128, 127).reshape(N, ldb)
+    dC = torch.full((M, ldc), 5, dtype=torch.int32, device=dev)
+    lib.gemm_s8s8s32(M, N, K, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, dC, ldc, stream=stream())
+    got = host(dC)
+    want = (A[:, :K].astype(np.float64) @ B[:, :K].astype(np.float64).T).astype(np.int64)
+    assert np.array_equal(got[:, :N].astype(np.int64), want), (M, N, K, pa, pb)
+    assert (got[:, N:] == 5).all()
