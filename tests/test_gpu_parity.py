@@ -912,3 +912,38 @@ def test_int8_route_sweep(lib, orc, dev, M, N, K, pa, pb):
     want = (A[:, :K].astype(np.float64) @ B[:, :K].astype(np.float64).T).astype(np.int64)
     assert np.array_equal(got[:, :N].astype(np.int64), want), (M, N, K, pa, pb)
     assert (got[:, N:] == 5).all()
+
+
+def _dynq_sweep_cases():
+    rng = np.random.default_rng(20261205)
+    cases = []
+    while len(cases) < 12:
+        band = len(cases) % 3
+        M = int(rng.integers(*((1, 9), (9, 17), (17, 300))[band]))
+        N, K = int(rng.integers(1, 2500)), int(rng.integers(1, 2500))
+        if M * N * K > 30_000_000:
+            continue
+        pa, pb = int(rng.integers(0, 5)), int(rng.integers(0, 5))
+        alpha = float(rng.choice([1.0, 0.5, -2.0]))
+        beta = float(rng.choice([0.0, 1.0, 0.25]))
+        cases.append((M, N, K, pa, pb, alpha, beta))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,pa,pb,alpha,beta", _dynq_sweep_cases())
+def test_int8_dynamic_quant_sweep(lib, orc, dev, M, N, K, pa, pb, alpha, beta):
+    """fp32-API gemm_int8 over every int8 route, padded strides (rows off
+    16-byte boundaries), assorted alpha / beta: bit-exact with the oracle."""
+    lda, ldb, ldc = K + pa, N + pb, N + 3
+    A = np.full((M, lda), np.nan, np.float32)
+    A[:, :K] = u.normal(orc, M * K, 1, 0, 1.5).reshape(M, K)
+    B = np.full((K, ldb), np.nan, np.float32)
+    B[:, :N] = u.uniform(orc, K * N, 2).reshape(K, N)
+    C0 = u.uniform(orc, M * ldc, 3).reshape(M, ldc)
+    Co, Ak, Bn = C0.copy(), np.ascontiguousarray(A[:, :K]), np.ascontiguousarray(B[:, :N])
+    orc.orc_gemm_int8_dynq(M, N, K, alpha, u.ptr(Ak), K, u.ptr(Bn), N, beta, u.ptr(Co), ldc)
+    dC = dev_copy(C0 if beta != 0.0 else np.where(np.arange(ldc)[None, :] < N, np.nan, C0).astype(np.float32), dev)
+    lib.gemm_int8_f32(M, N, K, alpha, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, beta, dC, ldc, stream=stream())
+    got = host(dC)
+    assert np.array_equal(got[:, :N].view(np.uint32), Co[:, :N].view(np.uint32)), (M, N, K)
+    assert np.array_equal(got[:, N:], C0[:, N:]), "wrote outside the C block"
