@@ -195,6 +195,45 @@ __device__ __forceinline__ float quant_scale_bits(uint32_t amax_bits) {
     return amax == 0.0f ? 1.0f : amax / 127.0f;
 }
 
+// Dynamic int8 quantization of one value (fp32-API gemm_int8,
+// src/gemm/gemm_pack_int8.cpp:29-71): q = clamp(rint(x * inv), -128, 127) as
+// an int.  The conversion of NaN gives 0 and large values saturate before the
+// clamp, so the result equals the clamp-then-convert form for every input.
+__device__ __forceinline__ int quant_s8(float x, float inv) {
+    const int v = (int)__builtin_rintf(x * inv);
+    return v > 127 ? 127 : (v < -128 ? -128 : v);
+}
+
+// The maxima of A (part[0, ga)) and B (part[ga, ga + gb)), ga + gb <= 1024,
+// reduced by one wave on its own (no barrier): 16 consecutive partials per
+// lane, read as four 16-byte loads.  The buffer range is rounded up to whole
+// 16-byte loads (the partials' allocation is padded to 256 bytes); values
+// past ga + gb are masked.
+__device__ __forceinline__ void wave_maxima(const unsigned* part, int ga, int gb, unsigned* ma, unsigned* mb) {
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(part, ((uint32_t)(ga + gb) * 4u + 15u) & ~15u);
+    const int lane = lane_id();
+    u32x4 v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = buf_load_x4(r, (uint32_t)(lane * 16 + 4 * j) * 4u);
+    unsigned a = 0, b = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = lane * 16 + 4 * j + e;
+            if (i < ga) a = v[j][e] > a ? v[j][e] : a;
+            else if (i < ga + gb) b = v[j][e] > b ? v[j][e] : b;
+        }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned oa = (unsigned)__shfl_xor((int)a, off, 64), ob = (unsigned)__shfl_xor((int)b, off, 64);
+        a = oa > a ? oa : a;
+        b = ob > b ? ob : b;
+    }
+    *ma = a;
+    *mb = b;
+}
+
 // fp32 output of an exact int32 accumulator (EPI 1 of the int8 kernels):
 //   amax == nullptr: per-column dequantization, (float)acc * scale[n];
 //   amax != nullptr: the dynamic per-tensor dequantization of the fp32-API

@@ -43,14 +43,6 @@ __device__ __forceinline__ unsigned block_max(unsigned m, unsigned* lds) {
     return m;
 }
 
-// q = clamp(rint(x * inv), -128, 127) as an int.  The conversion of NaN gives
-// 0 and large values saturate before the clamp, so the result equals the
-// clamp-then-convert form for every input.
-__device__ __forceinline__ int quantize(float x, float inv) {
-    const int v = (int)__builtin_rintf(x * inv);
-    return v > 127 ? 127 : (v < -128 ? -128 : v);
-}
-
 // Four quantized values as the bytes of one dword, the first in the low byte.
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     return (uint32_t)(a & 0xFF) | (uint32_t)(b & 0xFF) << 8 | (uint32_t)(c & 0xFF) << 16 | (uint32_t)d << 24;
@@ -70,36 +62,6 @@ __device__ __forceinline__ f32x4 load4(const float* row, int c, int cols) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[e] = c + e < cols ? row[c + e] : 0.0f;
     return v;
-}
-
-// The maxima of A (part[0, ga)) and B (part[ga, ga + gb)), ga + gb <= 1024,
-// reduced by one wave on its own (no barrier): 16 consecutive partials per
-// lane, read as four 16-byte loads.  The buffer range is rounded up to whole
-// 16-byte loads (the partials' allocation is padded to 256 bytes); values
-// past ga + gb are masked.
-__device__ __forceinline__ void wave_maxima(const unsigned* part, int ga, int gb, unsigned* ma, unsigned* mb) {
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(part, ((uint32_t)(ga + gb) * 4u + 15u) & ~15u);
-    const int lane = lane_id();
-    u32x4 v[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = buf_load_x4(r, (uint32_t)(lane * 16 + 4 * j) * 4u);
-    unsigned a = 0, b = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int i = lane * 16 + 4 * j + e;
-            if (i < ga) a = v[j][e] > a ? v[j][e] : a;
-            else if (i < ga + gb) b = v[j][e] > b ? v[j][e] : b;
-        }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const unsigned oa = (unsigned)__shfl_xor((int)a, off, 64), ob = (unsigned)__shfl_xor((int)b, off, 64);
-        a = oa > a ? oa : a;
-        b = ob > b ? ob : b;
-    }
-    *ma = a;
-    *mb = b;
 }
 
 }  // namespace
@@ -171,7 +133,7 @@ __global__ __launch_bounds__(256) void dnnopt_quantize_pair(const float* __restr
                 const f32x4 v = c < K ? load4<VEC>(row, c, K) : f32x4{0.f, 0.f, 0.f, 0.f};
                 // ldq is a multiple of 16, so c + 4 <= ldq
                 *reinterpret_cast<uint32_t*>(q + c) =
-                    pack4(quantize(v[0], inv), quantize(v[1], inv), quantize(v[2], inv), quantize(v[3], inv));
+                    pack4(quant_s8(v[0], inv), quant_s8(v[1], inv), quant_s8(v[2], inv), quant_s8(v[3], inv));
             }
         }
         return;
@@ -204,8 +166,8 @@ __global__ __launch_bounds__(256) void dnnopt_quantize_pair(const float* __restr
             u32x4 o;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                o[j] = pack4(quantize(v[4 * j][e], inv), quantize(v[4 * j + 1][e], inv),
-                             quantize(v[4 * j + 2][e], inv), quantize(v[4 * j + 3][e], inv));
+                o[j] = pack4(quant_s8(v[4 * j][e], inv), quant_s8(v[4 * j + 1][e], inv),
+                             quant_s8(v[4 * j + 2][e], inv), quant_s8(v[4 * j + 3][e], inv));
             *reinterpret_cast<u32x4*>(qB + (size_t)(n + e) * ldq + kr) = o;
         }
     }

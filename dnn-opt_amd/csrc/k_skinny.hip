@@ -161,6 +161,11 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     const int tile = sp.tile;
     const int split = sp.split;
     const int nsplit = sp.nsplit;
+    // A tile with one k-split stores C itself, unless a reduce kernel follows:
+    // that kernel then covers every column of C, so a one-split tile (G / T
+    // == 1 with a remainder gives tiles of one and two splits) publishes its
+    // sums like the others.
+    const bool direct = nsplit == 1 && !p.defer_reduce;
     const int col0 = tile * TW;
     // k is cut into blocks of U rows; chunk cw (wave w of split `split`)
     // owns a contiguous run of blocks, so every chunk but the last starts and
@@ -201,7 +206,7 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
                 const int gi = (int)threadIdx.x + i * NT;
                 const int m = pass * G + group_row(gi);
                 const int n = col0 + group_col(gi) + e;
-                if (nsplit == 1 && p.beta != 0.0f && gi < OG && m < MR && n < p.N)
+                if (direct && p.beta != 0.0f && gi < OG && m < MR && n < p.N)
                     c_pre[pass][i][e] = p.C[(size_t)m * p.ldc + n];
             }
 
@@ -305,7 +310,7 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
         }
     }
 
-    if (nsplit == 1) {
+    if (direct) {
 #pragma unroll
         for (int pass = 0; pass < P; ++pass)
 #pragma unroll

@@ -102,6 +102,32 @@ def test_sgemm_configs_c1_c2(lib, orc, dev, M, N, K):
     assert (d <= 2 * u.fp32_tol(K, scale)).all(), "far from the reference-path oracle"
 
 
+# Wide N with G / T == 1 and a remainder: column tiles of one and of two
+# k-splits in one launch, summed by the reduce kernel that follows.
+@pytest.mark.parametrize("kind,M,N,K", [("f32", 1, 33000, 512), ("f32", 3, 36988, 512), ("f32", 8, 34994, 300),
+                                        ("bf16", 1, 66000, 300), ("bf16", 8, 67999, 300)])
+def test_skinny_tiles_of_one_and_two_splits(lib, orc, dev, kind, M, N, K):
+    p = lib.plan_sgemm(M, N, K) if kind == "f32" else lib.plan_bf16(M, N, K)
+    T = -(-N // (256 if kind == "f32" else 512))
+    assert p["name"] == "dnnopt_skinny" and p["grid_x"] > T and p["grid_x"] % T and p["grid_x"] // T == 1, p
+    A = u.normal(orc, M * K, 1).reshape(M, K)
+    B = u.normal(orc, K * N, 2, 0, 0.02).reshape(K, N)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    if kind == "bf16":
+        A, B = u.bf16_bits(orc, A), u.bf16_bits(orc, B)
+        dA, dB, Av, Bv = dev_copy(A.view(np.int16), dev), dev_copy(B.view(np.int16), dev), u.bf16_value(A), u.bf16_value(B)
+    else:
+        dA, dB, Av, Bv = dev_copy(A, dev), dev_copy(B, dev), A, B
+    for alpha, beta in ((1.0, 1.0), (-0.5, 0.0)):
+        dC = dev_copy(C0 if beta else np.full_like(C0, np.nan), dev)
+        if kind == "bf16":
+            lib.gemm_bf16(M, N, K, alpha, dA, K, dB, N, beta, dC, N, stream=stream())
+        else:
+            lib.sgemm(M, N, K, alpha, dA, K, dB, N, beta, dC, N, stream=stream())
+        want, scale = u.exact(Av, Bv, alpha, beta, C0 if beta else None)
+        u.assert_fp32_close(host(dC), want, scale, K, f"{kind} {M}x{N}x{K} a={alpha} b={beta}")
+
+
 def test_sgemm_deterministic(lib, orc, dev):
     M, N, K = 7, 4099, 2048
     A, B = u.normal(orc, M * K, 1, 0, 0.02), u.normal(orc, K * N, 2, 0, 0.02)
