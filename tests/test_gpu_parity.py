@@ -973,3 +973,47 @@ def test_int8_dynamic_quant_sweep(lib, orc, dev, M, N, K, pa, pb, alpha, beta):
     got = host(dC)
     assert np.array_equal(got[:, :N].view(np.uint32), Co[:, :N].view(np.uint32)), (M, N, K)
     assert np.array_equal(got[:, N:], C0[:, N:]), "wrote outside the C block"
+
+
+def _wide_sweep_cases():
+    """Seeded wide-N, short-K shapes for the streaming kernels (skinny, row-dot,
+    int8 row-dot): many column tiles, so the k-split counts per tile vary."""
+    rng = np.random.default_rng(20261206)
+    cases = []
+    while len(cases) < 12:
+        kind = ("f32", "f32t", "bf16", "s8")[len(cases) % 4]
+        M = int(rng.integers(1, 9 if kind != "f32t" and kind != "s8" else 5))
+        N = int(rng.integers(12000, 160000))
+        K = int(rng.integers(1, 700))
+        if M * N * K > 200_000_000:
+            continue
+        cases.append((kind, M, N, K))
+    return cases
+
+
+@pytest.mark.parametrize("kind,M,N,K", _wide_sweep_cases())
+def test_wide_n_sweep(lib, orc, dev, kind, M, N, K):
+    if kind == "s8":
+        A = u.ints8(orc, M * K, 1, -128, 127).reshape(M, K)
+        B = u.ints8(orc, N * K, 2, -128, 127).reshape(N, K)
+        dC = torch.full((M, N), 3, dtype=torch.int32, device=dev)
+        lib.gemm_s8s8s32(M, N, K, dev_copy(A, dev), K, dev_copy(B, dev), K, dC, N, stream=stream())
+        want = (A.astype(np.float64) @ B.astype(np.float64).T).astype(np.int64)
+        assert np.array_equal(host(dC).astype(np.int64), want)
+        return
+    A = u.normal(orc, M * K, 1).reshape(M, K)
+    Bkn = u.normal(orc, K * N, 2, 0, 0.02).reshape(K, N)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    dC = dev_copy(C0, dev)
+    if kind == "bf16":
+        Ab, Bb = u.bf16_bits(orc, A), u.bf16_bits(orc, Bkn)
+        lib.gemm_bf16(M, N, K, 0.5, dev_copy(Ab.view(np.int16), dev), K, dev_copy(Bb.view(np.int16), dev), N, 1.0,
+                      dC, N, stream=stream())
+        A, Bkn = u.bf16_value(Ab), u.bf16_value(Bb)
+    elif kind == "f32t":
+        lib.sgemm(M, N, K, 0.5, dev_copy(A, dev), K, dev_copy(np.ascontiguousarray(Bkn.T), dev), K, 1.0, dC, N,
+                  transB=1, stream=stream())
+    else:
+        lib.sgemm(M, N, K, 0.5, dev_copy(A, dev), K, dev_copy(Bkn, dev), N, 1.0, dC, N, stream=stream())
+    want, scale = u.exact(A, Bkn, 0.5, 1.0, C0)
+    u.assert_fp32_close(host(dC), want, scale, K, f"wide {kind} {M}x{N}x{K}")
