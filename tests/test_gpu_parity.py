@@ -210,6 +210,36 @@ def test_sgemm_tall_large_c_stride(lib, orc, dev):
     torch.cuda.empty_cache()
 
 
+# B beyond 2 GiB (3.3 GB): every kernel addresses its operands with 32-bit
+# offsets from per-workgroup bases, so the planners shorten the k-range per
+# workgroup (skinny, MFMA tiles) or keep the row range small (B stored N x K).
+# Data comes from the device generator; checked on 96 columns against fp64.
+@pytest.mark.parametrize("kind,M,tb", [("f32", 2, 0), ("f32", 12, 0), ("f32", 6, 1), ("f32", 40, 0),
+                                       ("bf16", 4, 0), ("bf16", 32, 0)])
+def test_operands_beyond_2gib(lib, dev, kind, M, tb):
+    N, K = (16384 if kind == "bf16" else 8192), 100000
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234 + M)
+    A = torch.randn(M, K, device=dev, generator=g)
+    B = torch.randn(N, K, device=dev, generator=g) if tb else torch.randn(K, N, device=dev, generator=g)
+    if kind == "bf16":
+        A, B = A.to(torch.bfloat16), B.to(torch.bfloat16)
+    assert B.numel() * B.element_size() > 2 ** 31 + 2 ** 30
+    dC = torch.full((M, N), float("nan"), dtype=torch.float32, device=dev)
+    if kind == "bf16":
+        lib.gemm_bf16(M, N, K, 1.0, A, K, B, N, 0.0, dC, N, stream=stream())
+    else:
+        lib.sgemm(M, N, K, 1.0, A, K, B, K if tb else N, 0.0, dC, N, transB=tb, stream=stream())
+    cols = torch.randperm(N, generator=torch.Generator().manual_seed(7))[:96].to(dev)
+    Bc = (B[cols, :].T if tb else B[:, cols]).double()
+    want = (A.double() @ Bc).cpu().numpy()
+    scale = (A.double().abs() @ Bc.abs()).cpu().numpy()
+    got = host(dC[:, cols].contiguous())
+    del A, B, Bc, dC
+    torch.cuda.empty_cache()
+    u.assert_fp32_close(got, want, scale, K, f"{kind} {M}x{N}x{K} tb={tb}, B beyond 2 GiB")
+
+
 # k-major outer-product kernel (A stored K x M, B stored K x N, 32 < M, N <= 64,
 # K >= 32768, row strides multiples of 4): K not a multiple of 4, ragged M and
 # N, padded strides whose padding holds NaN (it may only reach outputs outside
