@@ -222,7 +222,9 @@ def kernel_key(lib, case):
     elif case.kind in ("bf16", "f2b"):
         p = lib.plan_bf16(case.M, case.N, case.K, fp32_inputs=int(case.kind == "f2b"))
     elif case.kind == "i8f":
-        p = lib.plan_s8(case.M, case.N, case.K, with_scale=1)
+        p = lib.plan_int8_f32(case.M, case.N, case.K)
+        if p["name"] == "dnnopt_skinny_q8":
+            return f"dnnopt_skinny_q8<{case.M}>", p
     else:
         p = lib.plan_s8(case.M, case.N, case.K, with_scale=int(case.kind == "s8s"))
     if p["name"] == "dnnopt_skinny":

@@ -5,6 +5,7 @@
 // kernel.  Nothing here falls back to the host: a failure is a status code.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdio.h>
 
 #include "dnnopt_hip.h"
 #include "host.h"
@@ -260,6 +261,23 @@ int dnnopt_hip_plan_gemm_s8(int with_scale, int M, int N, int K, dnnopt_plan* ou
     return st;
 }
 
+int dnnopt_hip_plan_gemm_int8_f32(int M, int N, int K, dnnopt_plan* out) {
+    if (!out || !dims_ok(M, N, K)) return DNNOPT_ERR_INVALID_ARG;
+    Launch L;
+    if (M <= 8 && plan_skinny(kSkinnyF32, M, N, K, N, &L) == DNNOPT_OK) {
+        // dnnopt_skinny_q8 runs on the fp32 skinny plan's grid and partials.
+        *out = L.pub;
+        out->kernel = DNNOPT_K_SKINNY_Q8;
+        out->block = skinny_q8_waves() * 64;
+        snprintf(out->name, sizeof out->name, "%s", "dnnopt_skinny_q8");
+        return DNNOPT_OK;
+    }
+    const int ldq = (K + 15) & ~15;
+    int st = plan_s8(1, M, N, K, &L, true, ldq, ldq, N);
+    if (st == DNNOPT_OK) *out = L.pub;
+    return st;
+}
+
 int dnnopt_hip_sgemm(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
                      const float* B, int ldb, float beta, float* C, int ldc, void* stream) {
     return sgemm_bias(transA, transB, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, nullptr, as_stream(stream));
@@ -425,9 +443,55 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
     if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
     if (lda < K || ldb < N || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
-    if (N > 0x7FFFFFFF / 2 || (long long)N * ((K + 15) & ~15) > 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
     hipStream_t s = as_stream(stream);
     StreamLock lock(s);
+    if (M <= 8) {
+        // Two passes over the fp32 B: the maxima, then dnnopt_skinny_q8, which
+        // quantizes B as it streams it (plus its reduce kernel when k is split
+        // over workgroups).  Staging (slot 1): [absmax partials][max|A|, max|B|].
+        Launch L;
+        if (plan_skinny(kSkinnyF32, M, N, K, ldb, &L) == DNNOPT_OK) {
+            int ga = 1, gb = 1;
+            absmax_blocks(M, N, K, &ga, &gb);
+            const size_t part_bytes = ((size_t)(ga + gb) * 4 + 255) & ~(size_t)255;
+            void* stage = nullptr;
+            unsigned* unused = nullptr;
+            int st = get_workspace(s, part_bytes + 256, &stage, &unused, kSlotQuant);
+            if (st != DNNOPT_OK) return st;
+            SkinnyQ8Args a{};
+            a.A = A;
+            a.B = B;
+            a.C = C;
+            unsigned* qpart = static_cast<unsigned*>(stage);
+            a.qpart = qpart;
+            a.amax = reinterpret_cast<unsigned*>(static_cast<char*>(stage) + part_bytes);
+            a.lda = lda;
+            a.ldb = ldb;
+            a.ldc = ldc;
+            a.M = M;
+            a.N = N;
+            a.K = K;
+            a.ga = ga;
+            a.gb = gb;
+            a.alpha = alpha;
+            a.beta = beta;
+            a.tiles = L.tiles;
+            a.splits = ((int)L.grid.x + L.tiles - 1) / L.tiles;
+            a.ncols_pad = L.tiles * skinny_tile_cols(kSkinnyF32);
+            a.defer = (int)L.grid.x > L.tiles ? 1 : 0;
+            if (a.defer) {
+                void* part = nullptr;
+                unsigned* tickets = nullptr;
+                st = get_workspace(s, L.part_bytes, &part, &tickets);
+                if (st != DNNOPT_OK) return st;
+                a.part = static_cast<int32_t*>(part);
+            }
+            st = finish_launch(launch_absmax(A, lda, B, ldb, M, N, K, qpart, s));
+            if (st != DNNOPT_OK) return st;
+            return finish_launch(launch_skinny_q8(M, L.grid, a, s));
+        }
+    }
+    if (N > 0x7FFFFFFF / 2 || (long long)N * ((K + 15) & ~15) > 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
     // Staging (slot 1): [qA M x ldq][qB N x ldq][absmax partials][max|A|, max|B|];
     // ldq pads K to 16 bytes so every quantized row is 16-byte aligned.
     // Three launches: maxima, quantization, and the int8 GEMM whose epilogue

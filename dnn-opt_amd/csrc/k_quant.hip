@@ -189,19 +189,30 @@ void absmax_blocks(int M, int N, int K, int* ga, int* gb) {
     *gb = (int)y;
 }
 
+// 16-byte loads when every row of both operands starts on a 16-byte boundary.
+static bool quant_vec(const float* A, int lda, const float* B, int ldb) {
+    return ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15u) == 0 && (lda & 3) == 0 &&
+           (ldb & 3) == 0;
+}
+
+hipError_t launch_absmax(const float* A, int lda, const float* B, int ldb, int M, int N, int K, unsigned* part,
+                         hipStream_t s) {
+    int ga = 1, gb = 1;
+    absmax_blocks(M, N, K, &ga, &gb);
+    if (quant_vec(A, lda, B, ldb))
+        hipLaunchKernelGGL(dnnopt_absmax_part<1>, dim3(ga + gb), dim3(256), 0, s, A, M, K, lda, ga, B, N, ldb, part);
+    else
+        hipLaunchKernelGGL(dnnopt_absmax_part<0>, dim3(ga + gb), dim3(256), 0, s, A, M, K, lda, ga, B, N, ldb, part);
+    return hipGetLastError();
+}
+
 hipError_t launch_quant_pair(const float* A, int lda, const float* B, int ldb, int M, int N, int K, int ldq,
                              unsigned* part, unsigned* amax, int8_t* qA, int8_t* qB, hipStream_t s) {
     if (ldq % 16 != 0) return hipErrorInvalidValue;
     int ga = 1, gb = 1;
     absmax_blocks(M, N, K, &ga, &gb);
-    // 16-byte loads when every row of both operands starts on a 16-byte boundary.
-    const bool vec = ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15u) == 0 &&
-                     (lda & 3) == 0 && (ldb & 3) == 0;
-    if (vec)
-        hipLaunchKernelGGL(dnnopt_absmax_part<1>, dim3(ga + gb), dim3(256), 0, s, A, M, K, lda, ga, B, N, ldb, part);
-    else
-        hipLaunchKernelGGL(dnnopt_absmax_part<0>, dim3(ga + gb), dim3(256), 0, s, A, M, K, lda, ga, B, N, ldb, part);
-    hipError_t e = hipGetLastError();
+    const bool vec = quant_vec(A, lda, B, ldb);
+    hipError_t e = launch_absmax(A, lda, B, ldb, M, N, K, part, s);
     if (e != hipSuccess) return e;
     const int qa = M < 256 ? M : 256;
     if (ga + gb > 1024) return hipErrorInvalidValue;  // one wave reduces the maxima

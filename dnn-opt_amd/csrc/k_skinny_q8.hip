@@ -1,0 +1,240 @@
+// k_skinny_q8.hip -- fp32-API gemm_int8 for M <= 8 in one pass over B (gfx950).
+//
+// The reference's fp32 gemm_int8 (src/gemm/gemm.cpp:418-455) quantizes A and
+// B per tensor (scales from the maxima, src/gemm/gemm_driver_generic.cpp:
+// 49-67; rounding, src/gemm/gemm_pack_int8.cpp:29-71) and sums exact int32
+// products.  With at most 8 rows of A the product is a stream over B, so this
+// kernel reads the fp32 B (K x N, row-major) once, after the maxima pass
+// (dnnopt_absmax_part), quantizes every element as it arrives, quantizes A's
+// values where the lanes use them, and accumulates exact int32 products: no
+// int8 copy of B is written or read.
+//
+// Lane layout and k-split follow dnnopt_skinny: a wave covers 256 columns (16
+// bytes of a row per lane), the 8 waves of a workgroup and the workgroups of
+// a column tile take contiguous k-ranges, waves are combined through LDS and
+// workgroups through int32 partial sums that dnnopt_skinny_q8_reduce adds up.
+// Integer sums are exact, so the order of the combine does not matter.  The
+// output is the int8 kernels' dequantizing epilogue (s8_out): C = (sA sB
+// alpha) acc, or fma(that, acc, beta C).
+#include "device_common.h"
+#include "kernels.h"
+
+using namespace dnnopt_dev;
+
+namespace dnnopt_hip {
+
+namespace {
+
+constexpr int kQ8Waves = 8;
+constexpr int kQ8Unroll = 16;  // rows of B in flight per wave
+constexpr int kQ8Cols = 256;   // columns per wave (4 per lane)
+
+// Four values in [-128, 127] as the bytes of one dword, the first in the low
+// byte (the operand layout of v_dot4_i32_i8).
+__device__ __forceinline__ uint32_t pack_q4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xFF) | (uint32_t)(b & 0xFF) << 8 | (uint32_t)(c & 0xFF) << 16 | (uint32_t)d << 24;
+}
+
+// B is read exactly once: streaming loads.
+__device__ __forceinline__ u32x4 load_row(__amdgpu_buffer_rsrc_t r, uint32_t off) { return buf_load_x4_stream(r, off); }
+
+
+}  // namespace
+
+template <int MR>
+__global__ __launch_bounds__(kQ8Waves * 64) void dnnopt_skinny_q8(SkinnyQ8Args p) {
+    constexpr int NW = kQ8Waves, U = kQ8Unroll, TW = kQ8Cols;
+    // LDS combine of the waves in passes of G rows (G * 8 KB).
+    constexpr int G = MR < 4 ? MR : 4;
+    constexpr int P = (MR + G - 1) / G;
+    __shared__ i32x4 red[NW * G * (TW / 4)];
+    // A's values of a block, quantized by the wave's lanes (lane l takes
+    // entries l, l + 64, ...: row e / U, k e % U) into bytes, read back as
+    // broadcasts of 16 k per row.
+    constexpr int QA = MR * U;
+    constexpr int QL = (QA + 63) / 64;
+    static_assert(U == 16, "one 16-byte broadcast per row of A per block");
+    __shared__ u32x4 qa_lds[NW][MR];
+
+    const int lane = lane_id(), w = wave_id();
+    const SplitPos sp = split_pos((int)blockIdx.x, (int)gridDim.x, p.tiles);
+    const int col0 = sp.tile * TW;
+    // With a reduce kernel to follow every tile publishes partial sums, also
+    // a tile of one k-split (the reduce kernel covers every column of C).
+    const bool direct = !p.defer;
+    const long long nblk = (p.K + U - 1) / U;
+    const long long chunks = (long long)sp.nsplit * NW;
+    const long long cw = (long long)sp.split * NW + w;
+    const int k_lo = (int)((nblk * cw) / chunks) * U;
+    const int k_hi = min(p.K, (int)((nblk * (cw + 1)) / chunks) * U);
+    const int kb = (int)((nblk * ((long long)sp.split * NW)) / chunks) * U;
+
+    // Buffer range from row kb, column col0 to the last element of B; lanes
+    // whose four columns all lie past N read nothing.  Columns past N inside
+    // a lane's group read the next row's values, which are never stored.
+    const float* bbase = p.B + (size_t)kb * p.ldb + col0;
+    const __amdgpu_buffer_rsrc_t rs =
+        make_rsrc(bbase, range31(((size_t)(p.K - 1 - kb) * p.ldb + (size_t)(p.N - col0)) * 4));
+    const uint32_t rowbytes = (uint32_t)p.ldb * 4u;
+    const uint32_t lane_off = col0 + lane * 4 < p.N ? (uint32_t)lane * 16u : kOobOffset;
+
+    // A: the range ends at the last element of row M - 1; lanes past the
+    // block's MR x U entries read nothing.
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, range31(((size_t)(p.M - 1) * p.lda + p.K) * 4));
+    uint32_t a_lane[QL];
+#pragma unroll
+    for (int j = 0; j < QL; ++j) {
+        const int e = lane + 64 * j;
+        a_lane[j] = e < QA ? (uint32_t)((e / U) * p.lda + e % U) * 4u : kOobOffset;
+    }
+    auto load_block = [&](u32x4 (&raw)[U], float (&av)[QL], int k0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) raw[u] = load_row(rs, (uint32_t)(k0 + u - kb) * rowbytes + lane_off);
+#pragma unroll
+        for (int j = 0; j < QL; ++j)
+            av[j] = as_f32(buf_load_x1(ra, a_lane[j] == kOobOffset ? kOobOffset : a_lane[j] + (uint32_t)k0 * 4u));
+    };
+
+    // The first block goes out before the maxima are read.
+    u32x4 raw[U];
+    float av[QL];
+    int k = k_lo;
+    if (k + U <= k_hi) load_block(raw, av, k);
+    unsigned ma, mb;
+    wave_maxima(p.qpart, p.ga, p.gb, &ma, &mb);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        p.amax[0] = ma;
+        p.amax[1] = mb;
+    }
+    const float inv_a = 1.0f / quant_scale_bits(ma), inv_b = 1.0f / quant_scale_bits(mb);
+
+    int acc[MR][4];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[m][e] = 0;
+
+    // Whole blocks: per 4 rows of B a lane packs each of its columns' 4
+    // quantized k into one dword and adds 4 products per v_dot4_i32_i8
+    // against the packed A bytes of the same 4 k.
+    int8_t* const qw = reinterpret_cast<int8_t*>(qa_lds[w]);
+    while (k + U <= k_hi) {
+#pragma unroll
+        for (int j = 0; j < QL; ++j)
+            if (lane + 64 * j < QA) qw[lane + 64 * j] = (int8_t)quant_s8(av[j], inv_a);
+        u32x4 a16[MR];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) a16[m] = qa_lds[w][m];
+#pragma unroll
+        for (int q = 0; q < U / 4; ++q) {
+            uint32_t b4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                b4[e] = pack_q4(quant_s8(as_f32(raw[4 * q][e]), inv_b), quant_s8(as_f32(raw[4 * q + 1][e]), inv_b),
+                                quant_s8(as_f32(raw[4 * q + 2][e]), inv_b), quant_s8(as_f32(raw[4 * q + 3][e]), inv_b));
+#pragma unroll
+            for (int m = 0; m < MR; ++m)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[m][e] = __builtin_amdgcn_sdot4((int)a16[m][q], (int)b4[e], acc[m][e], false);
+        }
+        k += U;
+        if (k + U <= k_hi) load_block(raw, av, k);
+    }
+    // The last k % 16 rows of the range, one at a time.
+    for (; k < k_hi; ++k) {
+        const u32x4 v = load_row(rs, (uint32_t)(k - kb) * rowbytes + lane_off);
+        int qb[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qb[e] = quant_s8(as_f32(v[e]), inv_b);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            const int qa = quant_s8(p.A[(size_t)m * p.lda + k], inv_a);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[m][e] += qa * qb[e];
+        }
+    }
+
+    // Combine the waves: thread t owns 4-column group t % 64 of row t / 64
+    // within a pass of G rows.
+    const float dq = mul_rn(mul_rn(quant_scale_bits(ma), quant_scale_bits(mb)), p.alpha);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part, range31((size_t)p.splits * MR * p.ncols_pad * 4));
+#pragma unroll
+    for (int pass = 0; pass < P; ++pass) {
+        if (pass) __syncthreads();
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int m = pass * G + g;
+            if (m < MR) red[(w * G + g) * (TW / 4) + lane] = i32x4{acc[m][0], acc[m][1], acc[m][2], acc[m][3]};
+        }
+        __syncthreads();
+        const int t = (int)threadIdx.x;
+        const int g = t / (TW / 4), c4 = t % (TW / 4);
+        const int m = pass * G + g;
+        if (t < G * (TW / 4) && m < MR) {
+            i32x4 s = red[g * (TW / 4) + c4];
+#pragma unroll
+            for (int w2 = 1; w2 < NW; ++w2) s += red[(w2 * G + g) * (TW / 4) + c4];
+            const int n = col0 + 4 * c4;
+            if (direct) {
+                float* c = p.C + (size_t)m * p.ldc + n;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (n + e < p.N)
+                        c[e] = p.beta == 0.0f ? mul_rn(dq, (float)s[e]) : __builtin_fmaf(dq, (float)s[e], mul_rn(p.beta, c[e]));
+            } else {
+                const uint32_t off = (uint32_t)((((size_t)sp.split * MR + m) * p.ncols_pad + n) * 4);
+                buf_store_x4_coherent(rp, off, __builtin_bit_cast(f32x4, s));
+            }
+        }
+    }
+}
+
+// Sum the int32 partials [split][M][ncols_pad] of a tile's splits (exact) and
+// store the dequantized C.
+__global__ __launch_bounds__(256) void dnnopt_skinny_q8_reduce(const int32_t* __restrict__ part, int G, int T, int M,
+                                                              int N, int ncols_pad, const unsigned* amax, float alpha,
+                                                              float beta, float* C, int ldc) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int m = blockIdx.y;
+    if (n >= N) return;
+    const int splits = splits_of_tile(n / kQ8Cols, G, T);
+    const size_t stride = (size_t)M * ncols_pad;
+    const int32_t* src = part + (size_t)m * ncols_pad + n;
+    int32_t s = 0;
+    int sp = 0;
+    for (; sp + 8 <= splits; sp += 8) {
+        int32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(sp + u) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; sp < splits; ++sp) s += src[(size_t)sp * stride];
+    float* c = C + (size_t)m * ldc + n;
+    *c = s8_out(s, n, nullptr, amax, dyn_dequant_scale(amax, alpha), beta, c);
+}
+
+hipError_t launch_skinny_q8(int mr, dim3 grid, const SkinnyQ8Args& a, hipStream_t s) {
+    const dim3 blk(kQ8Waves * 64);
+    switch (mr) {
+        case 1: hipLaunchKernelGGL(dnnopt_skinny_q8<1>, grid, blk, 0, s, a); break;
+        case 2: hipLaunchKernelGGL(dnnopt_skinny_q8<2>, grid, blk, 0, s, a); break;
+        case 3: hipLaunchKernelGGL(dnnopt_skinny_q8<3>, grid, blk, 0, s, a); break;
+        case 4: hipLaunchKernelGGL(dnnopt_skinny_q8<4>, grid, blk, 0, s, a); break;
+        case 5: hipLaunchKernelGGL(dnnopt_skinny_q8<5>, grid, blk, 0, s, a); break;
+        case 6: hipLaunchKernelGGL(dnnopt_skinny_q8<6>, grid, blk, 0, s, a); break;
+        case 7: hipLaunchKernelGGL(dnnopt_skinny_q8<7>, grid, blk, 0, s, a); break;
+        case 8: hipLaunchKernelGGL(dnnopt_skinny_q8<8>, grid, blk, 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    if (!a.defer) return hipGetLastError();
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(dnnopt_skinny_q8_reduce, dim3((a.N + 255) / 256, a.M), dim3(256), 0, s, a.part,
+                       (int)grid.x, a.tiles, a.M, a.N, a.ncols_pad, a.amax, a.alpha, a.beta, a.C, a.ldc);
+    return hipGetLastError();
+}
+
+int skinny_q8_waves() { return kQ8Waves; }
+
+}  // namespace dnnopt_hip

@@ -253,6 +253,32 @@ hipError_t launch_fill(void* dst, size_t n, int dtype, int dist, uint64_t seed,
 void absmax_blocks(int M, int N, int K, int* ga, int* gb);
 hipError_t launch_quant_pair(const float* A, int lda, const float* B, int ldb, int M, int N, int K, int ldq,
                              unsigned* part, unsigned* amax, int8_t* qA, int8_t* qB, hipStream_t s);
+// fp32-API gemm_int8 for M <= 8 in one pass over the fp32 B (K x N): the
+// elements are quantized as they are read, with the scales taken from the
+// maxima partials qpart[0, ga) (A) and qpart[ga, ga + gb) (B) of
+// dnnopt_absmax_part; exact int32 sums, dequantized into C.  The grid and the
+// partial buffer are those of the fp32 skinny plan (256 columns per wave);
+// defer = 1 (more workgroups than column tiles): every workgroup stores int32
+// partials [split][M][ncols_pad] and a reduce kernel, launched by
+// launch_skinny_q8, sums them.  amax[0..1] receive max|A|, max|B| bits.
+struct SkinnyQ8Args {
+    const float* A;
+    const float* B;
+    float* C;
+    int32_t* part;
+    const unsigned* qpart;
+    unsigned* amax;
+    int lda, ldb, ldc;
+    int M, N, K;
+    int ga, gb;
+    float alpha, beta;
+    int tiles, splits, ncols_pad, defer;
+};
+hipError_t launch_skinny_q8(int mr, dim3 grid, const SkinnyQ8Args& a, hipStream_t s);
+int skinny_q8_waves();  // waves per workgroup of dnnopt_skinny_q8 (256 columns each)
+// Maxima partials only (the first launch of the fp32-API int8 pipeline).
+hipError_t launch_absmax(const float* A, int lda, const float* B, int ldb, int M, int N, int K, unsigned* part,
+                         hipStream_t s);
 // Reduce skinny partials [split][M][ncols_pad] into C (epilogue applied);
 // tile t (of T, tile width tw) has splits_of_tile(t, G, T) partials.
 hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, int N, int ncols_pad,

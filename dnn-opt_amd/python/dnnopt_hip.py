@@ -35,7 +35,7 @@ OK, ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_OUT_OF_MEMORY,
 NOALLOC_SCRATCH_BYTES = 16 << 20  # DNNOPT_NOALLOC_SCRATCH_BYTES
 
 (K_NONE, K_SKINNY_F32, K_SKINNY_BF16, K_SKINNY_F2B, K_MFMA_S8, K_TILE_F32, K_TILE_BF16, K_NAIVE_F32, K_ROWDOT_F32,
- K_ROWDOT_BF16, K_TALL_F32, K_ROWDOT_S8) = range(12)
+ K_ROWDOT_BF16, K_TALL_F32, K_ROWDOT_S8, K_SKINNY_Q8) = range(13)
 
 # DNNOPT_HIP_ABI_VERSION of include/dnnopt_hip.h that these bindings follow.
 ABI_VERSION = 3
@@ -96,6 +96,7 @@ C_ABI = {
     "dnnopt_hip_plan_gemm_bf16": (_I, [_I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_plan_gemm_bf16_ex": (_I, [_I, _I, _I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_plan_gemm_s8": (_I, [_I, _I, _I, _I, POINTER(Plan)]),
+    "dnnopt_hip_plan_gemm_int8_f32": (_I, [_I, _I, _I, POINTER(Plan)]),
     "dnnopt_hip_fill": (_I, [_P, c_size_t, _I, _I, c_uint64, c_uint32, c_double, c_double, _P]),
     "dnnopt_hip_status_string": (ctypes.c_char_p, [_I]),
     "dnnopt_hip_last_status": (_I, []),
@@ -236,6 +237,11 @@ class Lib:
     def plan_s8(self, M, N, K, with_scale=0) -> dict:
         p = Plan()
         self._check(self.so.dnnopt_hip_plan_gemm_s8(with_scale, M, N, K, ctypes.byref(p)), "plan_s8")
+        return p.as_dict()
+
+    def plan_int8_f32(self, M, N, K) -> dict:
+        p = Plan()
+        self._check(self.so.dnnopt_hip_plan_gemm_int8_f32(M, N, K, ctypes.byref(p)), "plan_int8_f32")
         return p.as_dict()
 
     # ---------------------------------------------------------------- C-ABI (device pointers)

@@ -210,6 +210,8 @@ int dnnopt_onednn_gemm_bf16bf16f32(const char* transa, const char* transb,
 #define DNNOPT_K_ROWDOT_BF16 9  /* M <= 8, bf16 B stored N x K, rows once   */
 #define DNNOPT_K_TALL_F32   10  /* large M, N <= 64, fp32 B resident in LDS  */
 #define DNNOPT_K_ROWDOT_S8  11  /* M <= 8, int8 B stored N x K, rows once   */
+#define DNNOPT_K_SKINNY_Q8  12  /* M <= 8, fp32-API int8: fp32 B quantized  */
+                                /* as it is streamed (no int8 copy of B)   */
 
 typedef struct dnnopt_plan {
     int kernel;             /* DNNOPT_K_* */
@@ -235,6 +237,11 @@ int dnnopt_hip_plan_gemm_bf16_ex(int transA, int transB, int M, int N, int K,
                                  dnnopt_plan* out);
 int dnnopt_hip_plan_gemm_s8(int with_scale, int M, int N, int K,
                             dnnopt_plan* out);
+/* The GEMM launch of dnnopt_hip_gemm_int8_f32 with unpadded strides: after
+ * its maxima pass, for M <= 8 the skinny kernel that quantizes B as it
+ * streams it (DNNOPT_K_SKINNY_Q8), else (after a quantization pass) the int8
+ * kernel that reads the quantized operands. */
+int dnnopt_hip_plan_gemm_int8_f32(int M, int N, int K, dnnopt_plan* out);
 
 /* ---- synthetic inputs on the device ------------------------------------
  * Counter-based SplitMix64: element i of tensor `tensor_id` under `seed`

@@ -116,6 +116,14 @@ def test_plans_for_the_configs(lib):
         assert lib.plan_s8(M, 4096, 4096)["kernel"] == b.K_ROWDOT_S8
     for M in (5, 9):
         assert lib.plan_s8(M, 4096, 4096)["kernel"] == b.K_MFMA_S8
+    # fp32-API int8: M <= 8 quantizes B as it streams it (fp32 skinny grid)
+    for M in (1, 8):
+        p = lib.plan_int8_f32(M, 4096, 4096)
+        assert p["kernel"] == b.K_SKINNY_Q8 and p["name"] == "dnnopt_skinny_q8" and p["rows"] == M, p
+        q = lib.plan_sgemm(M, 4096, 4096)
+        assert (p["grid_x"], p["splits"], p["workspace_bytes"]) == (q["grid_x"], q["splits"], q["workspace_bytes"])
+    assert lib.plan_int8_f32(9, 4096, 4096)["kernel"] == b.K_MFMA_S8
+    assert lib.plan_int8_f32(128, 4096, 4096)["name"] == "dnnopt_s8_dma"
 
 
 def test_plan_split_never_exceeds_k(lib):
