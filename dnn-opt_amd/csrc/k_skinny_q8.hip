@@ -190,7 +190,11 @@ __global__ __launch_bounds__(kQ8Waves * 64) void dnnopt_skinny_q8(SkinnyQ8Args p
 }
 
 // Sum the int32 partials [split][M][ncols_pad] of a tile's splits (exact) and
-// store the dequantized C.
+// store the dequantized C.  All partial loads of an output (a batch of SB,
+// the smallest of 8, 16, 32, 64 that holds the largest split count) are
+// issued before the first add -- offsets past the tile's splits are out of
+// range and read zero -- so the sum costs one memory round trip.
+template <int SB>
 __global__ __launch_bounds__(256) void dnnopt_skinny_q8_reduce(const int32_t* __restrict__ part, int G, int T, int M,
                                                               int N, int ncols_pad, const unsigned* amax, float alpha,
                                                               float beta, float* C, int ldc) {
@@ -198,20 +202,22 @@ __global__ __launch_bounds__(256) void dnnopt_skinny_q8_reduce(const int32_t* __
     const int m = blockIdx.y;
     if (n >= N) return;
     const int splits = splits_of_tile(n / kQ8Cols, G, T);
-    const size_t stride = (size_t)M * ncols_pad;
-    const int32_t* src = part + (size_t)m * ncols_pad + n;
-    int32_t s = 0;
-    int sp = 0;
-    for (; sp + 8 <= splits; sp += 8) {
-        int32_t v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(sp + u) * stride];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) s += v[u];
-    }
-    for (; sp < splits; ++sp) s += src[(size_t)sp * stride];
+    const int max_splits = G / T + (G % T ? 1 : 0);
+    const uint32_t stride = (uint32_t)M * (uint32_t)ncols_pad * 4u;
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, range31((size_t)max_splits * M * ncols_pad * 4));
+    const uint32_t base = ((uint32_t)m * (uint32_t)ncols_pad + (uint32_t)n) * 4u;
     float* c = C + (size_t)m * ldc + n;
-    *c = s8_out(s, n, nullptr, amax, dyn_dequant_scale(amax, alpha), beta, c);
+    const float c_old = beta != 0.0f ? *c : 0.0f;
+    int32_t s = 0;
+    for (int sp0 = 0; sp0 < splits; sp0 += SB) {
+        uint32_t v[SB];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) v[u] = buf_load_x1(rp, sp0 + u < splits ? base + (uint32_t)(sp0 + u) * stride : kOobOffset);
+#pragma unroll
+        for (int u = 0; u < SB; ++u) s += (int32_t)v[u];  // out-of-range loads read 0
+    }
+    const float dq = dyn_dequant_scale(amax, alpha);
+    *c = beta == 0.0f ? mul_rn(dq, (float)s) : __builtin_fmaf(dq, (float)s, mul_rn(beta, c_old));
 }
 
 hipError_t launch_skinny_q8(int mr, dim3 grid, const SkinnyQ8Args& a, hipStream_t s) {
@@ -230,8 +236,16 @@ hipError_t launch_skinny_q8(int mr, dim3 grid, const SkinnyQ8Args& a, hipStream_
     if (!a.defer) return hipGetLastError();
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(dnnopt_skinny_q8_reduce, dim3((a.N + 255) / 256, a.M), dim3(256), 0, s, a.part,
-                       (int)grid.x, a.tiles, a.M, a.N, a.ncols_pad, a.amax, a.alpha, a.beta, a.C, a.ldc);
+    const dim3 rg((a.N + 255) / 256, a.M);
+    const int G = (int)grid.x, T = a.tiles, ms = G / T + (G % T ? 1 : 0);
+#define DNNOPT_Q8_REDUCE(SB)                                                                                   \
+    hipLaunchKernelGGL(dnnopt_skinny_q8_reduce<SB>, rg, dim3(256), 0, s, a.part, G, T, a.M, a.N, a.ncols_pad, \
+                       a.amax, a.alpha, a.beta, a.C, a.ldc)
+    if (ms <= 8) DNNOPT_Q8_REDUCE(8);
+    else if (ms <= 16) DNNOPT_Q8_REDUCE(16);
+    else if (ms <= 32) DNNOPT_Q8_REDUCE(32);
+    else DNNOPT_Q8_REDUCE(64);
+#undef DNNOPT_Q8_REDUCE
     return hipGetLastError();
 }
 
