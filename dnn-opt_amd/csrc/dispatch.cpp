@@ -254,6 +254,12 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         // 128 k per LDS block below M = 128 (fewer barriers, more bytes per
         // block in flight); measured on MI355X at N = 11008, K = 4096.
         cfg = M > 128 ? 13 : (M > 64 ? 23 : (M > 32 ? 21 : 19));
+        // B stored N x K (bf16 storage), M <= 32: 48-column tiles, more of
+        // them over the CUs (MI355X, us, 32 x 64 -> 32 x 48 / 16 x 48, N =
+        // 11008, K = 4096: M=32 25.8 -> 24.6, M=24 24.8 -> 23.6, M=16 23.9 ->
+        // 22.7 (16 x 48), M=8 21.2 -> 20.4 (16 x 48)).  A K x N B keeps the
+        // 64-column tiles (48 columns: 34 vs 26 us at M=32).
+        if (transB && mode == kTileBF16 && M <= 32) cfg = M <= 16 ? kTileBF16Tb48Few : kTileBF16Tb48;
         // bf16 storage above M = 128: the same 128 x 96 tile with the
         // operands copied into LDS by the memory unit (C4 M=256 43.1 vs 45.4
         // us; no gain measured at M = 32).  When 128-row tiles would take more
@@ -266,7 +272,8 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
             cfg = 26;
             if (ceil_div(M, 128) * ceil_div(N, 96) > num_cus()) cfg = 33;
         }
-        if (forced_cfg >= kTileFirstLds && forced_cfg < kTileF32Few &&
+        if (((forced_cfg >= kTileFirstLds && forced_cfg < kTileF32Few) || forced_cfg == kTileBF16Tb48 ||
+             forced_cfg == kTileBF16Tb48Few) &&
             (forced_cfg < kTileFirstDma || mode == kTileBF16))
             cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
@@ -350,7 +357,8 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     // for the LDS-DMA tiles (DNNOPT_TILE_TICKET=1): the last workgroup to
     // finish a tile adds the others' partials.
     static const bool dma_ticket = env_int("DNNOPT_TILE_TICKET", 0) == 1;
-    const bool ticket_ok = !lds || (dma_ticket && cfg >= kTileFirstDma);
+    const bool dma = cfg >= kTileFirstDma && cfg < kTileF32Few;  // LDS-DMA configurations
+    const bool ticket_ok = !lds || (dma_ticket && dma);
     L->defer_reduce =
         (s > 1 && (split_reduce_mode() || s > kTicketSplitLimit || tiles > kMaxTickets || !ticket_ok)) ? 1 : 0;
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(float) : 0;
@@ -358,7 +366,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     const int kernel = mode == kTileF32 ? DNNOPT_K_TILE_F32 : DNNOPT_K_TILE_BF16;
     fill_pub(L, kernel,
              mode == kTileF32 ? "dnnopt_tile_f32"
-                              : (cfg >= kTileFirstDma ? "dnnopt_tile_bf16_dma" : (lds ? "dnnopt_tile_bf16_lds" : "dnnopt_tile_bf16")),
+                              : (dma ? "dnnopt_tile_bf16_dma" : (lds ? "dnnopt_tile_bf16_lds" : "dnnopt_tile_bf16")),
              bm, bn, (int)s, waves_per_wg * 64);
     return DNNOPT_OK;
 }

@@ -1093,6 +1093,9 @@ static const TileConfig kTileConfigs[] = {
     // fp32 register tiles for few rows
     {1, 1, 1, 1, 8},          // 35: 16 x 16, k over the 8 waves of a workgroup
     {1, 4, 1, 2, 2},          // 36: 16 x 128, 2 column waves x 2 k-groups
+    // bf16 storage through LDS, B stored N x K, few rows
+    {2, 1, 1, 3, 1, 3, 128},  // 37: 32 x 48, 3 waves, 128 k per block, 3 ahead
+    {1, 1, 1, 3, 1, 3, 128},  // 38: 16 x 48, 3 waves, 128 k per block, 3 ahead
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -1177,6 +1180,8 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_DMA_CASE(34, 4, 4, 4, 2, 3, 64)
         DNNOPT_TILE_CASE(35, 1, 1, 1, 1, 8)
         DNNOPT_TILE_CASE(36, 1, 4, 1, 2, 2)
+        DNNOPT_TILE_LDS_CASE(37, 2, 1, 1, 3, 3, 128, 1)
+        DNNOPT_TILE_LDS_CASE(38, 1, 1, 1, 3, 3, 128, 1)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -418,6 +418,24 @@ def test_bf16_small_m_kn_tiles(lib, orc, dev, M, N, K, pa, pb, ta):
     u.assert_fp32_close(host(dC), want, scale, K, f"bf16 small-M K x N {M}x{N}x{K} ta={ta}")
 
 
+# bf16 storage, B stored N x K, M <= 32: 16 x 48 / 32 x 48 LDS-staged tiles;
+# ragged N (not a multiple of 48), K tails, padded even strides.
+@pytest.mark.parametrize("M,N,K,pa,pb", [(5, 1001, 300, 0, 2), (16, 4099, 130, 2, 0), (17, 11008, 4096, 0, 0),
+                                         (32, 97, 1000, 4, 4), (24, 48, 64, 0, 0), (9, 50, 520, 2, 2)])
+def test_bf16_tb_48_column_tiles(lib, orc, dev, M, N, K, pa, pb):
+    lda, ldb = K + pa, K + pb
+    p = lib.plan_bf16_ex(M, N, K, transB=1)
+    assert p["name"] == "dnnopt_tile_bf16_lds" and p["cols"] == 48 and p["rows"] == (16 if M <= 16 else 32), p
+    A = u.bf16_bits(orc, u.normal(orc, M * lda, 1)).reshape(M, lda)
+    B = u.bf16_bits(orc, u.normal(orc, N * ldb, 2, 0, 0.02)).reshape(N, ldb)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    want, scale = u.exact(u.bf16_value(A)[:, :K], np.ascontiguousarray(u.bf16_value(B)[:, :K].T), 0.5, 1.0, C0)
+    dC = dev_copy(C0, dev)
+    lib.gemm_bf16_ex(M, N, K, 0.5, dev_copy(A.view(np.int16), dev), lda, dev_copy(B.view(np.int16), dev), ldb, 1.0,
+                     dC, N, transB=1, stream=stream())
+    u.assert_fp32_close(host(dC), want, scale, K, f"bf16 TB 48-column tiles {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("tb", [0, 1])
 def test_bf16_dma_256_row_tiles(lib, orc, dev, tb):
     """bf16 storage with more 128-row tiles than CUs takes 256 x 96 tiles:
