@@ -5,9 +5,10 @@
 // 49-67; rounding, src/gemm/gemm_pack_int8.cpp:29-71) and sums exact int32
 // products.  With at most 8 rows of A the product is a stream over B, so this
 // kernel reads the fp32 B (K x N, row-major) once, after the maxima pass
-// (dnnopt_absmax_part), quantizes every element as it arrives, quantizes A's
-// values where the lanes use them, and accumulates exact int32 products: no
-// int8 copy of B is written or read.
+// (dnnopt_absmax_part), quantizes every element as it arrives (A's values of
+// each block are quantized by the wave's lanes into LDS bytes), and adds
+// exact int32 products with v_dot4_i32_i8: no int8 copy of B is written or
+// read.
 //
 // Lane layout and k-split follow dnnopt_skinny: a wave covers 256 columns (16
 // bytes of a row per lane), the 8 waves of a workgroup and the workgroups of
