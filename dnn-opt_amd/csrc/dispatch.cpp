@@ -260,6 +260,11 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         // 22.7 (16 x 48), M=8 21.2 -> 20.4 (16 x 48)).  A K x N B keeps the
         // 64-column tiles (48 columns: 34 vs 26 us at M=32).
         if (transB && mode == kTileBF16 && M <= 32) cfg = M <= 16 ? kTileBF16Tb48Few : kTileBF16Tb48;
+        // fp32 inputs rounded in registers, M > 64: 128 x 96 tiles with 128 k
+        // per block (MI355X, us, N = 11008, K = 4096: M = 72 / 96 / 128 / 256
+        // / 512 72.7 / 75.4 / 79.8 / 97.1 / 174.8 -> 67.1 / 69.3 / 73.6 / 84.5
+        // / 162.3; 1024 x 4096 x 4096 156.1 -> 144.6).
+        if (mode == kTileF2B && M > 64) cfg = 20;
         // bf16 storage above M = 128: the same 128 x 96 tile with the
         // operands copied into LDS by the memory unit (C4 M=256 43.1 vs 45.4
         // us; no gain measured at M = 32).  When 128-row tiles would take more
