@@ -225,6 +225,8 @@ def kernel_key(lib, case):
         p = lib.plan_int8_f32(case.M, case.N, case.K)
         if p["name"] == "dnnopt_skinny_q8":
             return f"dnnopt_skinny_q8<{case.M}>", p
+        if p["name"] == "dnnopt_s8_lds_q8b":
+            return "dnnopt_s8_lds<2, 1, 2, 2, 3, 1, 128, 1>", p
     else:
         p = lib.plan_s8(case.M, case.N, case.K, with_scale=int(case.kind == "s8s"))
     if p["name"] == "dnnopt_skinny":

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include "dnnopt_hip.h"
 #include "host.h"
@@ -272,7 +273,21 @@ int dnnopt_hip_plan_gemm_int8_f32(int M, int N, int K, dnnopt_plan* out) {
         snprintf(out->name, sizeof out->name, "%s", "dnnopt_skinny_q8");
         return DNNOPT_OK;
     }
+    // M > 8: the int8 tiles that quantize the fp32 B while staging it (as
+    // dnnopt_hip_gemm_int8_f32 with unpadded strides and DNNOPT_Q8B unset).
     const int ldq = (K + 15) & ~15;
+    if (((long long)K * N + N) * 4 < 0x7FFFFFFFll && ((long long)M + 64) * ldq < 0x7FFFFFFFll) {
+        *out = dnnopt_plan{};
+        out->kernel = DNNOPT_K_MFMA_S8;
+        out->rows = 64;
+        out->cols = 32;
+        out->splits = 1;
+        out->grid_x = xcd_grid((N + 31) / 32, (M + 63) / 64);
+        out->grid_y = out->grid_z = 1;
+        out->block = 256;
+        snprintf(out->name, sizeof out->name, "%s", "dnnopt_s8_lds_q8b");
+        return DNNOPT_OK;
+    }
     int st = plan_s8(1, M, N, K, &L, true, ldq, ldq, N);
     if (st == DNNOPT_OK) *out = L.pub;
     return st;
@@ -491,12 +506,57 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
             return finish_launch(launch_skinny_q8(M, L.grid, a, s));
         }
     }
+    static const bool q8b_ok = [] {
+        const char* e = getenv("DNNOPT_Q8B");
+        return !(e && *e && atoi(e) == 0);
+    }();
+    const int ldq = (K + 15) & ~15;
+    if (q8b_ok && ((long long)K * ldb + N) * 4 < 0x7FFFFFFFll && ((long long)M + 64) * ldq < 0x7FFFFFFFll) {
+        // Maxima, A quantized (M x ldq), then 64 x 32 int8 tiles that quantize
+        // the fp32 B while staging it: no int8 copy of B.  Staging (slot 1):
+        // [qA M x ldq][absmax partials][max|A|, max|B|].
+        int ga = 1, gb = 1;
+        absmax_blocks(M, N, K, &ga, &gb);
+        const size_t qa_bytes = ((size_t)M * ldq + 255) & ~(size_t)255;
+        const size_t part_bytes = ((size_t)(ga + gb) * 4 + 255) & ~(size_t)255;
+        void* stage = nullptr;
+        unsigned* unused = nullptr;
+        int st = get_workspace(s, qa_bytes + part_bytes + 256, &stage, &unused, kSlotQuant);
+        if (st != DNNOPT_OK) return st;
+        char* base = static_cast<char*>(stage);
+        int8_t* qa = reinterpret_cast<int8_t*>(base);
+        unsigned* part = reinterpret_cast<unsigned*>(base + qa_bytes);
+        unsigned* amax = reinterpret_cast<unsigned*>(base + qa_bytes + part_bytes);
+        st = finish_launch(launch_absmax(A, lda, B, ldb, M, N, K, part, s));
+        if (st != DNNOPT_OK) return st;
+        st = finish_launch(launch_quant_a(A, lda, M, K, ldq, part, ga, gb, amax, qa, s));
+        if (st != DNNOPT_OK) return st;
+        S8Args a{};
+        a.A = qa;
+        a.Bf = B;
+        a.C = C;
+        a.lda = ldq;
+        a.ldb = ldb;
+        a.ldc = ldc;
+        a.M = M;
+        a.N = N;
+        a.K = K;
+        a.splits = 1;
+        a.tiles_n = (N + 31) / 32;
+        a.tiles_m = (M + 63) / 64;
+        a.amax = amax;
+        a.alpha = alpha;
+        a.beta = beta;
+        a.qpart = part;
+        a.ga = ga;
+        a.gb = gb;
+        return finish_launch(launch_s8_q8b(dim3((unsigned)xcd_grid(a.tiles_n, a.tiles_m)), a, s));
+    }
     if (N > 0x7FFFFFFF / 2 || (long long)N * ((K + 15) & ~15) > 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
     // Staging (slot 1): [qA M x ldq][qB N x ldq][absmax partials][max|A|, max|B|];
     // ldq pads K to 16 bytes so every quantized row is 16-byte aligned.
     // Three launches: maxima, quantization, and the int8 GEMM whose epilogue
     // dequantizes straight into C.
-    const int ldq = (K + 15) & ~15;
     int ga = 1, gb = 1;
     absmax_blocks(M, N, K, &ga, &gb);
     const size_t qa_bytes = ((size_t)M * ldq + 255) & ~(size_t)255;

@@ -255,7 +255,15 @@ namespace {
 __device__ __forceinline__ int swz16(int row, int c) { return c ^ (row & 7); }
 }  // namespace
 
-template <int MT, int NT, int WM, int WN, int D, int EPI, int BK = 128>
+// QB = 1 (fp32-API gemm_int8; 32 x 128 B blocks, 256 threads): B is the
+// fp32 K x N matrix p.Bf.  Thread t loads 4 columns (4 cg .. 4 cg + 3, cg = t
+// mod 8) of 4 consecutive k rows (4 kq .. 4 kq + 3, kq = t / 8) with four
+// 16-byte loads (a wave's load covers 8 rows x 128 bytes), quantizes them
+// when the stage is written, and stores each column's 4 k bytes as one dword
+// of that column's LDS row: the LDS layout and the MFMAs are those of int8
+// B.  Columns past N hold whatever the loads return; their outputs are not
+// stored.
+template <int MT, int NT, int WM, int WN, int D, int EPI, int BK = 128, int QB = 0>
 __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     constexpr int BM = WM * MT * 16, BN = WN * NT * 16;  // BK: bytes (= k) per block
     constexpr int NTH = WM * WN * 64;
@@ -287,8 +295,14 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
         make_rsrc(p.A + (size_t)m0 * p.lda,
                   range31(((size_t)(p.M - 1 - m0) * p.lda + p.K + 3) & ~(size_t)3));
     const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(p.B + (size_t)n0 * p.ldb,
-                  range31(((size_t)(p.N - 1 - n0) * p.ldb + p.K + 3) & ~(size_t)3));
+        QB ? make_rsrc(p.Bf + n0, range31(((size_t)(p.K - 1) * p.ldb + (p.N - n0)) * 4))
+           : make_rsrc(p.B + (size_t)n0 * p.ldb, range31(((size_t)(p.N - 1 - n0) * p.ldb + p.K + 3) & ~(size_t)3));
+    float inv_b = 0.0f;
+    if constexpr (QB) {
+        unsigned ma, mb;
+        wave_maxima(p.qpart, p.ga, p.gb, &ma, &mb);
+        inv_b = 1.0f / quant_scale_bits(mb);
+    }
 
     uint32_t a_off[AU], b_off[BU];
     int a_lds[AU], b_lds[BU], a_c[AU];
@@ -302,19 +316,38 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
     }
 #pragma unroll
     for (int i = 0; i < BU; ++i) {
-        const int idx = t + i * NTH, row = idx / CPR, c = idx % CPR;
+        const int idx = t + i * NTH;
+        // QB: consecutive threads take consecutive columns of one k-chunk.
+        const int row = QB ? idx % BN : idx / CPR, c = QB ? idx / BN : idx % CPR;
         const bool ok = (BCH % NTH == 0 || idx < BCH) && n0 + row < p.N;
         b_off[i] = ok ? (uint32_t)row * p.ldb + 16 * c : kOobOffset;
         b_lds[i] = A_BYTES + row * ROWB + swz16(row, c) * 16;
     }
+    static_assert(!QB || (BN == 32 && BK == 128 && NTH == 256), "fp32 B staging: 32 x 128 blocks, 256 threads");
+    const int q_cg = t % 8, q_kq = t / 8;
+    const uint32_t q_off = ((uint32_t)(4 * q_kq) * (uint32_t)p.ldb + 4 * q_cg) * 4u;
+    int q_lds[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int row = 4 * q_cg + e, c = q_kq / 4;
+        q_lds[e] = A_BYTES + row * ROWB + swz16(row, c) * 16 + 4 * (q_kq % 4);
+    }
 
     i32x4 sa[D][AU], sb[D][BU];
+    f32x4 sbq[D][QB ? 4 : 1];
     auto load_stage = [&](int blk, int slot) {
         const uint32_t k0 = (uint32_t)(blk < b_hi ? blk : b_hi - 1) * BK;
 #pragma unroll
         for (int i = 0; i < AU; ++i) sa[slot][i] = __builtin_bit_cast(i32x4, buf_load_x4(ra, a_off[i] + k0));
+        if constexpr (QB) {
+            const uint32_t kb = k0 * (uint32_t)p.ldb * 4u + q_off;
 #pragma unroll
-        for (int i = 0; i < BU; ++i) sb[slot][i] = __builtin_bit_cast(i32x4, buf_load_x4(rb, b_off[i] + k0));
+            for (int j = 0; j < 4; ++j)
+                sbq[slot][j] = __builtin_bit_cast(f32x4, buf_load_x4(rb, kb + (uint32_t)j * (uint32_t)p.ldb * 4u));
+        } else {
+#pragma unroll
+            for (int i = 0; i < BU; ++i) sb[slot][i] = __builtin_bit_cast(i32x4, buf_load_x4(rb, b_off[i] + k0));
+        }
     };
     auto write_stage = [&](int slot, int buf, int blk) {
         char* St = lds + buf * STAGE;
@@ -327,9 +360,19 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_s8_lds(S8Args p) {
             if (tail) v = mask_chunk(v, p.K - (blk * BK + a_c[i]));
             if (ACH % NTH == 0 || t + i * NTH < ACH) *reinterpret_cast<i32x4*>(St + a_lds[i]) = v;
         }
+        if constexpr (QB) {
 #pragma unroll
-        for (int i = 0; i < BU; ++i)
-            if (BCH % NTH == 0 || t + i * NTH < BCH) *reinterpret_cast<i32x4*>(St + b_lds[i]) = sb[slot][i];
+            for (int e = 0; e < 4; ++e)
+                *reinterpret_cast<uint32_t*>(St + q_lds[e]) =
+                    (uint32_t)(quant_s8(sbq[slot][0][e], inv_b) & 0xFF) |
+                    (uint32_t)(quant_s8(sbq[slot][1][e], inv_b) & 0xFF) << 8 |
+                    (uint32_t)(quant_s8(sbq[slot][2][e], inv_b) & 0xFF) << 16 |
+                    (uint32_t)quant_s8(sbq[slot][3][e], inv_b) << 24;
+        } else {
+#pragma unroll
+            for (int i = 0; i < BU; ++i)
+                if (BCH % NTH == 0 || t + i * NTH < BCH) *reinterpret_cast<i32x4*>(St + b_lds[i]) = sb[slot][i];
+        }
     };
 
     int a_rd[KK][MT], b_rd[KK][NT];
@@ -718,6 +761,13 @@ static hipError_t launch_s8_cfg(int cfg, dim3 grid, const S8Args& a, hipStream_t
         case 29: hipLaunchKernelGGL((dnnopt_s8_dma<2, 2, 2, 2, 4, EPI, 128>), grid, dim3(256), 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+// 64 x 32 tiles, 3 blocks of 128 k in flight (MI355X, 128 x 4096 x 4096
+// call: 2 / 3 / 4 / 6 blocks 38.6 / 38.4 / 38.8 / 39.6 us).
+hipError_t launch_s8_q8b(dim3 grid, const S8Args& a, hipStream_t s) {
+    hipLaunchKernelGGL((dnnopt_s8_lds<2, 1, 2, 2, 3, 1, 128, 1>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -206,6 +206,43 @@ hipError_t launch_absmax(const float* A, int lda, const float* B, int ldb, int M
     return hipGetLastError();
 }
 
+// A alone: one thread per 4 consecutive elements of qA (M x ldq), so a call
+// is one memory round trip (its load goes out before the maxima are read).
+template <int VEC>
+__global__ __launch_bounds__(256) void dnnopt_quantize_a(const float* __restrict__ A, int M, int K, int lda,
+                                                        const unsigned* part, int ga, int gb, unsigned* amax,
+                                                        int8_t* qA, int ldq) {
+    const long long e = ((long long)blockIdx.x * 256 + threadIdx.x) * 4;
+    const int r = (int)(e / ldq), c = (int)(e % ldq);
+    const bool live = r < M;
+    const f32x4 v = live && c < K ? load4<VEC>(A + (size_t)r * lda, c, K) : f32x4{0.f, 0.f, 0.f, 0.f};
+    unsigned ma, mb;
+    wave_maxima(part, ga, gb, &ma, &mb);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        amax[0] = ma;
+        amax[1] = mb;
+    }
+    if (!live) return;
+    const float inv = 1.0f / quant_scale_bits(ma);
+    // ldq is a multiple of 16, so c + 4 <= ldq
+    *reinterpret_cast<uint32_t*>(qA + (size_t)r * ldq + c) =
+        pack4(quant_s8(v[0], inv), quant_s8(v[1], inv), quant_s8(v[2], inv), quant_s8(v[3], inv));
+}
+
+hipError_t launch_quant_a(const float* A, int lda, int M, int K, int ldq, const unsigned* part, int ga, int gb,
+                          unsigned* amax, int8_t* qA, hipStream_t s) {
+    if (ldq % 16 != 0 || ga + gb > 1024) return hipErrorInvalidValue;
+    const long long blocks = ((long long)M * ldq / 4 + 255) / 256;
+    if (blocks > 0x7FFFFFFFll) return hipErrorInvalidValue;
+    if (quant_vec(A, lda, A, lda))
+        hipLaunchKernelGGL(dnnopt_quantize_a<1>, dim3((unsigned)blocks), dim3(256), 0, s, A, M, K, lda, part, ga, gb,
+                           amax, qA, ldq);
+    else
+        hipLaunchKernelGGL(dnnopt_quantize_a<0>, dim3((unsigned)blocks), dim3(256), 0, s, A, M, K, lda, part, ga, gb,
+                           amax, qA, ldq);
+    return hipGetLastError();
+}
+
 hipError_t launch_quant_pair(const float* A, int lda, const float* B, int ldb, int M, int N, int K, int ldq,
                              unsigned* part, unsigned* amax, int8_t* qA, int8_t* qB, hipStream_t s) {
     if (ldq % 16 != 0) return hipErrorInvalidValue;

@@ -132,6 +132,12 @@ struct S8Args {
     // dequantization instead of the column scale (s8_out in device_common.h).
     const unsigned* amax;
     float alpha, beta;
+    // fp32-API gemm_int8, M > 8 (launch_s8_q8b): B is the fp32 K x N matrix
+    // (row stride ldb floats), quantized while it is staged with the scale
+    // from the maxima partials qpart[ga, ga + gb); A is already quantized.
+    const float* Bf;
+    const unsigned* qpart;
+    int ga, gb;
 };
 
 struct S8Config {
@@ -282,6 +288,14 @@ int skinny_q8_waves();  // waves per workgroup of dnnopt_skinny_q8 (256 columns 
 // Maxima partials only (the first launch of the fp32-API int8 pipeline).
 hipError_t launch_absmax(const float* A, int lda, const float* B, int ldb, int M, int N, int K, unsigned* part,
                          hipStream_t s);
+// Quantize A only (M x K fp32 -> qA, M x ldq int8) and store max|A|, max|B|
+// to amax[0..1] (maxima from launch_absmax's partials).
+hipError_t launch_quant_a(const float* A, int lda, int M, int K, int ldq, const unsigned* part, int ga, int gb,
+                          unsigned* amax, int8_t* qA, hipStream_t s);
+// fp32-API int8 GEMM, M > 8: int8 A (qA) x fp32 K x N B quantized while it is
+// staged (64 x 32 tiles through LDS), dequantizing epilogue.  grid.x =
+// xcd_grid(ceil(N / 32), ceil(M / 64)).
+hipError_t launch_s8_q8b(dim3 grid, const S8Args& a, hipStream_t s);
 // Reduce skinny partials [split][M][ncols_pad] into C (epilogue applied);
 // tile t (of T, tile width tw) has splits_of_tile(t, G, T) partials.
 hipError_t launch_skinny_reduce(const float* part, int G, int T, int tw, int M, int N, int ncols_pad,

@@ -122,8 +122,10 @@ def test_plans_for_the_configs(lib):
         assert p["kernel"] == b.K_SKINNY_Q8 and p["name"] == "dnnopt_skinny_q8" and p["rows"] == M, p
         q = lib.plan_sgemm(M, 4096, 4096)
         assert (p["grid_x"], p["splits"], p["workspace_bytes"]) == (q["grid_x"], q["splits"], q["workspace_bytes"])
-    assert lib.plan_int8_f32(9, 4096, 4096)["kernel"] == b.K_MFMA_S8
-    assert lib.plan_int8_f32(128, 4096, 4096)["name"] == "dnnopt_s8_dma"
+    # M > 8: int8 tiles that quantize the fp32 B while staging it
+    for M in (9, 128):
+        p = lib.plan_int8_f32(M, 4096, 4096)
+        assert p["kernel"] == b.K_MFMA_S8 and p["name"] == "dnnopt_s8_lds_q8b" and (p["rows"], p["cols"]) == (64, 32), p
 
 
 def test_plan_split_never_exceeds_k(lib):
