@@ -1065,3 +1065,35 @@ def test_wide_n_sweep(lib, orc, dev, kind, M, N, K):
         lib.sgemm(M, N, K, 0.5, dev_copy(A, dev), K, dev_copy(Bkn, dev), N, 1.0, dC, N, stream=stream())
     want, scale = u.exact(A, Bkn, 0.5, 1.0, C0)
     u.assert_fp32_close(host(dC), want, scale, K, f"wide {kind} {M}x{N}x{K}")
+
+
+def _bf16_ex_sweep_cases():
+    """Seeded bf16-storage shapes over every bf16 route of dnnopt_hip_gemm_bf16_ex:
+    skinny (B stored K x N, A either layout), row-dot and 16 / 32 x 48 tiles (B
+    stored N x K), 32 x 64 and 64-row LDS tiles, odd strides (register tiles)."""
+    rng = np.random.default_rng(20261207)
+    cases = []
+    while len(cases) < 16:
+        M = int(rng.choice([int(rng.integers(1, 9)), int(rng.integers(9, 33)), int(rng.integers(33, 200))]))
+        N, K = int(rng.integers(1, 3000)), int(rng.integers(1, 1200))
+        if M * N * K > 150_000_000:
+            continue
+        ta, tb = int(rng.integers(0, 2)), int(rng.integers(0, 2))
+        pa, pb = int(rng.integers(0, 4)), int(rng.integers(0, 4))
+        cases.append((M, N, K, ta, tb, pa, pb))
+    return cases
+
+
+@pytest.mark.parametrize("M,N,K,ta,tb,pa,pb", _bf16_ex_sweep_cases())
+def test_bf16_ex_route_sweep(lib, orc, dev, M, N, K, ta, tb, pa, pb):
+    lda, ldb = (M if ta else K) + pa, (K if tb else N) + pb
+    As = u.bf16_bits(orc, u.normal(orc, (K if ta else M) * lda, 1)).reshape(K if ta else M, lda)
+    Bs = u.bf16_bits(orc, u.normal(orc, (N if tb else K) * ldb, 2, 0, 0.02)).reshape(N if tb else K, ldb)
+    Amk = np.ascontiguousarray(u.bf16_value(As)[:, :M].T if ta else u.bf16_value(As)[:, :K])
+    Bkn = np.ascontiguousarray(u.bf16_value(Bs)[:, :K].T if tb else u.bf16_value(Bs)[:, :N])
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    dC = dev_copy(C0, dev)
+    lib.gemm_bf16_ex(M, N, K, -0.5, dev_copy(As.view(np.int16), dev), lda, dev_copy(Bs.view(np.int16), dev), ldb, 0.75,
+                     dC, N, transA=ta, transB=tb, stream=stream())
+    want, scale = u.exact(Amk, Bkn, -0.5, 0.75, C0)
+    u.assert_fp32_close(host(dC), want, scale, K, f"bf16_ex sweep {M}x{N}x{K} ta={ta} tb={tb} pads={pa},{pb}")
