@@ -1,0 +1,99 @@
+"""Seeded random shapes over every entry point and route (fp32 with both
+operand layouts, bf16 storage, int8, fp32-API int8): padded strides, C blocks
+inside wider matrices, assorted alpha / beta.  Each case is checked against
+fp64 (fp32 / bf16, the (2K+4)u tolerance), exact int64 products (int8) or a
+numpy restatement of the per-tensor quantization (fp32-API int8)."""
+
+import numpy as np
+import pytest
+
+import _util as u
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+def _cases(seed=20261208, count=120):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        kind = str(rng.choice(["f32", "bf16", "s8", "i8f"]))
+        M = int(rng.choice([rng.integers(1, 9), rng.integers(9, 65), rng.integers(65, 700), rng.integers(700, 20000)]))
+        N = int(rng.choice([rng.integers(1, 70), rng.integers(70, 3000), rng.integers(3000, 40000)]))
+        K = int(rng.choice([rng.integers(1, 70), rng.integers(70, 2000), rng.integers(2000, 20000)]))
+        if M * N * K > 2e8 or M * K > 4e7 or N * K > 4e7:
+            continue
+        ta, tb = int(rng.integers(0, 2)), int(rng.integers(0, 2))
+        pads = tuple(int(x) for x in rng.integers(0, 5, 3))
+        alpha, beta = float(rng.choice([1.0, -0.5])), float(rng.choice([0.0, 1.0, 0.25]))
+        out.append((len(out), kind, M, N, K, ta, tb, pads, alpha, beta))
+    return out
+
+
+def _bf16(x):
+    b = x.view(np.uint32)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: f"{c[0]}-{c[1]}-{c[2]}x{c[3]}x{c[4]}")
+def test_random_shape(lib, dev, case):
+    i, kind, M, N, K, ta, tb, (pa, pb, pc), alpha, beta = case
+    rng = np.random.default_rng(1000 + i)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def dc(x):
+        return torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+
+    ldc = N + pc
+    C0 = rng.standard_normal((M, ldc)).astype(np.float32)
+    if kind in ("f32", "bf16"):
+        lda, ldb = (M if ta else K) + pa, (K if tb else N) + pb
+        As = rng.standard_normal((K if ta else M, lda)).astype(np.float32)
+        Bs = (rng.standard_normal((N if tb else K, ldb)) * 0.05).astype(np.float32)
+        dC = dc(C0)
+        if kind == "bf16":
+            Ab, Bb = _bf16(As), _bf16(Bs)
+            As, Bs = u.bf16_value(Ab), u.bf16_value(Bb)
+            lib.gemm_bf16_ex(M, N, K, alpha, dc(Ab.view(np.int16)), lda, dc(Bb.view(np.int16)), ldb, beta, dC, ldc,
+                             transA=ta, transB=tb, stream=s)
+        else:
+            lib.sgemm(M, N, K, alpha, dc(As), lda, dc(Bs), ldb, beta, dC, ldc, transA=ta, transB=tb, stream=s)
+        got = dC.cpu().numpy()
+        Amk = np.ascontiguousarray(As[:, :M].T if ta else As[:, :K])
+        Bkn = np.ascontiguousarray(Bs[:, :K].T if tb else Bs[:, :N])
+        want, scale = u.exact(Amk, Bkn, alpha, beta, C0[:, :N])
+        u.assert_fp32_close(got[:, :N], want, scale, K, f"{kind} case {i}")
+    elif kind == "s8":
+        lda, ldb = K + pa, K + pb
+        A = rng.integers(-128, 128, (M, lda)).astype(np.int8)
+        B = rng.integers(-128, 128, (N, ldb)).astype(np.int8)
+        dC = torch.full((M, ldc), 7, dtype=torch.int32, device=dev)
+        lib.gemm_s8s8s32(M, N, K, dc(A), lda, dc(B), ldb, dC, ldc, stream=s)
+        got = dC.cpu().numpy()
+        want = A[:, :K].astype(np.int64) @ B[:, :K].astype(np.int64).T
+        assert np.array_equal(got[:, :N].astype(np.int64), want), f"s8 case {i}"
+        assert (got[:, N:] == 7).all()
+        return
+    else:
+        lda, ldb = K + pa, N + pb
+        A = rng.standard_normal((M, lda)).astype(np.float32)
+        B = rng.standard_normal((K, ldb)).astype(np.float32)
+        dC = dc(C0)
+        lib.gemm_int8_f32(M, N, K, alpha, dc(A), lda, dc(B), ldb, beta, dC, ldc, stream=s)
+        got = dC.cpu().numpy()
+        # scale_X = max|X| / 127 (1 if zero), q = clamp(rint(x * (1 / s)))
+        sa = np.float32(np.abs(A[:, :K]).max()) / np.float32(127)
+        sb = np.float32(np.abs(B[:, :N]).max()) / np.float32(127)
+        sa, sb = (sa if sa != 0 else np.float32(1)), (sb if sb != 0 else np.float32(1))
+        qa = np.clip(np.rint(A[:, :K] * (np.float32(1) / sa)), -128, 127).astype(np.int64)
+        qb = np.clip(np.rint(B[:, :N] * (np.float32(1) / sb)), -128, 127).astype(np.int64)
+        acc = (qa @ qb).astype(np.float32)
+        dq = np.float32(np.float32(sa * sb) * np.float32(alpha))
+        if beta == 0.0:
+            want = dq * acc
+        else:  # fma(dq, acc, beta * C): one rounding of the exact sum
+            want = (np.float64(dq) * acc.astype(np.float64) + (np.float32(beta) * C0[:, :N]).astype(np.float64))
+            want = want.astype(np.float32)
+        assert np.array_equal(got[:, :N].view(np.uint32), want.view(np.uint32)), f"i8f case {i}"
+    assert np.array_equal(got[:, N:], C0[:, N:]), f"case {i} wrote outside the C block"
