@@ -97,3 +97,48 @@ def test_random_shape(lib, dev, case):
             want = want.astype(np.float32)
         assert np.array_equal(got[:, :N].view(np.uint32), want.view(np.uint32)), f"i8f case {i}"
     assert np.array_equal(got[:, N:], C0[:, N:]), f"case {i} wrote outside the C block"
+
+
+def _cblas_cases(seed=20261209, count=32):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        M = int(rng.choice([rng.integers(1, 9), rng.integers(9, 300), rng.integers(300, 3000)]))
+        N = int(rng.choice([rng.integers(1, 70), rng.integers(70, 3000)]))
+        K = int(rng.choice([rng.integers(1, 70), rng.integers(70, 3000)]))
+        if M * N * K > 1e8:
+            continue
+        order = int(rng.choice([101, 102]))
+        ta, tb = int(rng.choice([111, 112])), int(rng.choice([111, 112]))
+        pads = tuple(int(x) for x in rng.integers(0, 4, 3))
+        out.append((len(out), order, ta, tb, M, N, K, pads, float(rng.choice([1.0, 0.5])), float(rng.choice([0.0, 1.0, -0.5]))))
+    return out
+
+
+@pytest.mark.parametrize("case", _cblas_cases(), ids=lambda c: f"{c[0]}-{c[1]}{c[2]}{c[3]}-{c[4]}x{c[5]}x{c[6]}")
+def test_random_cblas_host_arrays(lib, case):
+    """cblas_sgemm on host arrays (staged through the library's device
+    buffers): both orders, both transposes, padded leading dimensions."""
+    i, order, ta, tb, M, N, K, (pa, pb, pc), alpha, beta = case
+    rng = np.random.default_rng(2000 + i)
+    # op(A) is M x K, op(B) is K x N; stored row-major (order 101) as given or
+    # column-major (102), i.e. the transposed array row-major.
+    a_rows, a_cols = (M, K) if ta == 111 else (K, M)
+    b_rows, b_cols = (K, N) if tb == 111 else (N, K)
+    c_rows, c_cols = M, N
+    if order == 102:
+        a_rows, a_cols, b_rows, b_cols, c_rows, c_cols = a_cols, a_rows, b_cols, b_rows, c_cols, c_rows
+    lda, ldb, ldc = a_cols + pa, b_cols + pb, c_cols + pc
+    A = rng.standard_normal((a_rows, lda)).astype(np.float32)
+    B = rng.standard_normal((b_rows, ldb)).astype(np.float32)
+    C0 = rng.standard_normal((c_rows, ldc)).astype(np.float32)
+    C = C0.copy()
+    lib.cblas_sgemm(order, ta, tb, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc)
+    Am, Bm, Cm, Cg = A[:, :a_cols], B[:, :b_cols], C0[:, :c_cols], C[:, :c_cols]
+    if order == 102:  # the stored arrays are the transposes of the column-major matrices
+        Am, Bm, Cm, Cg = Am.T, Bm.T, Cm.T, Cg.T
+    opA = Am if ta == 111 else Am.T
+    opB = Bm if tb == 111 else Bm.T
+    want, scale = u.exact(np.ascontiguousarray(opA), np.ascontiguousarray(opB), alpha, beta, np.ascontiguousarray(Cm))
+    u.assert_fp32_close(np.ascontiguousarray(Cg), want, scale, K, f"cblas case {i}")
+    assert np.array_equal(C[:, c_cols:], C0[:, c_cols:]), f"cblas case {i} wrote outside the C block"
