@@ -142,3 +142,52 @@ def test_random_cblas_host_arrays(lib, case):
     want, scale = u.exact(np.ascontiguousarray(opA), np.ascontiguousarray(opB), alpha, beta, np.ascontiguousarray(Cm))
     u.assert_fp32_close(np.ascontiguousarray(Cg), want, scale, K, f"cblas case {i}")
     assert np.array_equal(C[:, c_cols:], C0[:, c_cols:]), f"cblas case {i} wrote outside the C block"
+
+
+def _hook_cases(seed=20261210, count=32):
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < count:
+        M = int(rng.choice([rng.integers(1, 70), rng.integers(70, 3000), rng.integers(3000, 12000)]))
+        N = int(rng.choice([rng.integers(1, 9), rng.integers(9, 300), rng.integers(300, 3000)]))
+        K = int(rng.choice([rng.integers(1, 70), rng.integers(70, 2500)]))
+        if M * N * K > 1e8:
+            continue
+        ta, tb = str(rng.choice(["N", "T"])), str(rng.choice(["N", "T"]))
+        bf16 = bool(rng.integers(0, 2))
+        out.append((len(out), M, N, K, ta, tb, int(rng.integers(0, 4)), bf16, float(rng.choice([0.0, 1.0])),
+                    int(rng.integers(0, 4)), bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("case", _hook_cases(), ids=lambda c: f"{c[0]}-{c[4]}{c[5]}-{c[1]}x{c[2]}x{c[3]}")
+def test_random_onednn_hook(lib, dev, case):
+    """The column-major oneDNN hook on device pointers: random shapes, both
+    transposes, fp32 (with or without bias) and bf16, padded C."""
+    i, M, N, K, ta, tb, pad, bf16, beta, dldc, with_bias = case
+    rng = np.random.default_rng(3000 + i)
+    opA = rng.standard_normal((M, K)).astype(np.float32)
+    opB = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+    if bf16:
+        opA, opB = u.bf16_value(_bf16(opA)), u.bf16_value(_bf16(opB))
+    A, lda, B, ldb = u.hook_operands(opA, opB, ta, tb, pad=pad)
+    if bf16:
+        A, B = _bf16(np.ascontiguousarray(A, np.float32)).view(np.int16), _bf16(np.ascontiguousarray(B, np.float32)).view(np.int16)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(M).astype(np.float32) if with_bias and not bf16 else None
+    ldc = M + dldc
+    Cbuf = u.cm_store(C0 if beta else np.full_like(C0, np.nan), ldc, fill=-777.0)
+    s = torch.cuda.current_stream().cuda_stream
+    dC = torch.from_numpy(Cbuf).to(dev)
+    dA, dB = torch.from_numpy(np.ascontiguousarray(A)).to(dev), torch.from_numpy(np.ascontiguousarray(B)).to(dev)
+    if bf16:
+        lib.ext_gemm_bf16bf16f32(ta, tb, M, N, K, 1.5, dA, lda, dB, ldb, beta, dC, ldc, stream=s)
+    else:
+        lib.ext_sgemm(ta, tb, M, N, K, 1.5, dA, lda, dB, ldb, beta, dC, ldc,
+                      bias=None if bias is None else torch.from_numpy(bias).to(dev), stream=s)
+    got = dC.cpu().numpy()
+    want, scale = u.exact(opA, opB, 1.5, beta, C0 if beta else None)
+    if bias is not None:
+        want, scale = want + bias[:, None], scale + np.abs(bias)[:, None]
+    u.assert_fp32_close(u.cm_load(got, M, N, ldc), want, scale, K + 1, f"hook case {i}")
+    assert (got.reshape(N, ldc)[:, M:] == -777.0).all(), f"hook case {i}: padding rows of C written"
