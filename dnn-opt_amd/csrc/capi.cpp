@@ -461,11 +461,14 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
     hipStream_t s = as_stream(stream);
     StreamLock lock(s);
     if (M <= 8) {
-        // Two passes over the fp32 B: the maxima, then dnnopt_skinny_q8, which
-        // quantizes B as it streams it (plus its reduce kernel when k is split
-        // over workgroups).  Staging (slot 1): [absmax partials][max|A|, max|B|].
+        // The reference's small-M route (division quantizer, its own
+        // epilogues), only in dnnopt_skinny_q8.  Two passes over the fp32 B:
+        // the maxima, then dnnopt_skinny_q8, which quantizes B as it streams
+        // it (plus its reduce kernel when k is split over workgroups).
+        // Staging (slot 1): [absmax partials][max|A|, max|B|].
         Launch L;
-        if (plan_skinny(kSkinnyF32, M, N, K, ldb, &L) == DNNOPT_OK) {
+        if (plan_skinny(kSkinnyF32, M, N, K, ldb, &L) != DNNOPT_OK) return DNNOPT_ERR_UNSUPPORTED;
+        {
             int ga = 1, gb = 1;
             absmax_blocks(M, N, K, &ga, &gb);
             const size_t part_bytes = ((size_t)(ga + gb) * 4 + 255) & ~(size_t)255;
@@ -511,7 +514,11 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
         return !(e && *e && atoi(e) == 0);
     }();
     const int ldq = (K + 15) & ~15;
-    if (q8b_ok && ((long long)K * ldb + N) * 4 < 0x7FFFFFFFll && ((long long)M + 64) * ldq < 0x7FFFFFFFll) {
+    // The q8b tiles address B, their quantized A and their 64-row block of C
+    // with 31-bit buffer offsets; larger strides take the quantization pass
+    // and gemm_s8_common, whose planner checks its own ranges.
+    if (q8b_ok && ((long long)K * ldb + N) * 4 < 0x7FFFFFFFll && ((long long)M + 64) * ldq < 0x7FFFFFFFll &&
+        ((long long)64 * ldc + N) * 4 < 0x7FFFFFFFll) {
         // Maxima, A quantized (M x ldq), then 64 x 32 int8 tiles that quantize
         // the fp32 B while staging it: no int8 copy of B.  Staging (slot 1):
         // [qA M x ldq][absmax partials][max|A|, max|B|].

@@ -204,6 +204,56 @@ __device__ __forceinline__ int quant_s8(float x, float inv) {
     return v > 127 ? 127 : (v < -128 ? -128 : v);
 }
 
+// Quantization of the fp32-API gemm_int8 at M <= 8, the reference's small-M
+// route (src/gemm/gemm_smallm_int8.cpp:151, 159, 233, 280-281): a true
+// division, q = clamp(rint(x / s), -128, 127).  With inv = 1 / s correctly
+// rounded, q0 = x * inv is within an ulp of x / s, the residual
+// r = fma(-q0, s, x) is exact, and fma(r, inv, q0) is the correctly rounded
+// quotient whenever nothing underflows (Markstein's theorem).  For scales in
+// [2^-64, 2^64] every quotient near a half-integer -- the only ones where the
+// rounding to an integer can change -- is far from underflow; quotients that
+// do underflow are below 0.5 and round to 0 either way.  Scales outside that
+// range take the compiler's correctly rounded division (QuantDiv::exact).
+struct QuantDiv {
+    float s, inv;
+    bool exact;
+};
+__device__ __forceinline__ QuantDiv quant_div_of(uint32_t amax_bits) {
+    const float s = quant_scale_bits(amax_bits);
+    const bool in_range = s >= 0x1p-64f && s <= 0x1p64f;
+    return QuantDiv{s, 1.0f / s, !in_range};
+}
+// CLAMP = false when |x| <= max|X| is known: then |x / s| <= 127 (1 + 2^-23)
+// and the rounded value lies in [-127, 127] already (NaN converts to 0).
+template <bool EXACT, bool CLAMP>
+__device__ __forceinline__ int quant_s8_div(float x, const QuantDiv& d) {
+    float q;
+    if constexpr (EXACT) {
+        q = x / d.s;
+    } else {
+        const float q0 = x * d.inv;
+        q = __builtin_fmaf(__builtin_fmaf(-q0, d.s, x), d.inv, q0);
+    }
+    const int v = (int)__builtin_rintf(q);
+    if constexpr (!CLAMP) return v;
+    return v > 127 ? 127 : (v < -128 ? -128 : v);
+}
+
+// Output of the fp32-API gemm_int8 at M <= 8 (t = alpha * (sA * sB)):
+//   M == 1 (gemm_mx1_int8, src/gemm/gemm_smallm_int8.cpp:170-175):
+//     beta == 0 ? t * acc : fma(beta, C, t * acc) -- the reference's
+//     `result + beta * C[j]` contracts only the beta * C product, since
+//     `result` also feeds the beta == 0 store;
+//   M >= 2 (gemm_smallm_int8_smmla, :243-250, :356-383): C is first set to 0
+//     or beta * C, then C + t * acc is stored -- two roundings.
+// C is read only when beta != 0 (c_old holds it then).
+__device__ __forceinline__ float smallm_out(int32_t acc, bool one_row, float t, float beta, float c_old) {
+    const float r = mul_rn(t, (float)acc);
+    if (one_row) return beta == 0.0f ? r : __builtin_fmaf(beta, c_old, r);
+    const float c0 = beta == 0.0f ? 0.0f : (beta == 1.0f ? c_old : mul_rn(c_old, beta));
+    return add_rn(c0, r);
+}
+
 // The maxima of A (part[0, ga)) and B (part[ga, ga + gb)), ga + gb <= 1024,
 // reduced by one wave on its own (no barrier): 16 consecutive partials per
 // lane, read as four 16-byte loads.  The buffer range is rounded up to whole

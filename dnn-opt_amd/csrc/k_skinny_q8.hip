@@ -1,22 +1,30 @@
 // k_skinny_q8.hip -- fp32-API gemm_int8 for M <= 8 in one pass over B (gfx950).
 //
-// The reference's fp32 gemm_int8 (src/gemm/gemm.cpp:418-455) quantizes A and
-// B per tensor (scales from the maxima, src/gemm/gemm_driver_generic.cpp:
-// 49-67; rounding, src/gemm/gemm_pack_int8.cpp:29-71) and sums exact int32
-// products.  With at most 8 rows of A the product is a stream over B, so this
-// kernel reads the fp32 B (K x N, row-major) once, after the maxima pass
-// (dnnopt_absmax_part), quantizes every element as it arrives (A's values of
-// each block are quantized by the wave's lanes into LDS bytes), and adds
-// exact int32 products with v_dot4_i32_i8: no int8 copy of B is written or
-// read.
+// With M <= 8 the reference's fp32 gemm_int8 (src/gemm/gemm.cpp:431-434)
+// takes its small-M route, gemm_smallm_int8 (src/gemm/gemm_smallm_int8.cpp):
+// per-tensor scales s_X = max|X| / 127 (1 if zero), quantization by a true
+// division, q = clamp(lrintf(x / s_X), -128, 127) (:151, :159, :233,
+// :280-281), exact int32 sums, and its own epilogues -- M = 1:
+// t acc or fma(beta, C, t acc) (:170-175); M = 2..8: C set to 0 or beta C
+// first (:243-250), then C + t acc (:356-383), with t = alpha (sA sB).
+// (The reference's M = 3 store skips row 2 and its M = 7 store touches a row
+// 7 past C, :391, :445; every row 0..M-1 is stored here, nothing else.)
+//
+// The product is a stream over B, so this kernel reads the fp32 B (K x N,
+// row-major) once, after the maxima pass (dnnopt_absmax_part), quantizes
+// every element as it arrives (A's values of each block are quantized by
+// the wave's lanes into LDS bytes), and adds exact int32 products with
+// v_dot4_i32_i8: no int8 copy of B is written or read.  The division is the
+// reciprocal product plus one fused correction (quant_s8_div), which gives
+// the correctly rounded quotient.
 //
 // Lane layout and k-split follow dnnopt_skinny: a wave covers 256 columns (16
 // bytes of a row per lane), the 8 waves of a workgroup and the workgroups of
 // a column tile take contiguous k-ranges, waves are combined through LDS and
 // workgroups through int32 partial sums that dnnopt_skinny_q8_reduce adds up.
-// Integer sums are exact, so the order of the combine does not matter.  The
-// output is the int8 kernels' dequantizing epilogue (s8_out): C = (sA sB
-// alpha) acc, or fma(that, acc, beta C).
+// Integer sums are exact, so the order of the combine does not matter.
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -31,9 +39,12 @@ constexpr int kQ8Unroll = 16;  // rows of B in flight per wave
 constexpr int kQ8Cols = 256;   // columns per wave (4 per lane)
 
 // Four values in [-128, 127] as the bytes of one dword, the first in the low
-// byte (the operand layout of v_dot4_i32_i8).
+// byte (the operand layout of v_dot4_i32_i8): each value's low byte, picked
+// by three byte permutes.
 __device__ __forceinline__ uint32_t pack_q4(int a, int b, int c, int d) {
-    return (uint32_t)(a & 0xFF) | (uint32_t)(b & 0xFF) << 8 | (uint32_t)(c & 0xFF) << 16 | (uint32_t)d << 24;
+    const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);  // [a0 b0 0 0]
+    const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);  // [c0 d0 0 0]
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);                                  // [a0 b0 c0 d0]
 }
 
 // B is read exactly once: streaming loads.
@@ -79,35 +90,38 @@ __global__ __launch_bounds__(kQ8Waves * 64) void dnnopt_skinny_q8(SkinnyQ8Args p
     const uint32_t rowbytes = (uint32_t)p.ldb * 4u;
     const uint32_t lane_off = col0 + lane * 4 < p.N ? (uint32_t)lane * 16u : kOobOffset;
 
-    // A: the range ends at the last element of row M - 1; lanes past the
-    // block's MR x U entries read nothing.
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, range31(((size_t)(p.M - 1) * p.lda + p.K) * 4));
-    uint32_t a_lane[QL];
+    // A: lane l of a block takes entries l, l + 64, ... (row e / U, k e % U)
+    // through a 64-bit pointer (A's rows may lie further apart than a
+    // buffer's 31-bit offsets reach); lanes past the block's MR x U entries
+    // load nothing.
+    const float* a_lane[QL];
 #pragma unroll
     for (int j = 0; j < QL; ++j) {
         const int e = lane + 64 * j;
-        a_lane[j] = e < QA ? (uint32_t)((e / U) * p.lda + e % U) * 4u : kOobOffset;
+        a_lane[j] = e < QA ? p.A + (size_t)(e / U) * p.lda + e % U : nullptr;
     }
     auto load_block = [&](u32x4 (&raw)[U], float (&av)[QL], int k0) {
 #pragma unroll
         for (int u = 0; u < U; ++u) raw[u] = load_row(rs, (uint32_t)(k0 + u - kb) * rowbytes + lane_off);
 #pragma unroll
-        for (int j = 0; j < QL; ++j)
-            av[j] = as_f32(buf_load_x1(ra, a_lane[j] == kOobOffset ? kOobOffset : a_lane[j] + (uint32_t)k0 * 4u));
+        for (int j = 0; j < QL; ++j) av[j] = (QA % 64 == 0 || lane + 64 * j < QA) ? a_lane[j][k0] : 0.0f;
     };
 
     // The first block goes out before the maxima are read.
-    u32x4 raw[U];
-    float av[QL];
+    u32x4 raw0[U], raw1[U];
+    float av0[QL], av1[QL];
     int k = k_lo;
-    if (k + U <= k_hi) load_block(raw, av, k);
+    if (k + U <= k_hi) load_block(raw0, av0, k);
     unsigned ma, mb;
     wave_maxima(p.qpart, p.ga, p.gb, &ma, &mb);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         p.amax[0] = ma;
         p.amax[1] = mb;
     }
-    const float inv_a = 1.0f / quant_scale_bits(ma), inv_b = 1.0f / quant_scale_bits(mb);
+    const QuantDiv qd_a = quant_div_of(ma), qd_b = quant_div_of(mb);
+    // Either scale outside the fast division's range: both take the exact
+    // division (the two forms agree wherever the fast one applies).
+    const bool exact = qd_a.exact || qd_b.exact;
 
     int acc[MR][4];
 #pragma unroll
@@ -115,14 +129,16 @@ __global__ __launch_bounds__(kQ8Waves * 64) void dnnopt_skinny_q8(SkinnyQ8Args p
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[m][e] = 0;
 
-    // Whole blocks: per 4 rows of B a lane packs each of its columns' 4
-    // quantized k into one dword and adds 4 products per v_dot4_i32_i8
-    // against the packed A bytes of the same 4 k.
+    // One whole block: A's MR x 16 values are quantized by the wave's lanes
+    // into LDS bytes and read back as one 16-byte broadcast per row; per 4
+    // rows of B a lane packs each of its columns' 4 quantized k into one
+    // dword and adds 4 products per v_dot4_i32_i8.  |x| <= max|X| bounds
+    // |x / s| by 127 (plus rounding), so the values need no clamp here.
     int8_t* const qw = reinterpret_cast<int8_t*>(qa_lds[w]);
-    while (k + U <= k_hi) {
+    auto compute_block = [&](const u32x4 (&raw)[U], const float (&av)[QL]) {
 #pragma unroll
         for (int j = 0; j < QL; ++j)
-            if (lane + 64 * j < QA) qw[lane + 64 * j] = (int8_t)quant_s8(av[j], inv_a);
+            if (lane + 64 * j < QA) qw[lane + 64 * j] = (int8_t)quant_s8_div<false, false>(av[j], qd_a);
         u32x4 a16[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) a16[m] = qa_lds[w][m];
@@ -131,33 +147,58 @@ __global__ __launch_bounds__(kQ8Waves * 64) void dnnopt_skinny_q8(SkinnyQ8Args p
             uint32_t b4[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                b4[e] = pack_q4(quant_s8(as_f32(raw[4 * q][e]), inv_b), quant_s8(as_f32(raw[4 * q + 1][e]), inv_b),
-                                quant_s8(as_f32(raw[4 * q + 2][e]), inv_b), quant_s8(as_f32(raw[4 * q + 3][e]), inv_b));
+                b4[e] = pack_q4(quant_s8_div<false, false>(as_f32(raw[4 * q][e]), qd_b),
+                                quant_s8_div<false, false>(as_f32(raw[4 * q + 1][e]), qd_b),
+                                quant_s8_div<false, false>(as_f32(raw[4 * q + 2][e]), qd_b),
+                                quant_s8_div<false, false>(as_f32(raw[4 * q + 3][e]), qd_b));
 #pragma unroll
             for (int m = 0; m < MR; ++m)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[m][e] = __builtin_amdgcn_sdot4((int)a16[m][q], (int)b4[e], acc[m][e], false);
+                for (int e = 0; e < 4; ++e)
+                    acc[m][e] = __builtin_amdgcn_sdot4((int)a16[m][q], (int)b4[e], acc[m][e], false);
         }
-        k += U;
-        if (k + U <= k_hi) load_block(raw, av, k);
-    }
-    // The last k % 16 rows of the range, one at a time.
-    for (; k < k_hi; ++k) {
-        const u32x4 v = load_row(rs, (uint32_t)(k - kb) * rowbytes + lane_off);
-        int qb[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) qb[e] = quant_s8(as_f32(v[e]), inv_b);
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-            const int qa = quant_s8(p.A[(size_t)m * p.lda + k], inv_a);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[m][e] += qa * qb[e];
+    };
+    // Whole blocks, two register sets alternating (the next block's loads
+    // are in flight while one is consumed, with no copies between sets).
+    // Only with both scales in the fast division's range; otherwise
+    // (wave-uniform) the whole range goes through the row-at-a-time loop
+    // below with the exact division.
+    if (!exact) {
+        while (k + U <= k_hi) {
+            if (k + 2 * U <= k_hi) load_block(raw1, av1, k + U);
+            compute_block(raw0, av0);
+            k += U;
+            if (k + U > k_hi) break;
+            if (k + 2 * U <= k_hi) load_block(raw0, av0, k + U);
+            compute_block(raw1, av1);
+            k += U;
         }
     }
+    // The last k % 16 rows of the range (all of it with the exact division),
+    // one at a time.
+    auto rows = [&](auto ex) {
+        constexpr bool EX = decltype(ex)::value;
+        for (; k < k_hi; ++k) {
+            const u32x4 v = load_row(rs, (uint32_t)(k - kb) * rowbytes + lane_off);
+            int qb[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qb[e] = quant_s8_div<EX, true>(as_f32(v[e]), qd_b);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const int qa = quant_s8_div<EX, true>(p.A[(size_t)m * p.lda + k], qd_a);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[m][e] += qa * qb[e];
+            }
+        }
+    };
+    if (exact)
+        rows(std::true_type{});
+    else
+        rows(std::false_type{});
 
     // Combine the waves: thread t owns 4-column group t % 64 of row t / 64
     // within a pass of G rows.
-    const float dq = mul_rn(mul_rn(quant_scale_bits(ma), quant_scale_bits(mb)), p.alpha);
+    const float t_dq = mul_rn(p.alpha, mul_rn(qd_a.s, qd_b.s));
     const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.part, range31((size_t)p.splits * MR * p.ncols_pad * 4));
 #pragma unroll
     for (int pass = 0; pass < P; ++pass) {
@@ -180,8 +221,7 @@ __global__ __launch_bounds__(kQ8Waves * 64) void dnnopt_skinny_q8(SkinnyQ8Args p
                 float* c = p.C + (size_t)m * p.ldc + n;
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    if (n + e < p.N)
-                        c[e] = p.beta == 0.0f ? mul_rn(dq, (float)s[e]) : __builtin_fmaf(dq, (float)s[e], mul_rn(p.beta, c[e]));
+                    if (n + e < p.N) c[e] = smallm_out(s[e], MR == 1, t_dq, p.beta, p.beta != 0.0f ? c[e] : 0.0f);
             } else {
                 const uint32_t off = (uint32_t)((((size_t)sp.split * MR + m) * p.ncols_pad + n) * 4);
                 buf_store_x4_coherent(rp, off, __builtin_bit_cast(f32x4, s));
@@ -191,7 +231,7 @@ __global__ __launch_bounds__(kQ8Waves * 64) void dnnopt_skinny_q8(SkinnyQ8Args p
 }
 
 // Sum the int32 partials [split][M][ncols_pad] of a tile's splits (exact) and
-// store the dequantized C.  All partial loads of an output (a batch of SB,
+// store C with the small-M epilogue (smallm_out).  All partial loads of an output (a batch of SB,
 // the smallest of 8, 16, 32, 64 that holds the largest split count) are
 // issued before the first add -- offsets past the tile's splits are out of
 // range and read zero -- so the sum costs one memory round trip.
@@ -217,8 +257,8 @@ __global__ __launch_bounds__(256) void dnnopt_skinny_q8_reduce(const int32_t* __
 #pragma unroll
         for (int u = 0; u < SB; ++u) s += (int32_t)v[u];  // out-of-range loads read 0
     }
-    const float dq = dyn_dequant_scale(amax, alpha);
-    *c = beta == 0.0f ? mul_rn(dq, (float)s) : __builtin_fmaf(dq, (float)s, mul_rn(beta, c_old));
+    const float t = mul_rn(alpha, mul_rn(quant_scale_bits(amax[0]), quant_scale_bits(amax[1])));
+    *c = smallm_out(s, M == 1, t, beta, c_old);
 }
 
 hipError_t launch_skinny_q8(int mr, dim3 grid, const SkinnyQ8Args& a, hipStream_t s) {

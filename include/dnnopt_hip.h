@@ -134,12 +134,18 @@ int dnnopt_hip_gemm_s8s8f32_colscale(int M, int N, int K,
                                      const float* col_scale,
                                      float* C, int ldc, void* stream);
 
-/* fp32 storage, dynamic symmetric per-tensor int8 quantization (scale =
+/* fp32 storage, dynamic symmetric per-tensor int8 quantization (scale s_X =
  * max|X|/127, or 1 for an all-zero operand; round to nearest even; clamp to
- * [-128, 127]), exact int32 contraction, then
- * C = alpha*sA*sB*acc (beta == 0) or fma(alpha*sA*sB, acc, beta*C).
- * Replaces dnnopt::gemm_int8 (src/gemm/gemm.cpp:418-455 with the packed-path
- * quantization of src/gemm/gemm_driver_generic.cpp:49-67). */
+ * [-128, 127]) and an exact int32 contraction, routed by M as the reference
+ * routes it on a CPU with I8MM (src/gemm/gemm.cpp:418-455):
+ *   M <= 8  gemm_smallm_int8 (src/gemm/gemm_smallm_int8.cpp:126-511):
+ *           q = rint(x / s_X) (true division), t = alpha*(sA*sB);
+ *           M == 1: C = t*acc (beta == 0) or fma(beta, C, t*acc);
+ *           M >= 2: C = (beta == 0 ? 0 : beta*C) + t*acc, two roundings;
+ *           DNNOPT_ERR_UNSUPPORTED when a row of B spans 2 GiB or more.
+ *   M > 8   the packed path (src/gemm/gemm_driver_generic.cpp:49-67,
+ *           src/gemm/gemm_pack_int8.cpp:29-71): q = rint(x * (1/s_X)),
+ *           C = alpha*sA*sB*acc (beta == 0) or fma(alpha*sA*sB, acc, beta*C). */
 int dnnopt_hip_gemm_int8_f32(int M, int N, int K,
                              float alpha, const float* A, int lda,
                              const float* B, int ldb,
@@ -239,8 +245,8 @@ int dnnopt_hip_plan_gemm_s8(int with_scale, int M, int N, int K,
                             dnnopt_plan* out);
 /* The GEMM launch of dnnopt_hip_gemm_int8_f32 with unpadded strides: after
  * its maxima pass, for M <= 8 the skinny kernel that quantizes B as it
- * streams it (DNNOPT_K_SKINNY_Q8), else (after a quantization pass) the int8
- * kernel that reads the quantized operands. */
+ * streams it (DNNOPT_K_SKINNY_Q8), else (after A's quantization pass) the
+ * int8 tiles that quantize the fp32 B while staging it. */
 int dnnopt_hip_plan_gemm_int8_f32(int M, int N, int K, dnnopt_plan* out);
 
 /* ---- synthetic inputs on the device ------------------------------------

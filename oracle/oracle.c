@@ -26,6 +26,15 @@
  *                         -2.5) and fractions (63.7): only round-to-nearest-
  *                         even passes (copies built with truncf or roundf
  *                         are compiled and rejected by the tests).
+ *   orc_gemm_int8_smallm  (and orc_gemm_int8, its M <= 8 / M > 8 routing)
+ *                         closed forms: max|X| = 128, x = 88.18897247 has
+ *                         x / s = 87.5 exactly (quantized 88) but
+ *                         x * (1 / s) = 87.49999 (87); the epilogues' roundings
+ *                         (M = 1: fma(beta, C, t acc); M >= 2: beta C and
+ *                         t acc rounded, then their rounded sum) by exact
+ *                         integer cases with 2^24-scale C; ties with scales
+ *                         1 and 2; copies built with the reciprocal or with
+ *                         one fused epilogue are compiled and rejected.
  *   orc_gemv_1xn_f32, orc_smallm_wide_f32, orc_adaptive_f32, orc_gemm_bf16,
  *   orc_cblas_sgemm, orc_onednn_sgemm,
  *   orc_onednn_gemm_bf16bf16f32:
@@ -383,6 +392,100 @@ void orc_gemm_int8_dynq(int M, int N, int K, float alpha, const float* A, int ld
             float* c = C + (size_t)i * ldc + j;
             *c = beta == 0.0f ? s * (float)acc : fmaf(s, (float)acc, beta * *c);
         }
+}
+
+/* ------------------------------------------------------------------------
+ * fp32-API int8 for M <= 8: the reference's gemm_smallm_int8 route, taken by
+ * gemm_int8 whenever M <= 8 on a CPU with I8MM (src/gemm/gemm.cpp:431-434).
+ *   M == 1     gemm_mx1_int8 (src/gemm/gemm_smallm_int8.cpp:126-189)
+ *   M == 2..8  gemm_smallm_int8_smmla (src/gemm/gemm_smallm_int8.cpp:198-488)
+ * Both take per-tensor scales s_X = max|X| / 127 (1 if max|X| == 0) and
+ * quantize with a true division, q = clamp(lrintf(x / s_X), -128, 127)
+ * (:151, :159, :233, :280-281) -- not the packed path's x * (1 / s_X), which
+ * rounds differently when x / s_X lies within an ulp of a half-integer.
+ * The int32 sums are exact; t = alpha * (sA * sB) (:146, :170, :223, :356).
+ *   M == 1: C = t * acc                          (beta == 0, C not read)
+ *           C = fma(beta, C, t * acc)            (beta != 0)
+ *     (:170-175: `result + beta * C[j]`, where `result` = t * acc also
+ *     feeds the beta == 0 store, so a contracting compiler -- GCC's
+ *     -ffp-contract=fast default, or clang's per-expression contraction --
+ *     can fuse only the beta * C[j] product into the addition.)
+ *   M >= 2: C is first set to 0 (beta == 0) or beta * C (beta != 1)
+ *     (:243-250), then C + t * acc is stored, two roundings (:356-383,
+ *     store_edge_tile_row :38-50; vfmaq_f32 with the factor 1.0 is the
+ *     rounded sum).
+ * Two defects of the reference's store code are fixed here, as in the
+ * library: for M = 3 the reference never stores row 2 (its second row pair
+ * is stored only when m_tile >= 4, :391), and for M = 7 it adds zeros to a
+ * row 7 past the end of C (:445); this restatement stores rows 0..M-1.
+ *
+ * ORC_SMALLM_RECIP / ORC_SMALLM_FUSED exist only so that tests can build
+ * deliberately wrong copies (reciprocal quantization; one fused epilogue)
+ * and show that the closed-form tests reject them.
+ * ---------------------------------------------------------------------- */
+static int8_t quant_div(float v, float s) {
+#ifdef ORC_SMALLM_RECIP
+    float q = rintf(v * (1.0f / s));
+#else
+    float q = rintf(v / s);
+#endif
+    if (q > 127.0f) q = 127.0f;
+    if (q < -128.0f) q = -128.0f;
+    return (int8_t)(int)q;
+}
+
+void orc_gemm_int8_smallm(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
+                          float beta, float* C, int ldc) {
+    if (M < 1 || M > 8 || N <= 0 || K <= 0) return;
+    float amax_a = 0.0f, amax_b = 0.0f;
+    for (int i = 0; i < M; ++i)
+        for (int k = 0; k < K; ++k) {
+            const float av = fabsf(A[(size_t)i * lda + k]);
+            if (av > amax_a) amax_a = av;
+        }
+    for (int k = 0; k < K; ++k)
+        for (int j = 0; j < N; ++j) {
+            const float bv = fabsf(B[(size_t)k * ldb + j]);
+            if (bv > amax_b) amax_b = bv;
+        }
+    const float sa = quant_scale(amax_a), sb = quant_scale(amax_b);
+    const float t = alpha * (sa * sb);
+    int8_t* qa = (int8_t*)malloc((size_t)M * K);
+    int8_t* qb = (int8_t*)malloc((size_t)K * N);
+    for (int i = 0; i < M; ++i)
+        for (int k = 0; k < K; ++k) qa[(size_t)i * K + k] = quant_div(A[(size_t)i * lda + k], sa);
+    for (int k = 0; k < K; ++k)
+        for (int j = 0; j < N; ++j) qb[(size_t)k * N + j] = quant_div(B[(size_t)k * ldb + j], sb);
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            int32_t acc = 0;
+            for (int k = 0; k < K; ++k) acc += (int32_t)qa[(size_t)i * K + k] * (int32_t)qb[(size_t)k * N + j];
+            float* c = C + (size_t)i * ldc + j;
+            const float r = t * (float)acc;
+#ifdef ORC_SMALLM_FUSED
+            *c = beta == 0.0f ? r : fmaf(t, (float)acc, beta * *c);
+#else
+            if (M == 1) {
+                *c = beta == 0.0f ? r : fmaf(beta, *c, r);
+            } else {
+                const float c0 = beta == 0.0f ? 0.0f : (beta == 1.0f ? *c : *c * beta);
+                *c = c0 + r;
+            }
+#endif
+        }
+    free(qa);
+    free(qb);
+}
+
+/* gemm_int8's routing on the reference's target (I8MM present): M <= 8 the
+ * small-M route above, otherwise the packed path (src/gemm/gemm.cpp:431-449). */
+void orc_gemm_int8(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb, float beta,
+                   float* C, int ldc) {
+    if (M <= 0 || N <= 0 || K <= 0) return;
+    if (M <= 8)
+        orc_gemm_int8_smallm(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
+    else
+        orc_gemm_int8_dynq(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
 }
 
 /* ------------------------------------------------------------------------

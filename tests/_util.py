@@ -74,6 +74,8 @@ ORACLE_ABI = {
     "orc_gemm_s8_colscale": (None, [I, I, I, P, I, P, I, P, P, I]),
     "orc_gemm_bf16": (None, [I, I, I, F, P, I, P, I, F, P, I]),
     "orc_gemm_int8_dynq": (None, [I, I, I, F, P, I, P, I, F, P, I]),
+    "orc_gemm_int8_smallm": (None, [I, I, I, F, P, I, P, I, F, P, I]),
+    "orc_gemm_int8": (None, [I, I, I, F, P, I, P, I, F, P, I]),
     "orc_cblas_sgemm": (None, [I, I, I, I, I, I, F, P, I, P, I, F, P, I]),
     "orc_saxpy": (None, [I, F, P, I, P, I, I]),
     "orc_onednn_sgemm": (I, [ctypes.c_char, ctypes.c_char, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, F, P,
@@ -266,3 +268,70 @@ def check_dynq_ties(gemm_int8_f32):
             bad = np.argwhere(got != want)[0]
             raise AssertionError(f"int8 quantization ties ({name}): C{tuple(bad)} = {got[tuple(bad)]}, "
                                  f"want {want[tuple(bad)]}")
+
+
+# ---------------------------------------------------------------- int8 small-M route (M <= 8)
+# The reference's gemm_int8 takes gemm_smallm_int8 for M <= 8
+# (src/gemm/gemm.cpp:431-434) and its packed path above.  The two differ in
+# the quantizer (x / s against x * (1 / s)) and in the epilogue, and these
+# closed forms tell every variant apart:
+#   "division": max|B| = 128, s_B = fl(128 / 127); x = 88.18897247314453 has
+#     x / s_B = 87.5 exactly in fp32 (quantized 88, ties to even) but
+#     x * fl(1 / s_B) = 87.49999 (87) (src/gemm/gemm_smallm_int8.cpp:159,
+#     280-281 against src/gemm/gemm_pack_int8.cpp:66-71).  A = [127] (s_A = 1),
+#     so C = fl(s_B * 127 q) with q = 127 for the column holding 128.
+#   "beta-fma" (scales 1, acc = 1, alpha = 2^-24, beta = fl(1/3), C = 3):
+#     beta * C = 1 + 2^-25 exactly.  M = 1 (`result + beta * C[j]`, the
+#     beta * C product fused, :170-175): fl(1 + 2^-25 + 2^-24) = 1 + 2^-23.
+#     M >= 2 (beta * C rounded to 1 first, :243-250, then C + t acc,
+#     :356-383): fl(1 + 2^-24) = 1 (tie, even).  Packed path
+#     fma(t, acc, fl(beta C)): 1.
+#   "fused-sum" (scales 1, acc = 3, alpha = fl(1/3), beta = 1, C = 2^24):
+#     t acc = 1 + 2^-25 exactly, rounded alone to 1.  M = 1 and M >= 2:
+#     fl(2^24 + 1) = 2^24 (tie, even); packed path fma(t, acc, C) =
+#     fl(2^24 + 1 + 2^-25) = 2^24 + 2.
+#   "zero-sign" (acc = 0, alpha = -1, beta = 0): t acc = -0.  M = 1 stores it
+#     (-0); M >= 2 stores 0 + (-0) = +0; the packed path stores -0.
+DIV_PIN_X = 88.18897247314453
+_S128 = np.float32(128.0) / np.float32(127.0)
+
+
+def int8_route_cases(M):
+    """(name, N, K, A (M x K), B (K x N), alpha, beta, C0 (M x N), want)
+    for the fp32-API gemm_int8 at M rows; want is the reference's result for
+    M's route (M <= 8 small-M, else packed)."""
+    small = M <= 8
+    f32 = np.float32
+    out = []
+    A = np.full((M, 1), 127.0, f32)
+    B = np.array([[128.0, DIV_PIN_X]], f32)
+    q = 88 if small else 87
+    want = np.tile(np.array([_S128 * f32(127 * 127), _S128 * f32(127 * q)], f32), (M, 1))
+    out.append(("division", 2, 1, A, B, 1.0, 0.0, np.full((M, 2), np.nan, f32), want))
+    A = np.tile(np.array([[127.0, 1.0, 0.0]], f32), (M, 1))
+    B = np.array([[0.0], [1.0], [127.0]], f32)
+    one_third = float(f32(1.0) / f32(3.0))
+    w = f32(1.0 + 2.0 ** -23) if M == 1 else f32(1.0)
+    out.append(("beta-fma", 1, 3, A, B, 2.0 ** -24, one_third, np.full((M, 1), 3.0, f32), np.full((M, 1), w, f32)))
+    B = np.array([[0.0], [3.0], [127.0]], f32)
+    w = f32(2.0 ** 24) if small else f32(2.0 ** 24 + 2)
+    out.append(("fused-sum", 1, 3, A, B, one_third, 1.0, np.full((M, 1), 2.0 ** 24, f32),
+                np.full((M, 1), w, f32)))
+    A = np.tile(np.array([[127.0, 0.0]], f32), (M, 1))
+    B = np.array([[0.0], [127.0]], f32)
+    w = f32(0.0) if (small and M > 1) else f32(-0.0)
+    out.append(("zero-sign", 1, 2, A, B, -1.0, 0.0, np.full((M, 1), np.nan, f32), np.full((M, 1), w, f32)))
+    return out
+
+
+def check_int8_routes(gemm_int8_f32, Ms=(1, 2, 3, 5, 7, 8, 9, 20)):
+    """gemm_int8_f32(M, N, K, A, B, alpha, beta, C0) -> C (M x N float32).
+    Raises AssertionError naming the first case and M whose C differs in any
+    bit from the reference's closed form."""
+    for M in Ms:
+        for name, N, K, A, B, alpha, beta, C0, want in int8_route_cases(M):
+            got = np.asarray(gemm_int8_f32(M, N, K, A, B, alpha, beta, C0), np.float32).reshape(M, N)
+            if not np.array_equal(got.view(np.uint32), want.view(np.uint32)):
+                bad = tuple(np.argwhere(got.view(np.uint32) != want.view(np.uint32))[0])
+                raise AssertionError(f"int8 route closed form ({name}, M={M}): C{bad} = {got[bad]!r}, "
+                                     f"want {want[bad]!r}")

@@ -82,16 +82,26 @@ def test_random_shape(lib, dev, case):
         dC = dc(C0)
         lib.gemm_int8_f32(M, N, K, alpha, dc(A), lda, dc(B), ldb, beta, dC, ldc, stream=s)
         got = dC.cpu().numpy()
-        # scale_X = max|X| / 127 (1 if zero), q = clamp(rint(x * (1 / s)))
+        # scale_X = max|X| / 127 (1 if zero); M <= 8 (the reference's small-M
+        # route): q = clamp(rint(x / s)), else q = clamp(rint(x * (1 / s)))
         sa = np.float32(np.abs(A[:, :K]).max()) / np.float32(127)
         sb = np.float32(np.abs(B[:, :N]).max()) / np.float32(127)
         sa, sb = (sa if sa != 0 else np.float32(1)), (sb if sb != 0 else np.float32(1))
-        qa = np.clip(np.rint(A[:, :K] * (np.float32(1) / sa)), -128, 127).astype(np.int64)
-        qb = np.clip(np.rint(B[:, :N] * (np.float32(1) / sb)), -128, 127).astype(np.int64)
+        if M <= 8:
+            qa = np.clip(np.rint(A[:, :K] / sa), -128, 127).astype(np.int64)
+            qb = np.clip(np.rint(B[:, :N] / sb), -128, 127).astype(np.int64)
+        else:
+            qa = np.clip(np.rint(A[:, :K] * (np.float32(1) / sa)), -128, 127).astype(np.int64)
+            qb = np.clip(np.rint(B[:, :N] * (np.float32(1) / sb)), -128, 127).astype(np.int64)
         acc = (qa @ qb).astype(np.float32)
         dq = np.float32(np.float32(sa * sb) * np.float32(alpha))
+        r = dq * acc
         if beta == 0.0:
-            want = dq * acc
+            want = r + np.float32(0) if 1 < M <= 8 else r  # M 2..8 store 0 + t acc
+        elif M == 1:  # fma(beta, C, t acc): one rounding of the exact sum
+            want = (np.float64(beta) * C0[:, :N].astype(np.float64) + r.astype(np.float64)).astype(np.float32)
+        elif M <= 8:  # beta C, then the rounded sum
+            want = (C0[:, :N] * np.float32(beta)) + r
         else:  # fma(dq, acc, beta * C): one rounding of the exact sum
             want = (np.float64(dq) * acc.astype(np.float64) + (np.float32(beta) * C0[:, :N]).astype(np.float64))
             want = want.astype(np.float32)

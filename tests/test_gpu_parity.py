@@ -675,7 +675,7 @@ def test_int8_dynamic_quant_matches_oracle(lib, orc, dev, M, N, K):
     A, B, C0 = u.uniform(orc, M * K, 1), u.uniform(orc, K * N, 2), u.uniform(orc, M * N, 3)
     for beta in (0.0, 0.5):
         Co = C0.copy()
-        orc.orc_gemm_int8_dynq(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, beta, u.ptr(Co), N)
+        orc.orc_gemm_int8(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, beta, u.ptr(Co), N)
         dC = dev_copy(C0, dev)
         lib.gemm_int8_f32(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, beta, dC, N, stream=stream())
         assert np.array_equal(host(dC).view(np.uint32), Co.view(np.uint32))
@@ -693,7 +693,7 @@ def test_int8_dynamic_quant_padded_strides(lib, orc, dev, M, N, K, pa, pb):
     B[:, :N] = u.normal(orc, K * N, 2, 0, 0.02).reshape(K, N)
     C0 = u.uniform(orc, M * ldc, 3).reshape(M, ldc)
     Co, Ak, Bn = C0.copy(), np.ascontiguousarray(A[:, :K]), np.ascontiguousarray(B[:, :N])
-    orc.orc_gemm_int8_dynq(M, N, K, 0.75, u.ptr(Ak), K, u.ptr(Bn), N, 0.5, u.ptr(Co), ldc)
+    orc.orc_gemm_int8(M, N, K, 0.75, u.ptr(Ak), K, u.ptr(Bn), N, 0.5, u.ptr(Co), ldc)
     dC = dev_copy(C0, dev)
     lib.gemm_int8_f32(M, N, K, 0.75, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, 0.5, dC, ldc, stream=stream())
     assert np.array_equal(host(dC).view(np.uint32), Co.view(np.uint32))
@@ -710,6 +710,79 @@ def test_int8_dynamic_quant_rounding_ties(lib, dev):
         return host(dC)
 
     u.check_dynq_ties(run)
+
+
+def _gpu_int8(lib, dev, a_scale=1.0, b_scale=1.0, alpha_scale=1.0):
+    """gemm_int8_f32 through the C-ABI for check_int8_routes; A and B are
+    scaled by powers of two and alpha by their inverse, which leaves every
+    quantized value and the dequantization factor unchanged."""
+
+    def run(M, N, K, A, B, alpha, beta, C0):
+        dA = dev_copy((np.asarray(A, np.float64) * a_scale).astype(np.float32), dev)
+        dB = dev_copy((np.asarray(B, np.float64) * b_scale).astype(np.float32), dev)
+        dC = dev_copy(C0, dev)
+        lib.gemm_int8_f32(M, N, K, float(np.float32(alpha * alpha_scale)), dA, K, dB, N, beta, dC, N,
+                          stream=stream())
+        return host(dC)
+
+    return run
+
+
+def test_int8_route_closed_forms(lib, dev):
+    """The reference's two gemm_int8 routes on closed-form inputs (division
+    quantizer and small-M epilogues at M <= 8, the packed path above),
+    independent of the oracle: every bit of C is fixed by the arithmetic."""
+    u.check_int8_routes(_gpu_int8(lib, dev))
+
+
+@pytest.mark.parametrize("b_scale", [2.0 ** -80, 2.0 ** -60, 2.0 ** 60, 2.0 ** 80])
+def test_int8_route_closed_forms_extreme_scales(lib, dev, b_scale):
+    """Scales outside [2^-64, 2^64] take the exact division (2^-80, 2^80), the
+    others the reciprocal with one correction (2^-60, 2^60): same bits."""
+    u.check_int8_routes(_gpu_int8(lib, dev, b_scale=b_scale, alpha_scale=1.0 / b_scale), Ms=(1, 3, 8, 9))
+
+
+def test_int8_smallm_far_apart_rows_of_a(lib, orc, dev):
+    """Rows of A 2^28 floats apart ((M - 1) * lda * 4 >= 2^31 bytes): the
+    small-M kernel reads A through 64-bit addresses."""
+    M, N, K = 3, 777, 300
+    lda = (1 << 28) + 64
+    A = u.uniform(orc, M * K, 1).reshape(M, K)
+    B = u.normal(orc, K * N, 2, 0, 0.5).reshape(K, N)
+    dA = torch.zeros((M - 1) * lda + K, dtype=torch.float32, device=dev)
+    for m in range(M):
+        dA[m * lda:m * lda + K] = torch.from_numpy(A[m]).to(dev)
+    C0 = u.uniform(orc, M * N, 3)
+    Co = C0.copy()
+    orc.orc_gemm_int8(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 0.5, u.ptr(Co), N)
+    dC = dev_copy(C0, dev)
+    lib.gemm_int8_f32(M, N, K, 1.0, dA, lda, dev_copy(B, dev), N, 0.5, dC, N, stream=stream())
+    got = host(dC)
+    del dA
+    assert np.array_equal(got.view(np.uint32), Co.view(np.uint32))
+
+
+def test_int8_f32_large_c_stride(lib, orc, dev):
+    """M > 8 with a C stride past the 64-row q8b tiles' 31-bit offsets
+    (64 * ldc * 4 >= 2^31): the call takes the quantization pass and the
+    planner-checked int8 kernels instead, bit-exact."""
+    M, N, K = 64, 500, 256
+    ldc = (1 << 23) + 300000
+    assert 64 * ldc * 4 >= 2 ** 31
+    A = u.uniform(orc, M * K, 1).reshape(M, K)
+    B = u.normal(orc, K * N, 2, 0, 0.5).reshape(K, N)
+    C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    Co = C0.copy()
+    orc.orc_gemm_int8(M, N, K, 0.5, u.ptr(A), K, u.ptr(B), N, 0.25, u.ptr(Co), N)
+    dC = torch.full(((M - 1) * ldc + N,), 7.0, dtype=torch.float32, device=dev)
+    rows = torch.as_strided(dC, (M, N), (ldc, 1))
+    rows.copy_(torch.from_numpy(C0).to(dev))
+    lib.gemm_int8_f32(M, N, K, 0.5, dev_copy(A, dev), K, dev_copy(B, dev), N, 0.25, dC, ldc, stream=stream())
+    got = host(rows.contiguous())
+    gap = host(dC[N:N + 1000])
+    del dC, rows
+    assert np.array_equal(got.view(np.uint32), Co.view(np.uint32))
+    assert (gap == 7.0).all()
 
 
 # ---------------------------------------------------------------- saxpy, C++ and BLAS APIs on host memory
@@ -794,7 +867,7 @@ def test_cxx_api_host_and_device_pointers(lib, orc, dev):
     u.assert_fp32_close(Cbb.reshape(M, N), wb, sb, K, "gemm_bf16_bf16bf16f32 host")
     Ci, Cio = C0.copy(), C0.copy()
     lib.cxx["gemm_int8"](M, N, K, 1.0, A.ctypes.data, K, B.ctypes.data, N, 0.5, Ci.ctypes.data, N)
-    orc.orc_gemm_int8_dynq(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 0.5, u.ptr(Cio), N)
+    orc.orc_gemm_int8(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 0.5, u.ptr(Cio), N)
     assert np.array_equal(Ci.view(np.uint32), Cio.view(np.uint32))
     A8, B8 = u.ints8(orc, M * K, 1), u.ints8(orc, N * K, 2)
     C8 = np.zeros(M * N, np.int32)
@@ -1015,7 +1088,7 @@ def test_int8_dynamic_quant_sweep(lib, orc, dev, M, N, K, pa, pb, alpha, beta):
     B[:, :N] = u.uniform(orc, K * N, 2).reshape(K, N)
     C0 = u.uniform(orc, M * ldc, 3).reshape(M, ldc)
     Co, Ak, Bn = C0.copy(), np.ascontiguousarray(A[:, :K]), np.ascontiguousarray(B[:, :N])
-    orc.orc_gemm_int8_dynq(M, N, K, alpha, u.ptr(Ak), K, u.ptr(Bn), N, beta, u.ptr(Co), ldc)
+    orc.orc_gemm_int8(M, N, K, alpha, u.ptr(Ak), K, u.ptr(Bn), N, beta, u.ptr(Co), ldc)
     dC = dev_copy(C0 if beta != 0.0 else np.where(np.arange(ldc)[None, :] < N, np.nan, C0).astype(np.float32), dev)
     lib.gemm_int8_f32(M, N, K, alpha, dev_copy(A, dev), lda, dev_copy(B, dev), ldb, beta, dC, ldc, stream=stream())
     got = host(dC)

@@ -249,12 +249,12 @@ def test_int8_dynq_closed_form(orc):
     assert C2.tolist() == [2.5, -3.5]
 
 
-def _oracle_dynq(so):
+def _oracle_dynq(so, fn="orc_gemm_int8_dynq"):
     def run(M, N, K, A, B):
         A = np.ascontiguousarray(A, np.float32)
         B = np.ascontiguousarray(B, np.float32)
         C = np.full(M * N, np.nan, np.float32)
-        so.orc_gemm_int8_dynq(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 0.0, u.ptr(C), N)
+        getattr(so, fn)(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 0.0, u.ptr(C), N)
         return C
 
     return run
@@ -289,14 +289,92 @@ def test_int8_dynq_ties_reject_other_roundings(tmp_path, wrong):
         u.check_dynq_ties(_oracle_dynq(bad))
 
 
+def _oracle_int8(so, fn="orc_gemm_int8"):
+    def run(M, N, K, A, B, alpha, beta, C0):
+        A = np.ascontiguousarray(A, np.float32)
+        B = np.ascontiguousarray(B, np.float32)
+        C = np.ascontiguousarray(C0, np.float32).copy()
+        getattr(so, fn)(M, N, K, alpha, u.ptr(A), K, u.ptr(B), N, beta, u.ptr(C), N)
+        return C
+
+    return run
+
+
+def test_int8_route_closed_forms(orc):
+    """gemm_int8's two routes (M <= 8 small-M, M > 8 packed) on inputs whose
+    results the arithmetic fixes: the small-M division quantizer (87.5 -> 88
+    where the reciprocal gives 87), the M = 1 and M >= 2 epilogues and the
+    packed path's fused one, and the sign of a zero result."""
+    u.check_int8_routes(_oracle_int8(orc))
+    # The ties (scales 1 and 2: division and reciprocal agree) hold on both routes.
+    u.check_dynq_ties(_oracle_dynq(orc, "orc_gemm_int8"))
+
+
+@pytest.mark.parametrize("define,case", [("ORC_SMALLM_RECIP", "division"), ("ORC_SMALLM_FUSED", "beta-fma")])
+def test_int8_route_rejects_planted(tmp_path, define, case):
+    """Copies of the oracle whose small-M route quantizes with the reciprocal,
+    or uses one fused epilogue, are built and rejected by the closed forms."""
+    import ctypes
+    import shutil
+    import subprocess
+
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler on this host")
+    so_path = tmp_path / f"liboracle_{define}.so"
+    subprocess.run([cc, "-O1", "-fPIC", "-ffp-contract=off", "-fopenmp", "-std=c11", "-shared", f"-D{define}",
+                    "-o", str(so_path), os.path.join(u.ROOT, "oracle", "oracle.c"), "-lm"], check=True)
+    bad = ctypes.CDLL(str(so_path))
+    res, args = u.ORACLE_ABI["orc_gemm_int8"]
+    bad.orc_gemm_int8.restype = res
+    bad.orc_gemm_int8.argtypes = args
+    with pytest.raises(AssertionError, match=f"closed form \\({case}"):
+        u.check_int8_routes(_oracle_int8(bad))
+
+
+def test_int8_smallm_stores_rows_0_to_m_minus_1(orc):
+    """The reference's M = 3 store skips row 2 and its M = 7 store adds zeros
+    to a row 7 past C (src/gemm/gemm_smallm_int8.cpp:391, 445); the
+    restatement stores exactly rows 0..M-1."""
+    name, N, K, A, B, alpha, beta, C0, want = u.int8_route_cases(3)[0]
+    C = _oracle_int8(orc)(3, N, K, A, B, alpha, beta, C0).reshape(3, N)
+    assert np.array_equal(C, want)  # row 2 written (the defect leaves 0 there)
+    name, N, K, A, B, alpha, beta, C0, want = u.int8_route_cases(7)[0]
+    buf = np.full((8, N), -0.0, np.float32)  # the defect would turn row 7's -0 into +0
+    buf[:7] = C0
+    orc.orc_gemm_int8(7, N, K, alpha, u.ptr(A), K, u.ptr(B), N, beta, u.ptr(buf), N)
+    assert np.array_equal(buf[:7], want)
+    assert np.array_equal(buf[7].view(np.uint32), np.full(N, 0x80000000, np.uint32))
+
+
+def test_int8_smallm_matches_dynq_when_division_is_exact(orc):
+    """With power-of-two scales (max|X| = 127 * 2^e) division and reciprocal
+    agree, and with beta = 0 and alpha > 0 the epilogues agree too: the two
+    routes then give the same bits (special case that reduces to the packed
+    restatement)."""
+    for M, N, K in [(1, 37, 19), (4, 64, 100), (8, 13, 257)]:
+        A = u.small_ints(orc, M * K, 1, 127)
+        A[0] = 127.0
+        B = (u.small_ints(orc, K * N, 2, 127) * 2.0).astype(np.float32)
+        B[0] = 254.0
+        C1 = np.full(M * N, np.nan, np.float32)
+        C2 = np.full(M * N, np.nan, np.float32)
+        orc.orc_gemm_int8_smallm(M, N, K, 0.5, u.ptr(A), K, u.ptr(B), N, 0.0, u.ptr(C1), N)
+        orc.orc_gemm_int8_dynq(M, N, K, 0.5, u.ptr(A), K, u.ptr(B), N, 0.0, u.ptr(C2), N)
+        assert np.array_equal(C1.view(np.uint32), C2.view(np.uint32))
+        want = 0.5 * 2.0 * (A.reshape(M, K).astype(np.float64) @ (B.reshape(K, N) / 2.0).astype(np.float64))
+        assert np.array_equal(C1.reshape(M, N), want.astype(np.float32))
+
+
 def test_int8_dynq_reference_tolerance(orc):
     # tests/test_gemm_correctness.cpp:145 bounds the int8 path by K * 2e-2.
     for M, N, K in [(1, 128, 64), (7, 13, 5), (3, 3, 1000), (13, 17, 19)]:
         A, B = u.uniform(orc, M * K, 1), u.uniform(orc, K * N, 2)
-        C = np.zeros(M * N, np.float32)
-        orc.orc_gemm_int8_dynq(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 0.0, u.ptr(C), N)
-        want, _ = u.exact(A.reshape(M, K), B.reshape(K, N))
-        assert np.abs(C.reshape(M, N) - want).max() < K * 2e-2
+        for fn in ("orc_gemm_int8_dynq", "orc_gemm_int8"):
+            C = np.zeros(M * N, np.float32)
+            getattr(orc, fn)(M, N, K, 1.0, u.ptr(A), K, u.ptr(B), N, 0.0, u.ptr(C), N)
+            want, _ = u.exact(A.reshape(M, K), B.reshape(K, N))
+            assert np.abs(C.reshape(M, N) - want).max() < K * 2e-2, (fn, M, N, K)
 
 
 def test_colscale_is_one_rounding(orc):
