@@ -673,203 +673,6 @@ def _graph_time_us(torch, stream, launches, reps=5):
     return statistics.median(out)
 
 
-def probe(which):
-    """Floors the routing decisions are judged against (one JSON line each):
-      launch   the cost of one empty kernel launch in a graph;
-      read     contiguous streaming reads of the byte counts of B at C1 / C2
-               (and 1 GiB): the HBM read ceiling per size;
-      tiles    the skinny kernel's access pattern without its arithmetic at
-               the C1 / C2 shapes, with the planner's workgroup count;
-      combine  the C1 and C2 workloads with the k-split partials combined by
-               the separate reduce kernel (default) and by the last-arriving
-               workgroup (DNNOPT_SPLIT_REDUCE=0), each in its own process;
-      overlap  LDS reads, loads into registers and bf16 MFMAs of the same
-               waves, alone and together (one workgroup of 8 waves per CU):
-               whether the LDS-staged tile kernels can hide one behind the
-               other;
-      dma      the LDS-DMA copy pattern of the int8 64 x 32 tile (384 KiB per
-               CU) from L2-resident and from HBM-resident sources;
-      narrow   C2's matrices read as narrow column strips, all of k in one
-               workgroup (no k-split across workgroups, no partial sums);
-      hostapi  C1 / C2 through cblas_sgemm with host (pageable numpy)
-               buffers: the PCIe-inclusive rate of the drop-in CBLAS
-               boundary (staging copies included; never the bench value);
-      mfma     sustained fp32 16x16x4 and bf16 16x16x32 MFMA rates (one or
-               two waves per SIMD, independent accumulators, no memory);
-      l2read   every workgroup reading the same 1 / 4 MiB: the L2 -> CU rate;
-      pieces   a 65536 x 256 fp32 matrix (64 MiB) read in the MFMA operand
-               layout (16 rows x 64 bytes per wave load) and as whole rows.
-    Buffers rotate over more than 600 MB so nothing is served from the
-    Infinity Cache between launches (except where a probe says L2)."""
-    import ctypes
-    import subprocess
-    import tempfile
-
-    import torch
-
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    b = _binding()
-    lib = b.load()
-    so = ctypes.CDLL(os.path.join(ROOT, "dnn-opt_amd", "lib", "libdnnopt_probe.so"))
-    so.dnnopt_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p]
-    so.dnnopt_probe_tiles.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                      ctypes.c_void_p]
-    so.dnnopt_probe_empty.argtypes = [ctypes.c_void_p]
-    so.dnnopt_probe_overlap.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                        ctypes.c_void_p]
-    so.dnnopt_probe_dma.argtypes = [ctypes.c_void_p, ctypes.c_uint, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    so.dnnopt_probe_narrow.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                       ctypes.c_void_p]
-    so.dnnopt_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                     ctypes.c_void_p]
-    so.dnnopt_probe_l2read.argtypes = [ctypes.c_void_p, ctypes.c_uint, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
-    so.dnnopt_probe_pieces.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-                                       ctypes.c_void_p]
-    for fn in (so.dnnopt_probe_read, so.dnnopt_probe_tiles, so.dnnopt_probe_empty, so.dnnopt_probe_overlap,
-               so.dnnopt_probe_dma, so.dnnopt_probe_narrow, so.dnnopt_probe_mfma, so.dnnopt_probe_l2read,
-               so.dnnopt_probe_pieces):
-        fn.restype = ctypes.c_int
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
-    stream = torch.cuda.Stream(device=dev)
-    sp = stream.cuda_stream
-    out = torch.zeros(1, dtype=torch.float32, device=dev)
-    lines = []
-
-    def emit(d):
-        lines.append(d)
-        print(json.dumps(d), flush=True)
-
-    def check(rc):
-        if rc != 0:
-            raise RuntimeError(f"probe launch failed (status {rc})")
-
-    if which in ("launch", "all"):
-        us = _graph_time_us(torch, stream, [lambda: check(so.dnnopt_probe_empty(sp))] * 64)
-        emit({"probe": "launch", "us_per_launch": round(us, 3)})
-    shapes = [(1, 4096, 4096)] + [(M, N, 2048) for M in (2, 7) for N in (1009, 4099, 11003)]
-    if which in ("read", "all"):
-        for nbytes in sorted({4 * K * N for _, N, K in shapes} | {1 << 30}):
-            nbytes = nbytes // 16 * 16
-            copies = max(2, -(-(600 << 20) // nbytes))
-            bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1) for _ in range(copies)]
-            launches = [lambda x=x: check(so.dnnopt_probe_read(x.data_ptr(), nbytes, out.data_ptr(), sp))
-                        for x in bufs] * max(1, 32 // copies)
-            us = _graph_time_us(torch, stream, launches)
-            emit({"probe": "read", "bytes": nbytes, "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1)})
-            del bufs
-    if which in ("tiles", "all"):
-        for M, N, K in shapes:
-            if N % 4:
-                N4 = N + 4 - N % 4  # the probe reads whole 16-byte chunks: next multiple of 4 columns
-            else:
-                N4 = N
-            G = lib.plan_sgemm(M, N, K)["grid_x"]
-            nbytes = 4 * K * N4
-            copies = max(2, -(-(600 << 20) // nbytes))
-            bufs = [torch.ones(K * N4, dtype=torch.float32, device=dev) for _ in range(copies)]
-            launches = [lambda x=x: check(so.dnnopt_probe_tiles(x.data_ptr(), N4, K, G, out.data_ptr(), sp))
-                        for x in bufs] * max(1, 32 // copies)
-            us = _graph_time_us(torch, stream, launches)
-            emit({"probe": "tiles", "M": M, "N": N4, "K": K, "workgroups": G, "bytes": nbytes, "us": round(us, 3),
-                  "GBps": round(nbytes / us / 1e3, 1)})
-            del bufs
-    if which in ("overlap", "all"):
-        src = torch.ones(1 << 21, dtype=torch.uint8, device=dev)
-        iters = 2000
-        for mode, name in ((1, "lds"), (2, "mfma"), (3, "lds+mfma"), (4, "vmem"), (6, "vmem+mfma")):
-            us = _graph_time_us(torch, stream, [lambda m=mode: check(so.dnnopt_probe_overlap(
-                m, src.data_ptr(), cus, iters, out.data_ptr(), sp))] * 4)
-            emit({"probe": "overlap", "mode": name, "ns_per_iter": round(us * 1e3 / iters, 1),
-                  "per_cu_iter": {"lds_read_KiB": 80 if mode & 1 else 0, "bf16_mfma_16x16x32": 96 if mode & 2 else 0,
-                                  "vmem_KiB": 32 if mode & 4 else 0}})
-        del src
-    if which in ("dma", "all"):
-        region = 96 * 4096
-        for name, nreg, copies in (("L2", 32, 1), ("HBM", cus, max(2, -(-(600 << 20) // (cus * region))))):
-            bufs = [torch.ones(nreg * region, dtype=torch.uint8, device=dev) for _ in range(copies)]
-            launches = [lambda x=x: check(so.dnnopt_probe_dma(x.data_ptr(), nreg, cus, out.data_ptr(), sp))
-                        for x in bufs] * max(1, 32 // copies)
-            us = _graph_time_us(torch, stream, launches)
-            emit({"probe": "dma", "source": name, "bytes_per_cu": region, "us": round(us, 3),
-                  "GBps_per_cu": round(region / us / 1e3, 1), "GBps_total": round(cus * region / us / 1e3, 1)})
-            del bufs
-    if which in ("narrow", "all"):
-        for N in (1012, 4100, 11004):
-            K = 2048
-            nbytes = 4 * K * N
-            copies = max(2, -(-(600 << 20) // nbytes))
-            bufs = [torch.ones(K * N, dtype=torch.float32, device=dev) for _ in range(copies)]
-            for cols in (16, 32, 64):
-                launches = [lambda x=x, c=cols: check(so.dnnopt_probe_narrow(x.data_ptr(), N, K, c, out.data_ptr(), sp))
-                            for x in bufs] * max(1, 32 // copies)
-                us = _graph_time_us(torch, stream, launches)
-                emit({"probe": "narrow", "N": N, "K": K, "cols": cols, "workgroups": -(-N // cols), "bytes": nbytes,
-                      "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1)})
-            del bufs
-    if which in ("mfma", "all"):
-        iters = 4000
-        for kind, name, macs in ((0, "fp32 16x16x4", 16 * 16 * 4), (1, "bf16 16x16x32", 16 * 16 * 32)):
-            for waves in (4, 8):
-                us = _graph_time_us(torch, stream, [lambda k=kind, wv=waves: check(so.dnnopt_probe_mfma(
-                    k, cus, wv, iters, out.data_ptr(), sp))] * 4)
-                flops = 2.0 * macs * 8 * iters * waves * cus
-                emit({"probe": "mfma", "kind": name, "waves_per_simd": waves // 4, "us": round(us, 2),
-                      "TFLOPs": round(flops / us / 1e6, 1)})
-    if which in ("l2read", "all"):
-        X = torch.ones(4 << 20, dtype=torch.uint8, device=dev)
-        for nbytes in (1 << 20, 4 << 20):
-            us = _graph_time_us(torch, stream, [lambda nb=nbytes: check(so.dnnopt_probe_l2read(
-                X.data_ptr(), nb, 2 * cus, out.data_ptr(), sp))] * 8)
-            emit({"probe": "l2read", "bytes_per_workgroup": nbytes, "workgroups": 2 * cus, "us": round(us, 2),
-                  "TBps": round(nbytes * 2 * cus / us / 1e6, 2)})
-        del X
-    if which in ("pieces", "all"):
-        M = 65536
-        nbytes = M * 1024
-        copies = max(2, -(-(600 << 20) // nbytes))
-        bufs = [torch.ones(M * 256, dtype=torch.float32, device=dev) for _ in range(copies)]
-        for pat, name in ((0, "16 rows x 64 B per wave load (MFMA operand layout)"), (1, "one 1 KiB row per wave load")):
-            launches = [lambda x=x, pt=pat: check(so.dnnopt_probe_pieces(x.data_ptr(), M, cus, pt, out.data_ptr(), sp))
-                        for x in bufs] * max(1, 32 // copies)
-            us = _graph_time_us(torch, stream, launches)
-            emit({"probe": "pieces", "pattern": name, "bytes": nbytes, "us": round(us, 2),
-                  "TBps": round(nbytes / us / 1e6, 2)})
-        del bufs
-    if which in ("hostapi", "all"):
-        import numpy as np
-
-        for M, N, K in shapes:
-            rng = np.random.default_rng(SEED)
-            A = rng.standard_normal((M, K), dtype=np.float32)
-            B = rng.standard_normal((K, N), dtype=np.float32)
-            C = np.zeros((M, N), dtype=np.float32)
-            ts = []
-            for rep in range(8):
-                t0 = time.perf_counter()
-                lib.cblas_sgemm(101, 111, 111, M, N, K, 1.0, A, K, B, N, 0.0, C, N)
-                ts.append(time.perf_counter() - t0)
-            us = statistics.median(ts[2:]) * 1e6
-            nbytes = 4 * (M * K + K * N + M * N)
-            emit({"probe": "hostapi", "entry": "cblas_sgemm (host buffers)", "M": M, "N": N, "K": K, "us": round(us, 1),
-                  "GBps": round(nbytes / us / 1e3, 2)})
-    if which in ("combine", "all"):
-        for wl in ("c1", "c2"):
-            for mode, env in (("reduce kernel", "1"), ("last workgroup", "0")):
-                with tempfile.TemporaryDirectory() as td:
-                    detail = os.path.join(td, "d.jsonl")
-                    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--workload", wl, "--no-cpu",
-                                        "--detail", detail], env=dict(os.environ, DNNOPT_SPLIT_REDUCE=env),
-                                       capture_output=True, text=True, timeout=300)
-                    if r.returncode != 0:
-                        raise RuntimeError(f"bench.py --workload {wl} failed: {r.stderr[-2000:]}")
-                    d = json.loads(open(detail).read().splitlines()[-1])
-                emit({"probe": "combine", "workload": wl, "mode": mode, "us_per_step": round(d["ms_per_step"] * 1e3, 2),
-                      "GBps_step": round(d["GBps_step"], 1),
-                      "cases_us": {c["case"]: round(c["us_median"], 2) for c in d["per_case"]}})
-    return lines
-
-
 def copy_calibration(mib):
     """Plain copies of a known size: what FETCH_SIZE / WRITE_SIZE read for
     them scales the counters of the GEMM kernels to bytes."""
@@ -918,12 +721,6 @@ def main():
     ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
-    ap.add_argument("--probe", choices=["launch", "read", "tiles", "combine", "overlap", "dma", "narrow", "hostapi",
-                                        "mfma", "l2read", "pieces", "all"],
-                    default=None,
-                    help="only run the measurement probes (launch cost, read ceilings, the skinny access pattern, "
-                         "split-k combine variants, LDS / MFMA overlap, LDS-DMA copy rate, narrow strips); one JSON "
-                         "line each")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (scale for HBM byte counters)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="ARG",
@@ -933,9 +730,6 @@ def main():
     args = ap.parse_args()
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
-        return
-    if args.probe:
-        probe(args.probe)
         return
     if args.rocprof_summary:
         a = args.rocprof_summary

@@ -8,7 +8,7 @@
 namespace dnnopt {
 
 void* aligned_malloc(size_t size, size_t alignment) {
-    if (size == 0) size = 1;
+    if (size == 0) return nullptr;  // as the reference (src/utils/aligned_alloc.cpp:16)
     if (alignment < sizeof(void*)) alignment = sizeof(void*);
     void* p = nullptr;
     if (posix_memalign(&p, alignment, size) != 0) return nullptr;

@@ -165,6 +165,7 @@ int sgemm_any(int ta, int tb, int M, int N, int K, float alpha, const float* A, 
     if (dnnopt_hip_device_count() == 0) return DNNOPT_ERR_NO_DEVICE;
     int st = DNNOPT_OK;
     void* s = api_stream(&st);
+    DrainGuard drain(s);
     Operand a = stage_in(A, ta ? extent(K, M, lda, 4) : extent(M, K, lda, 4), 0, true, s, &st);
     Operand b = stage_in(B, tb ? extent(N, K, ldb, 4) : extent(K, N, ldb, 4), 1, true, s, &st);
     Operand c = stage_in(C, extent(M, N, ldc, 4), 2, naive || c_read_or_kept(beta, ldc, N), s, &st);
@@ -178,7 +179,9 @@ int sgemm_any(int ta, int tb, int M, int N, int K, float alpha, const float* A, 
     if (st != DNNOPT_OK) return st;
     st = sync_stream(s);
     if (st != DNNOPT_OK) return st;
-    return stage_out(c, s);
+    st = stage_out(c, s);
+    if (st == DNNOPT_OK) drain.release();
+    return st;
 }
 
 }  // namespace dnnopt_api
@@ -208,6 +211,7 @@ void gemm_bf16(int M, int N, int K, float alpha, const float* A, int lda, const 
             st = DNNOPT_ERR_NO_DEVICE;
         } else {
             void* s = api_stream(&st);
+            DrainGuard drain(s);
             Operand a = stage_in(A, extent(M, K, lda, 4), 0, true, s, &st);
             Operand b = stage_in(B, extent(K, N, ldb, 4), 1, true, s, &st);
             Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), s, &st);
@@ -216,6 +220,7 @@ void gemm_bf16(int M, int N, int K, float alpha, const float* A, int lda, const 
                                                 beta, (float*)c.dev, ldc, s);
             if (st == DNNOPT_OK) st = sync_stream(s);
             if (st == DNNOPT_OK) st = stage_out(c, s);
+            if (st == DNNOPT_OK) drain.release();
         }
     }
     record(st, "gemm_bf16");
@@ -231,6 +236,7 @@ void gemm_bf16_bf16bf16f32(int M, int N, int K, float alpha, const bfloat16_t* A
             st = DNNOPT_ERR_NO_DEVICE;
         } else {
             void* s = api_stream(&st);
+            DrainGuard drain(s);
             Operand a = stage_in(A, extent(M, K, lda, 2), 0, true, s, &st);
             Operand b = stage_in(B, extent(K, N, ldb, 2), 1, true, s, &st);
             Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), s, &st);
@@ -239,6 +245,7 @@ void gemm_bf16_bf16bf16f32(int M, int N, int K, float alpha, const bfloat16_t* A
                                           beta, (float*)c.dev, ldc, s);
             if (st == DNNOPT_OK) st = sync_stream(s);
             if (st == DNNOPT_OK) st = stage_out(c, s);
+            if (st == DNNOPT_OK) drain.release();
         }
     }
     record(st, "gemm_bf16_bf16bf16f32");
@@ -254,6 +261,7 @@ void gemm_int8(int M, int N, int K, float alpha, const float* A, int lda, const 
             st = DNNOPT_ERR_NO_DEVICE;
         } else {
             void* s = api_stream(&st);
+            DrainGuard drain(s);
             Operand a = stage_in(A, extent(M, K, lda, 4), 0, true, s, &st);
             Operand b = stage_in(B, extent(K, N, ldb, 4), 1, true, s, &st);
             Operand c = stage_in(C, extent(M, N, ldc, 4), 2, c_read_or_kept(beta, ldc, N), s, &st);
@@ -262,6 +270,7 @@ void gemm_int8(int M, int N, int K, float alpha, const float* A, int lda, const 
                                               beta, (float*)c.dev, ldc, s);
             if (st == DNNOPT_OK) st = sync_stream(s);
             if (st == DNNOPT_OK) st = stage_out(c, s);
+            if (st == DNNOPT_OK) drain.release();
         }
     }
     record(st, "gemm_int8");
@@ -277,6 +286,7 @@ void gemm_int8_int8int8int32(int M, int N, int K, const int8_t* A, int lda, cons
             st = DNNOPT_ERR_NO_DEVICE;
         } else {
             void* s = api_stream(&st);
+            DrainGuard drain(s);
             Operand a = stage_in(A, extent(M, K, lda, 1), 0, true, s, &st);
             Operand b = stage_in(B, extent(N, K, ldb, 1), 1, true, s, &st);
             Operand c = stage_in(C, extent(M, N, ldc, 4), 2, ldc != N, s, &st);
@@ -285,6 +295,7 @@ void gemm_int8_int8int8int32(int M, int N, int K, const int8_t* A, int lda, cons
                                              (int32_t*)c.dev, ldc, s);
             if (st == DNNOPT_OK) st = sync_stream(s);
             if (st == DNNOPT_OK) st = stage_out(c, s);
+            if (st == DNNOPT_OK) drain.release();
         }
     }
     record(st, "gemm_int8_int8int8int32");

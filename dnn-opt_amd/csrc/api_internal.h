@@ -29,6 +29,22 @@ Operand stage_in(const void* host, size_t bytes, int slot, bool copy, void* stre
 // Copy a staged operand back to host memory and wait for `stream`.
 int stage_out(const Operand& o, void* stream);
 int sync_stream(void* stream);
+// Ends a synchronous call that stages operands: unless released once the
+// results are back, it waits for `stream` (status ignored) when the call
+// returns, so that an error return never leaves an upload from, or a copy
+// into, the caller's host buffers in flight (pinned host memory is staged
+// asynchronously).
+struct DrainGuard {
+    void* stream;
+    explicit DrainGuard(void* s) : stream(s) {}
+    ~DrainGuard() {
+        if (stream) (void)sync_stream(stream);
+    }
+    DrainGuard(const DrainGuard&) = delete;
+    DrainGuard& operator=(const DrainGuard&) = delete;
+    void release() { stream = nullptr; }
+};
+
 // Bytes spanned by a rows x cols row-major block with row stride ld.
 size_t extent(int rows, int cols, int ld, size_t esize);
 

@@ -50,17 +50,19 @@ void cblas_sgemm(enum CBLAS_ORDER Order, enum CBLAS_TRANSPOSE TransA, enum CBLAS
 void cblas_saxpy(int N, float alpha, const float* X, int incX, float* Y, int incY) {
     if (N <= 0 || alpha == 0.0f) return;
     int st = DNNOPT_OK;
-    if (!X || !Y || incX <= 0 || incY <= 0) {
+    if (!X || !Y || incX < 0 || incY < 0) {
         st = DNNOPT_ERR_INVALID_ARG;
     } else if (dnnopt_hip_device_count() == 0) {
         st = DNNOPT_ERR_NO_DEVICE;
     } else {
         void* s = api_stream(&st);
+        DrainGuard drain(s);
         Operand x = stage_in(X, ((size_t)(N - 1) * incX + 1) * 4, 0, true, s, &st);
         Operand y = stage_in(Y, ((size_t)(N - 1) * incY + 1) * 4, 2, true, s, &st);
         if (st == DNNOPT_OK) st = dnnopt_hip_saxpy(N, alpha, (const float*)x.dev, incX, (float*)y.dev, incY, s);
         if (st == DNNOPT_OK) st = sync_stream(s);
         if (st == DNNOPT_OK) st = stage_out(y, s);
+        if (st == DNNOPT_OK) drain.release();
     }
     record(st, "cblas_saxpy");
 }

@@ -25,8 +25,6 @@ int finish_launch(hipError_t e) {
     return DNNOPT_OK;
 }
 
-constexpr size_t kTicketBytes = (size_t)kMaxTickets * sizeof(unsigned);
-
 // Partial-sum space and tickets of a split-k launch: the stream's workspace,
 // or the caller's scratch when one is given.
 int take_workspace(hipStream_t s, size_t part_bytes, const ExtScratch* ext, void** part, unsigned** tickets) {
@@ -509,10 +507,7 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
             return finish_launch(launch_skinny_q8(M, L.grid, a, s));
         }
     }
-    static const bool q8b_ok = [] {
-        const char* e = getenv("DNNOPT_Q8B");
-        return !(e && *e && atoi(e) == 0);
-    }();
+    const bool q8b_ok = tunable(kTuneQ8B) != 0;
     const int ldq = (K + 15) & ~15;
     // The q8b tiles address B, their quantized A and their 64-row block of C
     // with 31-bit buffer offsets; larger strides take the quantization pass
@@ -586,7 +581,7 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
 
 int dnnopt_hip_saxpy(int N, float alpha, const float* X, int incX, float* Y, int incY, void* stream) {
     if (N <= 0 || alpha == 0.0f) return DNNOPT_OK;
-    if (!X || !Y || incX <= 0 || incY <= 0) return DNNOPT_ERR_INVALID_ARG;
+    if (!X || !Y || incX < 0 || incY < 0) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
     return finish_launch(launch_saxpy(N, alpha, X, incX, Y, incY, as_stream(stream)));
 }

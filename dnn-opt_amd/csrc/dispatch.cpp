@@ -61,58 +61,24 @@ namespace dnnopt_hip {
 
 namespace {
 
-int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    if (!v || !*v) return dflt;
-    int x = atoi(v);
-    return x > 0 ? x : dflt;
-}
-
 // k-major outer-product kernel: k-extent from which it replaces the
 // register tiles, and workgroups per CU.
 constexpr int kKOuterMinK = 32768;
-bool kouter_enabled() {
-    static const bool v = [] {
-        const char* e = getenv("DNNOPT_KOUTER");
-        return !(e && e[0] == '0');
-    }();
-    return v;
-}
-int kouter_wgs_per_cu() {
-    static int v = env_int("DNNOPT_KOUTER_WGS_PER_CU", 1);
-    return v;
-}
+bool kouter_enabled() { return tunable(kTuneKOuter) != 0; }
+int kouter_wgs_per_cu() { return std::max(1, tunable(kTuneKOuterWgsPerCu)); }
 
-int waves_per_cu() {
-    static int v = env_int("DNNOPT_WAVES_PER_CU", 8);
-    return v;
+int waves_per_cu() { return std::max(1, tunable(kTuneWavesPerCu)); }
+// Forced skinny waves per workgroup, or 0 when the planner chooses.
+int skinny_nw_forced() {
+    const int x = tunable(kTuneSkinnyNW);
+    return (x == 4 || x == 8 || x == 16) ? x : 0;
 }
-int skinny_nw() {
-    static int v = [] {
-        int x = env_int("DNNOPT_SKINNY_NW", 8);
-        return (x == 4 || x == 8 || x == 16) ? x : 8;
-    }();
-    return v;
-}
-int skinny_wgs_per_cu() {
-    static int v = env_int("DNNOPT_SKINNY_WGS_PER_CU", 1);
-    return v;
-}
-int max_splits() {
-    static int v = env_int("DNNOPT_MAX_SPLITS", 256);
-    return v;
-}
+int skinny_wgs_per_cu() { return std::max(1, tunable(kTuneSkinnyWgsPerCu)); }
+int max_splits() { return std::max(1, tunable(kTuneMaxSplits)); }
 
 }  // namespace
 
-int split_reduce_mode() {
-    static int v = [] {
-        const char* e = getenv("DNNOPT_SPLIT_REDUCE");
-        if (e && *e) return atoi(e) ? 1 : 0;
-        return 1;
-    }();
-    return v;
-}
+int split_reduce_mode() { return tunable(kTuneSplitReduce) != 0 ? 1 : 0; }
 
 namespace {
 
@@ -131,7 +97,7 @@ void fill_pub(Launch* L, int kernel, const char* name, int rows, int cols, int s
     L->pub.grid_y = (int)L->grid.y;
     L->pub.grid_z = (int)L->grid.z;
     L->pub.block = block;
-    L->pub.workspace_bytes = L->part_bytes + (L->tickets ? (size_t)kMaxTickets * sizeof(unsigned) : 0);
+    L->pub.workspace_bytes = L->part_bytes + (L->tickets ? kTicketBytes : 0);
     snprintf(L->pub.name, sizeof L->pub.name, "%s", name);
     L->family = kernel;
 }
@@ -147,8 +113,8 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
     const long long cus = num_cus();
     // Every wave should own at least one unrolled step of rows; problems too
     // small to give every CU a workgroup of 8 such waves use 4-wave groups.
-    int nw = skinny_nw();
-    if (!getenv("DNNOPT_SKINNY_NW") && T * std::max<long long>(1, K / (8ll * kSkinnyUnroll)) < cus) nw = 4;
+    int nw = skinny_nw_forced();
+    if (nw == 0) nw = T * std::max<long long>(1, K / (8ll * kSkinnyUnroll)) < cus ? 4 : 8;
     const long long smax = std::max<long long>(1, K / ((long long)nw * kSkinnyUnroll));
     // G workgroups, about skinny_wgs_per_cu() per CU, shared by the T column
     // tiles as G/T or G/T + 1 k-splits each (balanced work per workgroup).
@@ -176,7 +142,7 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
         else if (G % T * 5 <= G)
             G = G / T * T;
     }
-    static const int forced = env_int("DNNOPT_SKINNY_WGS", 0);
+    const int forced = tunable(kTuneSkinnyWgs);
     if (forced > 0) G = std::min<long long>(std::max<long long>(forced, T), T * smax);
     G = std::max<long long>(G, T);
     // Keep per-workgroup buffer offsets inside 31 bits: more splits shorten
@@ -207,7 +173,7 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
 int plan_kouter(int M, int N, int K, int lda, int ldb, Launch* L) {
     const long long cus = num_cus();
     const long long nsteps = ((long long)K + 3) / 4;
-    static const int forced_splits = env_int("DNNOPT_TILE_SPLITS", 0);
+    const int forced_splits = tunable(kTuneTileSplits);
     long long s = forced_splits > 0 ? forced_splits : cus * kouter_wgs_per_cu();
     s = std::min<long long>(s, std::max<long long>(1, nsteps / 16));
     // 32-bit offsets within one split's rows (plus one 16-row step).
@@ -249,7 +215,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
                      (transB ? ((long long)(N + 128) * ldb + K) : ((long long)K * ldb + N)) * es < 0x7FFFFFFFll &&
                      (long long)128 * ldc * 4 < 0x7FFFFFFFll;
     int cfg;
-    static const int forced_cfg = env_int("DNNOPT_TILE_CFG", 0);
+    const int forced_cfg = tunable(kTuneTileCfg);
     if (lds) {
         // 128 k per LDS block below M = 128 (fewer barriers, more bytes per
         // block in flight); measured on MI355X at N = 11008, K = 4096.
@@ -317,7 +283,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     const int waves_per_wg = c.wm * c.wn * c.kw;
     const long long cus = num_cus();
     long long s = 1;
-    static const int forced_splits = env_int("DNNOPT_TILE_SPLITS", 0);
+    const int forced_splits = tunable(kTuneTileSplits);
     if (lds) {
         // One LDS-staged workgroup per CU is the unit of work; split k only
         // when the tiles leave more than half of the CUs idle.
@@ -361,7 +327,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     // k-splits of the LDS-staged kernels are summed by a reduce kernel, except
     // for the LDS-DMA tiles (DNNOPT_TILE_TICKET=1): the last workgroup to
     // finish a tile adds the others' partials.
-    static const bool dma_ticket = env_int("DNNOPT_TILE_TICKET", 0) == 1;
+    const bool dma_ticket = tunable(kTuneTileTicket) == 1;
     const bool dma = cfg >= kTileFirstDma && cfg < kTileF32Few;  // LDS-DMA configurations
     const bool ticket_ok = !lds || (dma_ticket && dma);
     L->defer_reduce =
@@ -381,19 +347,16 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int l
     if (ldc <= 0) ldc = N;
     // The LDS-staged kernel addresses a C tile with 32-bit offsets.
     if ((long long)128 * ldc * 4 >= 0x7FFFFFFFll) lds_ok = false;
-    static const int forced_cfg = env_int("DNNOPT_S8_CFG", -1);
+    const int forced_cfg = tunable(kTuneS8Cfg);
     // M <= 4 (B is stored N x K): the row-dot kernel streams every row of B
     // once in 1 KiB steps with exact int32 dot products and needs no partial
-    // sums; DNNOPT_S8_ROWDOT=0 keeps the MFMA tiles.
-    static const bool rowdot_ok = [] {
-        const char* e = getenv("DNNOPT_S8_ROWDOT");
-        return !(e && *e && atoi(e) == 0);
-    }();
+    // sums; the kTuneS8Rowdot switch keeps the MFMA tiles when off.
+    const bool rowdot_ok = tunable(kTuneS8Rowdot) != 0;
     if (M <= kRowdotS8MaxM && rowdot_ok && forced_cfg < 0 &&
         plan_rowdot(2 + (epi ? 1 : 0), M, N, K, lda > 0 ? lda : K, ldb > 0 ? ldb : K, L) == DNNOPT_OK)
         return DNNOPT_OK;
     *L = Launch{};
-    static const int forced_splits = env_int("DNNOPT_S8_SPLITS", 0);
+    const int forced_splits = tunable(kTuneS8Splits);
     // M <= 16: 16 x 16 tiles with k split over the 8 waves of a workgroup
     // (one launch, no partial sums).  Larger M: operands copied into LDS by
     // the memory unit (LDS DMA), the largest of 64 x 64 (4 stages of
@@ -465,7 +428,7 @@ int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
     // per CU, as long as each wave keeps whole multi-step k-ranges.
     int kw = 1;
     while (kw < 8 && ceil_div(N, (kRowdotWaves / kw) * R) < 2 * cus && steps / (2 * kw) >= kSteps) kw *= 2;
-    static const int forced_kw = env_int("DNNOPT_ROWDOT_KW", 0);
+    const int forced_kw = tunable(kTuneRowdotKW);
     if (forced_kw == 1 || forced_kw == 2 || forced_kw == 4 || forced_kw == 8) kw = forced_kw;
     const long long rows_per_wg = (kRowdotWaves / kw) * R;
     const long long G = ceil_div(N, rows_per_wg);
@@ -509,7 +472,7 @@ int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int 
     const long long waves = num_cus() * tall_waves();
     int rt = 1;
     if (ceil_div(M, 32) * 4 < 3 * waves && (K < 256 || ceil_div(M, 16) * 2 < waves)) return DNNOPT_ERR_UNSUPPORTED;
-    static const int forced_rt = env_int("DNNOPT_TALL_RT", 0);
+    const int forced_rt = tunable(kTuneTallRT);
     if (forced_rt == 1 || forced_rt == 2) rt = forced_rt;
     const long long tiles = ceil_div(M, 16 * rt);
     // Persistent: one workgroup per CU by default, no more than there are row
@@ -517,7 +480,7 @@ int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int 
     // stores of different tiles overlapped; a second workgroup per CU (more
     // waves, one tile each) measured slower at every K.
     const long long per_cu = std::max<long long>(1, std::min<long long>(4, 160 * 1024 / (long long)lds));
-    static const int wgs_per_cu = env_int("DNNOPT_TALL_WGS_PER_CU", 1);
+    const int wgs_per_cu = tunable(kTuneTallWgsPerCu);
     const long long want = num_cus() * std::min<long long>(std::max(wgs_per_cu, 1), per_cu);
     const long long G = std::max<long long>(1, std::min<long long>(want, ceil_div(tiles, tall_waves())));
     L->cfg = nt;
@@ -540,10 +503,7 @@ int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, La
     // (The row-dot kernel reads B as N x K rows: never for a K x N B.)
     if (transB && M <= 8 && !transA && !few_rows_tile && plan_rowdot(0, M, N, K, lda, ldb, L) == DNNOPT_OK)
         return DNNOPT_OK;
-    static const bool tall_ok = [] {
-        const char* e = getenv("DNNOPT_TALL");
-        return !(e && *e && atoi(e) == 0);
-    }();
+    const bool tall_ok = tunable(kTuneTall) != 0;
     if (tall_ok && !transA && plan_tall(transB, M, N, K, lda, ldb, L, ldc) == DNNOPT_OK) return DNNOPT_OK;
     return plan_tile(kTileF32, transA, transB, M, N, K, lda, ldb, L, true, ldc);
 }

@@ -128,6 +128,7 @@ int onednn_common(bool bf16, const char* transa, const char* transb, const int64
     const size_t es = bf16 ? 2 : 4;
     int st = DNNOPT_OK;
     void* s = api_stream(&st);
+    DrainGuard drain(s);
     Operand a, b;
     if (*K > 0) {
         a = stage_in(A, (tA ? cm_extent(*K, *M, *lda) : cm_extent(*M, *K, *lda)) * es, 0, true, s, &st);
@@ -143,7 +144,9 @@ int onednn_common(bool bf16, const char* transa, const char* transb, const int64
     if (st != DNNOPT_OK) return st;
     st = sync_stream(s);
     if (st != DNNOPT_OK) return st;
-    return stage_out(c, s);
+    st = stage_out(c, s);
+    if (st == DNNOPT_OK) drain.release();
+    return st;
 }
 
 }  // namespace

@@ -22,7 +22,8 @@ int to_status(hipError_t e);
 // Slot 0 serves the GEMM kernels, slot 1 the int8 quantization staging.
 // The caller must hold a StreamLock for `s` from this call until its last
 // launch that uses the buffer is enqueued.
-constexpr int kMaxTickets = 16384;
+constexpr int kMaxTickets = 4096;  // ticket slots, kTicketStride words each
+constexpr size_t kTicketBytes = (size_t)kMaxTickets * kTicketStride * sizeof(unsigned);
 int get_workspace(hipStream_t s, size_t part_bytes, void** part, unsigned** tickets, int slot = 0);
 
 // Serialises the calls that enqueue work on one stream of one device (the
@@ -76,6 +77,34 @@ struct Launch {
 // Split-k reduction strategy: 0 = last-arriving workgroup (ticket),
 // 1 = separate reduce kernel.  DNNOPT_SPLIT_REDUCE overrides the default.
 int split_reduce_mode();
+
+// Tunable parameters of the planners (tune.cpp), in the order of the
+// DNNOPT_TUNE_* keys of dnnopt_hip.h.  Switches are 1 (on) / 0 (off);
+// forcing values are 0 (or -1 for kTuneS8Cfg) when the planner decides.
+enum Tunable {
+    kTuneQ8B = 0,           // fp32-API int8 M > 8: int8 tiles quantizing B while staging it
+    kTuneKOuter,            // k-outer kernel for TransA split-k shapes
+    kTuneKOuterWgsPerCu,    // its workgroups per CU
+    kTuneWavesPerCu,        // register tiles: waves per CU for the split count
+    kTuneSkinnyNW,          // skinny waves per workgroup (4, 8, 16; 0 = by size)
+    kTuneSkinnyWgsPerCu,    // skinny workgroups per CU
+    kTuneMaxSplits,         // register tiles: most k-splits
+    kTuneSplitReduce,       // split-k partials summed by a reduce kernel (1) or the last workgroup (0)
+    kTuneSkinnyWgs,         // forced skinny workgroup count
+    kTuneTileSplits,        // forced tile k-splits
+    kTuneTileCfg,           // forced tile configuration
+    kTuneTileTicket,        // LDS-DMA tiles: last-workgroup sum of their splits
+    kTuneS8Cfg,             // forced int8 tile configuration
+    kTuneS8Rowdot,          // int8 M <= 4 on the row-dot kernel
+    kTuneS8Splits,          // forced int8 k-splits
+    kTuneRowdotKW,          // forced row-dot k-split waves (1, 2, 4, 8)
+    kTuneTallRT,            // forced tall-kernel row tiles per wave (1, 2)
+    kTuneTallWgsPerCu,      // tall-kernel workgroups per CU
+    kTuneTall,              // tall-skinny kernel with B resident in LDS
+    kTuneCount
+};
+int tunable(Tunable t);
+int tunable_default(Tunable t);
 
 int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L);
 // fp32, large M, N <= 64, B small enough to stay in LDS (no transposed A).

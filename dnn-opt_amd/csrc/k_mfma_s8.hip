@@ -203,7 +203,7 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
                     }
         }
         if (p.defer_reduce) return;
-        if (!split_ticket(&p.tickets[tile_id], (unsigned)p.splits, &last_flag)) return;
+        if (!split_ticket(&p.tickets[(size_t)tile_id * kTicketStride], (unsigned)p.splits, &last_flag)) return;
         if (wk != 0) return;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)

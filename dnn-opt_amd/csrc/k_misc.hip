@@ -32,7 +32,9 @@ __global__ __launch_bounds__(256) void dnnopt_naive_f32(int M, int N, int K, flo
 #pragma clang fp contract(on)
 
 // Y[i*incy] = fma(alpha, X[i*incx], Y[i*incy])  (src/blas/cblas_saxpy.cpp:17-49
-// computes the same fused update on its NEON path).
+// computes the same fused update on its NEON path).  incx = 0 broadcasts
+// X[0] (cblas_saxpy.cpp:45-49 indexes X[i * incX]); incy > 0 gives every i
+// its own element of Y.
 __global__ __launch_bounds__(256) void dnnopt_saxpy(int n, float alpha, const float* x, int incx, float* y,
                                                    int incy) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -40,6 +42,15 @@ __global__ __launch_bounds__(256) void dnnopt_saxpy(int n, float alpha, const fl
         float* yp = y + i * (size_t)incy;
         *yp = __builtin_fmaf(alpha, x[i * (size_t)incx], *yp);
     }
+}
+
+// incy = 0: every update lands on Y[0], in i order (the reference's strided
+// loop, cblas_saxpy.cpp:45-49), so one thread applies them one after another.
+__global__ __launch_bounds__(64) void dnnopt_saxpy_one(int n, float alpha, const float* x, int incx, float* y) {
+    if (threadIdx.x != 0) return;
+    float acc = *y;
+    for (int i = 0; i < n; ++i) acc = __builtin_fmaf(alpha, x[(size_t)i * incx], acc);
+    *y = acc;
 }
 
 #pragma clang fp contract(off)
@@ -70,6 +81,10 @@ hipError_t launch_naive_f32(int M, int N, int K, float alpha, const float* A, in
 }
 
 hipError_t launch_saxpy(int n, float alpha, const float* x, int incx, float* y, int incy, hipStream_t s) {
+    if (incy == 0) {
+        hipLaunchKernelGGL(dnnopt_saxpy_one, dim3(1), dim3(64), 0, s, n, alpha, x, incx, y);
+        return hipGetLastError();
+    }
     int blocks = (n + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     hipLaunchKernelGGL(dnnopt_saxpy, dim3(blocks), dim3(256), 0, s, n, alpha, x, incx, y, incy);

@@ -141,7 +141,7 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     constexpr int ES = SkinnyTraits<MODE>::ES;
     constexpr int TW = 64 * VEC;
     constexpr int U = kSkinnyUnroll;  // rows of B in flight per wave
-    constexpr int UG = 8;             // rows per group of A values
+    constexpr int UG = U < 8 ? U : 8;  // rows per group of A values
     constexpr int NT = NW * 64;
     // LDS reduction in passes of G rows, at most 32 KiB of LDS per pass.
     constexpr int GMAX = 32768 / (NW * TW * 4) > 0 ? 32768 / (NW * TW * 4) : 1;
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
             }
         }
     if (p.defer_reduce) return;
-    if (!split_ticket(&p.tickets[tile], (unsigned)nsplit, &last_flag)) return;
+    if (!split_ticket(&p.tickets[(size_t)tile * kTicketStride], (unsigned)nsplit, &last_flag)) return;
 
     // Last workgroup of the tile: add the partials in split order.  Each
     // thread owns float4 outputs of the whole tile; C (for beta != 0) and a

@@ -129,7 +129,7 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
                     }
         }
         if (p.defer_reduce) return;
-        if (!split_ticket(&p.tickets[tile_id], (unsigned)p.splits, last_flag)) return;
+        if (!split_ticket(&p.tickets[(size_t)tile_id * kTicketStride], (unsigned)p.splits, last_flag)) return;
         if (wk != 0) return;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)

@@ -10,6 +10,11 @@
 
 namespace dnnopt_hip {
 
+// Split-k tickets (one arrival counter per output tile) lie 256 bytes apart:
+// atomics on one cache line are serialised (MI355X: 256 workgroups counting
+// on one line, +2.4 us per launch; 256 bytes apart, no measurable cost).
+constexpr int kTicketStride = 64;  // words
+
 // ---------------------------------------------------------------- skinny
 // M <= 8 rows against a row-major K x N operand B that is streamed once.
 // Workgroup (x, y) = (column tile, k-split); its NW waves split the k-range

@@ -25,7 +25,7 @@
 namespace {
 
 constexpr size_t kScratchBytes = DNNOPT_NOALLOC_SCRATCH_BYTES;
-constexpr int kTicketWords = dnnopt_hip::kMaxTickets;
+constexpr int kTicketWords = (int)(dnnopt_hip::kTicketBytes / 4);
 static_assert(kScratchBytes > (size_t)kTicketWords * 4, "scratch holds the ticket block and partials");
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];

@@ -54,8 +54,6 @@ struct Scratch {
 std::mutex g_ws_mu;
 std::map<std::pair<std::pair<int, int>, hipStream_t>, Scratch> g_ws;
 
-constexpr size_t kTicketBytes = (size_t)kMaxTickets * sizeof(unsigned);
-
 // Locks of StreamLock, per (device, stream).  Never destroyed: calls may
 // still run while the process's static objects are being torn down.
 std::mutex& lock_table_mu() {
@@ -146,17 +144,24 @@ int get_workspace(hipStream_t s, size_t part_bytes, void** part, unsigned** tick
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return to_status(e);
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    Scratch& w = g_ws[{{dev, slot}, s}];
-    if (w.ptr == nullptr || w.cap < part_bytes) {
+    // g_ws_mu guards only the map (entries are never erased, so a reference
+    // stays valid).  The entry of (device, stream) is used only under that
+    // stream's StreamLock, which the caller holds, so it is grown outside
+    // g_ws_mu: one stream's synchronize never stalls another's lookup.
+    Scratch* w = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_ws_mu);
+        w = &g_ws[{{dev, slot}, s}];
+    }
+    if (w->ptr == nullptr || w->cap < part_bytes) {
         size_t want = part_bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : part_bytes;
-        if (w.ptr) {
+        if (w->ptr) {
             // Launches already queued on this stream may still use the old buffer.
             e = hipStreamSynchronize(s);
             if (e != hipSuccess) return to_status(e);
-            (void)hipFree(w.ptr);
-            w.ptr = nullptr;
-            w.cap = 0;
+            (void)hipFree(w->ptr);
+            w->ptr = nullptr;
+            w->cap = 0;
         }
         void* p = nullptr;
         e = hipMalloc(&p, kTicketBytes + want);
@@ -170,11 +175,11 @@ int get_workspace(hipStream_t s, size_t part_bytes, void** part, unsigned** tick
             (void)hipFree(p);
             return to_status(e);
         }
-        w.ptr = p;
-        w.cap = want;
+        w->ptr = p;
+        w->cap = want;
     }
-    *tickets = static_cast<unsigned*>(w.ptr);
-    *part = static_cast<char*>(w.ptr) + kTicketBytes;
+    *tickets = static_cast<unsigned*>(w->ptr);
+    *part = static_cast<char*>(w->ptr) + kTicketBytes;
     return DNNOPT_OK;
 }
 

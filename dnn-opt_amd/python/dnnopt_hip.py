@@ -38,7 +38,7 @@ NOALLOC_SCRATCH_BYTES = 16 << 20  # DNNOPT_NOALLOC_SCRATCH_BYTES
  K_ROWDOT_BF16, K_TALL_F32, K_ROWDOT_S8, K_SKINNY_Q8) = range(13)
 
 # DNNOPT_HIP_ABI_VERSION of include/dnnopt_hip.h that these bindings follow.
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 CblasRowMajor, CblasColMajor = 101, 102
 CblasNoTrans, CblasTrans, CblasConjTrans = 111, 112, 113
@@ -102,7 +102,15 @@ C_ABI = {
     "dnnopt_hip_last_status": (_I, []),
     "dnnopt_hip_device_count": (_I, []),
     "dnnopt_hip_abi_version": (_I, []),
+    "dnnopt_hip_set_tunable": (_I, [_I, _I, POINTER(ctypes.c_int)]),
+    "dnnopt_hip_get_tunable": (_I, [_I, POINTER(ctypes.c_int)]),
 }
+
+# Keys of dnnopt_hip_set_tunable (include/dnnopt_hip.h DNNOPT_TUNE_*).
+TUNE = {"Q8B": 0, "KOUTER": 1, "KOUTER_WGS_PER_CU": 2, "WAVES_PER_CU": 3, "SKINNY_NW": 4,
+        "SKINNY_WGS_PER_CU": 5, "MAX_SPLITS": 6, "SPLIT_REDUCE": 7, "SKINNY_WGS": 8, "TILE_SPLITS": 9,
+        "TILE_CFG": 10, "TILE_TICKET": 11, "S8_CFG": 12, "S8_ROWDOT": 13, "S8_SPLITS": 14, "ROWDOT_KW": 15,
+        "TALL_RT": 16, "TALL_WGS_PER_CU": 17, "TALL": 18}
 
 BLAS_ABI = {
     "cblas_sgemm": (None, [_I, _I, _I, _I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I]),
@@ -211,6 +219,34 @@ class Lib:
 
     def last_status(self) -> int:
         return self.so.dnnopt_hip_last_status()
+
+    # ---------------------------------------------------------------- tunables
+    def set_tunable(self, name: str, value: int) -> int:
+        """Set one dispatcher tunable (TUNE key name); returns the old value."""
+        old = ctypes.c_int(0)
+        self._check(self.so.dnnopt_hip_set_tunable(TUNE[name], int(value), ctypes.byref(old)), "set_tunable")
+        return old.value
+
+    def get_tunable(self, name: str) -> int:
+        v = ctypes.c_int(0)
+        self._check(self.so.dnnopt_hip_get_tunable(TUNE[name], ctypes.byref(v)), "get_tunable")
+        return v.value
+
+    def tunables(self, **values):
+        """Context manager: set tunables for the enclosed calls, then restore them."""
+        lib = self
+
+        class _Ctx:
+            def __enter__(self):
+                self.old = {k: lib.set_tunable(k, v) for k, v in values.items()}
+                return lib
+
+            def __exit__(self, *exc):
+                for k, v in self.old.items():
+                    lib.set_tunable(k, v)
+                return False
+
+        return _Ctx()
 
     # ---------------------------------------------------------------- plans
     def plan_sgemm(self, M, N, K, transA=0, transB=0) -> dict:

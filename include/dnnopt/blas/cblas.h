@@ -39,7 +39,9 @@ void cblas_sgemm(enum CBLAS_ORDER Order,
                  float *C, int ldc);
 
 /// Y = alpha * X + Y.  Returns at once when N <= 0 or alpha == 0
-/// (cblas_saxpy.cpp:15).
+/// (cblas_saxpy.cpp:15).  Increments of 0 follow the reference's strided
+/// loop (X[0] broadcast; every update on Y[0], in order); negative ones are
+/// rejected (dnnopt_hip_last_status() reports DNNOPT_ERR_INVALID_ARG).
 void cblas_saxpy(int N, float alpha, const float *X, int incX,
                  float *Y, int incY);
 

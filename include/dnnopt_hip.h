@@ -152,7 +152,11 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K,
                              float beta, float* C, int ldc, void* stream);
 
 /* Y = alpha * X + Y (strided).  Replaces cblas_saxpy
- * (src/blas/cblas_saxpy.cpp:13-51): N <= 0 or alpha == 0 is a no-op. */
+ * (src/blas/cblas_saxpy.cpp:13-51): N <= 0 or alpha == 0 is a no-op;
+ * incX = 0 adds alpha*X[0] to every element, incY = 0 applies all N updates
+ * to Y[0] in order (the reference's strided loop, :45-49).  Negative
+ * increments are DNNOPT_ERR_INVALID_ARG (the reference would index before
+ * the start of X or Y). */
 int dnnopt_hip_saxpy(int N, float alpha, const float* X, int incX,
                      float* Y, int incY, void* stream);
 
@@ -265,7 +269,41 @@ const char* dnnopt_hip_status_string(int status);
 int dnnopt_hip_last_status(void);     /* last failure of the C++/cblas API on
                                          this thread, DNNOPT_OK if none      */
 int dnnopt_hip_device_count(void);    /* 0 when no device is visible        */
-#define DNNOPT_HIP_ABI_VERSION 3
+
+/* ---- tunable parameters of the shape dispatcher -------------------------
+ * No counterpart in the reference (its tile choice is an autotuned cache,
+ * src/gemm/gemm_autotune.cpp, outside this path).  Every routing or
+ * launch-shape choice the dispatcher can be steered in has a key; the
+ * library starts from built-in defaults and changes one only when a caller
+ * sets it here (process-wide, effective from the next planning call).  The
+ * default build never reads the environment; a build with -DDNNOPT_TUNING=1
+ * seeds the table once from DNNOPT_<NAME> variables.  Switches take 1 / 0;
+ * forcing keys take 0 (-1 for DNNOPT_TUNE_S8_CFG) to let the planner decide.
+ * *previous (if not NULL) receives the old value.                        */
+#define DNNOPT_TUNE_Q8B              0  /* 1: int8 tiles quantize the fp32 B while staging it */
+#define DNNOPT_TUNE_KOUTER           1  /* 1: k-outer kernel for A stored K x M, large K */
+#define DNNOPT_TUNE_KOUTER_WGS_PER_CU 2
+#define DNNOPT_TUNE_WAVES_PER_CU     3
+#define DNNOPT_TUNE_SKINNY_NW        4  /* 4, 8 or 16 waves; 0 = by problem size */
+#define DNNOPT_TUNE_SKINNY_WGS_PER_CU 5
+#define DNNOPT_TUNE_MAX_SPLITS       6
+#define DNNOPT_TUNE_SPLIT_REDUCE     7  /* 1: reduce kernel; 0: last-arriving workgroup */
+#define DNNOPT_TUNE_SKINNY_WGS       8
+#define DNNOPT_TUNE_TILE_SPLITS      9
+#define DNNOPT_TUNE_TILE_CFG        10
+#define DNNOPT_TUNE_TILE_TICKET     11
+#define DNNOPT_TUNE_S8_CFG          12
+#define DNNOPT_TUNE_S8_ROWDOT       13
+#define DNNOPT_TUNE_S8_SPLITS       14
+#define DNNOPT_TUNE_ROWDOT_KW       15
+#define DNNOPT_TUNE_TALL_RT         16
+#define DNNOPT_TUNE_TALL_WGS_PER_CU 17
+#define DNNOPT_TUNE_TALL            18
+#define DNNOPT_TUNE_COUNT           19
+int dnnopt_hip_set_tunable(int key, int value, int* previous);
+int dnnopt_hip_get_tunable(int key, int* value);
+
+#define DNNOPT_HIP_ABI_VERSION 4
 int dnnopt_hip_abi_version(void);     /* DNNOPT_HIP_ABI_VERSION; bumped on any signature change */
 
 #ifdef __cplusplus

@@ -334,6 +334,18 @@ def test_aligned_alloc(lib):
     q = lib.cxx["aligned_malloc_huge"](5 << 20, 64)
     assert q and q % 64 == 0
     lib.cxx["aligned_free_huge"](q, 5 << 20)
+    # size 0 gives no block (src/utils/aligned_alloc.cpp:16, :29), and freeing
+    # the null pointer is a no-op
+    assert not lib.cxx["aligned_malloc"](0, 64)
+    assert not lib.cxx["aligned_malloc_huge"](0, 64)
+    lib.cxx["aligned_free"](None)
+
+
+def test_aligned_malloc_zero_matches_reference(ref):
+    import ctypes
+    fn = getattr(ref, "_ZN6dnnopt14aligned_mallocEmm")
+    fn.restype, fn.argtypes = ctypes.c_void_p, [ctypes.c_size_t, ctypes.c_size_t]
+    assert fn(0, 64) is None
 
 
 def test_plans_route_lds_dma_kernels(lib):

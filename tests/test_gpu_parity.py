@@ -498,59 +498,34 @@ def test_bf16_storage_sweep(lib, orc, dev, M, N, K, tb, pa, pb, alpha, beta):
     u.assert_fp32_close(host(dC), want, scale, K, f"bf16 sweep {M}x{N}x{K} tb={tb} a={alpha} b={beta}")
 
 
-_TICKET_CHILD = r"""
-import os, sys
-import numpy as np
-import torch
-sys.path.insert(0, os.environ["TESTS_DIR"])
-import _util as u
-lib, orc = u.load_lib(), u.load_oracle()
-dev = torch.device("cuda:0")
-M, N, K = 300, 1000, 520
-A = u.bf16_bits(orc, u.normal(orc, M * K, 1)).reshape(M, K)
-B = u.bf16_bits(orc, u.normal(orc, K * N, 2, 0, 0.02)).reshape(K, N)
-C0 = u.uniform(orc, M * N, 3).reshape(M, N)
-p = lib.plan_bf16(M, N, K)
-assert p["name"] == "dnnopt_tile_bf16_dma" and p["splits"] == 2, p
-dA = torch.from_numpy(A.view(np.int16)).to(dev)
-dB = torch.from_numpy(B.view(np.int16)).to(dev)
-outs = []
-for rep in range(3):
-    dC = torch.from_numpy(C0.copy()).to(dev)
-    lib.gemm_bf16(M, N, K, 0.5, dA, K, dB, N, 1.0, dC, N, stream=torch.cuda.current_stream().cuda_stream)
-    torch.cuda.synchronize()
-    outs.append(dC.cpu().numpy())
-np.save(os.environ["OUT_NPY"], np.stack(outs))
-"""
-
-
-def test_bf16_dma_k_split_ticket_matches_reduce_kernel(orc, tmp_path):
+def test_bf16_dma_k_split_ticket_matches_reduce_kernel(lib, orc, dev):
     """A 2-way k-split of 256 x 96 LDS-DMA tiles summed by the last workgroup
-    to finish (DNNOPT_TILE_TICKET=1) gives the same bits as the reduce kernel
-    (the default), repeatably, within the fp32 bound of the exact result.
-    The options are read once per process, so each mode runs in a child."""
-    import os
-    import subprocess
-    import sys
-
-    res = {}
-    for ticket in ("0", "1"):
-        out = tmp_path / f"c{ticket}.npy"
-        env = dict(os.environ, DNNOPT_TILE_CFG="33", DNNOPT_TILE_SPLITS="2", DNNOPT_TILE_TICKET=ticket,
-                   TESTS_DIR=os.path.dirname(os.path.abspath(__file__)), OUT_NPY=str(out))
-        r = subprocess.run([sys.executable, "-c", _TICKET_CHILD], env=env, capture_output=True, text=True, timeout=300)
-        assert r.returncode == 0, r.stderr[-3000:]
-        res[ticket] = np.load(out)
+    to finish (tunable TILE_TICKET=1) gives the same bits as the reduce kernel
+    (the default), repeatably, within the fp32 bound of the exact result."""
     M, N, K = 300, 1000, 520
     A = u.bf16_bits(orc, u.normal(orc, M * K, 1)).reshape(M, K)
     B = u.bf16_bits(orc, u.normal(orc, K * N, 2, 0, 0.02)).reshape(K, N)
     C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+    dA = torch.from_numpy(A.view(np.int16)).to(dev)
+    dB = torch.from_numpy(B.view(np.int16)).to(dev)
+    res = {}
+    for ticket in (0, 1):
+        with lib.tunables(TILE_CFG=33, TILE_SPLITS=2, TILE_TICKET=ticket):
+            p = lib.plan_bf16(M, N, K)
+            assert p["name"] == "dnnopt_tile_bf16_dma" and p["splits"] == 2, p
+            outs = []
+            for rep in range(3):
+                dC = dev_copy(C0, dev)
+                lib.gemm_bf16(M, N, K, 0.5, dA, K, dB, N, 1.0, dC, N, stream=stream())
+                outs.append(host(dC))
+        res[ticket] = outs
+    assert (lib.get_tunable("TILE_CFG"), lib.get_tunable("TILE_SPLITS"), lib.get_tunable("TILE_TICKET")) == (0, 0, 0)
     want, scale = u.exact(u.bf16_value(A), u.bf16_value(B), 0.5, 1.0, C0)
     for ticket, outs in res.items():
         for o in outs:
             assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), f"ticket={ticket} not repeatable"
         u.assert_fp32_close(outs[0], want, scale, K, f"dma k-split ticket={ticket}")
-    assert np.array_equal(res["0"][0].view(np.uint32), res["1"][0].view(np.uint32))
+    assert np.array_equal(res[0][0].view(np.uint32), res[1][0].view(np.uint32))
 
 
 def test_bf16_lds_misaligned_falls_back(lib, orc, dev):
@@ -787,8 +762,8 @@ def test_int8_f32_large_c_stride(lib, orc, dev):
 
 # ---------------------------------------------------------------- saxpy, C++ and BLAS APIs on host memory
 def test_saxpy(lib, orc, dev):
-    for n, incx, incy in [(1, 1, 1), (1000, 1, 1), (777, 3, 2)]:
-        X, Y0 = u.uniform(orc, n * incx, 5), u.uniform(orc, n * incy, 6)
+    for n, incx, incy in [(1, 1, 1), (1000, 1, 1), (777, 3, 2), (500, 0, 1), (300, 2, 0), (300, 0, 0)]:
+        X, Y0 = u.uniform(orc, max(1, n * incx), 5), u.uniform(orc, max(1, n * incy), 6)
         Yo = Y0.copy()
         orc.orc_saxpy(n, 0.7, u.ptr(X), incx, u.ptr(Yo), incy, 1)
         dY = dev_copy(Y0, dev)

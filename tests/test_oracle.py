@@ -122,9 +122,11 @@ def test_int8_extremes_no_overflow(orc):
 
 
 def test_saxpy_bitwise_vs_reference(orc, ref):
-    for n, incx, incy in [(1, 1, 1), (37, 1, 1), (100, 3, 2)]:
-        X = u.uniform(orc, n * incx, 5)
-        Y0 = u.uniform(orc, n * incy, 6)
+    # increments of 0: X[0] broadcast, every update on Y[0] in order
+    # (cblas_saxpy.cpp:45-49)
+    for n, incx, incy in [(1, 1, 1), (37, 1, 1), (100, 3, 2), (50, 0, 1), (50, 2, 0), (50, 0, 0)]:
+        X = u.uniform(orc, max(1, n * incx), 5)
+        Y0 = u.uniform(orc, max(1, n * incy), 6)
         y1, y2 = Y0.copy(), Y0.copy()
         ref.ref_saxpy(n, 0.7, u.ptr(X), incx, u.ptr(y1), incy)
         orc.orc_saxpy(n, 0.7, u.ptr(X), incx, u.ptr(y2), incy, 0)

@@ -1,0 +1,85 @@
+"""The dispatcher's tunables (dnnopt_hip_set_tunable): the shipped library
+plans from built-in defaults whatever DNNOPT_* variables a process inherits,
+and changes a plan only when a caller sets a tunable explicitly.  Plans need
+no GPU (the planner assumes the MI355X's 256 CUs without one)."""
+
+import json
+import os
+import subprocess
+import sys
+
+import _util as u
+
+SHAPES = [  # (entry, M, N, K): every planner family the knobs below steer
+    ("sgemm", 1, 4096, 4096), ("sgemm", 7, 1009, 2048), ("sgemm", 7, 11003, 2048), ("sgemm", 300, 600, 2048),
+    ("sgemm", 65536, 64, 256), ("bf16", 256, 11008, 4096), ("bf16", 4, 11008, 4096), ("s8", 128, 4096, 4096),
+    ("s8", 1, 4096, 4096), ("int8_f32", 128, 4096, 4096),
+]
+
+_CHILD = r"""
+import json, os, sys
+sys.path.insert(0, os.environ["TESTS_DIR"])
+import _util as u
+from test_tunables import SHAPES, plans
+lib = u.load_lib()
+print(json.dumps({"plans": plans(lib), "tunables": {k: lib.get_tunable(k) for k in u.binding().TUNE}}))
+"""
+
+
+def plans(lib):
+    out = []
+    for entry, M, N, K in SHAPES:
+        if entry == "sgemm":
+            p = lib.plan_sgemm(M, N, K)
+        elif entry == "bf16":
+            p = lib.plan_bf16(M, N, K)
+        elif entry == "s8":
+            p = lib.plan_s8(M, N, K)
+        else:
+            p = lib.plan_int8_f32(M, N, K)
+        out.append({k: (v.decode() if isinstance(v, bytes) else v) for k, v in p.items()})
+    return out
+
+
+def _child(env_extra):
+    env = {k: v for k, v in os.environ.items() if not k.startswith("DNNOPT_")}
+    env.update(env_extra, TESTS_DIR=os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _CHILD], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-3000:]
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def test_inherited_environment_changes_no_plan():
+    base = _child({})
+    knobs = {"DNNOPT_TILE_CFG": "33", "DNNOPT_TILE_SPLITS": "2", "DNNOPT_SPLIT_REDUCE": "0",
+             "DNNOPT_SKINNY_WGS": "100", "DNNOPT_TALL": "0", "DNNOPT_S8_CFG": "2", "DNNOPT_Q8B": "0",
+             "DNNOPT_SKINNY_NW": "16", "DNNOPT_S8_ROWDOT": "0", "DNNOPT_KOUTER": "0"}
+    steered = _child(knobs)
+    assert steered["plans"] == base["plans"]
+    assert steered["tunables"] == base["tunables"]
+    assert base["tunables"]["SPLIT_REDUCE"] == 1 and base["tunables"]["S8_CFG"] == -1
+
+
+def test_explicit_tunable_changes_plan_and_restores():
+    lib = u.load_lib()
+    before = plans(lib)
+    with lib.tunables(TALL=0, SKINNY_WGS=100):
+        p = lib.plan_sgemm(65536, 64, 256)
+        assert p["name"] != "dnnopt_tall_f32", p
+        assert lib.plan_sgemm(7, 11003, 2048)["grid_x"] == 100
+    assert plans(lib) == before
+    old = lib.set_tunable("SPLIT_REDUCE", 0)
+    try:
+        assert old == 1 and lib.plan_sgemm(1, 4096, 4096)["workspace_bytes"] > 0
+    finally:
+        lib.set_tunable("SPLIT_REDUCE", old)
+
+
+def test_tunable_keys_are_checked():
+    import ctypes
+
+    lib = u.load_lib()
+    v = ctypes.c_int(0)
+    assert lib.so.dnnopt_hip_get_tunable(19, ctypes.byref(v)) != 0
+    assert lib.so.dnnopt_hip_set_tunable(-1, 0, None) != 0
+    assert lib.so.dnnopt_hip_get_tunable(7, None) != 0
