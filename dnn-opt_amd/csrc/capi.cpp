@@ -72,7 +72,7 @@ int run_skinny(const Launch& L, const void* A, int a_sm, int a_sk, const void* B
     const int b_aligned = !bf16 || ((reinterpret_cast<uintptr_t>(B) & 3u) == 0 && (ldb & 1) == 0);
     int a_layout = a_sk == 1 ? 0 : 1;
     if (bf16 && (a_sk != 1 || (reinterpret_cast<uintptr_t>(A) & 3u) != 0 || (a_sm & 1) != 0)) a_layout = 2;
-    int st = finish_launch(launch_skinny(L.mode, L.mr, L.nw, b_aligned, a_layout, L.grid, a, s));
+    int st = finish_launch(launch_skinny(L.mode, L.mr, L.nw, L.unroll, b_aligned, a_layout, L.grid, a, s));
     if (st != DNNOPT_OK || !L.defer_reduce) return st;
     return finish_launch(launch_skinny_reduce(a.part, G, T, skinny_tile_cols(L.mode), M, N, a.ncols_pad, alpha,
                                               beta, C, ldc, bias, s));

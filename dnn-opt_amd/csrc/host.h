@@ -63,6 +63,7 @@ struct Launch {
     int family = DNNOPT_K_NONE;
     int mode = 0;        // SkinnyMode / TileMode / int8 epilogue
     int mr = 0, nw = 0;  // skinny (rowdot: nw = waves splitting k)
+    int unroll = 16;     // skinny: rows of B per load block of a wave
     int cfg = 0;         // tile / int8 configuration index (tall: column tiles nt)
     size_t lds = 0;      // dynamic LDS bytes (tall)
     int bm = 0, bn = 0;  // tile shape

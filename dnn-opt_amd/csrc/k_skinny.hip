@@ -135,12 +135,14 @@ __device__ __forceinline__ void load_a_block(const SkinnyArgs& p, int k, float (
 // AL = 1: every row of B starts on a 4-byte boundary (always true for fp32);
 // AL = 0: bf16 rows may start on a 2-byte boundary and are funnel-shifted.
 // AK: layout of A, see load_a_block.
-template <int MR, int NW, int MODE, int AL, int AK>
+// U: rows of B per load block of a wave (16, or 4: on MI355X the 4-row
+// blocks stream the fp32 C1 / C2 shapes 0.5-0.7 us faster with 8-wave
+// workgroups, the 16-row ones suit the 4-wave groups of small problems).
+template <int MR, int NW, int MODE, int AL, int AK, int U>
 __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     constexpr int VEC = SkinnyTraits<MODE>::VEC;
     constexpr int ES = SkinnyTraits<MODE>::ES;
     constexpr int TW = 64 * VEC;
-    constexpr int U = kSkinnyUnroll;  // rows of B in flight per wave
     constexpr int UG = U < 8 ? U : 8;  // rows per group of A values
     constexpr int NT = NW * 64;
     // LDS reduction in passes of G rows, at most 32 KiB of LDS per pass.
@@ -238,33 +240,11 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
     };
 
     int k = k_lo;
-#if DNNOPT_SKINNY_PIPE
-    // Two blocks of U rows alternate: the loads of the next block are in
-    // flight while the current one is consumed.  At the end of the range the
-    // prefetch re-reads the last whole block (unused), keeping every load
-    // unconditional.
-    if (k + U <= k_hi) {
-        const int k_last = k_lo + ((k_hi - k_lo) / U - 1) * U;  // last whole block
-        u32x4 r0[U], r1[U];
-        load_block(r0, k);
-        for (; k + 2 * U <= k_hi; k += 2 * U) {
-            load_block(r1, k + U);
-            compute_block(r0, k);
-            load_block(r0, min(k + 2 * U, k_last));
-            compute_block(r1, k + U);
-        }
-        if (k + U <= k_hi) {
-            compute_block(r0, k);
-            k += U;
-        }
-    }
-#else
     for (; k + U <= k_hi; k += U) {
         u32x4 raw[U];
         load_block(raw, k);
         compute_block(raw, k);
     }
-#endif
     for (; k < k_hi; ++k) {
         const u32x4 raw = load_row<AL>(rs, (uint32_t)(k - kb) * rowbytes + lane_off);
         float bv[VEC];
@@ -422,46 +402,50 @@ __global__ __launch_bounds__(NW * 64) void dnnopt_skinny(SkinnyArgs p) {
 }
 
 // ---------------------------------------------------------------- launch table
-template <int MODE, int NW, int AL, int AK>
+template <int MODE, int NW, int AL, int AK, int U>
 static hipError_t launch_mr(int mr, dim3 grid, const SkinnyArgs& a, hipStream_t s) {
     dim3 block(NW * 64);
     switch (mr) {
-        case 1: hipLaunchKernelGGL((dnnopt_skinny<1, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
-        case 2: hipLaunchKernelGGL((dnnopt_skinny<2, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
-        case 3: hipLaunchKernelGGL((dnnopt_skinny<3, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
-        case 4: hipLaunchKernelGGL((dnnopt_skinny<4, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
-        case 5: hipLaunchKernelGGL((dnnopt_skinny<5, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
-        case 6: hipLaunchKernelGGL((dnnopt_skinny<6, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
-        case 7: hipLaunchKernelGGL((dnnopt_skinny<7, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
-        case 8: hipLaunchKernelGGL((dnnopt_skinny<8, NW, MODE, AL, AK>), grid, block, 0, s, a); break;
+        case 1: hipLaunchKernelGGL((dnnopt_skinny<1, NW, MODE, AL, AK, U>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((dnnopt_skinny<2, NW, MODE, AL, AK, U>), grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL((dnnopt_skinny<3, NW, MODE, AL, AK, U>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((dnnopt_skinny<4, NW, MODE, AL, AK, U>), grid, block, 0, s, a); break;
+        case 5: hipLaunchKernelGGL((dnnopt_skinny<5, NW, MODE, AL, AK, U>), grid, block, 0, s, a); break;
+        case 6: hipLaunchKernelGGL((dnnopt_skinny<6, NW, MODE, AL, AK, U>), grid, block, 0, s, a); break;
+        case 7: hipLaunchKernelGGL((dnnopt_skinny<7, NW, MODE, AL, AK, U>), grid, block, 0, s, a); break;
+        case 8: hipLaunchKernelGGL((dnnopt_skinny<8, NW, MODE, AL, AK, U>), grid, block, 0, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
 template <int MODE, int AL, int AK>
-static hipError_t launch_nw(int mr, int nw, dim3 grid, const SkinnyArgs& a, hipStream_t s) {
+static hipError_t launch_nw(int mr, int nw, int unroll, dim3 grid, const SkinnyArgs& a, hipStream_t s) {
+    if constexpr (MODE == kSkinnyF32) {
+        if (unroll == 4) return nw == 8 ? launch_mr<MODE, 8, AL, AK, 4>(mr, grid, a, s) : hipErrorInvalidValue;
+    }
+    if (unroll != 16) return hipErrorInvalidValue;
     switch (nw) {
-        case 4: return launch_mr<MODE, 4, AL, AK>(mr, grid, a, s);
-        case 8: return launch_mr<MODE, 8, AL, AK>(mr, grid, a, s);
-        case 16: return launch_mr<MODE, 16, AL, AK>(mr, grid, a, s);
+        case 4: return launch_mr<MODE, 4, AL, AK, 16>(mr, grid, a, s);
+        case 8: return launch_mr<MODE, 8, AL, AK, 16>(mr, grid, a, s);
+        case 16: return launch_mr<MODE, 16, AL, AK, 16>(mr, grid, a, s);
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_skinny(int mode, int mr, int nw, int b_aligned, int a_layout, dim3 grid, const SkinnyArgs& a,
-                         hipStream_t s) {
+hipError_t launch_skinny(int mode, int mr, int nw, int unroll, int b_aligned, int a_layout, dim3 grid,
+                         const SkinnyArgs& a, hipStream_t s) {
     switch (mode) {
         case kSkinnyF32:
-            return a_layout == 1 ? launch_nw<kSkinnyF32, 1, 1>(mr, nw, grid, a, s)
-                                 : launch_nw<kSkinnyF32, 1, 0>(mr, nw, grid, a, s);
+            return a_layout == 1 ? launch_nw<kSkinnyF32, 1, 1>(mr, nw, unroll, grid, a, s)
+                                 : launch_nw<kSkinnyF32, 1, 0>(mr, nw, unroll, grid, a, s);
         case kSkinnyBF16:
             if (b_aligned)
-                return a_layout == 2 ? launch_nw<kSkinnyBF16, 1, 2>(mr, nw, grid, a, s)
-                                     : launch_nw<kSkinnyBF16, 1, 0>(mr, nw, grid, a, s);
-            return a_layout == 2 ? launch_nw<kSkinnyBF16, 0, 2>(mr, nw, grid, a, s)
-                                 : launch_nw<kSkinnyBF16, 0, 0>(mr, nw, grid, a, s);
-        case kSkinnyF2B: return launch_nw<kSkinnyF2B, 1, 0>(mr, nw, grid, a, s);
+                return a_layout == 2 ? launch_nw<kSkinnyBF16, 1, 2>(mr, nw, unroll, grid, a, s)
+                                     : launch_nw<kSkinnyBF16, 1, 0>(mr, nw, unroll, grid, a, s);
+            return a_layout == 2 ? launch_nw<kSkinnyBF16, 0, 2>(mr, nw, unroll, grid, a, s)
+                                 : launch_nw<kSkinnyBF16, 0, 0>(mr, nw, unroll, grid, a, s);
+        case kSkinnyF2B: return launch_nw<kSkinnyF2B, 1, 0>(mr, nw, unroll, grid, a, s);
         default: return hipErrorInvalidValue;
     }
 }

@@ -43,20 +43,18 @@ struct SkinnyArgs {
     const float* bias;  // per-column bias added after the epilogue (or null)
 };
 
-#ifndef DNNOPT_SKINNY_UNROLL
-#define DNNOPT_SKINNY_UNROLL 16
-#endif
-constexpr int kSkinnyUnroll = DNNOPT_SKINNY_UNROLL;  // rows of B per load block of a wave
-#ifndef DNNOPT_SKINNY_PIPE
-#define DNNOPT_SKINNY_PIPE 0  // 1: double-buffered load blocks
-#endif
+// Rows of B per k-split unit of the planner; the kernel's load block (rows
+// of B in flight per wave) is 16 or 4 (launch_skinny's `unroll`).
+constexpr int kSkinnyUnroll = 16;
 inline int skinny_tile_cols(int mode) { return mode == kSkinnyBF16 ? 512 : 256; }
 inline int skinny_elem_bytes(int mode) { return mode == kSkinnyBF16 ? 2 : 4; }
 
 // b_aligned: every row of B starts on a 4-byte boundary (checked by the host).
 // a_layout: 0 = A row-major with 4-byte aligned rows, 1 = A stored K x M (fp32),
 // 2 = bf16 A rows off 4-byte alignment (element loads).
-hipError_t launch_skinny(int mode, int mr, int nw, int b_aligned, int a_layout, dim3 grid,
+// unroll: rows of B per load block of a wave, 16 or 4 (4 only for fp32 with
+// 8-wave workgroups).
+hipError_t launch_skinny(int mode, int mr, int nw, int unroll, int b_aligned, int a_layout, dim3 grid,
                          const SkinnyArgs& a, hipStream_t s);
 
 // ---------------------------------------------------------------- row dot (B stored N x K)
