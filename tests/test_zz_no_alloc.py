@@ -87,3 +87,96 @@ def test_noalloc_refuses_large_scratch(lib, orc, dev):
     ops = _operands(orc, M, N, K, 0, 0, dev, 1)
     ref, got = _both(lib, M, N, K, 0, 0, ops, 1.0)
     assert np.array_equal(ref.view(np.uint32), got.view(np.uint32))
+
+
+# Split-k skinny (partials summed by a reduce kernel), split-k register tiles
+# (tickets, last workgroup sums), the k-major TransA split-k kernel.
+CAPTURED = [(7, 1009, 2048, 0, 0), (100, 100, 65536, 0, 0), (64, 64, 65536, 1, 0)]
+
+
+def test_noalloc_graph_capture(lib, orc, dev):
+    """Calls captured into a CUDA graph replay to the eager result bit for bit,
+    three times, with eager calls on the same scratch array and NaN-filled
+    outputs between the replays; eager calls leave device free memory
+    unchanged."""
+    ops = [_operands(orc, M, N, K, ta, tb, dev, 1 + 3 * i) for i, (M, N, K, ta, tb) in enumerate(CAPTURED)]
+    refs = [torch.empty((M, N), dtype=torch.float32, device=dev) for (M, N, K, ta, tb) in CAPTURED]
+    outs = [torch.empty((M, N), dtype=torch.float32, device=dev) for (M, N, K, ta, tb) in CAPTURED]
+
+    def run(dst):
+        for (M, N, K, ta, tb), (dA, lda, dB, ldb, _), c in zip(CAPTURED, ops, dst):
+            st = lib.sgemm_noalloc(M, N, K, 1.25, dA, lda, dB, ldb, 0.0, c, N, transA=ta, transB=tb,
+                                   stream=_stream())
+            assert st == 0, lib.so.dnnopt_hip_status_string(st)
+
+    run(refs)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info(dev)[0]
+    for _ in range(3):
+        run(refs)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(dev)[0] == free0, "an eager noalloc call changed device free memory"
+    # each eager result against fp64 as well
+    for (M, N, K, ta, tb), (dA, _, dB, _, _), r in zip(CAPTURED, ops, refs):
+        A = dA.cpu().numpy().reshape((K, M) if ta else (M, K))
+        B = dB.cpu().numpy().reshape((N, K) if tb else (K, N))
+        want, scale = u.exact(A.T if ta else A, B.T if tb else B, 1.25)
+        u.assert_fp32_close(r.cpu().numpy(), want, scale, K, f"noalloc {M}x{N}x{K} ta={ta}")
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run(outs)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        run([torch.empty_like(r) for r in refs])  # eager work on the shared array between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for (M, N, K, ta, tb), o, r in zip(CAPTURED, outs, refs):
+            assert torch.equal(o.view(torch.int32), r.view(torch.int32)), (rep, M, N, K, ta, tb)
+
+
+_FIRST_CALL_CAPTURED = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+import _util as u
+lib = u.load_lib()
+dev = torch.device("cuda:0")
+g0 = torch.Generator(device=dev)
+g0.manual_seed(5)
+M, N, K = 7, 1009, 2048
+A = torch.randn(M, K, device=dev, generator=g0) * 0.02
+B = torch.randn(K, N, device=dev, generator=g0) * 0.02
+C = torch.empty(M, N, device=dev)
+ref = torch.empty(M, N, device=dev)
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    st = lib.sgemm_noalloc(M, N, K, 1.0, A, K, B, N, 0.0, C, N, stream=torch.cuda.current_stream().cuda_stream)
+assert st == 0, lib.so.dnnopt_hip_status_string(st)
+lib.sgemm(M, N, K, 1.0, A, K, B, N, 0.0, ref, N, stream=torch.cuda.current_stream().cuda_stream)
+for i in range(3):
+    C.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(C.view(torch.int32), ref.view(torch.int32)), i
+print("first call captured: ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture(dev):
+    """A process whose first noalloc call is made under graph capture (so the
+    scratch address lookup and the ticket clearing are recorded too) replays
+    to dnnopt_hip_sgemm's result."""
+    import os
+    import subprocess
+    import sys
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, here], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "first call captured: ok" in r.stdout
