@@ -647,6 +647,29 @@ def rocprof_summary(kernel, workload, trace_csv, pmc=None):
             lines.append(f"with its reduce kernel ({len(pairs)} pairs): durations summed "
                          f"{sum(p[0] for p in pairs) / len(pairs):.2f} us, start to end "
                          f"{sum(p[1] for p in pairs) / len(pairs):.2f} us")
+    # Every split-K launch of the run (any kernel followed by a reduce kernel),
+    # grouped by kernel and grid: the main kernel's duration, the gap from its
+    # end to the reduce kernel's start, and the reduce kernel's duration.
+    split = {}
+    for i, r in enumerate(tr[:-1]):
+        nxt = tr[i + 1]
+        if "reduce" in r["Kernel_Name"] or "reduce" not in nxt["Kernel_Name"]:
+            continue
+        key = (_short_kernel_name(r["Kernel_Name"]), int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])),
+               _short_kernel_name(nxt["Kernel_Name"]))
+        t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        t2, t3 = int(nxt["Start_Timestamp"]), int(nxt["End_Timestamp"])
+        split.setdefault(key, []).append(((t1 - t0) / 1000.0, (t2 - t1) / 1000.0, (t3 - t2) / 1000.0))
+    if split:
+        lines.append("")
+        lines.append("split-K launches: main kernel, gap to the reduce kernel's start, reduce kernel (mean us)")
+        lines.append(f"{'kernel':<36} {'wgs':>5} {'reduce':<26} {'pairs':>6} {'main':>7} {'gap':>6} {'reduce':>7} "
+                     f"{'min_red':>7}")
+        for (nm, gx, rn), v in sorted(split.items(), key=lambda kv: (kv[0][0], kv[0][1])):
+            n = len(v)
+            lines.append(f"{nm:<36} {gx:>5} {rn:<26} {n:>6} {sum(x[0] for x in v) / n:7.2f} "
+                         f"{sum(x[1] for x in v) / n:6.2f} {sum(x[2] for x in v) / n:7.2f} "
+                         f"{min(x[2] for x in v):7.2f}")
     return "\n".join(lines) + "\n", traffic
 
 
