@@ -36,7 +36,10 @@
 //     32 x 32 tiles staged through LDS (256-byte k-blocks) above that (4-byte
 //     aligned rows), split-k only when the tiles leave more than half of the
 //     CUs idle.
-// Tunables (environment, read once, for sweeps):
+//   The LDS-DMA tile and k-split of bf16 storage above M = 128 come from a
+//   fitted cost model (pick_bf16_dma) when it beats the rule by 5%.
+// Tunables (dnnopt_hip_set_tunable; a DNNOPT_TUNING build seeds them from
+// these environment variables):
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
 //   DNNOPT_SKINNY_WGS_PER_CU (default 1), DNNOPT_SKINNY_WGS (force G),
 //   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel),
@@ -201,6 +204,61 @@ int plan_kouter(int M, int N, int K, int lda, int ldb, Launch* L) {
     return DNNOPT_OK;
 }
 
+// bf16 storage above M = 128: the LDS-DMA tile and k-split count from a cost
+// model fitted on MI355X (bf16 storage, M = 96..512, N = 2048..11008, K =
+// 1024 and 4096, B stored K x N and N x K, within about 10% of every point
+// measured).  Every workgroup owns one CU, so a launch of W workgroups takes
+// ceil(W / CUs) rounds of one workgroup's time, that time being the MACs of
+// its tile and k-range at a per-configuration rate (us per MAC: 128 x 96 on
+// 8 waves of 32 x 48 0.83e-6, 256 x 96 on 8 waves of 64 x 48 0.57e-6, 128 x
+// 128 on 4 waves of 64 x 64 0.715e-6); a k-split adds its fp32 partial
+// tiles, written and read at 5 TB/s, and 3 us for the reduce launch.
+struct DmaPick {
+    int cfg;
+    long long s;
+    double us;
+};
+
+static double bf16_dma_cost(int cfg, long long s, int M, int N, int K, long long cus) {
+    const TileConfig c = tile_config(cfg);
+    const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
+    const int kb = tile_lds_bk(bm, bn, c.kblk);
+    const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, kb);
+    const double rate = cfg == 33 ? 0.57e-6 : (cfg == kTileBF16Dma4w ? 0.715e-6 : 0.83e-6);
+    const double macs = (double)bm * bn * (double)ceil_div(nblk, s) * kb;
+    double us = (double)ceil_div(tiles * s, cus) * macs * rate;
+    if (s > 1) us += 2.0 * (double)s * tiles * bm * bn * 4 / 5e6 + 3.0;
+    return us;
+}
+
+// The tile and split count for bf16 storage, M > 128: the measured default
+// (128 x 96, or 256 x 96 once 128-row tiles need more than one round, split
+// by the LDS rule) unless the model puts another choice at least 5% faster.
+static DmaPick pick_bf16_dma(int M, int N, int K, int def_cfg) {
+    const long long cus = num_cus();
+    auto lds_splits = [&](int cfg) {
+        const TileConfig c = tile_config(cfg);
+        const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
+        const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, tile_lds_bk(bm, bn, c.kblk));
+        if (tiles * 2 >= cus) return 1LL;
+        return std::min<long long>({ceil_div(cus, tiles), std::max<long long>(1, nblk / 2), (long long)max_splits()});
+    };
+    const long long s_def = lds_splits(def_cfg);
+    DmaPick best{def_cfg, s_def, bf16_dma_cost(def_cfg, s_def, M, N, K, cus)};
+    const double def_us = best.us;
+    for (int cfg : {26, 33, kTileBF16Dma4w}) {
+        const TileConfig c = tile_config(cfg);
+        const long long nblk = ceil_div(K, tile_lds_bk(c.wm * c.mt * 16, c.wn * c.nt * 16, c.kblk));
+        const long long smax = std::min<long long>({16, std::max<long long>(1, nblk / 2), (long long)max_splits()});
+        for (long long s = 1; s <= smax; ++s) {
+            const double us = bf16_dma_cost(cfg, s, M, N, K, cus);
+            if (us < best.us) best = DmaPick{cfg, s, us};
+        }
+    }
+    if (best.us > 0.95 * def_us) return DmaPick{def_cfg, s_def, def_us};
+    return best;
+}
+
 int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, bool lds_ok,
               int ldc) {
     *L = Launch{};
@@ -219,6 +277,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
                      (transB ? ((long long)(N + 128) * ldb + K) : ((long long)K * ldb + N)) * es < 0x7FFFFFFFll &&
                      (long long)128 * ldc * 4 < 0x7FFFFFFFll;
     int cfg;
+    long long model_splits = 0;  // bf16 LDS-DMA: the cost model's split count
     const int forced_cfg = tunable(kTuneTileCfg);
     if (lds) {
         // 128 k per LDS block below M = 128 (fewer barriers, more bytes per
@@ -242,14 +301,25 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         // fewer LDS bytes read per MFMA) in fewer rounds: 512 x 11008 x 4096
         // 67 vs 86 us, 1024 x 4096 x 4096 58 vs 77 us, 384 x 11008 x 4096 66
         // vs 82 us; 512 x 4096 x 4096 (one round of 128-row tiles) keeps the
-        // 128-row tile, 42 vs 51 us.
+        // 128-row tile, 42 vs 51 us.  Where the cost model above puts another
+        // tile or split count at least 5% ahead, that one (measured, us,
+        // default -> picked: 256 x 4096 x 4096 35.7 -> 22.2 on 128 x 128 with
+        // 4 splits, 192 x 8192 x 4096 38.4 -> 31.5 (128 x 128, 2 splits),
+        // 384 x 8192 x 4096 53.2 -> 47.0 (128 x 128), 512 x 2048 x 4096 30.8
+        // -> 22.1; C4's 256 x 11008 x 4096 keeps 128 x 96).
         if (M > 128 && mode == kTileBF16) {
             cfg = 26;
             if (ceil_div(M, 128) * ceil_div(N, 96) > num_cus()) cfg = 33;
+            if (forced_cfg < kTileFirstLds && tunable(kTuneTileSplits) <= 0) {  // nothing forced
+                const DmaPick pick = pick_bf16_dma(M, N, K, cfg);
+                cfg = pick.cfg;
+                model_splits = pick.s;
+            }
         }
+        const bool forced_dma = forced_cfg >= kTileFirstDma && forced_cfg < kTileF32Few;
         if (((forced_cfg >= kTileFirstLds && forced_cfg < kTileF32Few) || forced_cfg == kTileBF16Tb48 ||
-             forced_cfg == kTileBF16Tb48Few) &&
-            (forced_cfg < kTileFirstDma || mode == kTileBF16))
+             forced_cfg == kTileBF16Tb48Few || forced_cfg == kTileBF16Dma4w) &&
+            ((!forced_dma && forced_cfg != kTileBF16Dma4w) || mode == kTileBF16))
             cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {
         cfg = 0;
@@ -293,6 +363,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         // when the tiles leave more than half of the CUs idle.
         if (tiles * 2 < cus) s = std::min<long long>({ceil_div(cus, tiles), std::max<long long>(1, nblk / 2),
                                                       (long long)max_splits()});
+        if (model_splits > 0) s = model_splits;
     } else {
         const long long target_wgs = cus * waves_per_cu() / waves_per_wg;
         if (tiles < target_wgs) {
@@ -332,7 +403,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     // for the LDS-DMA tiles (DNNOPT_TILE_TICKET=1): the last workgroup to
     // finish a tile adds the others' partials.
     const bool dma_ticket = tunable(kTuneTileTicket) == 1;
-    const bool dma = cfg >= kTileFirstDma && cfg < kTileF32Few;  // LDS-DMA configurations
+    const bool dma = (cfg >= kTileFirstDma && cfg < kTileF32Few) || cfg == kTileBF16Dma4w;  // LDS-DMA tiles
     const bool ticket_ok = !lds || (dma_ticket && dma);
     L->defer_reduce =
         (s > 1 && (split_reduce_mode() || s > kTicketSplitLimit || tiles > kMaxTickets || !ticket_ok)) ? 1 : 0;

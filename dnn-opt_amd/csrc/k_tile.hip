@@ -1096,6 +1096,8 @@ static const TileConfig kTileConfigs[] = {
     // bf16 storage through LDS, B stored N x K, few rows
     {2, 1, 1, 3, 1, 3, 128},  // 37: 32 x 48, 3 waves, 128 k per block, 3 ahead
     {1, 1, 1, 3, 1, 3, 128},  // 38: 16 x 48, 3 waves, 128 k per block, 3 ahead
+    // bf16 storage, LDS DMA (continued)
+    {4, 4, 2, 2, 1, 3, 64},   // 39: 128 x 128, 4 waves of 64 x 64, 3 stages
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -1182,6 +1184,7 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_CASE(36, 1, 4, 1, 2, 2)
         DNNOPT_TILE_LDS_CASE(37, 2, 1, 1, 3, 3, 128, 1)
         DNNOPT_TILE_LDS_CASE(38, 1, 1, 1, 3, 3, 128, 1)
+        DNNOPT_TILE_DMA_CASE(39, 4, 4, 2, 2, 3, 64)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

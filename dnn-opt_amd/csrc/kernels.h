@@ -232,6 +232,9 @@ constexpr int kTileF32Few128 = 36;
 // bf16 storage, B stored N x K, M <= 32: LDS-staged tiles 48 columns wide
 // (16 x 48 up to M = 16, 32 x 48 above), 230 tiles at N = 11008 instead of 172.
 constexpr int kTileBF16Tb48 = 37, kTileBF16Tb48Few = 38;
+// bf16 storage, LDS DMA: 128 x 128 tiles on 4 waves of 64 x 64 (bf16
+// storage only, like the LDS-DMA entries from kTileFirstDma).
+constexpr int kTileBF16Dma4w = 39;
 // k per LDS block of an LDS-staged configuration: its kblk (or
 // DNNOPT_LDS_KB) when both stages fit in 128 KiB of LDS, else 64.
 constexpr int tile_lds_bk(int bm, int bn, int kblk) {

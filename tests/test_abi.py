@@ -365,9 +365,17 @@ def test_plans_route_lds_dma_kernels(lib):
         assert lib.plan_bf16_ex(M, 11008, 4096, transB=1)["name"] == "dnnopt_tile_bf16_dma"
         assert lib.plan_bf16(M, 11008, 4096, fp32_inputs=1)["name"] == "dnnopt_tile_bf16_lds"
     assert lib.plan_bf16(128, 11008, 4096)["name"] == "dnnopt_tile_bf16_lds"
-    # 256 x 96 tiles once 128 x 96 tiles take more than one round over the CUs
-    cus = 256  # MI355X (and the planner's figure when no GPU is visible)
-    for (M, N), rows in {(256, 11008): 128, (384, 11008): 256, (1024, 4096): 256, (512, 4096): 128}.items():
-        want = 256 if -(-M // 128) * -(-N // 96) > cus else 128
+    # bf16 storage above M = 128 (planner's figure of 256 CUs when no GPU is
+    # visible): 128 x 96 tiles, 256 x 96 once those take more than one round,
+    # and 128 x 128 tiles on 4 waves where the cost model puts them 5% ahead
+    # (measured on MI355X: 256 x 4096 35.7 -> 22.2 us, 192 x 8192 38.4 ->
+    # 31.5, 384 x 8192 53.2 -> 47.0, 512 x 4096 37.9 -> 32.3).
+    cases = {(256, 11008): (128, 96, 1), (384, 11008): (256, 96, 1), (512, 11008): (256, 96, 1),
+             (256, 4096): (128, 128, 4), (192, 8192): (128, 128, 2), (384, 8192): (128, 128, 1),
+             (512, 4096): (128, 128, 2)}
+    for (M, N), want in cases.items():
         for p in (lib.plan_bf16(M, N, 4096), lib.plan_bf16_ex(M, N, 4096, transB=1)):
-            assert p["name"] == "dnnopt_tile_bf16_dma" and (p["rows"], p["cols"]) == (want, 96), (M, N, p)
+            assert p["name"] == "dnnopt_tile_bf16_dma" and (p["rows"], p["cols"], p["splits"]) == want, (M, N, p)
+    # a forced tile or split count turns the model off
+    with lib.tunables(TILE_SPLITS=2):
+        assert (lib.plan_bf16(256, 4096, 4096)["rows"], lib.plan_bf16(256, 4096, 4096)["cols"]) == (128, 96)

@@ -473,7 +473,7 @@ def _bf16_storage_sweep_cases():
         alpha = float(rng.choice([1.0, 0.5, -2.0]))
         beta = float(rng.choice([0.0, 1.0, 0.25]))
         cases.append((M, N, K, tb, pa, pb, alpha, beta))
-    # two shapes that take the 256-row tiles for certain (more 128-row tiles than CUs)
+    # two shapes with more 128 x 96 tiles than CUs (the cost model gives them 128 x 128 tiles)
     cases += [(1100, 3000, 96, 0, 2, 0, 1.0, 0.0), (1024, 3100, 130, 1, 0, 4, -2.0, 0.25)]
     return cases
 
@@ -484,8 +484,8 @@ def test_bf16_storage_sweep(lib, orc, dev, M, N, K, tb, pa, pb, alpha, beta):
     p = lib.plan_bf16_ex(M, N, K, transB=tb)
     # rows of A and B on 4-byte boundaries: the LDS-DMA tiles; else the register tiles
     assert p["name"] == ("dnnopt_tile_bf16_dma" if lda % 2 == 0 and ldb % 2 == 0 else "dnnopt_tile_bf16"), p
-    if -(-M // 128) * -(-N // 96) > 256 and lda % 2 == 0 and ldb % 2 == 0:
-        assert p["rows"] == 256, p
+    if lda % 2 == 0 and ldb % 2 == 0:
+        assert (p["rows"], p["cols"]) in ((128, 96), (256, 96), (128, 128)), p
     A = u.bf16_bits(orc, u.normal(orc, M * lda, 11)).reshape(M, lda)
     rows = N if tb else K
     Bs = u.bf16_bits(orc, u.normal(orc, rows * ldb, 12, 0, 0.02)).reshape(rows, ldb)
@@ -496,6 +496,40 @@ def test_bf16_storage_sweep(lib, orc, dev, M, N, K, tb, pa, pb, alpha, beta):
     lib.gemm_bf16_ex(M, N, K, alpha, dev_copy(A.view(np.int16), dev), lda, dev_copy(Bs.view(np.int16), dev), ldb,
                      beta, dC, N, transB=tb, stream=stream())
     u.assert_fp32_close(host(dC), want, scale, K, f"bf16 sweep {M}x{N}x{K} tb={tb} a={alpha} b={beta}")
+
+
+@pytest.mark.parametrize("tb", [0, 1])
+def test_bf16_dma_128x128_four_wave_tiles(lib, orc, dev, tb):
+    """128 x 128 LDS-DMA tiles on 4 waves of 64 x 64: forced with 1 to 4
+    k-splits on a ragged shape (M and N off the tile, a K tail inside a 64-k
+    block, padded even strides, beta != 0), and as the planner's own choice
+    (1000 x 4000 x 100 unsplit, 256 x 4096 x 4096 with 4 k-splits); B stored
+    K x N and N x K."""
+    def run(M, N, K, pa, pb, alpha, beta, seed):
+        lda, ldb = K + pa, (K + pb if tb else N + pb)
+        A = u.bf16_bits(orc, u.normal(orc, M * lda, seed)).reshape(M, lda)
+        rows = N if tb else K
+        Bs = u.bf16_bits(orc, u.normal(orc, rows * ldb, seed + 1, 0, 0.02)).reshape(rows, ldb)
+        Bkn = np.ascontiguousarray(Bs[:, :K].T if tb else Bs[:, :N])
+        C0 = u.uniform(orc, M * N, seed + 2).reshape(M, N)
+        want, scale = u.exact(u.bf16_value(A)[:, :K], u.bf16_value(Bkn), alpha, beta, C0 if beta else None)
+        dC = dev_copy(C0 if beta else np.full_like(C0, np.nan), dev)
+        lib.gemm_bf16_ex(M, N, K, alpha, dev_copy(A.view(np.int16), dev), lda, dev_copy(Bs.view(np.int16), dev),
+                         ldb, beta, dC, N, transB=tb, stream=stream())
+        return host(dC), want, scale
+
+    M, N, K = 300, 1000, 520
+    for splits in (1, 2, 3, 4):
+        with lib.tunables(TILE_CFG=39, TILE_SPLITS=splits):
+            p = lib.plan_bf16_ex(M, N, K, transB=tb)
+            assert (p["name"], p["rows"], p["cols"], p["splits"]) == ("dnnopt_tile_bf16_dma", 128, 128, splits), p
+            got, want, scale = run(M, N, K, 2, 4, 0.5, 0.25, 21)
+        u.assert_fp32_close(got, want, scale, K, f"128x128 forced, {splits} splits, tb={tb}")
+    for (M, N, K), splits in (((1000, 4000, 100), 1), ((256, 4096, 4096), 4)):
+        p = lib.plan_bf16_ex(M, N, K, transB=tb)
+        assert (p["name"], p["rows"], p["cols"], p["splits"]) == ("dnnopt_tile_bf16_dma", 128, 128, splits), p
+        got, want, scale = run(M, N, K, 0, 0, 1.0, 0.0, 31)
+        u.assert_fp32_close(got, want, scale, K, f"128x128 planned {M}x{N}x{K} tb={tb}")
 
 
 def test_bf16_dma_k_split_ticket_matches_reduce_kernel(lib, orc, dev):
