@@ -400,7 +400,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     const bool xcd = lds || (mode == kTileF32 && c.mt == 1 && c.wm == 1);
     L->grid = xcd ? dim3((unsigned)xcd_grid((int)tn, (int)tm), 1, (unsigned)s) : dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
     // k-splits of the LDS-staged kernels are summed by a reduce kernel, except
-    // for the LDS-DMA tiles (DNNOPT_TILE_TICKET=1): the last workgroup to
+    // for the LDS-DMA tiles (tunable TILE_TICKET = 1): the last workgroup to
     // finish a tile adds the others' partials.
     const bool dma_ticket = tunable(kTuneTileTicket) == 1;
     const bool dma = (cfg >= kTileFirstDma && cfg < kTileF32Few) || cfg == kTileBF16Dma4w;  // LDS-DMA tiles
