@@ -25,6 +25,28 @@ int finish_launch(hipError_t e) {
     return DNNOPT_OK;
 }
 
+// The 64-bit last-resort kernel (DNNOPT_K_WIDE) for an fp32 / bf16 GEMM;
+// `mode` is a TileMode (the WideMode of the same number).
+int run_wide(int mode, int ta, int tb, const void* A, int lda, const void* B, int ldb, float* C, int ldc, int M,
+             int N, int K, float alpha, float beta, hipStream_t s, const float* bias = nullptr) {
+    WideArgs w{};
+    w.A = A;
+    w.B = B;
+    w.C = C;
+    w.lda = lda;
+    w.ldb = ldb;
+    w.ldc = ldc;
+    w.M = M;
+    w.N = N;
+    w.K = K;
+    w.transA = ta;
+    w.transB = tb;
+    w.alpha = alpha;
+    w.beta = beta;
+    w.bias = bias;
+    return finish_launch(launch_wide(mode, w, s));
+}
+
 // Partial-sum space and tickets of a split-k launch: the stream's workspace,
 // or the caller's scratch when one is given.
 int take_workspace(hipStream_t s, size_t part_bytes, const ExtScratch* ext, void** part, unsigned** tickets) {
@@ -90,6 +112,8 @@ int run_tile(const Launch& L0, int ta, int tb, const void* A, int lda, const voi
          ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 3u) != 0) ||
         (L.cfg == kTileKOuter && ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15u) != 0)) {
         const int st = plan_tile(L.mode, ta, tb, M, N, K, lda, ldb, &L, false, ldc);
+        if (st == DNNOPT_ERR_UNSUPPORTED)
+            return run_wide(L0.mode, ta, tb, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
         if (st != DNNOPT_OK) return st;
     }
     TileArgs a{};
@@ -164,6 +188,8 @@ static int sgemm_planned(int transA, int transB, int M, int N, int K, float alph
     Launch L;
     int st = plan_sgemm(transA, transB, M, N, K, lda, ldb, &L, ldc);
     if (st != DNNOPT_OK) return st;
+    if (L.family == DNNOPT_K_WIDE)
+        return run_wide(kTileF32, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
     if (L.family == DNNOPT_K_SKINNY_F32)
         return run_skinny(L, A, transA ? 1 : lda, transA ? lda : 1, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias,
                           ext);
@@ -246,8 +272,11 @@ int dnnopt_hip_plan_gemm_bf16_ex(int transA, int transB, int M, int N, int K, dn
     // first copied to an even row stride).
     const int lda = transA ? (K + 1) & ~1 : K;
     Launch L;
-    int st = transA && !transB && M <= 8 ? plan_skinny(kSkinnyBF16, M, N, K, N, &L)
-                                         : plan_bf16(0, M, N, K, lda, transB ? K : N, &L, transB);
+    if (transA && !transB && M <= 8 && !tunable(kTuneWide) && plan_skinny(kSkinnyBF16, M, N, K, N, &L) == DNNOPT_OK) {
+        *out = L.pub;
+        return DNNOPT_OK;
+    }
+    int st = plan_bf16(0, M, N, K, lda, transB ? K : N, &L, transB);
     if (st == DNNOPT_OK) *out = L.pub;
     return st;
 }
@@ -302,7 +331,6 @@ int dnnopt_hip_sgemm_naive(int M, int N, int K, float alpha, const float* A, int
     if (!A || !B || !C) return DNNOPT_ERR_INVALID_ARG;
     if (lda < K || ldb < N || ldc < N) return DNNOPT_ERR_INVALID_ARG;
     if (visible_devices() == 0) return DNNOPT_ERR_NO_DEVICE;
-    if ((long long)(M + 3) / 4 > 65535) return DNNOPT_ERR_UNSUPPORTED;
     return finish_launch(launch_naive_f32(M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, as_stream(stream)));
 }
 
@@ -317,6 +345,8 @@ static int gemm_bf16_common(int fp32_inputs, int M, int N, int K, float alpha, c
     Launch L;
     int st = plan_bf16(fp32_inputs, M, N, K, lda, ldb, &L, 0, ldc);
     if (st != DNNOPT_OK) return st;
+    if (L.family == DNNOPT_K_WIDE)
+        return run_wide(fp32_inputs ? kTileF2B : kTileBF16, 0, 0, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     if (L.family == DNNOPT_K_SKINNY_BF16 || L.family == DNNOPT_K_SKINNY_F2B)
         return run_skinny(L, A, lda, 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     return run_tile(L, 0, 0, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
@@ -337,27 +367,30 @@ int dnnopt_hip_gemm_bf16_ex(int transA, int transB, int M, int N, int K, float a
     hipStream_t s = as_stream(stream);
     StreamLock lock(s);
     Launch L;
-    if (transA && !transB && M <= 8) {
+    if (transA && !transB && M <= 8 && !tunable(kTuneWide)) {
         // The skinny kernel reads a K x M A in place (A is M*K elements).
-        int st = plan_skinny(kSkinnyBF16, M, N, K, ldb, &L);
-        if (st != DNNOPT_OK) return st;
-        return run_skinny(L, A, 1, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
+        if (plan_skinny(kSkinnyBF16, M, N, K, ldb, &L) == DNNOPT_OK)
+            return run_skinny(L, A, 1, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     }
+    // MFMA tiles read k-contiguous rows of A: a K x M A is first transposed
+    // into workspace (M x K, even row stride so rows stay 4-byte aligned),
+    // unless no tile can take the shape (then the last-resort kernel reads
+    // it in place).
+    const int ldt = transA ? (K + 1) & ~1 : lda;
+    int st = plan_bf16(0, M, N, K, ldt, ldb, &L, transB, ldc);
+    if (st != DNNOPT_OK) return st;
+    if (L.family == DNNOPT_K_WIDE)
+        return run_wide(kTileBF16, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     if (transA) {
-        // MFMA tiles read k-contiguous rows of A: transpose the K x M A into
-        // workspace (M x K, even row stride so rows stay 4-byte aligned).
-        const int ldt = (K + 1) & ~1;
         void* ws = nullptr;
         unsigned* unused = nullptr;
-        int st = get_workspace(s, (size_t)M * ldt * sizeof(uint16_t), &ws, &unused, kSlotTransA);
+        st = get_workspace(s, (size_t)M * ldt * sizeof(uint16_t), &ws, &unused, kSlotTransA);
         if (st != DNNOPT_OK) return st;
         st = finish_launch(launch_transpose_u16(A, K, M, lda, static_cast<uint16_t*>(ws), ldt, s));
         if (st != DNNOPT_OK) return st;
         A = static_cast<const uint16_t*>(ws);
         lda = ldt;
     }
-    int st = plan_bf16(0, M, N, K, lda, ldb, &L, transB, ldc);
-    if (st != DNNOPT_OK) return st;
     if (L.family == DNNOPT_K_SKINNY_BF16) return run_skinny(L, A, lda, 1, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     if (L.family == DNNOPT_K_ROWDOT_BF16) return run_rowdot(L, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
     return run_tile(L, 0, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s);
@@ -388,6 +421,25 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
     Launch L;
     int st = plan_s8(epi, M, N, K, &L, aligned != 0, lda, ldb, ldc);
     if (st != DNNOPT_OK) return st;
+    if (L.family == DNNOPT_K_WIDE) {
+        WideArgs w{};
+        w.A = A;
+        w.B = B;
+        w.C = C;
+        w.lda = lda;
+        w.ldb = ldb;
+        w.ldc = ldc;
+        w.M = M;
+        w.N = N;
+        w.K = K;
+        w.transB = 1;  // int8 B is stored N x K
+        w.epi = epi;
+        w.scale = scale;
+        w.amax = dyn ? dyn->amax : nullptr;
+        w.alpha = dyn ? dyn->alpha : 1.0f;
+        w.beta = dyn ? dyn->beta : 0.0f;
+        return finish_launch(launch_wide(kWideS8, w, s));
+    }
     if (L.family == DNNOPT_K_ROWDOT_S8) {
         RowdotArgs r{};
         r.A = A;
@@ -406,8 +458,6 @@ static int gemm_s8_common(int epi, int M, int N, int K, const int8_t* A, int lda
         r.K = K;
         return finish_launch(launch_rowdot(L.mode, L.mr, L.nw, aligned, L.grid, r, s));
     }
-    if ((long long)L.bm * lda + K >= 0x7FFFFFFFll || (long long)L.bn * ldb + K >= 0x7FFFFFFFll)
-        return DNNOPT_ERR_UNSUPPORTED;
     S8Args a{};
     a.A = A;
     a.B = B;

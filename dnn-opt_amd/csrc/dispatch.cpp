@@ -38,6 +38,8 @@
 //     CUs idle.
 //   The LDS-DMA tile and k-split of bf16 storage above M = 128 come from a
 //   fitted cost model (pick_bf16_dma) when it beats the rule by 5%.
+//   * any shape whose operand spans none of these kernels can address with
+//     32-bit offsets: the 64-bit last-resort kernel (k_wide.hip).
 // Tunables (dnnopt_hip_set_tunable; a DNNOPT_TUNING build seeds them from
 // these environment variables):
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
@@ -51,7 +53,8 @@
 //   tall tiles: 1 or 2), DNNOPT_ROWDOT_KW (force the row-dot k-split: 1, 2,
 //   4 or 8 waves), DNNOPT_S8_ROWDOT=0 (int8 M <= 4 on
 //   the MFMA tiles), DNNOPT_KOUTER=0 (k-major fp32 operands on the register
-//   tiles), DNNOPT_KOUTER_WGS_PER_CU (default 1).
+//   tiles), DNNOPT_KOUTER_WGS_PER_CU (default 1), DNNOPT_WIDE=1 (every
+//   fp32 / bf16 / int8 GEMM on the last-resort kernel, for its tests).
 #include <stdlib.h>
 #include <string.h>
 
@@ -417,7 +420,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     return DNNOPT_OK;
 }
 
-int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int ldb, int ldc) {
+static int plan_s8_kernels(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int ldb, int ldc) {
     *L = Launch{};
     if (ldc <= 0) ldc = N;
     // The LDS-staged kernel addresses a C tile with 32-bit offsets.
@@ -472,6 +475,9 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int l
     }
     if (forced_splits > 0) s = std::min<long long>(forced_splits, std::max<long long>(1, nblk / c.kw));
     if (s > 1 && tiles > kMaxTickets && !split_reduce_mode() && !lds) s = 1;
+    // The tiles address A and B from their first row with 32-bit offsets.
+    if ((long long)bm * (lda > 0 ? lda : K) + K >= 0x7FFFFFFFll || (long long)bn * (ldb > 0 ? ldb : K) + K >= 0x7FFFFFFFll)
+        return DNNOPT_ERR_UNSUPPORTED;
     if (tm > 65535 || s > 65535) return DNNOPT_ERR_UNSUPPORTED;
     // The LDS-staged kernel always hands its k-splits to the reduce kernel.
     L->defer_reduce = (s > 1 && (split_reduce_mode() || lds)) ? 1 : 0;
@@ -487,6 +493,16 @@ int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int l
     fill_pub(L, DNNOPT_K_MFMA_S8, dma ? "dnnopt_s8_dma" : (lds ? "dnnopt_s8_lds" : "dnnopt_mfma_s8"), bm, bn, (int)s,
              waves_per_wg * 64);
     return DNNOPT_OK;
+}
+
+int plan_s8(int epi, int M, int N, int K, Launch* L, bool lds_ok, int lda, int ldb, int ldc) {
+    if (tunable(kTuneWide)) {
+        plan_wide(M, N, L);
+        return DNNOPT_OK;
+    }
+    const int st = plan_s8_kernels(epi, M, N, K, L, lds_ok, lda, ldb, ldc);
+    if (st == DNNOPT_ERR_UNSUPPORTED) plan_wide(M, N, L);
+    return st == DNNOPT_ERR_UNSUPPORTED ? DNNOPT_OK : st;
 }
 
 int plan_rowdot(int mode, int M, int N, int K, int lda, int ldb, Launch* L) {
@@ -567,8 +583,19 @@ int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int 
     return DNNOPT_OK;
 }
 
-int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc) {
-    if (M <= 8 && !transB) return plan_skinny(kSkinnyF32, M, N, K, ldb, L);
+void plan_wide(int M, int N, Launch* L) {
+    *L = Launch{};
+    L->grid = wide_grid(M, N);
+    fill_pub(L, DNNOPT_K_WIDE, "dnnopt_wide", 1, 64, 1, wide_threads());
+}
+
+namespace {
+
+int plan_sgemm_kernels(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc) {
+    // The skinny kernel for M <= 8 unless its spans exceed 32-bit offsets
+    // (then the tiles, which split k into shorter ranges).
+    if (M <= 8 && !transB && plan_skinny(kSkinnyF32, M, N, K, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
+    *L = Launch{};
     // B stored N x K: the row-dot kernel up to M = 4 and for narrow N; from
     // M = 5 at N >= 2048 the 16-row MFMA tiles (us, row-dot -> tiles: M=5 / 6
     // / 8 x 11003 x 2048 27.6 / 29.8 / 32.4 -> 26.1 / 26.5 / 28.1, x 4096 x
@@ -583,7 +610,7 @@ int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, La
     return plan_tile(kTileF32, transA, transB, M, N, K, lda, ldb, L, true, ldc);
 }
 
-int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB, int ldc) {
+int plan_bf16_kernels(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB, int ldc) {
     // B stored N x K has k-contiguous columns: MFMA tiles read it in place
     // for every M (the skinny kernel streams rows of a K x N B).  bf16
     // storage with a K x N B and 4-byte aligned rows: the skinny kernel up to
@@ -592,7 +619,10 @@ int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L,
     // 31.0 -> 22.4; 8 x 4096 x 4096 16.2 -> 13.5; M=5 22.6 vs 22.4, M=4 21.0
     // vs 22.2, 5 x 4096 x 4096 13.6 vs 13.8).
     const bool tile_kn = !transB && !fp32_inputs && M >= 6 && (lda & 1) == 0 && (ldb & 1) == 0;
-    if (M <= 8 && !transB && !tile_kn) return plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L);
+    if (M <= 8 && !transB && !tile_kn &&
+        plan_skinny(fp32_inputs ? kSkinnyF2B : kSkinnyBF16, M, N, K, ldb, L) == DNNOPT_OK)
+        return DNNOPT_OK;
+    *L = Launch{};
     if (transB && fp32_inputs) return DNNOPT_ERR_UNSUPPORTED;
     // B stored N x K: the row-dot kernel up to M = 4 and for rows off 4-byte
     // boundaries; from M = 5 the LDS-staged tiles (us, row-dot -> 32 x 64
@@ -602,6 +632,31 @@ int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L,
     const bool tile_tb = transB && M >= 5 && (lda & 1) == 0 && (ldb & 1) == 0;
     if (transB && M <= 8 && !tile_tb && plan_rowdot(1, M, N, K, lda, ldb, L) == DNNOPT_OK) return DNNOPT_OK;
     return plan_tile(fp32_inputs ? kTileF2B : kTileBF16, 0, transB, M, N, K, lda, ldb, L, true, ldc);
+}
+
+}  // namespace
+
+// Shapes no tiled kernel can address (operand spans past 32-bit offsets)
+// run on the 64-bit last-resort kernel.
+int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc) {
+    if (tunable(kTuneWide)) {
+        plan_wide(M, N, L);
+        return DNNOPT_OK;
+    }
+    const int st = plan_sgemm_kernels(transA, transB, M, N, K, lda, ldb, L, ldc);
+    if (st == DNNOPT_ERR_UNSUPPORTED) plan_wide(M, N, L);
+    return st == DNNOPT_ERR_UNSUPPORTED ? DNNOPT_OK : st;
+}
+
+int plan_bf16(int fp32_inputs, int M, int N, int K, int lda, int ldb, Launch* L, int transB, int ldc) {
+    if (transB && fp32_inputs) return DNNOPT_ERR_UNSUPPORTED;  // no entry point takes this combination
+    if (tunable(kTuneWide)) {
+        plan_wide(M, N, L);
+        return DNNOPT_OK;
+    }
+    const int st = plan_bf16_kernels(fp32_inputs, M, N, K, lda, ldb, L, transB, ldc);
+    if (st == DNNOPT_ERR_UNSUPPORTED) plan_wide(M, N, L);
+    return st == DNNOPT_ERR_UNSUPPORTED ? DNNOPT_OK : st;
 }
 
 }  // namespace dnnopt_hip

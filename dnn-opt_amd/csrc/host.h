@@ -102,6 +102,7 @@ enum Tunable {
     kTuneTallRT,            // forced tall-kernel row tiles per wave (1, 2)
     kTuneTallWgsPerCu,      // tall-kernel workgroups per CU
     kTuneTall,              // tall-skinny kernel with B resident in LDS
+    kTuneWide,              // 1: every fp32 / bf16 / int8 GEMM on the last-resort kernel (tests)
     kTuneCount
 };
 int tunable(Tunable t);
@@ -142,7 +143,10 @@ int sgemm_bias(int transA, int transB, int M, int N, int K, float alpha, const f
                int ldb, float beta, float* C, int ldc, const float* bias, hipStream_t s,
                const ExtScratch* ext = nullptr);
 
-// Route an fp32 GEMM to a kernel family (skinny or tile).
+// The 64-bit last-resort kernel (dnnopt_wide) for an M x N output.
+void plan_wide(int M, int N, Launch* L);
+// Route an fp32 GEMM to a kernel family (skinny, row-dot, tall, tile; the
+// last-resort kernel when no other one can address the operands).
 int plan_sgemm(int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, int ldc = 0);
 // Route a bf16 GEMM (fp32_inputs: operands are fp32 and rounded in registers;
 // transB: B stored N x K, bf16 storage only).

@@ -14,9 +14,9 @@ namespace dnnopt_hip {
 #pragma clang fp contract(off)
 __global__ __launch_bounds__(256) void dnnopt_naive_f32(int M, int N, int K, float alpha, const float* A,
                                                        int lda, const float* B, int ldb, float beta, float* C,
-                                                       int ldc) {
+                                                       int ldc, int row0) {
     const int j = blockIdx.x * 64 + (threadIdx.x & 63);
-    const int i = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const int i = row0 + blockIdx.y * 4 + (threadIdx.x >> 6);
     if (i >= M || j >= N) return;
     const float* a = A + (size_t)i * lda;
     float acc = 0.0f;
@@ -75,9 +75,17 @@ __global__ __launch_bounds__(256) void dnnopt_fill(void* dst, size_t n, int dtyp
 
 hipError_t launch_naive_f32(int M, int N, int K, float alpha, const float* A, int lda, const float* B, int ldb,
                             float beta, float* C, int ldc, hipStream_t s) {
-    dim3 grid((N + 63) / 64, (M + 3) / 4);
-    hipLaunchKernelGGL(dnnopt_naive_f32, grid, dim3(256), 0, s, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc);
-    return hipGetLastError();
+    // Rows in launches of at most 65535 * 4 (the grid's y limit).
+    constexpr int kRowsPerLaunch = 65535 * 4;
+    for (int row0 = 0; row0 < M; row0 += kRowsPerLaunch) {
+        const int rows = M - row0 < kRowsPerLaunch ? M - row0 : kRowsPerLaunch;
+        dim3 grid((N + 63) / 64, (rows + 3) / 4);
+        hipLaunchKernelGGL(dnnopt_naive_f32, grid, dim3(256), 0, s, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc,
+                           row0);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_saxpy(int n, float alpha, const float* x, int incx, float* y, int incy, hipStream_t s) {

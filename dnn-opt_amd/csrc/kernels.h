@@ -252,6 +252,27 @@ hipError_t launch_kouter_f32(dim3 grid, const TileArgs& a, hipStream_t s);
 hipError_t launch_tile(int mode, int cfg_idx, int transA, int transB, int aligned, dim3 grid,
                        const TileArgs& a, hipStream_t s);
 
+// ---------------------------------------------------------------- last resort
+// dnnopt_wide (k_wide.hip): any layout and size with 64-bit addressing, for
+// shapes whose operand spans the tiled kernels' 32-bit offsets cannot reach.
+enum WideMode { kWideF32 = 0, kWideBF16 = 1, kWideF2B = 2, kWideS8 = 3 };
+struct WideArgs {
+    const void* A;  // fp32, bf16 bits (kWideBF16), fp32 rounded to bf16 (kWideF2B) or int8
+    const void* B;
+    void* C;        // fp32, or int32 for kWideS8 with epi 0
+    long long lda, ldb, ldc;
+    int M, N, K;
+    int transA, transB;  // A stored K x M / B stored N x K
+    float alpha, beta;
+    const float* bias;   // fp32 modes: per-column bias after the epilogue (or null)
+    int epi;             // kWideS8: 0 int32 C, 1 fp32 C through s8_out (scale or amax)
+    const float* scale;
+    const unsigned* amax;
+};
+hipError_t launch_wide(int mode, const WideArgs& a, hipStream_t s);
+dim3 wide_grid(int M, int N);
+int wide_threads();
+
 // ---------------------------------------------------------------- small kernels
 hipError_t launch_naive_f32(int M, int N, int K, float alpha, const float* A, int lda,
                             const float* B, int ldb, float beta, float* C, int ldc,

@@ -36,7 +36,7 @@ constexpr TuneDef kDefs[kTuneCount] = {
     {"DNNOPT_S8_CFG", -1, false},      {"DNNOPT_S8_ROWDOT", 1, true},
     {"DNNOPT_S8_SPLITS", 0, false},    {"DNNOPT_ROWDOT_KW", 0, false},
     {"DNNOPT_TALL_RT", 0, false},      {"DNNOPT_TALL_WGS_PER_CU", 1, false},
-    {"DNNOPT_TALL", 1, true},
+    {"DNNOPT_TALL", 1, true},          {"DNNOPT_WIDE", 0, true},
 };
 
 std::atomic<int> g_val[kTuneCount];

@@ -35,7 +35,7 @@ OK, ERR_INVALID_ARG, ERR_NO_DEVICE, ERR_HIP, ERR_UNSUPPORTED, ERR_OUT_OF_MEMORY,
 NOALLOC_SCRATCH_BYTES = 16 << 20  # DNNOPT_NOALLOC_SCRATCH_BYTES
 
 (K_NONE, K_SKINNY_F32, K_SKINNY_BF16, K_SKINNY_F2B, K_MFMA_S8, K_TILE_F32, K_TILE_BF16, K_NAIVE_F32, K_ROWDOT_F32,
- K_ROWDOT_BF16, K_TALL_F32, K_ROWDOT_S8, K_SKINNY_Q8) = range(13)
+ K_ROWDOT_BF16, K_TALL_F32, K_ROWDOT_S8, K_SKINNY_Q8, K_WIDE) = range(14)
 
 # DNNOPT_HIP_ABI_VERSION of include/dnnopt_hip.h that these bindings follow.
 ABI_VERSION = 4
@@ -110,7 +110,7 @@ C_ABI = {
 TUNE = {"Q8B": 0, "KOUTER": 1, "KOUTER_WGS_PER_CU": 2, "WAVES_PER_CU": 3, "SKINNY_NW": 4,
         "SKINNY_WGS_PER_CU": 5, "MAX_SPLITS": 6, "SPLIT_REDUCE": 7, "SKINNY_WGS": 8, "TILE_SPLITS": 9,
         "TILE_CFG": 10, "TILE_TICKET": 11, "S8_CFG": 12, "S8_ROWDOT": 13, "S8_SPLITS": 14, "ROWDOT_KW": 15,
-        "TALL_RT": 16, "TALL_WGS_PER_CU": 17, "TALL": 18}
+        "TALL_RT": 16, "TALL_WGS_PER_CU": 17, "TALL": 18, "WIDE": 19}
 
 BLAS_ABI = {
     "cblas_sgemm": (None, [_I, _I, _I, _I, _I, _I, _F, _P, _I, _P, _I, _F, _P, _I]),

@@ -222,6 +222,9 @@ int dnnopt_onednn_gemm_bf16bf16f32(const char* transa, const char* transb,
 #define DNNOPT_K_ROWDOT_S8  11  /* M <= 8, int8 B stored N x K, rows once   */
 #define DNNOPT_K_SKINNY_Q8  12  /* M <= 8, fp32-API int8: fp32 B quantized  */
                                 /* as it is streamed (no int8 copy of B)   */
+#define DNNOPT_K_WIDE       13  /* any layout, 64-bit addressing: operands  */
+                                /* whose spans exceed the other kernels'   */
+                                /* 32-bit offsets (rows of gigabytes)      */
 
 typedef struct dnnopt_plan {
     int kernel;             /* DNNOPT_K_* */
@@ -299,7 +302,8 @@ int dnnopt_hip_device_count(void);    /* 0 when no device is visible        */
 #define DNNOPT_TUNE_TALL_RT         16
 #define DNNOPT_TUNE_TALL_WGS_PER_CU 17
 #define DNNOPT_TUNE_TALL            18
-#define DNNOPT_TUNE_COUNT           19
+#define DNNOPT_TUNE_WIDE            19  /* 1: every GEMM on the last-resort kernel (tests) */
+#define DNNOPT_TUNE_COUNT           20
 int dnnopt_hip_set_tunable(int key, int value, int* previous);
 int dnnopt_hip_get_tunable(int key, int* value);
 

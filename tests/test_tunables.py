@@ -80,6 +80,6 @@ def test_tunable_keys_are_checked():
 
     lib = u.load_lib()
     v = ctypes.c_int(0)
-    assert lib.so.dnnopt_hip_get_tunable(19, ctypes.byref(v)) != 0
+    assert lib.so.dnnopt_hip_get_tunable(20, ctypes.byref(v)) != 0
     assert lib.so.dnnopt_hip_set_tunable(-1, 0, None) != 0
     assert lib.so.dnnopt_hip_get_tunable(7, None) != 0
