@@ -14,7 +14,9 @@ gemm_int8 (c5f) -- each as its own workload, and reports every timed
 workload's step rate, dominant kernel and per-shape GB/s, TFLOP/s and
 roofline fractions under `configs` (C2's own per-shape figures included).  `--workload NAME` times one workload (its rate
 becomes `value`); `--workload all` adds the oneDNN-hook workload;
-`--detail FILE` appends the full per-workload records.
+`--detail FILE` appends the full per-workload records.  `--yardstick` instead
+times the vendor library (torch.mm / torch._int_mm, hipBLASLt or rocBLAS)
+beside this library on the configs' shapes, one JSON line per shape.
 
 `value` is the algorithmic bytes of a step (sA*M*K + sB*K*N + sC*M*N*(1 +
 [beta != 0]), each operand counted once) divided by the wall time of the
@@ -696,6 +698,83 @@ def _graph_time_us(torch, stream, launches, reps=5):
     return statistics.median(out)
 
 
+def vendor_yardstick():
+    """The vendor library on the configs' shapes, timed beside this library
+    under one harness: torch.mm / torch._int_mm (hipBLASLt / rocBLAS on this
+    image) against the library's C-ABI, each a graph of back-to-back calls
+    over operand copies rotated through at least 600 MB, median of 5
+    replays.  Differences of the calls: torch.mm on bf16 operands writes a
+    bf16 C (the library an fp32 C, 2 more bytes per output); torch._int_mm
+    needs M > 16 (the int8 rows use M = 17 and 128); beta = 0 throughout.
+    One JSON line per shape, then a summary line."""
+    import torch
+
+    b = _binding()
+    lib = b.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    s = torch.cuda.Stream(device=dev)
+    rows = []
+
+    def copies(nbytes):
+        return max(16, -(-(600 << 20) // nbytes))
+
+    def both(name, torch_fns, ours_fns):
+        with torch.cuda.stream(s):
+            for f in torch_fns[:2] + ours_fns[:2]:
+                f()
+        torch.cuda.synchronize()
+        t = _graph_time_us(torch, s, torch_fns)
+        o = _graph_time_us(torch, s, ours_fns)
+        row = {"shape": name, "torch_us": round(t, 2), "ours_us": round(o, 2), "torch_over_ours": round(t / o, 3)}
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+
+    cs = lambda: s.cuda_stream  # noqa: E731
+    for M in (1, 4, 32, 256):
+        N, K = 11008, 4096
+        n = copies(N * K * 2)
+        A = [torch.randn(M, K, device=dev).to(torch.bfloat16) for _ in range(n)]
+        B = [(torch.randn(K, N, device=dev) * 0.02).to(torch.bfloat16) for _ in range(n)]
+        C = torch.empty(M, N, device=dev, dtype=torch.float32)
+        both(f"bf16 {M}x{N}x{K}, B K x N", [lambda k=k: torch.mm(A[k], B[k]) for k in range(n)],
+             [lambda k=k: lib.gemm_bf16(M, N, K, 1.0, A[k], K, B[k], N, 0.0, C, N, stream=cs()) for k in range(n)])
+        Bt = [x.t().contiguous() for x in B]
+        del B
+        both(f"bf16 {M}x{N}x{K}, B N x K", [lambda k=k: torch.mm(A[k], Bt[k].t()) for k in range(n)],
+             [lambda k=k: lib.gemm_bf16_ex(M, N, K, 1.0, A[k], K, Bt[k], K, 0.0, C, N, transB=1, stream=cs())
+              for k in range(n)])
+        del A, Bt, C
+        torch.cuda.empty_cache()
+    for M in (17, 128):
+        N, K = 4096, 4096
+        n = copies(N * K)
+        A = [torch.randint(-127, 128, (M, K), device=dev, dtype=torch.int8) for _ in range(n)]
+        B = [torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8) for _ in range(n)]
+        C = torch.empty(M, N, device=dev, dtype=torch.int32)
+        both(f"int8 {M}x{N}x{K}", [lambda k=k: torch._int_mm(A[k], B[k].t()) for k in range(n)],
+             [lambda k=k: lib.gemm_s8s8s32(M, N, K, A[k], K, B[k], K, C, N, stream=cs()) for k in range(n)])
+        del A, B, C
+        torch.cuda.empty_cache()
+    fp32 = [(M, N, 2048) for M in (1, 7) for N in (1009, 4099, 11003)] + [(65536, 16, 256), (65536, 64, 256)]
+    for M, N, K in fp32:
+        n = copies((M * K if M > N else K * N) * 4)
+        A = [torch.randn(M, K, device=dev) for _ in range(n if M > N else 1)]
+        B = [torch.randn(K, N, device=dev) * 0.02 for _ in range(1 if M > N else n)]
+        C = torch.empty(M, N, device=dev)
+        a = lambda k: A[k % len(A)]  # noqa: E731
+        bb = lambda k: B[k % len(B)]  # noqa: E731
+        both(f"fp32 {M}x{N}x{K}", [lambda k=k: torch.mm(a(k), bb(k)) for k in range(n)],
+             [lambda k=k: lib.sgemm(M, N, K, 1.0, a(k), K, bb(k), N, 0.0, C, N, stream=cs()) for k in range(n)])
+        del A, B, C
+        torch.cuda.empty_cache()
+    wins = sum(1 for r in rows if r["torch_over_ours"] >= 1.0)
+    geo = statistics.geometric_mean([r["torch_over_ours"] for r in rows])
+    print(json.dumps({"yardstick": "torch (hipBLASLt/rocBLAS) vs this library", "shapes": len(rows),
+                      "library_faster": wins, "geomean_torch_over_ours": round(geo, 3),
+                      "torch": torch.__version__}), flush=True)
+
+
 def copy_calibration(mib):
     """Plain copies of a known size: what FETCH_SIZE / WRITE_SIZE read for
     them scales the counters of the GEMM kernels to bytes."""
@@ -744,6 +823,9 @@ def main():
     ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
+    ap.add_argument("--yardstick", action="store_true",
+                    help="only time the vendor library (torch.mm / torch._int_mm) beside this library on the "
+                         "configs' shapes, one JSON line per shape")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (scale for HBM byte counters)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="ARG",
@@ -751,6 +833,9 @@ def main():
                          "summary of rocprofv3 CSV output (no GPU use); with the counter files also write "
                          "profiles/<kernel>_<workload>_traffic.json")
     args = ap.parse_args()
+    if args.yardstick:
+        vendor_yardstick()
+        return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
         return
