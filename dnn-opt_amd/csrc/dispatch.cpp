@@ -36,8 +36,9 @@
 //     32 x 32 tiles staged through LDS (256-byte k-blocks) above that (4-byte
 //     aligned rows), split-k only when the tiles leave more than half of the
 //     CUs idle.
-//   The LDS-DMA tile and k-split of bf16 storage above M = 128 come from a
-//   fitted cost model (pick_bf16_dma) when it beats the rule by 5%.
+//   The LDS-staged tile and k-split of bf16 storage above M = 128, and of
+//   fp32 inputs above M = 64, come from a fitted cost model (pick_tile) when
+//   it beats the rule by 5%.
 //   * any shape whose operand spans none of these kernels can address with
 //     32-bit offsets: the 64-bit last-resort kernel (k_wide.hip).
 // Tunables (dnnopt_hip_set_tunable; a DNNOPT_TUNING build seeds them from
@@ -207,37 +208,46 @@ int plan_kouter(int M, int N, int K, int lda, int ldb, Launch* L) {
     return DNNOPT_OK;
 }
 
-// bf16 storage above M = 128: the LDS-DMA tile and k-split count from a cost
-// model fitted on MI355X (bf16 storage, M = 96..512, N = 2048..11008, K =
-// 1024 and 4096, B stored K x N and N x K, within about 10% of every point
-// measured).  Every workgroup owns one CU, so a launch of W workgroups takes
-// ceil(W / CUs) rounds of one workgroup's time, that time being the MACs of
-// its tile and k-range at a per-configuration rate (us per MAC: 128 x 96 on
-// 8 waves of 32 x 48 0.83e-6, 256 x 96 on 8 waves of 64 x 48 0.57e-6, 128 x
-// 128 on 4 waves of 64 x 64 0.715e-6); a k-split adds its fp32 partial
-// tiles, written and read at 5 TB/s, and 3 us for the reduce launch.
-struct DmaPick {
+// The LDS-staged tile and k-split count from a cost model fitted on MI355X.
+// Every workgroup owns one CU, so a launch of W workgroups takes ceil(W /
+// CUs) rounds of one workgroup's time: the MACs of its tile and k-range at a
+// per-configuration rate, plus a fixed cost per round; a k-split adds its
+// fp32 partial tiles, written and read at 5 TB/s, and 3 us for the reduce
+// launch.  Rates (us per MAC) and fixed costs (us per round):
+//   bf16 storage (LDS DMA; M = 96..512, N = 2048..11008, K = 1024 and 4096,
+//   B stored K x N and N x K, within about 10% of every point measured):
+//   128 x 96 on 8 waves of 32 x 48 0.83e-6, 256 x 96 on 8 waves of 64 x 48
+//   0.57e-6, 128 x 128 on 4 waves of 64 x 64 0.715e-6, no fixed cost;
+//   fp32 inputs rounded in registers (M = 96..512, N = 4096 and 11008, K =
+//   1024 and 4096; the pick is within 1% of the best of 6 measured choices
+//   on 21 of 24 shapes): 128 x 96 1.35e-6 + 3 us, 256 x 96 1.15e-6 + 9 us.
+struct TilePick {
     int cfg;
     long long s;
     double us;
 };
 
-static double bf16_dma_cost(int cfg, long long s, int M, int N, int K, long long cus) {
+static double tile_cost(int mode, int cfg, long long s, int M, int N, int K, long long cus) {
     const TileConfig c = tile_config(cfg);
     const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
     const int kb = tile_lds_bk(bm, bn, c.kblk);
     const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, kb);
-    const double rate = cfg == 33 ? 0.57e-6 : (cfg == kTileBF16Dma4w ? 0.715e-6 : 0.83e-6);
+    double rate, fixed = 0.0;
+    if (mode == kTileF2B) {
+        rate = cfg == kTileF2BTall ? 1.15e-6 : 1.35e-6;
+        fixed = cfg == kTileF2BTall ? 9.0 : 3.0;
+    } else {
+        rate = cfg == 33 ? 0.57e-6 : (cfg == kTileBF16Dma4w ? 0.715e-6 : 0.83e-6);
+    }
     const double macs = (double)bm * bn * (double)ceil_div(nblk, s) * kb;
-    double us = (double)ceil_div(tiles * s, cus) * macs * rate;
+    double us = (double)ceil_div(tiles * s, cus) * (macs * rate + fixed);
     if (s > 1) us += 2.0 * (double)s * tiles * bm * bn * 4 / 5e6 + 3.0;
     return us;
 }
 
-// The tile and split count for bf16 storage, M > 128: the measured default
-// (128 x 96, or 256 x 96 once 128-row tiles need more than one round, split
-// by the LDS rule) unless the model puts another choice at least 5% faster.
-static DmaPick pick_bf16_dma(int M, int N, int K, int def_cfg) {
+// The measured default (def_cfg, split by the LDS rule) unless the model puts
+// another candidate at least 5% ahead.
+static TilePick pick_tile(int mode, int M, int N, int K, int def_cfg, bool tall_ok) {
     const long long cus = num_cus();
     auto lds_splits = [&](int cfg) {
         const TileConfig c = tile_config(cfg);
@@ -247,18 +257,23 @@ static DmaPick pick_bf16_dma(int M, int N, int K, int def_cfg) {
         return std::min<long long>({ceil_div(cus, tiles), std::max<long long>(1, nblk / 2), (long long)max_splits()});
     };
     const long long s_def = lds_splits(def_cfg);
-    DmaPick best{def_cfg, s_def, bf16_dma_cost(def_cfg, s_def, M, N, K, cus)};
+    TilePick best{def_cfg, s_def, tile_cost(mode, def_cfg, s_def, M, N, K, cus)};
     const double def_us = best.us;
-    for (int cfg : {26, 33, kTileBF16Dma4w}) {
+    static const int kBf16[] = {26, 33, kTileBF16Dma4w};
+    static const int kF2B[] = {20, kTileF2BTall};
+    const int* cand = mode == kTileF2B ? kF2B : kBf16;
+    const int ncand = mode == kTileF2B ? (tall_ok ? 2 : 1) : 3;
+    for (int i = 0; i < ncand; ++i) {
+        const int cfg = cand[i];
         const TileConfig c = tile_config(cfg);
         const long long nblk = ceil_div(K, tile_lds_bk(c.wm * c.mt * 16, c.wn * c.nt * 16, c.kblk));
         const long long smax = std::min<long long>({16, std::max<long long>(1, nblk / 2), (long long)max_splits()});
         for (long long s = 1; s <= smax; ++s) {
-            const double us = bf16_dma_cost(cfg, s, M, N, K, cus);
-            if (us < best.us) best = DmaPick{cfg, s, us};
+            const double us = tile_cost(mode, cfg, s, M, N, K, cus);
+            if (us < best.us) best = TilePick{cfg, s, us};
         }
     }
-    if (best.us > 0.95 * def_us) return DmaPick{def_cfg, s_def, def_us};
+    if (best.us > 0.95 * def_us) return TilePick{def_cfg, s_def, def_us};
     return best;
 }
 
@@ -280,7 +295,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
                      (transB ? ((long long)(N + 128) * ldb + K) : ((long long)K * ldb + N)) * es < 0x7FFFFFFFll &&
                      (long long)128 * ldc * 4 < 0x7FFFFFFFll;
     int cfg;
-    long long model_splits = 0;  // bf16 LDS-DMA: the cost model's split count
+    long long model_splits = 0;  // the cost model's split count
     const int forced_cfg = tunable(kTuneTileCfg);
     if (lds) {
         // 128 k per LDS block below M = 128 (fewer barriers, more bytes per
@@ -295,7 +310,11 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         // fp32 inputs rounded in registers, M > 64: 128 x 96 tiles with 128 k
         // per block (MI355X, us, N = 11008, K = 4096: M = 72 / 96 / 128 / 256
         // / 512 72.7 / 75.4 / 79.8 / 97.1 / 174.8 -> 67.1 / 69.3 / 73.6 / 84.5
-        // / 162.3; 1024 x 4096 x 4096 156.1 -> 144.6).
+        // / 162.3; 1024 x 4096 x 4096 156.1 -> 144.6).  The cost model may
+        // pick another split count or 256 x 96 tiles (register ring, 64 k
+        // per block; measured, us, default -> picked: 128 x 11008 x 1024 32.4
+        // -> 23.4 (2 splits instead of 3), 256 x 4096 x 4096 62.1 -> 47.1 (2
+        // instead of 3), 512 x 11008 x 4096 145.7 -> 121.5 (256 x 96)).
         if (mode == kTileF2B && M > 64) cfg = 20;
         // bf16 storage above M = 128: the same 128 x 96 tile with the
         // operands copied into LDS by the memory unit (C4 M=256 43.1 vs 45.4
@@ -313,15 +332,19 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         if (M > 128 && mode == kTileBF16) {
             cfg = 26;
             if (ceil_div(M, 128) * ceil_div(N, 96) > num_cus()) cfg = 33;
-            if (forced_cfg < kTileFirstLds && tunable(kTuneTileSplits) <= 0) {  // nothing forced
-                const DmaPick pick = pick_bf16_dma(M, N, K, cfg);
-                cfg = pick.cfg;
-                model_splits = pick.s;
-            }
+        }
+        // 256-row register-staged tiles: 32-bit C offsets over 256 rows.
+        const bool tall_ok = 256LL * ldc * 4 < 0x7FFFFFFFll;
+        const bool nothing_forced = forced_cfg < kTileFirstLds && tunable(kTuneTileSplits) <= 0;
+        if (nothing_forced && ((M > 128 && mode == kTileBF16) || (M > 64 && mode == kTileF2B))) {
+            const TilePick pick = pick_tile(mode, M, N, K, cfg, tall_ok);
+            cfg = pick.cfg;
+            model_splits = pick.s;
         }
         const bool forced_dma = forced_cfg >= kTileFirstDma && forced_cfg < kTileF32Few;
         if (((forced_cfg >= kTileFirstLds && forced_cfg < kTileF32Few) || forced_cfg == kTileBF16Tb48 ||
-             forced_cfg == kTileBF16Tb48Few || forced_cfg == kTileBF16Dma4w) &&
+             forced_cfg == kTileBF16Tb48Few || forced_cfg == kTileBF16Dma4w ||
+             (forced_cfg == kTileF2BTall && tall_ok)) &&
             ((!forced_dma && forced_cfg != kTileBF16Dma4w) || mode == kTileBF16))
             cfg = forced_cfg;
     } else if (mode == kTileF32 && N <= 16) {

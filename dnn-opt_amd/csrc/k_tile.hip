@@ -1098,6 +1098,8 @@ static const TileConfig kTileConfigs[] = {
     {1, 1, 1, 3, 1, 3, 128},  // 38: 16 x 48, 3 waves, 128 k per block, 3 ahead
     // bf16 storage, LDS DMA (continued)
     {4, 4, 2, 2, 1, 3, 64},   // 39: 128 x 128, 4 waves of 64 x 64, 3 stages
+    // LDS-staged (continued)
+    {4, 3, 4, 2, 1, 2, 64},   // 40: 256 x 96, 8 waves of 64 x 48, 64 k per block
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -1185,6 +1187,7 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_LDS_CASE(37, 2, 1, 1, 3, 3, 128, 1)
         DNNOPT_TILE_LDS_CASE(38, 1, 1, 1, 3, 3, 128, 1)
         DNNOPT_TILE_DMA_CASE(39, 4, 4, 2, 2, 3, 64)
+        DNNOPT_TILE_LDS_CASE(40, 4, 3, 4, 2, 2, 64, 1)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

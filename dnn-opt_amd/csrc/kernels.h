@@ -235,6 +235,11 @@ constexpr int kTileBF16Tb48 = 37, kTileBF16Tb48Few = 38;
 // bf16 storage, LDS DMA: 128 x 128 tiles on 4 waves of 64 x 64 (bf16
 // storage only, like the LDS-DMA entries from kTileFirstDma).
 constexpr int kTileBF16Dma4w = 39;
+// LDS-staged (register ring), 256 x 96 on 8 waves of 64 x 48, 64 k per
+// block: fp32 inputs rounded in registers, many tiles.  Its unsplit epilogue
+// addresses C with 32-bit offsets from the tile's first row, so it needs
+// 256 * ldc * 4 < 2^31.
+constexpr int kTileF2BTall = 40;
 // k per LDS block of an LDS-staged configuration: its kblk (or
 // DNNOPT_LDS_KB) when both stages fit in 128 KiB of LDS, else 64.
 constexpr int tile_lds_bk(int bm, int bn, int kblk) {

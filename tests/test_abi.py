@@ -376,6 +376,19 @@ def test_plans_route_lds_dma_kernels(lib):
     for (M, N), want in cases.items():
         for p in (lib.plan_bf16(M, N, 4096), lib.plan_bf16_ex(M, N, 4096, transB=1)):
             assert p["name"] == "dnnopt_tile_bf16_dma" and (p["rows"], p["cols"], p["splits"]) == want, (M, N, p)
+    # fp32 inputs above M = 64: 128 x 96 tiles split by the model, 256 x 96
+    # tiles (register ring) where they cut the rounds (measured on MI355X:
+    # 128 x 11008 x 1024 32.4 -> 23.4 us, 256 x 4096 x 4096 62.1 -> 47.1,
+    # 512 x 11008 x 4096 145.7 -> 121.5); unaligned strides change nothing.
+    cases = {(96, 4096, 1024): (128, 96, 4), (128, 11008, 1024): (128, 96, 2), (256, 4096, 4096): (128, 96, 2),
+             (512, 4096, 4096): (128, 96, 1), (256, 11008, 4096): (128, 96, 1), (384, 11008, 1024): (256, 96, 1),
+             (512, 11008, 4096): (256, 96, 1), (1024, 4096, 4096): (256, 96, 1)}
+    for (M, N, K), want in cases.items():
+        p = lib.plan_bf16(M, N, K, fp32_inputs=1)
+        assert p["name"] == "dnnopt_tile_bf16_lds" and (p["rows"], p["cols"], p["splits"]) == want, (M, N, K, p)
+    with lib.tunables(TILE_CFG=40, TILE_SPLITS=3):
+        p = lib.plan_bf16(300, 1000, 520, fp32_inputs=1)
+        assert (p["name"], p["rows"], p["cols"], p["splits"]) == ("dnnopt_tile_bf16_lds", 256, 96, 3), p
     # a forced tile or split count turns the model off
     with lib.tunables(TILE_SPLITS=2):
         assert (lib.plan_bf16(256, 4096, 4096)["rows"], lib.plan_bf16(256, 4096, 4096)["cols"]) == (128, 96)

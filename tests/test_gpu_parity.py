@@ -532,6 +532,85 @@ def test_bf16_dma_128x128_four_wave_tiles(lib, orc, dev, tb):
         u.assert_fp32_close(got, want, scale, K, f"128x128 planned {M}x{N}x{K} tb={tb}")
 
 
+@pytest.mark.parametrize("mode", ["f2b", "bf16", "bf16_tb"])
+def test_lds_256x96_register_ring_tiles(lib, orc, dev, mode):
+    """256 x 96 LDS-staged tiles on 8 waves of 64 x 48, operands staged through
+    a register ring (fp32 inputs rounded in registers, or bf16 storage with B
+    stored K x N or N x K): forced with 1 to 3 k-splits on a ragged shape (M
+    and N off the tile, a K tail inside a 64-k block, padded strides, beta !=
+    0, alpha != 1)."""
+    M, N, K, pa, pb = 300, 1000, 520, 2, 4
+    tb = int(mode == "bf16_tb")
+    lda, ldb = K + pa, (K + pb if tb else N + pb)
+    rows = N if tb else K
+    A32 = u.normal(orc, M * lda, 41).reshape(M, lda)
+    B32 = u.normal(orc, rows * ldb, 42, 0, 0.02).reshape(rows, ldb)
+    C0 = u.uniform(orc, M * N, 43).reshape(M, N)
+    A, Bs = u.bf16_bits(orc, A32), u.bf16_bits(orc, B32)
+    Bkn = np.ascontiguousarray(Bs[:, :K].T if tb else Bs[:, :N])
+    want, scale = u.exact(u.bf16_value(A)[:, :K], u.bf16_value(Bkn), 0.5, 0.25, C0)
+    for splits in (1, 2, 3):
+        with lib.tunables(TILE_CFG=40, TILE_SPLITS=splits):
+            if mode == "f2b":
+                p = lib.plan_bf16(M, N, K, fp32_inputs=1)
+            else:
+                p = lib.plan_bf16_ex(M, N, K, transB=tb)
+            assert (p["name"], p["rows"], p["cols"], p["splits"]) == ("dnnopt_tile_bf16_lds", 256, 96, splits), p
+            dC = dev_copy(C0, dev)
+            if mode == "f2b":
+                lib.gemm_bf16_f32in(M, N, K, 0.5, dev_copy(A32, dev), lda, dev_copy(B32, dev), ldb, 0.25, dC, N,
+                                    stream=stream())
+            else:
+                lib.gemm_bf16_ex(M, N, K, 0.5, dev_copy(A.view(np.int16), dev), lda, dev_copy(Bs.view(np.int16), dev),
+                                 ldb, 0.25, dC, N, transB=tb, stream=stream())
+            got = host(dC)
+        u.assert_fp32_close(got, want, scale, K, f"256x96 register ring, {mode}, {splits} splits")
+
+
+@pytest.mark.parametrize("M,N,K,rows,splits", [(96, 4096, 1024, 128, 4), (128, 11008, 1024, 128, 2),
+                                               (384, 11008, 1024, 256, 1), (1024, 4096, 1024, 256, 1)])
+def test_bf16_fp32_inputs_cost_model_picks(lib, orc, dev, M, N, K, rows, splits):
+    """fp32 inputs above M = 64: the tile and split count the cost model
+    picks (128 x 96 with its own split count, 256 x 96 tiles in fewer
+    rounds), each within the fp32 bound of the exact product of the
+    bf16-rounded operands."""
+    p = lib.plan_bf16(M, N, K, fp32_inputs=1)
+    assert (p["name"], p["rows"], p["cols"], p["splits"]) == ("dnnopt_tile_bf16_lds", rows, 96, splits), p
+    A = u.normal(orc, M * K, 51).reshape(M, K)
+    B = u.normal(orc, K * N, 52, 0, 0.02).reshape(K, N)
+    dC = torch.full((M * N,), float("nan"), dtype=torch.float32, device=dev)
+    lib.gemm_bf16_f32in(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, 0.0, dC, N, stream=stream())
+    want, scale = u.exact(u.bf16_value(u.bf16_bits(orc, A)), u.bf16_value(u.bf16_bits(orc, B)))
+    u.assert_fp32_close(host(dC).reshape(M, N), want, scale, K, f"f32 inputs planned {M}x{N}x{K}")
+
+
+def test_bf16_fp32_inputs_wide_c_stride_keeps_128_row_tiles(lib, orc, dev):
+    """A C row stride at which 256 rows span more than 2^31 bytes (ldc =
+    2^21 + 2^14 floats): the 256 x 96 register-ring tile, whose unsplit
+    epilogue addresses C with 32-bit offsets from the tile's first row, is
+    not used (the model would pick it for 384 x 11008 x 1024) and every row
+    is written; the padding columns between rows stay untouched."""
+    M, N, K = 384, 11008, 1024
+    ldc = (1 << 21) + (1 << 14)
+    assert lib.plan_bf16(M, N, K, fp32_inputs=1)["rows"] == 256
+    A = u.normal(orc, M * K, 61).reshape(M, K)
+    B = u.normal(orc, K * N, 62, 0, 0.02).reshape(K, N)
+    dC = torch.full(((M - 1) * ldc + N,), float("nan"), dtype=torch.float32, device=dev)
+    with lib.tunables(TILE_CFG=40):  # a forced 256-row tile is refused at this stride too
+        lib.gemm_bf16_f32in(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, 0.0, dC, ldc, stream=stream())
+        got_forced = host(torch.as_strided(dC, (M, N), (ldc, 1)))
+    dC.fill_(float("nan"))
+    lib.gemm_bf16_f32in(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(B, dev), N, 0.0, dC, ldc, stream=stream())
+    got = host(torch.as_strided(dC, (M, N), (ldc, 1)))
+    pad = host(torch.as_strided(dC, (M - 1, 64), (ldc, 1), N))
+    del dC
+    torch.cuda.empty_cache()
+    want, scale = u.exact(u.bf16_value(u.bf16_bits(orc, A)), u.bf16_value(u.bf16_bits(orc, B)))
+    u.assert_fp32_close(got, want, scale, K, "f32 inputs, ldc 2^21 + 2^14")
+    u.assert_fp32_close(got_forced, want, scale, K, "f32 inputs, forced 256-row tile, ldc 2^21 + 2^14")
+    assert np.isnan(pad).all(), "a write landed between the rows of C"
+
+
 def test_bf16_dma_k_split_ticket_matches_reduce_kernel(lib, orc, dev):
     """A 2-way k-split of 256 x 96 LDS-DMA tiles summed by the last workgroup
     to finish (tunable TILE_TICKET=1) gives the same bits as the reduce kernel
