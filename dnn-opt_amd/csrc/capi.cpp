@@ -303,7 +303,8 @@ int dnnopt_hip_plan_gemm_int8_f32(int M, int N, int K, dnnopt_plan* out) {
     // M > 8: the int8 tiles that quantize the fp32 B while staging it (as
     // dnnopt_hip_gemm_int8_f32 with unpadded strides and DNNOPT_Q8B unset).
     const int ldq = (K + 15) & ~15;
-    if (((long long)K * N + N) * 4 < 0x7FFFFFFFll && ((long long)M + 64) * ldq < 0x7FFFFFFFll) {
+    if (((long long)K * N + N) * 4 < 0x7FFFFFFFll && ((long long)M + 64) * ldq < 0x7FFFFFFFll &&
+        (long long)((N + 31) / 32) * ((M + 63) / 64) <= 0x7FFFFFF0ll) {
         *out = dnnopt_plan{};
         out->kernel = DNNOPT_K_MFMA_S8;
         out->rows = 64;
@@ -563,7 +564,7 @@ int dnnopt_hip_gemm_int8_f32(int M, int N, int K, float alpha, const float* A, i
     // with 31-bit buffer offsets; larger strides take the quantization pass
     // and gemm_s8_common, whose planner checks its own ranges.
     if (q8b_ok && ((long long)K * ldb + N) * 4 < 0x7FFFFFFFll && ((long long)M + 64) * ldq < 0x7FFFFFFFll &&
-        ((long long)64 * ldc + N) * 4 < 0x7FFFFFFFll) {
+        ((long long)64 * ldc + N) * 4 < 0x7FFFFFFFll && (long long)((N + 31) / 32) * ((M + 63) / 64) <= 0x7FFFFFF0ll) {
         // Maxima, A quantized (M x ldq), then 64 x 32 int8 tiles that quantize
         // the fp32 B while staging it: no int8 copy of B.  Staging (slot 1):
         // [qA M x ldq][absmax partials][max|A|, max|B|].

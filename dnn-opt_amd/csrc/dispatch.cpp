@@ -38,7 +38,9 @@
 //     CUs idle.
 //   The LDS-staged tile and k-split of bf16 storage above M = 128, and of
 //   fp32 inputs above M = 64, come from a fitted cost model (pick_tile) when
-//   it beats the rule by 5%.
+//   it beats the rule by 5%; the fp32 register tile and k-split (A stored
+//   M x K, M >= 12, N >= 64) from another (pick_f32_tile) when it beats the
+//   rule by 10%.
 //   * any shape whose operand spans none of these kernels can address with
 //     32-bit offsets: the 64-bit last-resort kernel (k_wide.hip).
 // Tunables (dnnopt_hip_set_tunable; a DNNOPT_TUNING build seeds them from
@@ -277,6 +279,80 @@ static TilePick pick_tile(int mode, int M, int N, int K, int def_cfg, bool tall_
     return best;
 }
 
+// k-splits of an fp32 register-tile launch by the occupancy rule: split k
+// when the tiles give fewer workgroups than waves_per_cu() waves on every CU.
+static long long reg_tile_splits(int cfg, int M, int N, int K) {
+    const TileConfig c = tile_config(cfg);
+    const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
+    const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, 64);
+    const long long target_wgs = num_cus() * waves_per_cu() / (c.wm * c.wn * c.kw);
+    if (tiles >= target_wgs) return 1;
+    return std::max<long long>(1, std::min<long long>({ceil_div(target_wgs, tiles),
+                                                      std::max<long long>(1, nblk / (2 * c.kw)),
+                                                      (long long)max_splits()}));
+}
+
+// fp32 register tiles (A stored M x K, M >= 12, N >= 64, at most 10^10
+// MACs): the configuration and k-split from a cost model fitted on MI355X
+// (320 measured cases: M = 10..12544, N = 64..11008, K = 64..4608, B stored
+// K x N and N x K; six configurations, 1 to 16 splits; median error 5%, 90%
+// of the cases within 13%).  A launch of W waves gives each SIMD ceil(W / (4
+// CUs)) waves, occ of them resident at a time (the configuration's
+// occupancy, from its register use); each of a wave's 64-k blocks takes
+// max(lat + m, r m), m being the block's 16 MT NT MFMAs (32 cycles at 2.4
+// GHz, times a fitted factor) and r the waves resident on its SIMD; every CU
+// also reads its workgroups' A and B tiles (at a fitted cost per byte);
+// 3.23 us per launch, and a k-split adds 2.22 us plus its fp32 partials
+// written and read at 6.4 TB/s.
+struct F32Fit {
+    int cfg, tb, occ;
+    double lat, mfma, ps_per_byte;
+};
+static const F32Fit kF32Fit[] = {
+    {1, 0, 4, 0.394, 0.140, 45.3}, {1, 1, 4, 0.762, 0.297, 55.9}, {2, 0, 4, 0.502, 0.185, 41.9},
+    {2, 1, 8, 1.130, 0.189, 46.6}, {3, 0, 4, 0.558, 0.371, 39.3}, {3, 1, 8, 0.978, 0.163, 48.8},
+    {4, 0, 3, 0.638, 0.119, 50.6}, {4, 1, 4, 2.089, 0.406, 45.1}, {35, 0, 8, 0.457, 1.144, 15.0},
+    {35, 1, 8, 0.248, 0.785, 20.7}, {36, 0, 4, 0.707, 0.251, 14.5}, {36, 1, 4, 0.952, 0.249, 25.5},
+};
+
+static double f32_tile_cost(const F32Fit& f, long long s, int M, int N, int K, long long cus) {
+    const TileConfig c = tile_config(f.cfg);
+    const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
+    const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, 64);
+    s = std::min(s, nblk);
+    const long long blocks = ceil_div(nblk, s * c.kw);  // k-blocks of one wave
+    const long long per_simd = ceil_div(tiles * s * c.wm * c.wn * c.kw, cus * 4);
+    const long long resident = std::min<long long>(f.occ, per_simd);
+    const double m = 16.0 * c.mt * c.nt * 32 / 2400.0 * f.mfma;
+    double us = 3.23 + (double)ceil_div(per_simd, f.occ) * (double)blocks * std::max(f.lat + m, (double)resident * m);
+    us += (double)ceil_div(tiles * s, cus) * (bm + bn) * (double)(ceil_div(nblk, s) * 64) * 4 * f.ps_per_byte * 1e-6;
+    if (s > 1) us += 2.22 + 2.0 * (double)s * tiles * bm * bn * 4 * 0.1574e-6;
+    return us;
+}
+
+// The rule's configuration and split count unless the model puts another
+// choice at least 10% ahead.
+static TilePick pick_f32_tile(int tb, int M, int N, int K, int def_cfg) {
+    const long long cus = num_cus(), def_s = reg_tile_splits(def_cfg, M, N, K);
+    const F32Fit* d = nullptr;
+    for (const F32Fit& f : kF32Fit)
+        if (f.cfg == def_cfg && f.tb == tb) d = &f;
+    if (!d) return TilePick{def_cfg, 0, 0.0};
+    const double def_us = f32_tile_cost(*d, def_s, M, N, K, cus);
+    TilePick best{def_cfg, def_s, def_us};
+    const long long nblk = ceil_div(K, 64);
+    for (const F32Fit& f : kF32Fit) {
+        if (f.tb != tb) continue;
+        for (long long s : {1, 2, 3, 4, 6, 8, 12, 16}) {
+            if (s > nblk || s > max_splits()) break;
+            const double us = f32_tile_cost(f, s, M, N, K, cus);
+            if (us < best.us) best = TilePick{f.cfg, s, us};
+        }
+    }
+    if (best.us > 0.9 * def_us) return TilePick{def_cfg, 0, def_us};
+    return best;
+}
+
 int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, bool lds_ok,
               int ldc) {
     *L = Launch{};
@@ -375,6 +451,17 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     } else {
         cfg = 2;
     }
+    // fp32 register tiles: the cost model's choice when nothing is forced, or
+    // a forced configuration (tunable TILE_CFG).
+    if (!lds && mode == kTileF32 && !transA && M >= 12 && N >= 64 && (double)M * N * K <= 1e10 && forced_cfg <= 0 &&
+        tunable(kTuneTileSplits) <= 0) {
+        const TilePick pick = pick_f32_tile(transB ? 1 : 0, M, N, K, cfg);
+        cfg = pick.cfg;
+        model_splits = pick.s;
+    }
+    if (!lds && mode == kTileF32 &&
+        ((forced_cfg >= 1 && forced_cfg <= 4) || forced_cfg == kTileF32Few || forced_cfg == kTileF32Few128))
+        cfg = forced_cfg;
     const TileConfig c = tile_config(cfg);
     const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
     const int kb = lds ? tile_lds_bk(bm, bn, c.kblk) : (mode == kTileF32 ? 64 : 128);
@@ -390,6 +477,8 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
         if (tiles * 2 < cus) s = std::min<long long>({ceil_div(cus, tiles), std::max<long long>(1, nblk / 2),
                                                       (long long)max_splits()});
         if (model_splits > 0) s = model_splits;
+    } else if (mode == kTileF32) {
+        s = model_splits > 0 ? model_splits : reg_tile_splits(cfg, M, N, K);
     } else {
         const long long target_wgs = cus * waves_per_cu() / waves_per_wg;
         if (tiles < target_wgs) {
@@ -413,14 +502,13 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     while (!span_ok(s) && s < nblk) s *= 2;
     if (s > nblk) s = nblk;
     if (!span_ok(s)) return DNNOPT_ERR_UNSUPPORTED;
-    if (tm > 65535 || s > 65535) return DNNOPT_ERR_UNSUPPORTED;
+    if (tm > 65535 || s > 65535 || tn * tm > 0x7FFFFFF0ll) return DNNOPT_ERR_UNSUPPORTED;
     L->mode = mode;
     L->cfg = cfg;
     L->bm = bm;
     L->bn = bn;
     L->tn = (int)tn;
     L->tm = (int)tm;
-    // LDS-staged tiles are launched as one XCD-ordered row of workgroups.
     // LDS-staged tiles and the 16-row fp32 tiles are launched as one
     // XCD-ordered row of workgroups.
     const bool xcd = lds || (mode == kTileF32 && c.mt == 1 && c.wm == 1);
@@ -501,7 +589,7 @@ static int plan_s8_kernels(int epi, int M, int N, int K, Launch* L, bool lds_ok,
     // The tiles address A and B from their first row with 32-bit offsets.
     if ((long long)bm * (lda > 0 ? lda : K) + K >= 0x7FFFFFFFll || (long long)bn * (ldb > 0 ? ldb : K) + K >= 0x7FFFFFFFll)
         return DNNOPT_ERR_UNSUPPORTED;
-    if (tm > 65535 || s > 65535) return DNNOPT_ERR_UNSUPPORTED;
+    if (tm > 65535 || s > 65535 || tn * tm > 0x7FFFFFF0ll) return DNNOPT_ERR_UNSUPPORTED;
     // The LDS-staged kernel always hands its k-splits to the reduce kernel.
     L->defer_reduce = (s > 1 && (split_reduce_mode() || lds)) ? 1 : 0;
     L->mode = epi;

@@ -188,23 +188,24 @@ struct TileArgs {
 };
 
 // LDS-staged kernels walk the tiles in an XCD-aware order: workgroup L runs on
-// XCD L % 8 (the hardware dispatches workgroups to XCDs round robin) and
-// takes the tiles of the column strips n = x, x + 8, x + 16, ... with all
-// their row tiles back to back, so the row tiles that share a strip of B run
-// together on one XCD and share its L2.  Workgroups past the last tile of
-// their XCD exit.  The order affects speed only, never which tiles exist.
+// XCD L % 8 (the hardware dispatches workgroups to XCDs round robin).  The
+// tiles are numbered strip by strip (t = n tm + m) and XCD x takes the run
+// t = x P .. x P + P - 1, P = ceil(tn tm / 8), in order, so the row tiles that
+// share a strip of B run together on one XCD and share its L2, and every XCD
+// gets P tiles (the last one fewer) however few column strips there are.
+// Workgroups past the last tile exit.  The order affects speed only, never
+// which tiles exist.  The host keeps tn tm below 2^31 - 8.
 struct TileXY {
     int n, m;
     bool ok;
 };
 __host__ __device__ inline TileXY xcd_tile(int L, int tn, int tm) {
-    const int x = L & 7, j = L >> 3;
-    const int strips = tn > x ? (tn - x + 7) >> 3 : 0;  // tiles n = x (mod 8)
-    if (j >= strips * tm) return TileXY{0, 0, false};
-    return TileXY{(j / tm) * 8 + x, j % tm, true};
+    const int per = (tn * tm + 7) >> 3, j = L >> 3, t = (L & 7) * per + j;
+    if (j >= per || t >= tn * tm) return TileXY{0, 0, false};
+    return TileXY{t / tm, t % tm, true};
 }
 // Workgroups to launch for a tn x tm tile grid in that order.
-inline int xcd_grid(int tn, int tm) { return 8 * ((tn + 7) / 8) * tm; }
+inline int xcd_grid(int tn, int tm) { return 8 * ((tn * tm + 7) / 8); }
 
 struct TileConfig {
     int mt, nt, wm, wn, kw;

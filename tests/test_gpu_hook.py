@@ -323,9 +323,9 @@ def test_ticket_reduction_mode(lib, orc, dev):
         torch.cuda.synchronize()
         return t.cpu().numpy()
 
-    with lib.tunables(SPLIT_REDUCE=0):
-        # row-major fp32: skinny with k-splits, tiles with k-splits (tiles take
-        # the ticket path up to 16 splits, the skinny kernel always)
+    with lib.tunables(SPLIT_REDUCE=0, TILE_SPLITS=4):
+        # row-major fp32: skinny with k-splits, tiles with 4 forced k-splits
+        # (tiles take the ticket path up to 16 splits, the skinny kernel always)
         for M, N, K in ((1, 4096, 4096), (7, 1009, 2048), (3, 257, 5000), (1024, 256, 1024), (300, 600, 2048)):
             p = lib.plan_sgemm(M, N, K)
             assert p["splits"] > 1 and (M <= 8 or p["splits"] <= 16), (M, N, K, p)

@@ -65,7 +65,11 @@ FEW_TA = [(7, 11003, 300, 1, 0), (8, 4096, 129, 1, 3), (13, 2053, 517, 1, 1), (1
 
 @pytest.mark.parametrize("M,N,K,tb,pad,ta", [f + (0,) for f in FEW] + [f + (1,) for f in FEW_TA])
 def test_sgemm_few_rows_tiles(lib, orc, dev, M, N, K, tb, pad, ta):
-    p = lib.plan_sgemm(M, N, K, transA=ta, transB=tb)
+    """The 16-row tiles (forced where the cost model may pick another tile),
+    then the planner's own choice on the same inputs."""
+    cfg = 35 if tb and M <= 16 else 36
+    with lib.tunables(TILE_CFG=cfg):
+        p = lib.plan_sgemm(M, N, K, transA=ta, transB=tb)
     assert p["name"] == "dnnopt_tile_f32" and p["rows"] == 16 and p["cols"] == (16 if tb and M <= 16 else 128), p
     lda, ldb = (M + pad if ta else K + pad), (K + pad if tb else N + pad)
     As = u.normal(orc, (K if ta else M) * lda, 1, 0, 0.02).reshape(K if ta else M, lda)
@@ -74,11 +78,14 @@ def test_sgemm_few_rows_tiles(lib, orc, dev, M, N, K, tb, pad, ta):
     Bkn = np.ascontiguousarray(Bs[:, :K].T if tb else Bs[:, :N])
     C0 = u.uniform(orc, M * N, 3).reshape(M, N)
     dA, dB = dev_copy(As, dev), dev_copy(Bs, dev)
-    for alpha, beta in ((1.0, 1.0), (-0.75, 0.0)):
-        dC = dev_copy(C0 if beta != 0.0 else np.full_like(C0, np.nan), dev)
-        lib.sgemm(M, N, K, alpha, dA, lda, dB, ldb, beta, dC, N, transA=ta, transB=tb, stream=stream())
-        want, scale = u.exact(Amk, Bkn, alpha, beta, C0)
-        u.assert_fp32_close(host(dC), want, scale, K, f"few rows {M}x{N}x{K} ta={ta} tb={tb} a={alpha} b={beta}")
+    for forced in (True, False):
+        for alpha, beta in ((1.0, 1.0), (-0.75, 0.0)):
+            dC = dev_copy(C0 if beta != 0.0 else np.full_like(C0, np.nan), dev)
+            with lib.tunables(TILE_CFG=cfg if forced else 0):
+                lib.sgemm(M, N, K, alpha, dA, lda, dB, ldb, beta, dC, N, transA=ta, transB=tb, stream=stream())
+            want, scale = u.exact(Amk, Bkn, alpha, beta, C0)
+            u.assert_fp32_close(host(dC), want, scale, K,
+                                f"few rows {M}x{N}x{K} ta={ta} tb={tb} a={alpha} b={beta} forced={forced}")
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096)] + [(M, N, 2048) for M in (2, 3, 5, 7) for N in (1009, 4099, 11003)])
