@@ -49,7 +49,8 @@
 //   DNNOPT_SKINNY_WGS_PER_CU (default 1), DNNOPT_SKINNY_WGS (force G),
 //   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel),
 //   DNNOPT_TILE_SPLITS (force the k-splits of a tile launch), DNNOPT_TILE_CFG
-//   (force an LDS-staged bf16 tile configuration, index 5 and up),
+//   (force a tile configuration: an LDS-staged bf16 one, index 5 and up, or
+//   an fp32 register tile, 1-4, 35 or 36; either turns the cost models off),
 //   DNNOPT_S8_CFG / DNNOPT_S8_SPLITS (force the int8 configuration / splits),
 //   DNNOPT_TALL=0 (keep tall-skinny fp32 GEMMs on the register-only tiles),
 //   DNNOPT_TALL_WGS_PER_CU (default 1), DNNOPT_TALL_RT (force 16- or 32-row

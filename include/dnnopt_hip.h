@@ -292,8 +292,9 @@ int dnnopt_hip_device_count(void);    /* 0 when no device is visible        */
 #define DNNOPT_TUNE_MAX_SPLITS       6
 #define DNNOPT_TUNE_SPLIT_REDUCE     7  /* 1: reduce kernel; 0: last-arriving workgroup */
 #define DNNOPT_TUNE_SKINNY_WGS       8
-#define DNNOPT_TUNE_TILE_SPLITS      9
-#define DNNOPT_TUNE_TILE_CFG        10
+#define DNNOPT_TUNE_TILE_SPLITS      9  /* force the k-splits of a tile launch */
+#define DNNOPT_TUNE_TILE_CFG        10  /* force a tile configuration (bf16 LDS-staged: 5 and up;
+                                           fp32 register tiles: 1-4, 35, 36) */
 #define DNNOPT_TUNE_TILE_TICKET     11
 #define DNNOPT_TUNE_S8_CFG          12
 #define DNNOPT_TUNE_S8_ROWDOT       13
