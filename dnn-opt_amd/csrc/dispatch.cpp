@@ -40,7 +40,9 @@
 //   fp32 inputs above M = 64, come from a fitted cost model (pick_tile) when
 //   it beats the rule by 5%; the fp32 register tile and k-split (A stored
 //   M x K, M >= 12, N >= 64) from another (pick_f32_tile) when it beats the
-//   rule by 10%.
+//   rule by 10%; and, for bf16 storage from M = 12, every LDS-staged and
+//   LDS-DMA tile and k-split from a third (pick_bf16_tile) when it beats
+//   the choice above by 10%.
 //   * any shape whose operand spans none of these kernels can address with
 //     32-bit offsets: the 64-bit last-resort kernel (k_wide.hip).
 // Tunables (dnnopt_hip_set_tunable; a DNNOPT_TUNING build seeds them from
@@ -248,18 +250,23 @@ static double tile_cost(int mode, int cfg, long long s, int M, int N, int K, lon
     return us;
 }
 
+// k-splits of an LDS-staged tile launch by the occupancy rule: one workgroup
+// per CU is the unit of work, so split k only when the tiles leave more than
+// half of the CUs idle.
+static long long lds_rule_splits(int cfg, int M, int N, int K) {
+    const TileConfig c = tile_config(cfg);
+    const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
+    const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, tile_lds_bk(bm, bn, c.kblk));
+    const long long cus = num_cus();
+    if (tiles * 2 >= cus) return 1;
+    return std::min<long long>({ceil_div(cus, tiles), std::max<long long>(1, nblk / 2), (long long)max_splits()});
+}
+
 // The measured default (def_cfg, split by the LDS rule) unless the model puts
 // another candidate at least 5% ahead.
 static TilePick pick_tile(int mode, int M, int N, int K, int def_cfg, bool tall_ok) {
     const long long cus = num_cus();
-    auto lds_splits = [&](int cfg) {
-        const TileConfig c = tile_config(cfg);
-        const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
-        const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, tile_lds_bk(bm, bn, c.kblk));
-        if (tiles * 2 >= cus) return 1LL;
-        return std::min<long long>({ceil_div(cus, tiles), std::max<long long>(1, nblk / 2), (long long)max_splits()});
-    };
-    const long long s_def = lds_splits(def_cfg);
+    const long long s_def = lds_rule_splits(def_cfg, M, N, K);
     TilePick best{def_cfg, s_def, tile_cost(mode, def_cfg, s_def, M, N, K, cus)};
     const double def_us = best.us;
     static const int kBf16[] = {26, 33, kTileBF16Dma4w};
@@ -277,6 +284,75 @@ static TilePick pick_tile(int mode, int M, int N, int K, int def_cfg, bool tall_
         }
     }
     if (best.us > 0.95 * def_us) return TilePick{def_cfg, s_def, def_us};
+    return best;
+}
+
+// bf16 storage through LDS (M >= 12, N >= 64): every LDS-staged and LDS-DMA
+// tile and k-split priced by a second model fitted on MI355X (248 measured
+// cases: M = 12..4096, N = 64..11008, K = 64..4608, both B layouts; 14
+// configurations, 1 to 16 splits; median error 7%, 90% of the cases within
+// 19%).  A launch of W workgroups gives each CU ceil(W / CUs) of them, occ at
+// a time (the configuration's workgroups per CU, from its LDS and register
+// use); a workgroup fills its pipeline once (fill) and then takes max(m, c)
+// per k-block times the workgroups sharing its CU, m being the block's MFMAs
+// per SIMD (16 cycles each at 2.4 GHz, times a fitted factor) and c the
+// copy of its A and B block at a fitted cost per byte; the whole launch
+// takes at least its operands' and C's bytes at 3.3 TB/s; 2.72 us per launch;
+// a k-split adds 1.83 us plus its fp32 partials written and read at 6.8
+// TB/s.
+struct Bf16Fit {
+    int cfg, tb, occ;
+    double fill, mfma, ps_per_byte;
+};
+static const Bf16Fit kBf16Fit[] = {
+    {19, 0, 2, 1.554, 7.035, 12.05}, {19, 1, 2, 1.754, 3.739, 14.44}, {21, 0, 2, 2.192, 3.347, 16.11},
+    {21, 1, 1, 2.300, 2.732, 17.49}, {22, 0, 1, 2.550, 1.912, 20.50}, {22, 1, 1, 2.924, 2.862, 18.74},
+    {23, 0, 1, 2.333, 0.400, 17.36}, {23, 1, 1, 2.396, 0.353, 16.76}, {26, 0, 1, 2.293, 3.010, 16.87},
+    {26, 1, 1, 2.139, 0.636, 15.85}, {28, 0, 1, 1.974, 1.334, 20.25}, {28, 1, 2, 1.632, 0.602, 12.84},
+    {29, 0, 1, 2.686, 1.010, 19.61}, {29, 1, 1, 2.165, 1.259, 16.65}, {30, 0, 1, 2.417, 0.847, 15.05},
+    {30, 1, 1, 2.482, 2.219, 14.83}, {31, 0, 1, 2.905, 0.051, 19.32}, {31, 1, 1, 2.678, 0.893, 18.93},
+    {32, 0, 1, 2.479, 1.655, 15.85}, {32, 1, 1, 2.427, 0.941, 15.87}, {33, 0, 1, 2.957, 0.035, 16.75},
+    {33, 1, 1, 2.869, 2.173, 15.43}, {37, 1, 2, 1.792, 1.107, 14.87}, {38, 1, 2, 1.478, 0.319, 15.10},
+    {39, 0, 1, 3.676, 1.549, 18.18}, {39, 1, 2, 3.846, 0.005, 19.16},
+};
+
+static double bf16_tile_cost(const Bf16Fit& f, long long s, int M, int N, int K, long long cus) {
+    const TileConfig c = tile_config(f.cfg);
+    const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16, kb = tile_lds_bk(bm, bn, c.kblk);
+    const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, kb);
+    s = std::min(s, nblk);
+    const long long per_cu = ceil_div(tiles * s, cus), resident = std::min<long long>(f.occ, per_cu);
+    const double m = c.wm * c.wn * c.kw / 4.0 * c.mt * c.nt * (kb / 32.0) * 16 / 2400.0 * f.mfma;
+    const double copy = (double)(bm + bn) * kb * 2 * f.ps_per_byte * 1e-6;
+    const double core =
+        (double)ceil_div(per_cu, f.occ) * (f.fill + (double)ceil_div(nblk, s) * resident * std::max(m, copy));
+    const double hbm = (2.0 * ((double)M * K + (double)K * N) + 4.0 * M * N) * 0.2994e-6;
+    double us = 2.72 + std::max(core, hbm);
+    if (s > 1) us += 1.83 + 2.0 * (double)s * tiles * bm * bn * 4 * 0.1467e-6;
+    return us;
+}
+
+// The given default (configuration, k-splits) unless the model puts another
+// choice at least 10% ahead (s = 0 in the result: keep the default).
+static TilePick pick_bf16_tile(int tb, int M, int N, int K, int def_cfg, long long def_s) {
+    const long long cus = num_cus();
+    const Bf16Fit* d = nullptr;
+    for (const Bf16Fit& f : kBf16Fit)
+        if (f.cfg == def_cfg && f.tb == tb) d = &f;
+    if (!d) return TilePick{def_cfg, 0, 0.0};
+    const double def_us = bf16_tile_cost(*d, def_s, M, N, K, cus);
+    TilePick best{def_cfg, 0, def_us};
+    for (const Bf16Fit& f : kBf16Fit) {
+        if (f.tb != tb) continue;
+        const TileConfig c = tile_config(f.cfg);
+        const long long nblk = ceil_div(K, tile_lds_bk(c.wm * c.mt * 16, c.wn * c.nt * 16, c.kblk));
+        for (long long s : {1, 2, 4, 8, 16}) {
+            if (s > nblk || s > max_splits()) break;
+            const double us = bf16_tile_cost(f, s, M, N, K, cus);
+            if (us < best.us) best = TilePick{f.cfg, s, us};
+        }
+    }
+    if (best.us > 0.9 * def_us) return TilePick{def_cfg, 0, def_us};
     return best;
 }
 
@@ -417,6 +493,15 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
             const TilePick pick = pick_tile(mode, M, N, K, cfg, tall_ok);
             cfg = pick.cfg;
             model_splits = pick.s;
+        }
+        // bf16 storage from M = 12: the second model, against that choice.
+        if (nothing_forced && mode == kTileBF16 && M >= 12 && N >= 64) {
+            const long long def_s = model_splits > 0 ? model_splits : lds_rule_splits(cfg, M, N, K);
+            const TilePick pick = pick_bf16_tile(transB ? 1 : 0, M, N, K, cfg, def_s);
+            if (pick.s > 0) {
+                cfg = pick.cfg;
+                model_splits = pick.s;
+            }
         }
         const bool forced_dma = forced_cfg >= kTileFirstDma && forced_cfg < kTileF32Few;
         if (((forced_cfg >= kTileFirstLds && forced_cfg < kTileF32Few) || forced_cfg == kTileBF16Tb48 ||

@@ -387,15 +387,28 @@ def test_plans_route_lds_dma_kernels(lib):
     assert lib.plan_bf16(128, 11008, 4096)["name"] == "dnnopt_tile_bf16_lds"
     # bf16 storage above M = 128 (planner's figure of 256 CUs when no GPU is
     # visible): 128 x 96 tiles, 256 x 96 once those take more than one round,
-    # and 128 x 128 tiles on 4 waves where the cost model puts them 5% ahead
-    # (measured on MI355X: 256 x 4096 35.7 -> 22.2 us, 192 x 8192 38.4 ->
-    # 31.5, 384 x 8192 53.2 -> 47.0, 512 x 4096 37.9 -> 32.3).
-    cases = {(256, 11008): (128, 96, 1), (384, 11008): (256, 96, 1), (512, 11008): (256, 96, 1),
-             (256, 4096): (128, 128, 4), (192, 8192): (128, 128, 2), (384, 8192): (128, 128, 1),
-             (512, 4096): (128, 128, 2)}
+    # and 128 x 128 tiles on 4 waves where the first cost model puts them 5%
+    # ahead (measured on MI355X: 256 x 4096 35.7 -> 22.2 us).
+    cases = {(256, 11008): (128, 96, 1, 512), (384, 11008): (256, 96, 1, 512), (512, 11008): (256, 96, 1, 512),
+             (256, 4096): (128, 128, 4, 256)}
     for (M, N), want in cases.items():
         for p in (lib.plan_bf16(M, N, 4096), lib.plan_bf16_ex(M, N, 4096, transB=1)):
-            assert p["name"] == "dnnopt_tile_bf16_dma" and (p["rows"], p["cols"], p["splits"]) == want, (M, N, p)
+            assert p["name"] == "dnnopt_tile_bf16_dma" and (p["rows"], p["cols"], p["splits"], p["block"]) == want, (M, N, p)
+    # bf16 storage from M = 12: the second model's tile and split where it
+    # puts them 10% ahead (measured on MI355X, us, before -> after, B stored
+    # K x N): 384 x 8192 x 4096 49.4 -> 42.5 and 1024 x 4096 x 4096 51.0 ->
+    # 44.1 (128 x 128 on 8 waves), 512 x 2048 x 4096 22.8 -> 21.1 (8 waves,
+    # 4 splits), 200 x 512 x 512 8.5 -> 5.5 (32 x 64 unsplit instead of 128 x
+    # 96 with 4 splits); B stored N x K 200 x 512 x 512 8.3 -> 5.1 and 32 x
+    # 768 x 768 7.3 -> 5.7 (16 x 48 unsplit).  C4's shapes keep their tiles.
+    cases = {(384, 8192, 4096, 0): ("dma", 128, 128, 1, 512), (1024, 4096, 4096, 0): ("dma", 128, 128, 1, 512),
+             (512, 2048, 4096, 0): ("dma", 128, 128, 4, 512), (200, 512, 512, 0): ("lds", 32, 64, 1, 256),
+             (200, 512, 512, 1): ("lds", 16, 48, 1, 192), (32, 768, 768, 1): ("lds", 16, 48, 1, 192),
+             (32, 11008, 4096, 0): ("lds", 32, 64, 1, 256), (32, 11008, 4096, 1): ("lds", 32, 48, 1, 192)}
+    for (M, N, K, tb), (kind, *want) in cases.items():
+        p = lib.plan_bf16_ex(M, N, K, transB=tb)
+        assert p["name"] == "dnnopt_tile_bf16_" + kind and [p["rows"], p["cols"], p["splits"], p["block"]] == want, (
+            M, N, K, tb, p)
     # fp32 inputs above M = 64: 128 x 96 tiles split by the model, 256 x 96
     # tiles (register ring) where they cut the rounds (measured on MI355X:
     # 128 x 11008 x 1024 32.4 -> 23.4 us, 256 x 4096 x 4096 62.1 -> 47.1,

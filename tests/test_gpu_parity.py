@@ -430,17 +430,23 @@ def test_bf16_small_m_kn_tiles(lib, orc, dev, M, N, K, pa, pb, ta):
 @pytest.mark.parametrize("M,N,K,pa,pb", [(5, 1001, 300, 0, 2), (16, 4099, 130, 2, 0), (17, 11008, 4096, 0, 0),
                                          (32, 97, 1000, 4, 4), (24, 48, 64, 0, 0), (9, 50, 520, 2, 2)])
 def test_bf16_tb_48_column_tiles(lib, orc, dev, M, N, K, pa, pb):
+    """The 48-column tiles (forced where the cost model may pick another),
+    then the planner's own choice on the same inputs."""
     lda, ldb = K + pa, K + pb
-    p = lib.plan_bf16_ex(M, N, K, transB=1)
+    cfg = 38 if M <= 16 else 37
+    with lib.tunables(TILE_CFG=cfg):
+        p = lib.plan_bf16_ex(M, N, K, transB=1)
     assert p["name"] == "dnnopt_tile_bf16_lds" and p["cols"] == 48 and p["rows"] == (16 if M <= 16 else 32), p
     A = u.bf16_bits(orc, u.normal(orc, M * lda, 1)).reshape(M, lda)
     B = u.bf16_bits(orc, u.normal(orc, N * ldb, 2, 0, 0.02)).reshape(N, ldb)
     C0 = u.uniform(orc, M * N, 3).reshape(M, N)
     want, scale = u.exact(u.bf16_value(A)[:, :K], np.ascontiguousarray(u.bf16_value(B)[:, :K].T), 0.5, 1.0, C0)
-    dC = dev_copy(C0, dev)
-    lib.gemm_bf16_ex(M, N, K, 0.5, dev_copy(A.view(np.int16), dev), lda, dev_copy(B.view(np.int16), dev), ldb, 1.0,
-                     dC, N, transB=1, stream=stream())
-    u.assert_fp32_close(host(dC), want, scale, K, f"bf16 TB 48-column tiles {M}x{N}x{K}")
+    dA, dB = dev_copy(A.view(np.int16), dev), dev_copy(B.view(np.int16), dev)
+    for forced in (True, False):
+        dC = dev_copy(C0, dev)
+        with lib.tunables(TILE_CFG=cfg if forced else 0):
+            lib.gemm_bf16_ex(M, N, K, 0.5, dA, lda, dB, ldb, 1.0, dC, N, transB=1, stream=stream())
+        u.assert_fp32_close(host(dC), want, scale, K, f"bf16 TB 48-column tiles {M}x{N}x{K} forced={forced}")
 
 
 @pytest.mark.parametrize("tb", [0, 1])
@@ -450,17 +456,20 @@ def test_bf16_dma_256_row_tiles(lib, orc, dev, tb):
     K x N and N x K."""
     M, N, K = 1030, 4100, 200
     lda, ldb = K + 8, (K + 4 if tb else N + 2)
-    p = lib.plan_bf16_ex(M, N, K, transB=tb)
+    with lib.tunables(TILE_CFG=33):  # the cost model may pick another tile here
+        p = lib.plan_bf16_ex(M, N, K, transB=tb)
     assert p["name"] == "dnnopt_tile_bf16_dma" and p["rows"] == 256, p
     A = u.bf16_bits(orc, u.normal(orc, M * lda, 1)).reshape(M, lda)
     Bs = u.bf16_bits(orc, u.normal(orc, (N if tb else K) * ldb, 2, 0, 0.02)).reshape(N if tb else K, ldb)
     Bkn = Bs[:, :K].T if tb else Bs[:, :N]
     C0 = u.uniform(orc, M * N, 3).reshape(M, N)
     want, scale = u.exact(u.bf16_value(A)[:, :K], u.bf16_value(np.ascontiguousarray(Bkn)), 0.5, 1.0, C0)
-    dC = dev_copy(C0, dev)
-    lib.gemm_bf16_ex(M, N, K, 0.5, dev_copy(A.view(np.int16), dev), lda, dev_copy(Bs.view(np.int16), dev), ldb, 1.0,
-                     dC, N, transB=tb, stream=stream())
-    u.assert_fp32_close(host(dC), want, scale, K, f"dma 256-row tiles tb={tb}")
+    dA, dB = dev_copy(A.view(np.int16), dev), dev_copy(Bs.view(np.int16), dev)
+    for forced in (True, False):
+        dC = dev_copy(C0, dev)
+        with lib.tunables(TILE_CFG=33 if forced else 0):
+            lib.gemm_bf16_ex(M, N, K, 0.5, dA, lda, dB, ldb, 1.0, dC, N, transB=tb, stream=stream())
+        u.assert_fp32_close(host(dC), want, scale, K, f"dma 256-row tiles tb={tb} forced={forced}")
 
 
 def _bf16_storage_sweep_cases():
@@ -489,10 +498,12 @@ def _bf16_storage_sweep_cases():
 def test_bf16_storage_sweep(lib, orc, dev, M, N, K, tb, pa, pb, alpha, beta):
     lda, ldb = K + pa, (K + pb if tb else N + pb)
     p = lib.plan_bf16_ex(M, N, K, transB=tb)
-    # rows of A and B on 4-byte boundaries: the LDS-DMA tiles; else the register tiles
-    assert p["name"] == ("dnnopt_tile_bf16_dma" if lda % 2 == 0 and ldb % 2 == 0 else "dnnopt_tile_bf16"), p
+    # rows of A and B on 4-byte boundaries: the LDS-staged tiles (the cost
+    # models pick LDS-DMA or register-ring staging); else the register tiles
     if lda % 2 == 0 and ldb % 2 == 0:
-        assert (p["rows"], p["cols"]) in ((128, 96), (256, 96), (128, 128)), p
+        assert p["name"] in ("dnnopt_tile_bf16_dma", "dnnopt_tile_bf16_lds"), p
+    else:
+        assert p["name"] == "dnnopt_tile_bf16", p
     A = u.bf16_bits(orc, u.normal(orc, M * lda, 11)).reshape(M, lda)
     rows = N if tb else K
     Bs = u.bf16_bits(orc, u.normal(orc, rows * ldb, 12, 0, 0.02)).reshape(rows, ldb)
@@ -510,8 +521,7 @@ def test_bf16_dma_128x128_four_wave_tiles(lib, orc, dev, tb):
     """128 x 128 LDS-DMA tiles on 4 waves of 64 x 64: forced with 1 to 4
     k-splits on a ragged shape (M and N off the tile, a K tail inside a 64-k
     block, padded even strides, beta != 0), and as the planner's own choice
-    (1000 x 4000 x 100 unsplit, 256 x 4096 x 4096 with 4 k-splits); B stored
-    K x N and N x K."""
+    (256 x 4096 x 4096 with 4 k-splits); B stored K x N and N x K."""
     def run(M, N, K, pa, pb, alpha, beta, seed):
         lda, ldb = K + pa, (K + pb if tb else N + pb)
         A = u.bf16_bits(orc, u.normal(orc, M * lda, seed)).reshape(M, lda)
@@ -532,9 +542,10 @@ def test_bf16_dma_128x128_four_wave_tiles(lib, orc, dev, tb):
             assert (p["name"], p["rows"], p["cols"], p["splits"]) == ("dnnopt_tile_bf16_dma", 128, 128, splits), p
             got, want, scale = run(M, N, K, 2, 4, 0.5, 0.25, 21)
         u.assert_fp32_close(got, want, scale, K, f"128x128 forced, {splits} splits, tb={tb}")
-    for (M, N, K), splits in (((1000, 4000, 100), 1), ((256, 4096, 4096), 4)):
+    for (M, N, K), splits in (((256, 4096, 4096), 4),):
         p = lib.plan_bf16_ex(M, N, K, transB=tb)
-        assert (p["name"], p["rows"], p["cols"], p["splits"]) == ("dnnopt_tile_bf16_dma", 128, 128, splits), p
+        assert (p["name"], p["rows"], p["cols"], p["splits"], p["block"]) == ("dnnopt_tile_bf16_dma", 128, 128, splits,
+                                                                             256), p
         got, want, scale = run(M, N, K, 0, 0, 1.0, 0.0, 31)
         u.assert_fp32_close(got, want, scale, K, f"128x128 planned {M}x{N}x{K} tb={tb}")
 
