@@ -40,9 +40,10 @@
 //   fp32 inputs above M = 64, come from a fitted cost model (pick_tile) when
 //   it beats the rule by 5%; the fp32 register tile and k-split (A stored
 //   M x K, M >= 12, N >= 64) from another (pick_f32_tile) when it beats the
-//   rule by 10%; and, for bf16 storage from M = 12, every LDS-staged and
-//   LDS-DMA tile and k-split from a third (pick_bf16_tile) when it beats
-//   the choice above by 10%.
+//   rule by 10%; and, from M = 12, every LDS-staged and LDS-DMA tile and
+//   k-split from a third (pick_lds_tile, one parameter set for bf16
+//   storage and one for fp32 inputs) when it beats the choice above by 10%
+//   (bf16 storage) or 5% (fp32 inputs).
 //   * any shape whose operand spans none of these kernels can address with
 //     32-bit offsets: the 64-bit last-resort kernel (k_wide.hip).
 // Tunables (dnnopt_hip_set_tunable; a DNNOPT_TUNING build seeds them from
@@ -287,24 +288,35 @@ static TilePick pick_tile(int mode, int M, int N, int K, int def_cfg, bool tall_
     return best;
 }
 
-// bf16 storage through LDS (M >= 12, N >= 64): every LDS-staged and LDS-DMA
-// tile and k-split priced by a second model fitted on MI355X (248 measured
-// cases: M = 12..4096, N = 64..11008, K = 64..4608, both B layouts; 14
-// configurations, 1 to 16 splits; median error 7%, 90% of the cases within
-// 19%).  A launch of W workgroups gives each CU ceil(W / CUs) of them, occ at
-// a time (the configuration's workgroups per CU, from its LDS and register
-// use); a workgroup fills its pipeline once (fill) and then takes max(m, c)
-// per k-block times the workgroups sharing its CU, m being the block's MFMAs
-// per SIMD (16 cycles each at 2.4 GHz, times a fitted factor) and c the
-// copy of its A and B block at a fitted cost per byte; the whole launch
-// takes at least its operands' and C's bytes at 3.3 TB/s; 2.72 us per launch;
-// a k-split adds 1.83 us plus its fp32 partials written and read at 6.8
-// TB/s.
-struct Bf16Fit {
+// LDS-staged tiles (bf16 storage from M = 12, fp32 inputs from M = 12; N >=
+// 64): every LDS-staged and LDS-DMA tile and k-split priced by models fitted
+// on MI355X.  A launch of W workgroups gives each CU ceil(W / CUs) of them,
+// occ at a time (the configuration's workgroups per CU, from its LDS and
+// register use); a workgroup fills its pipeline once (fill) and then takes
+// max(m, c) per k-block times the workgroups sharing its CU, m being the
+// block's MFMAs per SIMD (16 cycles each at 2.4 GHz, times a fitted factor)
+// and c the copy of its A and B block at a fitted cost per byte; the whole
+// launch takes at least its operands' and C's bytes at the fitted HBM rate;
+// a fixed cost per launch, and a k-split adds a fixed cost plus its fp32
+// partials written and read at the fitted rate.
+//   bf16 storage: 248 measured cases (M = 12..4096, N = 64..11008, K =
+//   64..4608, both B layouts; 14 configurations, 1 to 16 splits; median
+//   error 7%, 90% of the cases within 19%); 2.72 us per launch, 3.3 TB/s;
+//   a split 1.83 us plus its partials at 6.8 TB/s.
+//   fp32 inputs rounded in registers: 124 measured cases (same shapes, B
+//   stored K x N; 9 configurations; median error 6%, 90% within 17%); 1.99 us
+//   per launch, 3.3 TB/s; a split 2.73 us plus its partials at 6.6 TB/s.
+struct LdsFit {
     int cfg, tb, occ;
     double fill, mfma, ps_per_byte;
 };
-static const Bf16Fit kBf16Fit[] = {
+struct LdsModel {
+    const LdsFit* fits;
+    int n;
+    int es;  // operand bytes per element
+    double launch_us, split_us, partial_ps, hbm_ps;
+};
+static const LdsFit kBf16Fit[] = {
     {19, 0, 2, 1.554, 7.035, 12.05}, {19, 1, 2, 1.754, 3.739, 14.44}, {21, 0, 2, 2.192, 3.347, 16.11},
     {21, 1, 1, 2.300, 2.732, 17.49}, {22, 0, 1, 2.550, 1.912, 20.50}, {22, 1, 1, 2.924, 2.862, 18.74},
     {23, 0, 1, 2.333, 0.400, 17.36}, {23, 1, 1, 2.396, 0.353, 16.76}, {26, 0, 1, 2.293, 3.010, 16.87},
@@ -315,44 +327,54 @@ static const Bf16Fit kBf16Fit[] = {
     {33, 1, 1, 2.869, 2.173, 15.43}, {37, 1, 2, 1.792, 1.107, 14.87}, {38, 1, 2, 1.478, 0.319, 15.10},
     {39, 0, 1, 3.676, 1.549, 18.18}, {39, 1, 2, 3.846, 0.005, 19.16},
 };
+static const LdsFit kF2BFit[] = {
+    {14, 0, 1, 2.250, 7.797, 21.59}, {16, 0, 1, 2.357, 1.674, 22.14}, {18, 0, 1, 2.400, 2.607, 20.58},
+    {19, 0, 2, 2.255, 1.381, 16.62}, {20, 0, 1, 3.124, 6.880, 6.68}, {21, 0, 1, 2.956, 5.461, 19.89},
+    {22, 0, 1, 3.047, 0.031, 22.17}, {23, 0, 1, 2.674, 0.063, 19.12}, {40, 0, 1, 3.112, 5.685, 17.17},
+};
+static const LdsModel kBf16Model{kBf16Fit, (int)(sizeof kBf16Fit / sizeof kBf16Fit[0]), 2, 2.72, 1.83, 0.1467, 0.2994};
+static const LdsModel kF2BModel{kF2BFit, (int)(sizeof kF2BFit / sizeof kF2BFit[0]), 4, 1.99, 2.73, 0.1509, 0.3039};
 
-static double bf16_tile_cost(const Bf16Fit& f, long long s, int M, int N, int K, long long cus) {
+static double lds_tile_cost(const LdsModel& md, const LdsFit& f, long long s, int M, int N, int K, long long cus) {
     const TileConfig c = tile_config(f.cfg);
     const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16, kb = tile_lds_bk(bm, bn, c.kblk);
     const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, kb);
     s = std::min(s, nblk);
     const long long per_cu = ceil_div(tiles * s, cus), resident = std::min<long long>(f.occ, per_cu);
     const double m = c.wm * c.wn * c.kw / 4.0 * c.mt * c.nt * (kb / 32.0) * 16 / 2400.0 * f.mfma;
-    const double copy = (double)(bm + bn) * kb * 2 * f.ps_per_byte * 1e-6;
+    const double copy = (double)(bm + bn) * kb * md.es * f.ps_per_byte * 1e-6;
     const double core =
         (double)ceil_div(per_cu, f.occ) * (f.fill + (double)ceil_div(nblk, s) * resident * std::max(m, copy));
-    const double hbm = (2.0 * ((double)M * K + (double)K * N) + 4.0 * M * N) * 0.2994e-6;
-    double us = 2.72 + std::max(core, hbm);
-    if (s > 1) us += 1.83 + 2.0 * (double)s * tiles * bm * bn * 4 * 0.1467e-6;
+    const double hbm = ((double)md.es * ((double)M * K + (double)K * N) + 4.0 * M * N) * md.hbm_ps * 1e-6;
+    double us = md.launch_us + std::max(core, hbm);
+    if (s > 1) us += md.split_us + 2.0 * (double)s * tiles * bm * bn * 4 * md.partial_ps * 1e-6;
     return us;
 }
 
 // The given default (configuration, k-splits) unless the model puts another
-// choice at least 10% ahead (s = 0 in the result: keep the default).
-static TilePick pick_bf16_tile(int tb, int M, int N, int K, int def_cfg, long long def_s) {
+// choice at least `margin` ahead (s = 0 in the result: keep the default).
+// tall_ok: 256-row register-ring tiles may be used (C offsets fit).
+static TilePick pick_lds_tile(const LdsModel& md, int tb, int M, int N, int K, int def_cfg, long long def_s,
+                              double margin, bool tall_ok) {
     const long long cus = num_cus();
-    const Bf16Fit* d = nullptr;
-    for (const Bf16Fit& f : kBf16Fit)
-        if (f.cfg == def_cfg && f.tb == tb) d = &f;
+    const LdsFit* d = nullptr;
+    for (int i = 0; i < md.n; ++i)
+        if (md.fits[i].cfg == def_cfg && md.fits[i].tb == tb) d = &md.fits[i];
     if (!d) return TilePick{def_cfg, 0, 0.0};
-    const double def_us = bf16_tile_cost(*d, def_s, M, N, K, cus);
+    const double def_us = lds_tile_cost(md, *d, def_s, M, N, K, cus);
     TilePick best{def_cfg, 0, def_us};
-    for (const Bf16Fit& f : kBf16Fit) {
-        if (f.tb != tb) continue;
+    for (int i = 0; i < md.n; ++i) {
+        const LdsFit& f = md.fits[i];
+        if (f.tb != tb || (f.cfg == kTileF2BTall && !tall_ok)) continue;
         const TileConfig c = tile_config(f.cfg);
         const long long nblk = ceil_div(K, tile_lds_bk(c.wm * c.mt * 16, c.wn * c.nt * 16, c.kblk));
         for (long long s : {1, 2, 4, 8, 16}) {
             if (s > nblk || s > max_splits()) break;
-            const double us = bf16_tile_cost(f, s, M, N, K, cus);
+            const double us = lds_tile_cost(md, f, s, M, N, K, cus);
             if (us < best.us) best = TilePick{f.cfg, s, us};
         }
     }
-    if (best.us > 0.9 * def_us) return TilePick{def_cfg, 0, def_us};
+    if (best.us > (1.0 - margin) * def_us) return TilePick{def_cfg, 0, def_us};
     return best;
 }
 
@@ -494,10 +516,14 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
             cfg = pick.cfg;
             model_splits = pick.s;
         }
-        // bf16 storage from M = 12: the second model, against that choice.
-        if (nothing_forced && mode == kTileBF16 && M >= 12 && N >= 64) {
+        // From M = 12: every LDS-staged tile and split priced by the second
+        // models, against that choice (bf16 storage: 10% margin, fp32
+        // inputs: 5%).
+        if (nothing_forced && M >= 12 && N >= 64) {
             const long long def_s = model_splits > 0 ? model_splits : lds_rule_splits(cfg, M, N, K);
-            const TilePick pick = pick_bf16_tile(transB ? 1 : 0, M, N, K, cfg, def_s);
+            const TilePick pick = mode == kTileBF16
+                                      ? pick_lds_tile(kBf16Model, transB ? 1 : 0, M, N, K, cfg, def_s, 0.10, false)
+                                      : pick_lds_tile(kF2BModel, 0, M, N, K, cfg, def_s, 0.05, tall_ok);
             if (pick.s > 0) {
                 cfg = pick.cfg;
                 model_splits = pick.s;
