@@ -16,7 +16,8 @@ roofline fractions under `configs` (C2's own per-shape figures included).  `--wo
 becomes `value`); `--workload all` adds the oneDNN-hook workload;
 `--detail FILE` appends the full per-workload records.  `--yardstick` instead
 times the vendor library (torch.mm / torch._int_mm, hipBLASLt or rocBLAS)
-beside this library on the configs' shapes, one JSON line per shape.
+beside this library on the configs' shapes (`--yardstick dnn`: on DNN
+inference shapes, BERT and ResNet-50 GEMMs), one JSON line per shape.
 
 `value` is the algorithmic bytes of a step (sA*M*K + sB*K*N + sC*M*N*(1 +
 [beta != 0]), each operand counted once) divided by the wall time of the
@@ -698,6 +699,64 @@ def _graph_time_us(torch, stream, launches, reps=5):
     return statistics.median(out)
 
 
+def vendor_yardstick_dnn():
+    """The vendor library beside this library on DNN_SHAPES: fp32 and bf16
+    storage with B stored K x N and N x K, int8 (B stored N x K), under the
+    same harness as vendor_yardstick (graphs of back-to-back calls over
+    operand copies rotated through at least 600 MB, median of 5 replays;
+    torch.mm on bf16 writes a bf16 C, this library an fp32 C; beta = 0)."""
+    import torch
+
+    b = _binding()
+    lib = b.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    s = torch.cuda.Stream(device=dev)
+    rows = []
+    cs = lambda: s.cuda_stream  # noqa: E731
+
+    def both(name, torch_fns, ours_fns):
+        with torch.cuda.stream(s):
+            for f in torch_fns[:2] + ours_fns[:2]:
+                f()
+        torch.cuda.synchronize()
+        t = _graph_time_us(torch, s, torch_fns)
+        o = _graph_time_us(torch, s, ours_fns)
+        row = {"shape": name, "torch_us": round(t, 2), "ours_us": round(o, 2), "torch_over_ours": round(t / o, 3)}
+        rows.append(row)
+        print(json.dumps(row), flush=True)
+
+    for M, N, K in DNN_SHAPES:
+        for dt, es in ((torch.float32, 4), (torch.bfloat16, 2)):
+            n = max(2, min(64, -(-(600 << 20) // ((M * K + K * N) * es))))
+            A = [torch.randn(M, K, device=dev).to(dt) for _ in range(n)]
+            B = [(torch.randn(K, N, device=dev) * 0.05).to(dt) for _ in range(n)]
+            Bt = [x.t().contiguous() for x in B]
+            C = torch.empty(M, N, device=dev)
+            tag = "fp32" if es == 4 else "bf16"
+            if es == 4:
+                ours = lambda k, tb: lib.sgemm(M, N, K, 1.0, A[k], K, Bt[k] if tb else B[k], K if tb else N, 0.0, C, N,  # noqa: E731
+                                               transB=tb, stream=cs())
+            else:
+                ours = lambda k, tb: lib.gemm_bf16_ex(M, N, K, 1.0, A[k], K, Bt[k] if tb else B[k], K if tb else N,  # noqa: E731
+                                                      0.0, C, N, transB=tb, stream=cs())
+            both(f"{tag} {M}x{N}x{K}, B K x N", [lambda k=k: torch.mm(A[k], B[k]) for k in range(n)],
+                 [lambda k=k: ours(k, 0) for k in range(n)])
+            both(f"{tag} {M}x{N}x{K}, B N x K", [lambda k=k: torch.mm(A[k], Bt[k].t()) for k in range(n)],
+                 [lambda k=k: ours(k, 1) for k in range(n)])
+            del A, B, Bt, C
+        if M > 16:
+            n = max(2, min(64, -(-(600 << 20) // (M * K + K * N))))
+            A8 = [torch.randint(-127, 128, (M, K), device=dev, dtype=torch.int8) for _ in range(n)]
+            B8 = [torch.randint(-127, 128, (N, K), device=dev, dtype=torch.int8) for _ in range(n)]
+            C8 = torch.empty(M, N, device=dev, dtype=torch.int32)
+            both(f"int8 {M}x{N}x{K}", [lambda k=k: torch._int_mm(A8[k], B8[k].t()) for k in range(n)],
+                 [lambda k=k: lib.gemm_s8s8s32(M, N, K, A8[k], K, B8[k], K, C8, N, stream=cs()) for k in range(n)])
+            del A8, B8, C8
+        torch.cuda.empty_cache()
+    _yardstick_summary(torch, rows, "DNN inference shapes")
+
+
 def vendor_yardstick():
     """The vendor library on the configs' shapes, timed beside this library
     under one harness: torch.mm / torch._int_mm (hipBLASLt / rocBLAS on this
@@ -768,9 +827,22 @@ def vendor_yardstick():
              [lambda k=k: lib.sgemm(M, N, K, 1.0, a(k), K, bb(k), N, 0.0, C, N, stream=cs()) for k in range(n)])
         del A, B, C
         torch.cuda.empty_cache()
+    _yardstick_summary(torch, rows, "the configs' shapes")
+
+
+# DNN inference GEMMs outside the configs: BERT-base encoder layers at 128 /
+# 384 / 32 tokens (hidden 768, MLP 3072), ResNet-50 convolutions as im2col
+# GEMMs (56x56x64 3x3, 28x28x128 3x3, 14x14x256 3x3, 7x7x512 3x3, 56x56x256
+# 1x1), and two square-ish blocks.
+DNN_SHAPES = [(128, 768, 768), (128, 3072, 768), (128, 768, 3072), (384, 768, 768), (384, 3072, 768),
+              (384, 768, 3072), (32, 768, 768), (3136, 64, 576), (784, 128, 1152), (196, 256, 2304),
+              (49, 512, 4608), (3136, 256, 64), (64, 1024, 1024), (200, 512, 512)]
+
+
+def _yardstick_summary(torch, rows, what):
     wins = sum(1 for r in rows if r["torch_over_ours"] >= 1.0)
     geo = statistics.geometric_mean([r["torch_over_ours"] for r in rows])
-    print(json.dumps({"yardstick": "torch (hipBLASLt/rocBLAS) vs this library", "shapes": len(rows),
+    print(json.dumps({"yardstick": f"torch (hipBLASLt/rocBLAS) vs this library, {what}", "shapes": len(rows),
                       "library_faster": wins, "geomean_torch_over_ours": round(geo, 3),
                       "torch": torch.__version__}), flush=True)
 
@@ -823,9 +895,9 @@ def main():
     ap.add_argument("--detail", default=None, help="append per-shape results (JSON lines) to this file")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cases", default=None, help="comma-separated case names of the workload to run (profiling)")
-    ap.add_argument("--yardstick", action="store_true",
+    ap.add_argument("--yardstick", nargs="?", const="configs", choices=("configs", "dnn"),
                     help="only time the vendor library (torch.mm / torch._int_mm) beside this library on the "
-                         "configs' shapes, one JSON line per shape")
+                         "configs' shapes (default) or on DNN inference shapes, one JSON line per shape")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device-to-device copies of MIB MiB (scale for HBM byte counters)")
     ap.add_argument("--rocprof-summary", nargs="+", metavar="ARG",
@@ -834,7 +906,7 @@ def main():
                          "profiles/<kernel>_<workload>_traffic.json")
     args = ap.parse_args()
     if args.yardstick:
-        vendor_yardstick()
+        vendor_yardstick() if args.yardstick == "configs" else vendor_yardstick_dnn()
         return
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
