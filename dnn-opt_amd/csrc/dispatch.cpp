@@ -43,7 +43,9 @@
 //   rule by 10%; and, from M = 12, every LDS-staged and LDS-DMA tile and
 //   k-split from a third (pick_lds_tile, one parameter set for bf16
 //   storage and one for fp32 inputs) when it beats the choice above by 10%
-//   (bf16 storage) or 5% (fp32 inputs).
+//   (bf16 storage) or 5% (fp32 inputs); fp32 with A stored M x K also
+//   prices the fp32 LDS-DMA tiles (the same model form) and takes one where
+//   it is 10% ahead of the register tiles' choice, or beyond 10^10 MACs.
 //   * any shape whose operand spans none of these kernels can address with
 //     32-bit offsets: the 64-bit last-resort kernel (k_wide.hip).
 // Tunables (dnnopt_hip_set_tunable; a DNNOPT_TUNING build seeds them from
@@ -313,7 +315,8 @@ struct LdsFit {
 struct LdsModel {
     const LdsFit* fits;
     int n;
-    int es;  // operand bytes per element
+    int es;              // operand bytes per element
+    double mfma_cyc_k;   // MFMA cycles per k of one 16 x 16 tile (bf16 16x16x32: 0.5, fp32 16x16x4: 8)
     double launch_us, split_us, partial_ps, hbm_ps;
 };
 static const LdsFit kBf16Fit[] = {
@@ -332,8 +335,20 @@ static const LdsFit kF2BFit[] = {
     {19, 0, 2, 2.255, 1.381, 16.62}, {20, 0, 1, 3.124, 6.880, 6.68}, {21, 0, 1, 2.956, 5.461, 19.89},
     {22, 0, 1, 3.047, 0.031, 22.17}, {23, 0, 1, 2.674, 0.063, 19.12}, {40, 0, 1, 3.112, 5.685, 17.17},
 };
-static const LdsModel kBf16Model{kBf16Fit, (int)(sizeof kBf16Fit / sizeof kBf16Fit[0]), 2, 2.72, 1.83, 0.1467, 0.2994};
-static const LdsModel kF2BModel{kF2BFit, (int)(sizeof kF2BFit / sizeof kF2BFit[0]), 4, 1.99, 2.73, 0.1509, 0.3039};
+// fp32 LDS-DMA tiles (A stored M x K, both B layouts): 320 measured cases (M
+// = 10..12544, N = 64..11008, K = 64..4608; 7 configurations, 1 to 16
+// splits; median error 5%, 90% within 18%); 4.83 us per launch, 3.4 TB/s; a
+// split 1.25 us plus its partials at 4.3 TB/s.
+static const LdsFit kF32DmaFit[] = {
+    {41, 0, 2, 2.028, 1.231, 22.32}, {41, 1, 2, 0.044, 1.187, 2.87}, {42, 0, 1, 4.222, 1.196, 29.55},
+    {42, 1, 1, 0.890, 1.158, 1.51}, {43, 0, 3, 1.021, 1.249, 17.30}, {43, 1, 3, 0.000, 1.165, 24.82},
+    {44, 0, 2, 2.168, 1.215, 5.68}, {44, 1, 2, 0.008, 1.186, 0.00}, {45, 0, 1, 3.558, 1.130, 43.81},
+    {45, 1, 1, 0.000, 1.150, 4.66}, {46, 0, 4, 0.953, 1.952, 9.64}, {46, 1, 4, 0.000, 1.834, 0.25},
+    {47, 0, 2, 1.767, 1.154, 29.23}, {47, 1, 2, 0.000, 1.113, 8.54},
+};
+static const LdsModel kBf16Model{kBf16Fit, (int)(sizeof kBf16Fit / sizeof kBf16Fit[0]), 2, 0.5, 2.72, 1.83, 0.1467, 0.2994};
+static const LdsModel kF32DmaModel{kF32DmaFit, (int)(sizeof kF32DmaFit / sizeof kF32DmaFit[0]), 4, 8.0, 4.83, 1.25, 0.2347, 0.2924};
+static const LdsModel kF2BModel{kF2BFit, (int)(sizeof kF2BFit / sizeof kF2BFit[0]), 4, 0.5, 1.99, 2.73, 0.1509, 0.3039};
 
 static double lds_tile_cost(const LdsModel& md, const LdsFit& f, long long s, int M, int N, int K, long long cus) {
     const TileConfig c = tile_config(f.cfg);
@@ -341,7 +356,7 @@ static double lds_tile_cost(const LdsModel& md, const LdsFit& f, long long s, in
     const long long tiles = ceil_div(M, bm) * ceil_div(N, bn), nblk = ceil_div(K, kb);
     s = std::min(s, nblk);
     const long long per_cu = ceil_div(tiles * s, cus), resident = std::min<long long>(f.occ, per_cu);
-    const double m = c.wm * c.wn * c.kw / 4.0 * c.mt * c.nt * (kb / 32.0) * 16 / 2400.0 * f.mfma;
+    const double m = c.wm * c.wn * c.kw / 4.0 * c.mt * c.nt * kb * md.mfma_cyc_k / 2400.0 * f.mfma;
     const double copy = (double)(bm + bn) * kb * md.es * f.ps_per_byte * 1e-6;
     const double core =
         (double)ceil_div(per_cu, f.occ) * (f.fill + (double)ceil_div(nblk, s) * resident * std::max(m, copy));
@@ -349,6 +364,26 @@ static double lds_tile_cost(const LdsModel& md, const LdsFit& f, long long s, in
     double us = md.launch_us + std::max(core, hbm);
     if (s > 1) us += md.split_us + 2.0 * (double)s * tiles * bm * bn * 4 * md.partial_ps * 1e-6;
     return us;
+}
+
+// The model's best configuration and split count of layout tb among those
+// `usable` accepts (s = 0 when there is none).
+template <class Usable>
+static TilePick best_lds_tile(const LdsModel& md, int tb, int M, int N, int K, Usable usable) {
+    const long long cus = num_cus();
+    TilePick best{0, 0, 0.0};
+    for (int i = 0; i < md.n; ++i) {
+        const LdsFit& f = md.fits[i];
+        if (f.tb != tb || !usable(f.cfg)) continue;
+        const TileConfig c = tile_config(f.cfg);
+        const long long nblk = ceil_div(K, tile_lds_bk(c.wm * c.mt * 16, c.wn * c.nt * 16, c.kblk));
+        for (long long s : {1, 2, 4, 8, 16}) {
+            if (s > nblk || s > max_splits()) break;
+            const double us = lds_tile_cost(md, f, s, M, N, K, cus);
+            if (best.s == 0 || us < best.us) best = TilePick{f.cfg, s, us};
+        }
+    }
+    return best;
 }
 
 // The given default (configuration, k-splits) unless the model puts another
@@ -450,6 +485,17 @@ static TilePick pick_f32_tile(int tb, int M, int N, int K, int def_cfg) {
     }
     if (best.us > 0.9 * def_us) return TilePick{def_cfg, 0, def_us};
     return best;
+}
+
+// fp32 LDS-DMA tiles address A from the tile's first row and B from its
+// first row (N x K) or column (K x N) with 32-bit offsets over all of k.
+static bool f32_dma_fits(int cfg, int transA, int transB, int M, int K, int lda, int ldb) {
+    (void)M;
+    if (transA) return false;
+    const TileConfig c = tile_config(cfg);
+    const long long bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
+    return (bm * lda + K) * 4 < 0x7FFFFFFFll &&
+           (transB ? (bn * ldb + K) : ((long long)K * ldb + bn)) * 4 < 0x7FFFFFFFll;
 }
 
 int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, int ldb, Launch* L, bool lds_ok,
@@ -565,18 +611,34 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     }
     // fp32 register tiles: the cost model's choice when nothing is forced, or
     // a forced configuration (tunable TILE_CFG).
-    if (!lds && mode == kTileF32 && !transA && M >= 12 && N >= 64 && (double)M * N * K <= 1e10 && forced_cfg <= 0 &&
+    if (!lds && mode == kTileF32 && !transA && M >= 12 && N >= 64 && forced_cfg <= 0 &&
         tunable(kTuneTileSplits) <= 0) {
-        const TilePick pick = pick_f32_tile(transB ? 1 : 0, M, N, K, cfg);
-        cfg = pick.cfg;
-        model_splits = pick.s;
+        auto dma_ok = [&](int k) { return f32_dma_fits(k, transA, transB, M, K, lda, ldb); };
+        const TilePick dma = best_lds_tile(kF32DmaModel, transB ? 1 : 0, M, N, K, dma_ok);
+        if ((double)M * N * K <= 1e10) {
+            // the register tiles' model, then the LDS-DMA tiles where their
+            // model puts them 10% ahead of that choice
+            const TilePick pick = pick_f32_tile(transB ? 1 : 0, M, N, K, cfg);
+            cfg = pick.cfg;
+            model_splits = pick.s;
+            if (dma.s > 0 && pick.us > 0.0 && dma.us < 0.9 * pick.us) {
+                cfg = dma.cfg;
+                model_splits = dma.s;
+            }
+        } else if (dma.s > 0) {
+            // beyond the fitted range (MFMA-bound): the LDS-DMA tiles
+            cfg = dma.cfg;
+            model_splits = dma.s;
+        }
     }
     if (!lds && mode == kTileF32 &&
-        ((forced_cfg >= 1 && forced_cfg <= 4) || forced_cfg == kTileF32Few || forced_cfg == kTileF32Few128))
+        ((forced_cfg >= 1 && forced_cfg <= 4) || forced_cfg == kTileF32Few || forced_cfg == kTileF32Few128 ||
+         (tile_f32_dma(forced_cfg) && f32_dma_fits(forced_cfg, transA, transB, M, K, lda, ldb))))
         cfg = forced_cfg;
+    const bool f32dma = mode == kTileF32 && tile_f32_dma(cfg);
     const TileConfig c = tile_config(cfg);
     const int bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
-    const int kb = lds ? tile_lds_bk(bm, bn, c.kblk) : (mode == kTileF32 ? 64 : 128);
+    const int kb = lds || f32dma ? tile_lds_bk(bm, bn, c.kblk) : (mode == kTileF32 ? 64 : 128);
     const long long tn = ceil_div(N, bn), tm = ceil_div(M, bm), tiles = tn * tm;
     const long long nblk = ceil_div(K, kb);
     const int waves_per_wg = c.wm * c.wn * c.kw;
@@ -590,7 +652,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
                                                       (long long)max_splits()});
         if (model_splits > 0) s = model_splits;
     } else if (mode == kTileF32) {
-        s = model_splits > 0 ? model_splits : reg_tile_splits(cfg, M, N, K);
+        s = model_splits > 0 ? model_splits : (f32dma ? lds_rule_splits(cfg, M, N, K) : reg_tile_splits(cfg, M, N, K));
     } else {
         const long long target_wgs = cus * waves_per_cu() / waves_per_wg;
         if (tiles < target_wgs) {
@@ -605,7 +667,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     // one workgroup.  More splits shorten that range.  (The LDS kernel
     // addresses k from 0; its spans were checked above.)
     auto span_ok = [&](long long splits) {
-        if (lds) return true;
+        if (lds || f32dma) return true;  // checked above, over all of k
         const long long kext = ceil_div(nblk, splits) * kb;
         const long long a = transA ? kext * lda : (long long)bm * lda;
         const long long b = transB ? (long long)bn * ldb : kext * ldb;
@@ -623,7 +685,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     L->tm = (int)tm;
     // LDS-staged tiles and the 16-row fp32 tiles are launched as one
     // XCD-ordered row of workgroups.
-    const bool xcd = lds || (mode == kTileF32 && c.mt == 1 && c.wm == 1);
+    const bool xcd = lds || f32dma || (mode == kTileF32 && c.mt == 1 && c.wm == 1);
     L->grid = xcd ? dim3((unsigned)xcd_grid((int)tn, (int)tm), 1, (unsigned)s) : dim3((unsigned)tn, (unsigned)tm, (unsigned)s);
     // k-splits of the LDS-staged kernels are summed by a reduce kernel, except
     // for the LDS-DMA tiles (tunable TILE_TICKET = 1): the last workgroup to
@@ -637,7 +699,7 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
     const int kernel = mode == kTileF32 ? DNNOPT_K_TILE_F32 : DNNOPT_K_TILE_BF16;
     fill_pub(L, kernel,
-             mode == kTileF32 ? "dnnopt_tile_f32"
+             mode == kTileF32 ? (f32dma ? "dnnopt_tile_f32_dma" : "dnnopt_tile_f32")
                               : (dma ? "dnnopt_tile_bf16_dma" : (lds ? "dnnopt_tile_bf16_lds" : "dnnopt_tile_bf16")),
              bm, bn, (int)s, waves_per_wg * 64);
     return DNNOPT_OK;

@@ -1051,6 +1051,207 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_dma(TileArgs p) 
                                    p.tiles_n * p.tiles_m);
 }
 
+// ---------------------------------------------------------------- fp32, LDS DMA
+// fp32 tiles with both operands copied into LDS by the memory unit, as the
+// bf16 LDS-DMA tiles above: 32 k per block (128-byte rows of A, and of B
+// stored N x K, with the same chunk swizzle), NS stages, blocks NS - 1 ahead,
+// one barrier per block.  v_mfma_f32_16x16x4_f32 takes one fp32 of A and one
+// of B per lane: a lane's 16-byte fragment read (k = 16 kk + 4 g .. + 3 of
+// its row) feeds four MFMAs, k-slot g of MFMA c holding k = 16 kk + 4 g + c
+// for A and B alike.  B stored K x N is staged as 32 rows of BN floats and
+// read 16 bytes of one k row at a time (columns 4 r .. 4 r + 3 of a
+// 64-column group), whose components feed the four sub-tiles of the group
+// (their columns interleave over 64, as in the 16-row register tiles).
+// Bytes of A (and of B stored N x K) past K are zeroed in registers in the
+// last block; rows of B stored K x N past K read zero.  A stored M x K only.
+template <int MT, int NT, int WM, int WN, int NS, int TB>
+__global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_f32_dma(TileArgs p) {
+    static_assert(NT % 4 == 0, "whole 64-column groups per wave");
+    using SH = TileShape<MT, NT, WM, WN, 1>;
+    constexpr int BM = SH::BM, BN = SH::BN;
+    constexpr int NW = WM * WN;
+    constexpr int BK = 32;
+    constexpr int ROWB = BK * 4;  // 128 bytes: one row of A (or of B stored N x K) per block
+    constexpr int BROW = BN * 4;  // one k row of B stored K x N
+    constexpr int KK = BK / 16;   // fragment reads per row and block
+    constexpr int NG = NT / 4;    // 64-column groups per wave (B stored K x N)
+    constexpr bool ILV = TB == 0;
+    constexpr int A_BYTES = BM * ROWB, B_BYTES = TB ? BN * ROWB : BK * BROW, STAGE = A_BYTES + B_BYTES;
+    static_assert(NS >= 2 && NS <= 4, "2 to 4 stages");
+    static_assert(A_BYTES % 1024 == 0 && B_BYTES % 1024 == 0, "whole 1 KB wave loads per operand");
+    constexpr int UNITS = STAGE / 1024;
+    constexpr int IPW = (UNITS + NW - 1) / NW;  // wave loads per wave and block
+    __shared__ __attribute__((aligned(1024))) char st0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st1[STAGE];
+    __shared__ __attribute__((aligned(1024))) char st2[NS > 2 ? STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) char st3[NS > 3 ? STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) char spare[UNITS % NW ? 1024 : 16];
+    __shared__ float red_unused[1];
+    __shared__ int last_flag;
+    auto stage = [&](int i) -> char* { return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3; };
+
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+    const int w = wave_id();
+    const int wn = w % WN, wm = w / WN;
+    const TileXY tile = xcd_tile((int)blockIdx.x, p.tiles_n, p.tiles_m);
+    if (!tile.ok) return;
+    const int m0 = tile.m * BM, n0 = tile.n * BN;
+    const int nblk = (p.K + BK - 1) / BK;
+    const int b_lo = (int)(((long long)nblk * blockIdx.z) / p.splits);
+    const int b_hi = (int)(((long long)nblk * (blockIdx.z + 1)) / p.splits);
+    const int nb = b_hi - b_lo;
+
+    const char* abase = static_cast<const char*>(p.A) + (size_t)m0 * p.lda * 4;
+    const char* bbase = static_cast<const char*>(p.B) + (TB ? (size_t)n0 * p.ldb : (size_t)n0) * 4;
+    // Ranges end at the last element of each operand.
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(abase, clamp_rec(((size_t)(p.M - 1 - m0) * p.lda + p.K) * 4));
+    const size_t b_last = TB ? (size_t)(p.N - 1 - n0) * p.ldb + p.K : (size_t)(p.K - 1) * p.ldb + (p.N - n0);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase, clamp_rec(b_last * 4));
+
+    // This lane's global byte offset (block 0) for each of its wave's loads;
+    // rows past M / N, columns past N and padding slots start at kOobOffset
+    // (read zero).
+    uint32_t goff[IPW];
+    bool gb[IPW];
+    int unit[IPW];
+#pragma unroll
+    for (int j = 0; j < IPW; ++j) {
+        const int u = j * NW + w;
+        unit[j] = u < UNITS ? u : -1;
+        gb[j] = u * 1024 >= A_BYTES;
+        goff[j] = kOobOffset;
+        if (u >= UNITS) continue;
+        const int q = u * 1024 + 16 * lane;
+        if (q < A_BYTES) {
+            const int row = q / ROWB, c = swz_a(row, (q % ROWB) / 16);
+            if (m0 + row < p.M) goff[j] = ((uint32_t)row * p.lda + 4 * c) * 4u;
+        } else if constexpr (TB) {
+            const int qq = q - A_BYTES, row = qq / ROWB, c = swz_a(row, (qq % ROWB) / 16);
+            if (n0 + row < p.N) goff[j] = ((uint32_t)row * p.ldb + 4 * c) * 4u;
+        } else {
+            const int qq = q - A_BYTES, kr = qq / BROW, cb = qq % BROW;
+            if (n0 + cb / 4 < p.N) goff[j] = (uint32_t)kr * p.ldb * 4u + (uint32_t)cb;
+        }
+    }
+    // Block `blk` into stage `st`; blocks past the split read nothing
+    // (out-of-range offsets) but are issued, so every wave's count of
+    // outstanding loads per block is the same.
+    auto dma = [&](int st, int blk) {
+        const bool live = blk < b_hi;
+        const uint32_t ka = live ? (uint32_t)blk * BK * 4u : kOobOffset;
+        const uint32_t kb = TB ? ka : (live ? (uint32_t)blk * BK * (uint32_t)p.ldb * 4u : kOobOffset);
+        char* base = stage(st);
+#pragma unroll
+        for (int j = 0; j < IPW; ++j)
+            lds_dma16(gb[j] ? rb : ra, unit[j] >= 0 ? base + unit[j] * 1024 : spare, goff[j] + (gb[j] ? kb : ka));
+    };
+
+    // LDS byte offsets of this lane's fragment reads.
+    int a_rd[KK][MT], b_rd[KK][TB ? NT : 1], b_rdk[KK][4][TB ? 1 : NG];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+        const int c = kk * 4 + g;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int row = (wm * MT + mt) * 16 + r;
+            a_rd[kk][mt] = row * ROWB + swz_a(row, c) * 16;
+        }
+        if constexpr (TB) {
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                const int n = (wn * NT + nt) * 16 + r;
+                b_rd[kk][nt] = A_BYTES + n * ROWB + swz_a(n, c) * 16;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int q = 0; q < NG; ++q)
+                    b_rdk[kk][e][q] = A_BYTES + (16 * kk + 4 * g + e) * BROW + ((wn * NG + q) * 64 + 4 * r) * 4;
+        }
+    }
+    f32x4 acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto compute_blk = [&](int st, int blk, auto tail_tag) {
+        constexpr bool TAIL = decltype(tail_tag)::value;
+        const char* St = stage(st);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+            u32x4 af[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) af[mt] = *reinterpret_cast<const u32x4*>(St + a_rd[kk][mt]);
+            const int kv = p.K - (blk * BK + 16 * kk + 4 * g);  // valid k of this lane's chunk
+            if constexpr (TAIL) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) af[mt] = keep_dwords(af[mt], kv);
+            }
+            if constexpr (TB) {
+                u32x4 bf[NT];
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    bf[nt] = *reinterpret_cast<const u32x4*>(St + b_rd[kk][nt]);
+                    if constexpr (TAIL) bf[nt] = keep_dwords(bf[nt], kv);
+                }
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt)
+                            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(as_f32(af[mt][c]), as_f32(bf[nt][c]),
+                                                                              acc[mt][nt], 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    u32x4 bv[NG];
+#pragma unroll
+                    for (int q = 0; q < NG; ++q) bv[q] = *reinterpret_cast<const u32x4*>(St + b_rdk[kk][c][q]);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int nt = 0; nt < NT; ++nt)
+                            acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                                as_f32(af[mt][c]), as_f32(bv[nt / 4][nt & 3]), acc[mt][nt], 0, 0, 0);
+                }
+            }
+        }
+    };
+    auto compute = [&](int st, int blk) {
+        if ((blk + 1) * BK > p.K) compute_blk(st, blk, std::true_type{});
+        else compute_blk(st, blk, std::false_type{});
+    };
+    auto iter = [&](int i, int st) {
+        // This wave's copies of block i are done (the NS - 2 later blocks'
+        // may still be in flight); after the barrier every wave's are, and
+        // every wave has consumed block i - 1's fragments.
+        wait_vmcnt<(NS - 2) * IPW>();
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        dma((st + NS - 1) % NS, b_lo + i + NS - 1);
+        compute(st, b_lo + i);
+    };
+
+    if (nb > 0) {
+#pragma unroll
+        for (int s = 0; s < NS - 1; ++s) dma(s, b_lo + s);
+    }
+    int i0 = 0;
+    for (; i0 + NS <= nb; i0 += NS) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) iter(i0 + s, s);
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+        if (i0 + s < nb) iter(i0 + s, s);
+    // Every copy has landed before the workgroup ends.
+    wait_vmcnt<0>();
+    tile_finish<MT, NT, WM, WN, 1, ILV>(p, acc, red_unused, &last_flag, w, lane, tile.n, tile.m, p.tiles_n,
+                                        p.tiles_n * p.tiles_m);
+}
+
 // ---------------------------------------------------------------- launch table
 // {MT, NT, WM, WN, KW}
 static const TileConfig kTileConfigs[] = {
@@ -1100,6 +1301,14 @@ static const TileConfig kTileConfigs[] = {
     {4, 4, 2, 2, 1, 3, 64},   // 39: 128 x 128, 4 waves of 64 x 64, 3 stages
     // LDS-staged (continued)
     {4, 3, 4, 2, 1, 2, 64},   // 40: 256 x 96, 8 waves of 64 x 48, 64 k per block
+    // fp32, LDS DMA: {MT, NT, WM, WN, 1, stages, k per block}
+    {2, 4, 2, 2, 1, 3, 32},   // 41: 64 x 128, 4 waves of 32 x 64
+    {4, 4, 2, 2, 1, 3, 32},   // 42: 128 x 128, 4 waves of 64 x 64
+    {1, 4, 4, 1, 1, 3, 32},   // 43: 64 x 64, 4 waves of 16 x 64
+    {2, 4, 4, 1, 1, 3, 32},   // 44: 128 x 64, 4 waves of 32 x 64
+    {2, 4, 4, 2, 1, 3, 32},   // 45: 128 x 128, 8 waves of 32 x 64
+    {1, 4, 2, 1, 1, 3, 32},   // 46: 32 x 64, 2 waves of 16 x 64
+    {1, 4, 4, 2, 1, 3, 32},   // 47: 64 x 128, 8 waves of 16 x 64
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -1128,6 +1337,13 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
         if (mode == kTileBF16 && tb) hipLaunchKernelGGL((dnnopt_tile_bf16_dma<MT, NT, WM, WN, NS, 1, BK>), grid, blk, 0, s, a); \
         else if (mode == kTileBF16) hipLaunchKernelGGL((dnnopt_tile_bf16_dma<MT, NT, WM, WN, NS, 0, BK>), grid, blk, 0, s, a); \
         else return hipErrorInvalidValue;                                                                  \
+        break;
+
+#define DNNOPT_TILE_F32DMA_CASE(IDX, MT, NT, WM, WN, NS)                                                 \
+    case IDX:                                                                                              \
+        if (mode != kTileF32 || ta) return hipErrorInvalidValue;                                           \
+        if (tb) hipLaunchKernelGGL((dnnopt_tile_f32_dma<MT, NT, WM, WN, NS, 1>), grid, blk, 0, s, a);       \
+        else hipLaunchKernelGGL((dnnopt_tile_f32_dma<MT, NT, WM, WN, NS, 0>), grid, blk, 0, s, a);          \
         break;
 
 #define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN, D, KB, KW)                                              \
@@ -1188,6 +1404,13 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_LDS_CASE(38, 1, 1, 1, 3, 3, 128, 1)
         DNNOPT_TILE_DMA_CASE(39, 4, 4, 2, 2, 3, 64)
         DNNOPT_TILE_LDS_CASE(40, 4, 3, 4, 2, 2, 64, 1)
+        DNNOPT_TILE_F32DMA_CASE(41, 2, 4, 2, 2, 3)
+        DNNOPT_TILE_F32DMA_CASE(42, 4, 4, 2, 2, 3)
+        DNNOPT_TILE_F32DMA_CASE(43, 1, 4, 4, 1, 3)
+        DNNOPT_TILE_F32DMA_CASE(44, 2, 4, 4, 1, 3)
+        DNNOPT_TILE_F32DMA_CASE(45, 2, 4, 4, 2, 3)
+        DNNOPT_TILE_F32DMA_CASE(46, 1, 4, 2, 1, 3)
+        DNNOPT_TILE_F32DMA_CASE(47, 1, 4, 4, 2, 3)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

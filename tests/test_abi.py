@@ -157,23 +157,28 @@ def test_plans_for_weights_stored_n_by_k(lib):
     for M, tb in ((17, 1), (32, 1), (9, 0), (16, 0), (32, 0)):
         p = lib.plan_sgemm(M, 4096, 4096, transB=tb)
         assert p["kernel"] == b.K_TILE_F32 and (p["rows"], p["cols"], p["block"]) == (16, 128, 256), (M, tb, p)
-    # From M = 12 (A stored M x K, N >= 64) the fitted cost model picks the
-    # register tile and k-split where it puts them 10% ahead of the rule
-    # (measured on MI355X, us, rule -> model): B stored N x K 128 x 768 x 768
-    # 16.1 -> 8.6 and 200 x 512 x 512 15.7 -> 6.9 (16 x 16 tiles, k over 8
-    # waves, no split instead of 64 x 128 with 6 / 4 splits), 196 x 256 x 2304
-    # 18.7 -> 11.5, 64 x 4096 x 4096 49.7 -> 43.9 (64 x 64 with two k-groups);
-    # B stored K x N 784 x 128 x 1152 14.1 -> 10.8, 128 x 4096 x 4096 55.7 ->
-    # 54.1 (4 splits instead of 2); 512 x 4096 x 4096 keeps 16 x 128 unsplit.
-    cases = {(128, 768, 768, 1): (16, 16, 1, 512), (200, 512, 512, 1): (16, 16, 1, 512),
-             (196, 256, 2304, 1): (16, 16, 1, 512), (64, 4096, 4096, 1): (64, 64, 8, 512),
-             (784, 128, 1152, 0): (16, 16, 1, 512), (128, 4096, 4096, 0): (16, 128, 4, 256),
-             (512, 4096, 4096, 0): (16, 128, 1, 256)}
-    for (M, N, K, tb), want in cases.items():
+    # From M = 12 (A stored M x K, N >= 64) the fitted cost models pick the
+    # tile and k-split: the register tiles' model where it puts them 10% ahead
+    # of the rule, then the LDS-DMA tiles' where theirs puts them 10% ahead of
+    # that (measured on MI355X, us): B stored N x K 128 x 768 x 768 16.1 ->
+    # 8.6 and 200 x 512 x 512 15.7 -> 6.9 (16 x 16 tiles, k over 8 waves, no
+    # split, instead of 64 x 128 with 6 / 4 splits), 196 x 256 x 2304 18.7 ->
+    # 11.5; 128 x 4096 x 4096 77.6 -> 49.1 (B stored N x K) and 57.7 -> 53.0
+    # (K x N) on 64 x 64 LDS-DMA tiles with 2 splits, 512 x 4096 x 4096 178.3
+    # -> 159.9 (64 x 128 LDS-DMA, 8 waves), 1024 x 1024 x 1024 (B stored N x
+    # K) 40.7 -> 22.9; beyond 10^10 MACs the LDS-DMA tiles alone (2048 x 2048
+    # x 2048, B stored N x K, 198.6 -> 131.5).
+    cases = {(128, 768, 768, 1): ("", 16, 16, 1, 512), (200, 512, 512, 1): ("", 16, 16, 1, 512),
+             (196, 256, 2304, 1): ("", 16, 16, 1, 512), (784, 128, 1152, 0): ("", 16, 16, 1, 512),
+             (128, 4096, 4096, 1): ("_dma", 64, 64, 2, 256), (128, 4096, 4096, 0): ("_dma", 64, 64, 2, 256),
+             (512, 4096, 4096, 0): ("_dma", 64, 128, 1, 512), (1024, 1024, 1024, 1): ("_dma", 64, 64, 1, 256),
+             (2048, 2048, 2048, 1): ("_dma", 64, 128, 1, 512)}
+    for (M, N, K, tb), (kind, *want) in cases.items():
         p = lib.plan_sgemm(M, N, K, transB=tb)
-        assert p["kernel"] == b.K_TILE_F32 and (p["rows"], p["cols"], p["splits"], p["block"]) == want, (M, N, K, tb, p)
-    # outside its range (above 10^10 MACs) the rule: 64 x 128 tiles above M = 512
-    assert lib.plan_sgemm(1024, 4096, 4096)["rows"] == 64
+        assert p["kernel"] == b.K_TILE_F32 and p["name"] == "dnnopt_tile_f32" + kind, (M, N, K, tb, p)
+        assert [p["rows"], p["cols"], p["splits"], p["block"]] == want, (M, N, K, tb, p)
+    # the LDS-DMA tiles need A stored M x K: A stored K x M keeps the rule
+    assert lib.plan_sgemm(2048, 2048, 2048, transA=1)["name"] == "dnnopt_tile_f32"
     # a forced configuration or split count turns the model off
     with lib.tunables(TILE_CFG=2):
         assert (lib.plan_sgemm(128, 768, 768, transB=1)["rows"], lib.plan_sgemm(128, 768, 768, transB=1)["cols"]) == (64, 64)

@@ -88,6 +88,34 @@ def test_sgemm_few_rows_tiles(lib, orc, dev, M, N, K, tb, pad, ta):
                                 f"few rows {M}x{N}x{K} ta={ta} tb={tb} a={alpha} b={beta} forced={forced}")
 
 
+@pytest.mark.parametrize("cfg", [41, 42, 43, 44, 45, 46, 47])
+@pytest.mark.parametrize("tb", [0, 1])
+def test_sgemm_lds_dma_tiles(lib, orc, dev, cfg, tb):
+    """fp32 tiles with both operands copied into LDS by the memory unit,
+    forced with 1 to 3 k-splits: ragged M and N, a K tail inside a 32-k
+    block, padded strides filled with NaN (they must reach no product of a
+    stored output), alpha and beta != 0; and a K of 5 with N off the
+    64-column groups."""
+    for M, N, K, pa, pb in ((300, 1000, 520, 3, 5), (17, 1001, 5, 0, 1)):
+        lda, ldb = K + pa, (K + pb if tb else N + pb)
+        As = np.full((M, lda), np.nan, np.float32)
+        As[:, :K] = u.normal(orc, M * K, 1).reshape(M, K)
+        rows, cols = (N, K) if tb else (K, N)
+        Bs = np.full((rows, ldb), np.nan, np.float32)
+        Bs[:, :cols] = u.normal(orc, rows * cols, 2, 0, 0.02).reshape(rows, cols)
+        Bkn = np.ascontiguousarray(Bs[:, :K].T if tb else Bs[:, :N])
+        C0 = u.uniform(orc, M * N, 3).reshape(M, N)
+        want, scale = u.exact(As[:, :K], Bkn, 0.5, 0.25, C0)
+        dA, dB = dev_copy(As, dev), dev_copy(Bs, dev)
+        for splits in (1, 2, 3):
+            with lib.tunables(TILE_CFG=cfg, TILE_SPLITS=splits):
+                p = lib.plan_sgemm(M, N, K, transB=tb)
+                assert p["name"] == "dnnopt_tile_f32_dma", p
+                dC = dev_copy(C0, dev)
+                lib.sgemm(M, N, K, 0.5, dA, lda, dB, ldb, 0.25, dC, N, transB=tb, stream=stream())
+            u.assert_fp32_close(host(dC), want, scale, K, f"f32 dma cfg {cfg} tb={tb} {M}x{N}x{K} splits={splits}")
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096)] + [(M, N, 2048) for M in (2, 3, 5, 7) for N in (1009, 4099, 11003)])
 def test_sgemm_configs_c1_c2(lib, orc, dev, M, N, K):
     """Full benchmark shapes: C1 (beta 0, C pre-filled NaN) and C2 (beta 1),
@@ -319,7 +347,10 @@ def _routes_tall(M, N, K):
 @pytest.mark.parametrize("tb", [0, 1])
 def test_sgemm_tall_skinny(lib, orc, dev, M, N, K, pa, pb, tb):
     p = lib.plan_sgemm(M, N, K, transB=tb)
-    assert p["name"] == ("dnnopt_tall_f32" if _routes_tall(M, N, K) else "dnnopt_tile_f32"), p
+    if _routes_tall(M, N, K):
+        assert p["name"] == "dnnopt_tall_f32", p
+    else:
+        assert p["name"] in ("dnnopt_tile_f32", "dnnopt_tile_f32_dma"), p
     lda = K + pa
     opA = np.zeros((M, lda), np.float32)
     opA[:, :K] = u.uniform(orc, M * K, 1).reshape(M, K)

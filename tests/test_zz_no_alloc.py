@@ -73,11 +73,12 @@ def test_noalloc_refuses_large_scratch(lib, orc, dev):
     refused before anything is enqueued; a following small call still works."""
     b = u.binding()
     M, N, K = 600, 600, 300000
-    assert lib.plan_sgemm(M, N, K)["workspace_bytes"] > b.NOALLOC_SCRATCH_BYTES - 4 * 16384
     dA = torch.zeros(M * K, dtype=torch.float32, device=dev)
     dB = torch.zeros(K * N, dtype=torch.float32, device=dev)
     dC = torch.full((M, N), 7.0, dtype=torch.float32, device=dev)
-    st = lib.sgemm_noalloc(M, N, K, 1.0, dA, K, dB, N, 0.0, dC, N, stream=_stream())
+    with lib.tunables(TILE_SPLITS=32):  # a plan whose partial sums exceed the array
+        assert lib.plan_sgemm(M, N, K)["workspace_bytes"] > b.NOALLOC_SCRATCH_BYTES - 4 * 16384
+        st = lib.sgemm_noalloc(M, N, K, 1.0, dA, K, dB, N, 0.0, dC, N, stream=_stream())
     assert st == b.ERR_SCRATCH_LIMIT
     assert "scratch" in lib.so.dnnopt_hip_status_string(st).decode()
     torch.cuda.synchronize()
