@@ -833,10 +833,10 @@ def vendor_yardstick():
 # DNN inference GEMMs outside the configs: BERT-base encoder layers at 128 /
 # 384 / 32 tokens (hidden 768, MLP 3072), ResNet-50 convolutions as im2col
 # GEMMs (56x56x64 3x3, 28x28x128 3x3, 14x14x256 3x3, 7x7x512 3x3, 56x56x256
-# 1x1), and two square-ish blocks.
+# 1x1), two square-ish blocks, and a 4096-wide projection at 512 tokens.
 DNN_SHAPES = [(128, 768, 768), (128, 3072, 768), (128, 768, 3072), (384, 768, 768), (384, 3072, 768),
               (384, 768, 3072), (32, 768, 768), (3136, 64, 576), (784, 128, 1152), (196, 256, 2304),
-              (49, 512, 4608), (3136, 256, 64), (64, 1024, 1024), (200, 512, 512)]
+              (49, 512, 4608), (3136, 256, 64), (64, 1024, 1024), (200, 512, 512), (512, 4096, 4096)]
 
 
 def _yardstick_summary(torch, rows, what):
