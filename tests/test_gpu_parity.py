@@ -116,6 +116,23 @@ def test_sgemm_lds_dma_tiles(lib, orc, dev, cfg, tb):
             u.assert_fp32_close(host(dC), want, scale, K, f"f32 dma cfg {cfg} tb={tb} {M}x{N}x{K} splits={splits}")
 
 
+@pytest.mark.parametrize("M,N,K,tb", [(128, 4096, 4096, 0), (128, 4096, 4096, 1), (1024, 1024, 1024, 1),
+                                      (384, 3072, 768, 1), (2048, 2048, 2048, 1)])
+def test_sgemm_planned_lds_dma_tiles(lib, orc, dev, M, N, K, tb):
+    """Shapes where the planner itself takes the fp32 LDS-DMA tiles (with
+    and without k-splits), against the fp64 product; beta != 0."""
+    p = lib.plan_sgemm(M, N, K, transB=tb)
+    assert p["name"] == "dnnopt_tile_f32_dma", p
+    A = u.normal(orc, M * K, 71).reshape(M, K)
+    Bs = u.normal(orc, N * K, 72, 0, 0.02).reshape((N, K) if tb else (K, N))
+    C0 = u.uniform(orc, M * N, 73).reshape(M, N)
+    dC = dev_copy(C0, dev)
+    lib.sgemm(M, N, K, 1.0, dev_copy(A, dev), K, dev_copy(Bs, dev), K if tb else N, -0.5, dC, N, transB=tb,
+              stream=stream())
+    want, scale = u.exact(A, np.ascontiguousarray(Bs.T) if tb else Bs, 1.0, -0.5, C0)
+    u.assert_fp32_close(host(dC), want, scale, K, f"planned f32 dma {M}x{N}x{K} tb={tb}")
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096)] + [(M, N, 2048) for M in (2, 3, 5, 7) for N in (1009, 4099, 11003)])
 def test_sgemm_configs_c1_c2(lib, orc, dev, M, N, K):
     """Full benchmark shapes: C1 (beta 0, C pre-filled NaN) and C2 (beta 1),
