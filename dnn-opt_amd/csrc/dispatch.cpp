@@ -335,19 +335,21 @@ static const LdsFit kF2BFit[] = {
     {19, 0, 2, 2.255, 1.381, 16.62}, {20, 0, 1, 3.124, 6.880, 6.68}, {21, 0, 1, 2.956, 5.461, 19.89},
     {22, 0, 1, 3.047, 0.031, 22.17}, {23, 0, 1, 2.674, 0.063, 19.12}, {40, 0, 1, 3.112, 5.685, 17.17},
 };
-// fp32 LDS-DMA tiles (A stored M x K, both B layouts): 320 measured cases (M
-// = 10..12544, N = 64..11008, K = 64..4608; 7 configurations, 1 to 16
-// splits; median error 5%, 90% within 18%); 4.83 us per launch, 3.4 TB/s; a
-// split 1.25 us plus its partials at 4.3 TB/s.
+// fp32 LDS-DMA tiles (A stored M x K; the 32-column wave tiles with B
+// stored N x K only): 320 measured cases (M = 10..12544, N = 64..11008, K =
+// 64..4608; 10 configurations, 1 to 16 splits; median error 5%, 90% within
+// 19%); 4.72 us per launch, 3.5 TB/s; a split 1.25 us plus its partials at
+// 4.6 TB/s.
 static const LdsFit kF32DmaFit[] = {
-    {41, 0, 2, 2.028, 1.231, 22.32}, {41, 1, 2, 0.044, 1.187, 2.87}, {42, 0, 1, 4.222, 1.196, 29.55},
-    {42, 1, 1, 0.890, 1.158, 1.51}, {43, 0, 3, 1.021, 1.249, 17.30}, {43, 1, 3, 0.000, 1.165, 24.82},
-    {44, 0, 2, 2.168, 1.215, 5.68}, {44, 1, 2, 0.008, 1.186, 0.00}, {45, 0, 1, 3.558, 1.130, 43.81},
-    {45, 1, 1, 0.000, 1.150, 4.66}, {46, 0, 4, 0.953, 1.952, 9.64}, {46, 1, 4, 0.000, 1.834, 0.25},
-    {47, 0, 2, 1.767, 1.154, 29.23}, {47, 1, 2, 0.000, 1.113, 8.54},
+    {41, 0, 2, 2.274, 1.228, 0.26}, {41, 1, 2, 0.261, 1.185, 19.57}, {42, 0, 1, 4.514, 1.193, 8.00},
+    {42, 1, 1, 1.171, 1.155, 34.31}, {43, 0, 3, 1.236, 1.247, 11.13}, {43, 1, 3, 0.000, 1.186, 11.69},
+    {44, 0, 2, 2.429, 1.212, 17.13}, {44, 1, 2, 0.217, 1.184, 41.16}, {45, 0, 1, 3.863, 1.126, 7.86},
+    {45, 1, 1, 0.237, 1.148, 2.48}, {46, 0, 4, 1.143, 1.949, 31.79}, {46, 1, 4, 0.083, 1.846, 15.47},
+    {47, 0, 2, 2.006, 1.152, 9.30}, {47, 1, 2, 0.074, 1.122, 19.73}, {48, 1, 6, 0.000, 1.683, 3.93},
+    {49, 1, 3, 0.000, 1.171, 20.76}, {50, 1, 4, 0.000, 1.212, 12.92},
 };
 static const LdsModel kBf16Model{kBf16Fit, (int)(sizeof kBf16Fit / sizeof kBf16Fit[0]), 2, 0.5, 2.72, 1.83, 0.1467, 0.2994};
-static const LdsModel kF32DmaModel{kF32DmaFit, (int)(sizeof kF32DmaFit / sizeof kF32DmaFit[0]), 4, 8.0, 4.83, 1.25, 0.2347, 0.2924};
+static const LdsModel kF32DmaModel{kF32DmaFit, (int)(sizeof kF32DmaFit / sizeof kF32DmaFit[0]), 4, 8.0, 4.72, 1.25, 0.2168, 0.2869};
 static const LdsModel kF2BModel{kF2BFit, (int)(sizeof kF2BFit / sizeof kF2BFit[0]), 4, 0.5, 1.99, 2.73, 0.1509, 0.3039};
 
 static double lds_tile_cost(const LdsModel& md, const LdsFit& f, long long s, int M, int N, int K, long long cus) {
@@ -488,10 +490,11 @@ static TilePick pick_f32_tile(int tb, int M, int N, int K, int def_cfg) {
 }
 
 // fp32 LDS-DMA tiles address A from the tile's first row and B from its
-// first row (N x K) or column (K x N) with 32-bit offsets over all of k.
+// first row (N x K) or column (K x N) with 32-bit offsets over all of k; the
+// 32-column wave tiles need B stored N x K.
 static bool f32_dma_fits(int cfg, int transA, int transB, int M, int K, int lda, int ldb) {
     (void)M;
-    if (transA) return false;
+    if (transA || (!transB && cfg >= kTileF32DmaTbFirst)) return false;
     const TileConfig c = tile_config(cfg);
     const long long bm = c.wm * c.mt * 16, bn = c.wn * c.nt * 16;
     return (bm * lda + K) * 4 < 0x7FFFFFFFll &&
@@ -613,7 +616,14 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     // a forced configuration (tunable TILE_CFG).
     if (!lds && mode == kTileF32 && !transA && M >= 12 && N >= 64 && forced_cfg <= 0 &&
         tunable(kTuneTileSplits) <= 0) {
-        auto dma_ok = [&](int k) { return f32_dma_fits(k, transA, transB, M, K, lda, ldb); };
+        // The 32-column wave tiles only while 64 x 128 tiles would fill the
+        // chip fewer than 4 times: beyond that their extra re-reads of A and
+        // B, which the model does not price, cost more than they save
+        // (measured 10-16% slower at 1200-1600 such tiles).
+        const bool small_grid = ceil_div(M, 64) * ceil_div(N, 128) < 4 * num_cus();
+        auto dma_ok = [&](int k) {
+            return (k < kTileF32DmaTbFirst || small_grid) && f32_dma_fits(k, transA, transB, M, K, lda, ldb);
+        };
         const TilePick dma = best_lds_tile(kF32DmaModel, transB ? 1 : 0, M, N, K, dma_ok);
         if ((double)M * N * K <= 1e10) {
             // the register tiles' model, then the LDS-DMA tiles where their

@@ -1061,12 +1061,13 @@ __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_bf16_dma(TileArgs p) 
 // for A and B alike.  B stored K x N is staged as 32 rows of BN floats and
 // read 16 bytes of one k row at a time (columns 4 r .. 4 r + 3 of a
 // 64-column group), whose components feed the four sub-tiles of the group
-// (their columns interleave over 64, as in the 16-row register tiles).
+// (their columns interleave over 64, as in the 16-row register tiles), so
+// that layout needs wave tiles of whole 64-column groups.
 // Bytes of A (and of B stored N x K) past K are zeroed in registers in the
 // last block; rows of B stored K x N past K read zero.  A stored M x K only.
 template <int MT, int NT, int WM, int WN, int NS, int TB>
 __global__ __launch_bounds__(WM* WN * 64) void dnnopt_tile_f32_dma(TileArgs p) {
-    static_assert(NT % 4 == 0, "whole 64-column groups per wave");
+    static_assert(TB || NT % 4 == 0, "B stored K x N: whole 64-column groups per wave");
     using SH = TileShape<MT, NT, WM, WN, 1>;
     constexpr int BM = SH::BM, BN = SH::BN;
     constexpr int NW = WM * WN;
@@ -1309,6 +1310,10 @@ static const TileConfig kTileConfigs[] = {
     {2, 4, 4, 2, 1, 3, 32},   // 45: 128 x 128, 8 waves of 32 x 64
     {1, 4, 2, 1, 1, 3, 32},   // 46: 32 x 64, 2 waves of 16 x 64
     {1, 4, 4, 2, 1, 3, 32},   // 47: 64 x 128, 8 waves of 16 x 64
+    // fp32, LDS DMA, B stored N x K only (wave tiles of 32 columns)
+    {1, 2, 2, 1, 1, 3, 32},   // 48: 32 x 32, 2 waves of 16 x 32
+    {2, 2, 2, 2, 1, 3, 32},   // 49: 64 x 64, 4 waves of 32 x 32
+    {1, 2, 2, 2, 1, 3, 32},   // 50: 32 x 64, 4 waves of 16 x 32
 };
 
 int tile_config_count() { return (int)(sizeof(kTileConfigs) / sizeof(kTileConfigs[0])); }
@@ -1344,6 +1349,12 @@ TileConfig tile_config(int idx) { return kTileConfigs[idx]; }
         if (mode != kTileF32 || ta) return hipErrorInvalidValue;                                           \
         if (tb) hipLaunchKernelGGL((dnnopt_tile_f32_dma<MT, NT, WM, WN, NS, 1>), grid, blk, 0, s, a);       \
         else hipLaunchKernelGGL((dnnopt_tile_f32_dma<MT, NT, WM, WN, NS, 0>), grid, blk, 0, s, a);          \
+        break;
+
+#define DNNOPT_TILE_F32DMA_TB_CASE(IDX, MT, NT, WM, WN, NS)                                              \
+    case IDX:                                                                                              \
+        if (mode != kTileF32 || ta || !tb) return hipErrorInvalidValue;                                    \
+        hipLaunchKernelGGL((dnnopt_tile_f32_dma<MT, NT, WM, WN, NS, 1>), grid, blk, 0, s, a);               \
         break;
 
 #define DNNOPT_TILE_LDS_CASE(IDX, MT, NT, WM, WN, D, KB, KW)                                              \
@@ -1411,6 +1422,9 @@ hipError_t launch_tile(int mode, int cfg_idx, int ta, int tb, int al, dim3 grid,
         DNNOPT_TILE_F32DMA_CASE(45, 2, 4, 4, 2, 3)
         DNNOPT_TILE_F32DMA_CASE(46, 1, 4, 2, 1, 3)
         DNNOPT_TILE_F32DMA_CASE(47, 1, 4, 4, 2, 3)
+        DNNOPT_TILE_F32DMA_TB_CASE(48, 1, 2, 2, 1, 3)
+        DNNOPT_TILE_F32DMA_TB_CASE(49, 2, 2, 2, 2, 3)
+        DNNOPT_TILE_F32DMA_TB_CASE(50, 1, 2, 2, 2, 3)
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

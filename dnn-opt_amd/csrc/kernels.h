@@ -241,10 +241,11 @@ constexpr int kTileBF16Dma4w = 39;
 // addresses C with 32-bit offsets from the tile's first row, so it needs
 // 256 * ldc * 4 < 2^31.
 constexpr int kTileF2BTall = 40;
-// fp32, both operands copied into LDS by the memory unit (A stored M x K;
-// B stored K x N or N x K): configurations kTileF32DmaFirst..Last, 32 k per
-// block, wave tiles of 16, 32 or 64 rows by 64 columns.
-constexpr int kTileF32DmaFirst = 41, kTileF32DmaLast = 47;
+// fp32, both operands copied into LDS by the memory unit (A stored M x K):
+// configurations kTileF32DmaFirst..Last, 32 k per block; wave tiles of 16,
+// 32 or 64 rows by 64 columns (B stored K x N or N x K), and from
+// kTileF32DmaTbFirst by 32 columns (B stored N x K only).
+constexpr int kTileF32DmaFirst = 41, kTileF32DmaTbFirst = 48, kTileF32DmaLast = 50;
 constexpr bool tile_f32_dma(int cfg) { return cfg >= kTileF32DmaFirst && cfg <= kTileF32DmaLast; }
 // k per LDS block of an LDS-staged configuration: its kblk (or
 // DNNOPT_LDS_KB) when both stages fit in 128 KiB of LDS, else 64.

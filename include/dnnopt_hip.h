@@ -294,7 +294,8 @@ int dnnopt_hip_device_count(void);    /* 0 when no device is visible        */
 #define DNNOPT_TUNE_SKINNY_WGS       8
 #define DNNOPT_TUNE_TILE_SPLITS      9  /* force the k-splits of a tile launch */
 #define DNNOPT_TUNE_TILE_CFG        10  /* force a tile configuration (bf16 LDS-staged: 5 and up;
-                                           fp32 register tiles: 1-4, 35, 36) */
+                                           fp32 register tiles: 1-4, 35, 36; fp32 LDS-DMA tiles,
+                                           A stored M x K: 41-47, and 48-50 with B stored N x K) */
 #define DNNOPT_TUNE_TILE_TICKET     11
 #define DNNOPT_TUNE_S8_CFG          12
 #define DNNOPT_TUNE_S8_ROWDOT       13

@@ -163,20 +163,26 @@ def test_plans_for_weights_stored_n_by_k(lib):
     # that (measured on MI355X, us): B stored N x K 128 x 768 x 768 16.1 ->
     # 8.6 and 200 x 512 x 512 15.7 -> 6.9 (16 x 16 tiles, k over 8 waves, no
     # split, instead of 64 x 128 with 6 / 4 splits), 196 x 256 x 2304 18.7 ->
-    # 11.5; 128 x 4096 x 4096 77.6 -> 49.1 (B stored N x K) and 57.7 -> 53.0
-    # (K x N) on 64 x 64 LDS-DMA tiles with 2 splits, 512 x 4096 x 4096 178.3
-    # -> 159.9 (64 x 128 LDS-DMA, 8 waves), 1024 x 1024 x 1024 (B stored N x
-    # K) 40.7 -> 22.9; beyond 10^10 MACs the LDS-DMA tiles alone (2048 x 2048
-    # x 2048, B stored N x K, 198.6 -> 131.5).
+    # 9.4 (32 x 64 LDS-DMA tiles of 32-column waves, 8 splits); 128 x 4096 x
+    # 4096 77.6 -> 52 (B stored N x K, 32 x 64 LDS-DMA) and 57.7 -> 52 (K x
+    # N, 64 x 128 LDS-DMA with 4 splits), 512 x 4096 x 4096 178.3 -> 150 (64
+    # x 128 LDS-DMA, 8 waves), 1024 x 1024 x 1024 (B stored N x K) 40.7 ->
+    # 23.3; beyond 10^10 MACs the LDS-DMA tiles alone (2048 x 2048 x 2048, B
+    # stored N x K, 198.6 -> 134.6).
     cases = {(128, 768, 768, 1): ("", 16, 16, 1, 512), (200, 512, 512, 1): ("", 16, 16, 1, 512),
-             (196, 256, 2304, 1): ("", 16, 16, 1, 512), (784, 128, 1152, 0): ("", 16, 16, 1, 512),
-             (128, 4096, 4096, 1): ("_dma", 64, 64, 2, 256), (128, 4096, 4096, 0): ("_dma", 64, 64, 2, 256),
+             (196, 256, 2304, 1): ("_dma", 32, 64, 8, 256), (784, 128, 1152, 0): ("", 16, 16, 1, 512),
+             (128, 4096, 4096, 1): ("_dma", 32, 64, 1, 256), (128, 4096, 4096, 0): ("_dma", 64, 128, 4, 512),
              (512, 4096, 4096, 0): ("_dma", 64, 128, 1, 512), (1024, 1024, 1024, 1): ("_dma", 64, 64, 1, 256),
              (2048, 2048, 2048, 1): ("_dma", 64, 128, 1, 512)}
     for (M, N, K, tb), (kind, *want) in cases.items():
         p = lib.plan_sgemm(M, N, K, transB=tb)
         assert p["kernel"] == b.K_TILE_F32 and p["name"] == "dnnopt_tile_f32" + kind, (M, N, K, tb, p)
         assert [p["rows"], p["cols"], p["splits"], p["block"]] == want, (M, N, K, tb, p)
+    # the 32-column wave tiles only while 64 x 128 tiles would fill the chip
+    # fewer than 4 times (3303 x 3922 x 2969: 1612 such tiles; 32 x 64 tiles
+    # measured 763 us against 639 us for 64 x 128 with 2 splits)
+    p = lib.plan_sgemm(3303, 3922, 2969, transB=1)
+    assert (p["name"], p["rows"], p["cols"], p["splits"], p["block"]) == ("dnnopt_tile_f32_dma", 64, 128, 2, 512), p
     # the LDS-DMA tiles need A stored M x K: A stored K x M keeps the rule
     assert lib.plan_sgemm(2048, 2048, 2048, transA=1)["name"] == "dnnopt_tile_f32"
     # a forced configuration or split count turns the model off

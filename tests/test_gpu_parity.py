@@ -88,14 +88,18 @@ def test_sgemm_few_rows_tiles(lib, orc, dev, M, N, K, tb, pad, ta):
                                 f"few rows {M}x{N}x{K} ta={ta} tb={tb} a={alpha} b={beta} forced={forced}")
 
 
-@pytest.mark.parametrize("cfg", [41, 42, 43, 44, 45, 46, 47])
-@pytest.mark.parametrize("tb", [0, 1])
+@pytest.mark.parametrize("cfg,tb", [(c, tb) for c in (41, 42, 43, 44, 45, 46, 47) for tb in (0, 1)] +
+                         [(c, 1) for c in (48, 49, 50)])
 def test_sgemm_lds_dma_tiles(lib, orc, dev, cfg, tb):
     """fp32 tiles with both operands copied into LDS by the memory unit,
     forced with 1 to 3 k-splits: ragged M and N, a K tail inside a 32-k
     block, padded strides filled with NaN (they must reach no product of a
     stored output), alpha and beta != 0; and a K of 5 with N off the
-    64-column groups."""
+    64-column groups.  The 32-column wave tiles (48-50) take B stored N x K
+    only; with B stored K x N a forced one is refused (the rule's tile)."""
+    if cfg >= 48:
+        with lib.tunables(TILE_CFG=cfg):
+            assert lib.plan_sgemm(300, 1000, 520, transB=0)["name"] == "dnnopt_tile_f32"
     for M, N, K, pa, pb in ((300, 1000, 520, 3, 5), (17, 1001, 5, 0, 1)):
         lda, ldb = K + pa, (K + pb if tb else N + pb)
         As = np.full((M, lda), np.nan, np.float32)
