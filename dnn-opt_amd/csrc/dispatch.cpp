@@ -52,7 +52,8 @@
 // these environment variables):
 //   DNNOPT_WAVES_PER_CU (default 8), DNNOPT_SKINNY_NW (4, 8 or 16; default 8),
 //   DNNOPT_SKINNY_WGS_PER_CU (default 1), DNNOPT_SKINNY_WGS (force G),
-//   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 kernel),
+//   DNNOPT_MAX_SPLITS (default 256), DNNOPT_SPLIT_REDUCE (0 ticket, 1 the
+//   planners' choice, 2 reduce kernel),
 //   DNNOPT_TILE_SPLITS (force the k-splits of a tile launch), DNNOPT_TILE_CFG
 //   (force a tile configuration: an LDS-staged bf16 one, index 5 and up, or
 //   an fp32 register tile, 1-4, 35 or 36; either turns the cost models off),
@@ -165,7 +166,7 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
     auto span_ok = [&](long long g) { return ceil_div(K, g / T) * (long long)ldb * es + (long long)tw * es < 0x7FFFFFFFll; };
     while (!span_ok(G) && G / T < K) G += T;
     if (!span_ok(G) || G > 0x7FFFFFFFll) return DNNOPT_ERR_UNSUPPORTED;
-    if (G > T && T > kMaxTickets && !split_reduce_mode()) return DNNOPT_ERR_UNSUPPORTED;
+    if (G > T && T > kMaxTickets && tunable(kTuneSplitReduce) == 0) return DNNOPT_ERR_UNSUPPORTED;
     const long long smax_tile = ceil_div(G, T);
     L->mode = mode;
     L->mr = M;
@@ -176,7 +177,16 @@ int plan_skinny(int mode, int M, int N, int K, int ldb, Launch* L) {
     L->unroll = (mode == kSkinnyF32 && nw == 8) ? 4 : 16;
     L->tiles = (int)T;
     L->grid = dim3((unsigned)G, 1, 1);
-    L->defer_reduce = (G > T && split_reduce_mode()) ? 1 : 0;
+    // Split-k sums: the last-arriving workgroup of a tile adds the partials
+    // itself (one kernel) when they are few rows and few bytes, else the
+    // reduce kernel (MI355X, graph replays, us: C1 14.57 -> 14.23, bf16 1 x
+    // 11008 x 4096 18.77 -> 18.05, M = 2 / 3 x 4099 / 11003 0.1 less; but M
+    // = 5 x 11003 (25 KiB) +0.43, M = 2 x 1009 (64 KiB) +0.30, M = 7 x 1009
+    // (224 KiB) +2.6).
+    const int srm = tunable(kTuneSplitReduce);
+    const bool ticket = srm == 0 || (srm == 1 && M <= 3 && T <= kMaxTickets &&
+                                     smax_tile * M * tw * 4 <= kSkinnyTicketBytes);
+    L->defer_reduce = (G > T && !ticket) ? 1 : 0;
     L->part_bytes = G > T ? (size_t)smax_tile * M * T * tw * sizeof(float) : 0;
     L->tickets = (G > T && !L->defer_reduce) ? (int)T : 0;
     const int kernel = mode == kSkinnyF32 ? DNNOPT_K_SKINNY_F32

@@ -75,8 +75,13 @@ struct Launch {
     int defer_reduce = 0;
 };
 
-// Split-k reduction strategy: 0 = last-arriving workgroup (ticket),
-// 1 = separate reduce kernel.  DNNOPT_SPLIT_REDUCE overrides the default.
+// Split-k reduction strategy (tunable SPLIT_REDUCE): 0 = last-arriving
+// workgroup (ticket) wherever the kernel has one; 1 (default) = the
+// planners' choice: the separate reduce kernel, except skinny launches of at
+// most 3 rows whose last workgroup reads at most kSkinnyTicketBytes of
+// partials; 2 = the reduce kernel everywhere.  split_reduce_mode() is 0 for
+// the ticket, 1 for the reduce kernel (the planners' default).
+constexpr long long kSkinnyTicketBytes = 48 * 1024;
 int split_reduce_mode();
 
 // Tunable parameters of the planners (tune.cpp), in the order of the
@@ -90,7 +95,7 @@ enum Tunable {
     kTuneSkinnyNW,          // skinny waves per workgroup (4, 8, 16; 0 = by size)
     kTuneSkinnyWgsPerCu,    // skinny workgroups per CU
     kTuneMaxSplits,         // register tiles: most k-splits
-    kTuneSplitReduce,       // split-k partials summed by a reduce kernel (1) or the last workgroup (0)
+    kTuneSplitReduce,       // split-k sums: 0 last workgroup, 1 planners' choice, 2 reduce kernel
     kTuneSkinnyWgs,         // forced skinny workgroup count
     kTuneTileSplits,        // forced tile k-splits
     kTuneTileCfg,           // forced tile configuration

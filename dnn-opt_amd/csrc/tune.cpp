@@ -30,7 +30,7 @@ constexpr TuneDef kDefs[kTuneCount] = {
     {"DNNOPT_Q8B", 1, true},           {"DNNOPT_KOUTER", 1, true},
     {"DNNOPT_KOUTER_WGS_PER_CU", 1, false}, {"DNNOPT_WAVES_PER_CU", 8, false},
     {"DNNOPT_SKINNY_NW", 0, false},    {"DNNOPT_SKINNY_WGS_PER_CU", 1, false},
-    {"DNNOPT_MAX_SPLITS", 256, false}, {"DNNOPT_SPLIT_REDUCE", 1, true},
+    {"DNNOPT_MAX_SPLITS", 256, false}, {"DNNOPT_SPLIT_REDUCE", 1, false},
     {"DNNOPT_SKINNY_WGS", 0, false},   {"DNNOPT_TILE_SPLITS", 0, false},
     {"DNNOPT_TILE_CFG", 0, false},     {"DNNOPT_TILE_TICKET", 0, false},
     {"DNNOPT_S8_CFG", -1, false},      {"DNNOPT_S8_ROWDOT", 1, true},

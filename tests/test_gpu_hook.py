@@ -348,3 +348,26 @@ def test_ticket_reduction_mode(lib, orc, dev):
             u.assert_fp32_close(u.cm_load(host(dC), M, N, M), want + bias[:, None],
                                 scale + np.abs(bias)[:, None], K + 1, f"ticket hook {ta} {M}x{N}x{K}")
     assert lib.get_tunable("SPLIT_REDUCE") == 1
+
+
+@pytest.mark.parametrize("M,N,K,dt", [(1, 4096, 4096, "f32"), (2, 4099, 2048, "f32"), (3, 11003, 2048, "f32"),
+                                      (7, 1009, 2048, "f32"), (1, 11008, 4096, "bf16"), (3, 1001, 5000, "bf16")])
+def test_split_sums_bit_identical_across_modes(lib, dev, M, N, K, dt):
+    """The skinny kernel's split-k sums, by the last-arriving workgroup
+    (SPLIT_REDUCE=0), the planner's choice (1) or the reduce kernel (2), add
+    the splits in the same order: the three give the same bits."""
+    g = torch.Generator(device="cpu").manual_seed(M * N + K)
+    dtype = torch.float32 if dt == "f32" else torch.bfloat16
+    A = torch.randn(M, K, generator=g).to(dtype).to(dev)
+    B = (torch.randn(K, N, generator=g) * 0.02).to(dtype).to(dev)
+    C0 = (torch.rand(M, N, generator=g) * 2 - 1).to(dev)
+    outs = []
+    for mode in (0, 1, 2):
+        C = C0.clone()
+        with lib.tunables(SPLIT_REDUCE=mode):
+            assert lib.plan_sgemm(M, N, K)["splits"] > 1
+            fn = lib.sgemm if dt == "f32" else lib.gemm_bf16
+            fn(M, N, K, 1.0, A, K, B, N, 1.0, C, N, stream=torch.cuda.current_stream().cuda_stream)
+        outs.append(C)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2]), (M, N, K, dt)

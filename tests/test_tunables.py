@@ -83,3 +83,29 @@ def test_tunable_keys_are_checked():
     assert lib.so.dnnopt_hip_get_tunable(20, ctypes.byref(v)) != 0
     assert lib.so.dnnopt_hip_set_tunable(-1, 0, None) != 0
     assert lib.so.dnnopt_hip_get_tunable(7, None) != 0
+
+
+def test_split_reduce_choice():
+    """SPLIT_REDUCE 1 (default) lets the skinny planner sum the splits in the
+    last-arriving workgroup (a plan that takes the ticket slots) for at most 3
+    rows and 48 KiB of partials per tile, the reduce kernel otherwise; 0 and
+    2 force one or the other."""
+    lib = u.load_lib()
+    ticket_bytes = 4096 * 64 * 4
+
+    def ticket(plan_fn):
+        base = plan_fn()
+        with lib.tunables(SPLIT_REDUCE=2):
+            red = plan_fn()
+        assert (base["grid_x"], base["splits"]) == (red["grid_x"], red["splits"])
+        return base["workspace_bytes"] - red["workspace_bytes"] == ticket_bytes
+
+    assert lib.get_tunable("SPLIT_REDUCE") == 1
+    for M, N, K, want in ((1, 4096, 4096, True), (2, 4099, 2048, True), (3, 4099, 2048, True),
+                          (3, 11003, 2048, True), (2, 1009, 2048, False), (3, 1009, 2048, False),
+                          (4, 11003, 2048, False), (5, 11003, 2048, False), (7, 4099, 2048, False)):
+        assert ticket(lambda: lib.plan_sgemm(M, N, K)) == want, (M, N, K)
+    assert ticket(lambda: lib.plan_bf16(1, 11008, 4096))
+    assert not ticket(lambda: lib.plan_bf16(4, 11008, 4096))
+    with lib.tunables(SPLIT_REDUCE=0):
+        assert lib.plan_sgemm(7, 1009, 2048)["workspace_bytes"] > lib.plan_sgemm(1, 1, 1)["workspace_bytes"]
