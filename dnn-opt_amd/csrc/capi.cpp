@@ -197,6 +197,13 @@ static int sgemm_planned(int transA, int transB, int M, int N, int K, float alph
         return run_rowdot(L, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias);
     if (L.family == DNNOPT_K_TALL_F32) {
         TallArgs a{A, B, C, lda, ldb, ldc, M, N, K, alpha, beta, bias};
+        if (L.mr == 0) {
+            // A copied by LDS-DMA needs 16-byte aligned rows; otherwise the
+            // register-ring kernel takes the same grid.
+            if ((reinterpret_cast<uintptr_t>(A) & 15u) == 0)
+                return finish_launch(launch_tall_dma_f32(L.mode, L.grid, a, s));
+            return finish_launch(launch_tall_f32(1, L.mode, 1, L.grid, tall_lds_bytes(1, K), a, s));
+        }
         return finish_launch(launch_tall_f32(L.cfg, L.mode, L.mr, L.grid, L.lds, a, s));
     }
     return run_tile(L, transA, transB, A, lda, B, ldb, C, ldc, M, N, K, alpha, beta, s, bias, ext);

@@ -843,10 +843,13 @@ int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int 
     if (ldc <= 0) ldc = N;
     // N <= 12 (a quarter or more of the padded 16-column MFMA tile wasted)
     // and N <= 16 with short K stream faster through the register tiles
-    // (64 x 16), whose per-k re-reads of B are small at that width; measured
-    // at 65536 x 16 x 256: 18.5 (here) vs 19.3 us, 65536 x 12 x 256: 20.4 vs
-    // 19.5, 262144 x 16 x 64: 20.9 vs 19.9.
-    if (N <= 12 || (N <= 16 && K < 128) || N > 64 || M < 4096) return DNNOPT_ERR_UNSUPPORTED;
+    // (64 x 16) than through the register-ring kernel here (65536 x 12 x
+    // 256: 20.4 vs 19.5 us, 262144 x 16 x 64: 20.9 vs 19.9), but slower than
+    // through the LDS-DMA kernel below where it fits (MI355X, us, register
+    // tiles -> LDS-DMA: 65536 x 12 x 256 17.7 -> 16.8, 65536 x 1 x 256 23.3
+    // -> 16.4, 262144 x 16 x 64 20.0 -> 17.6, 131072 x 8 x 128 18.7 -> 16.2).
+    if ((N <= 12 || (N <= 16 && K < 128)) && !tall_dma_fits(N, K, lda)) return DNNOPT_ERR_UNSUPPORTED;
+    if (N > 64 || M < 4096) return DNNOPT_ERR_UNSUPPORTED;
     const int nt = (N + 15) / 16;
     const size_t lds = tall_lds_bytes(nt, K);
     if (lds > 65536) return DNNOPT_ERR_UNSUPPORTED;
@@ -870,6 +873,26 @@ int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int 
     if (ceil_div(M, 32) * 4 < 3 * waves && (K < 256 || ceil_div(M, 16) * 2 < waves)) return DNNOPT_ERR_UNSUPPORTED;
     const int forced_rt = tunable(kTuneTallRT);
     if (forced_rt == 1 || forced_rt == 2) rt = forced_rt;
+    // N <= 16 with K = 64 .. 256 (a multiple of 64) and 16-byte rows of A:
+    // A copied into LDS by the memory unit, a whole 16-row tile per wave in
+    // flight (dnnopt_tall_dma_f32); persistent 4-wave workgroups, as many
+    // per CU as their LDS allows (at most 4).  Against the register-ring
+    // kernel (MI355X, us): 65536 x 16 x 256 16.9 -> 16.8 (B stored N x K
+    // 18.3 -> 17.2), 65536 x 13 x 128 11.3 -> 9.9, 16384 x 16 x 256 9.0 ->
+    // 7.1, 65536 x 16 x 192 14.7 -> 13.5.
+    if (nt == 1 && forced_rt <= 0 && tall_dma_fits(N, K, lda)) {
+        const size_t dlds = tall_dma_lds_bytes(K);
+        const long long per_cu_d = std::max<long long>(1, std::min<long long>(4, 160 * 1024 / (long long)dlds));
+        const long long Gd = std::max<long long>(
+            1, std::min<long long>(num_cus() * per_cu_d, ceil_div(ceil_div(M, 16), tall_dma_waves())));
+        L->cfg = 1;
+        L->mr = 0;
+        L->lds = dlds;
+        L->mode = transB;
+        L->grid = dim3((unsigned)Gd, 1, 1);
+        fill_pub(L, DNNOPT_K_TALL_F32, "dnnopt_tall_dma_f32", 16, 16, 1, tall_dma_waves() * 64);
+        return DNNOPT_OK;
+    }
     const long long tiles = ceil_div(M, 16 * rt);
     // Persistent: one workgroup per CU by default, no more than there are row
     // tiles for their waves.  More row tiles per wave keep loads, MFMAs and

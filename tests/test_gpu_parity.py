@@ -352,24 +352,35 @@ TALL = [(65536, 64, 256, 0, 0), (65536, 16, 256, 1, 0), (65537, 33, 300, 0, 3), 
         (4096, 1, 1024, 0, 0), (100003, 7, 64, 1, 2), (50000, 48, 333, 0, 0), (49999, 17, 5, 3, 0),
         (60000, 60, 250, 1, 1), (70000, 32, 128, 0, 0), (8192, 33, 300, 0, 3), (4097, 17, 5, 3, 0),
         (65536, 13, 130, 1, 2), (50001, 16, 64, 0, 0), (65536, 12, 256, 0, 0), (16384, 64, 256, 0, 0),
-        (20001, 40, 300, 1, 0), (16383, 64, 256, 0, 0), (30000, 33, 255, 0, 1)]
+        (20001, 40, 300, 1, 0), (16383, 64, 256, 0, 0), (30000, 33, 255, 0, 1),
+        # A by LDS-DMA (N <= 16, K = 128 / 192 / 256, rows of A a multiple of 16 bytes)
+        (65536, 16, 256, 0, 0), (65537, 13, 128, 4, 1), (70001, 16, 192, 0, 3), (50000, 15, 256, 8, 0),
+        (16384, 16, 256, 0, 0), (131072, 14, 128, 0, 0),
+        # ... and N <= 12 or K = 64 on the same kernel
+        (65536, 1, 256, 0, 0), (65536, 8, 256, 4, 0), (262144, 16, 64, 0, 2), (131075, 5, 128, 0, 0)]
 
 
-def _routes_tall(M, N, K):
+def _routes_tall(M, N, K, lda=None):
     # one 32-row tile for at least 3/4 of the waves of one 8-wave workgroup per CU (256 CUs),
     # or (K >= 256) one 16-row tile for every other wave; N <= 12, and N <= 16 with K < 128,
-    # stay on the register tiles
+    # stay on the register tiles; N <= 16 with K a multiple of 64 up to 256 and rows of A a
+    # multiple of 16 bytes take the LDS-DMA kernel
     waves = 256 * 8
     rows_ok = -(-M // 32) * 4 >= 3 * waves or (K >= 256 and -(-M // 16) * 2 >= waves)
-    return N > 12 and (N > 16 or K >= 128) and N <= 64 and rows_ok
+    lda = K if lda is None else lda
+    dma = N <= 16 and K % 64 == 0 and 64 <= K <= 256 and lda % 4 == 0
+    if not ((dma or (N > 12 and (N > 16 or K >= 128))) and N <= 64 and rows_ok):
+        return None
+    return "dnnopt_tall_dma_f32" if dma else "dnnopt_tall_f32"
 
 
 @pytest.mark.parametrize("M,N,K,pa,pb", TALL)
 @pytest.mark.parametrize("tb", [0, 1])
 def test_sgemm_tall_skinny(lib, orc, dev, M, N, K, pa, pb, tb):
-    p = lib.plan_sgemm(M, N, K, transB=tb)
-    if _routes_tall(M, N, K):
-        assert p["name"] == "dnnopt_tall_f32", p
+    p = lib.plan_sgemm_ex(M, N, K, K + pa, (K if tb else N) + pb, N, transB=tb)
+    route = _routes_tall(M, N, K, K + pa)
+    if route:
+        assert p["name"] == route, p
     else:
         assert p["name"] in ("dnnopt_tile_f32", "dnnopt_tile_f32_dma"), p
     lda = K + pa
@@ -388,6 +399,59 @@ def test_sgemm_tall_skinny(lib, orc, dev, M, N, K, pa, pb, tb):
                   stream=stream())
         want, scale = u.exact(opA[:, :K], opB, 1.25, beta, C0 if beta else None)
         u.assert_fp32_close(host(dC), want, scale, K, f"tall {M}x{N}x{K} tb={tb} beta={beta}")
+
+
+@pytest.mark.parametrize("M,N,K", [(65536, 16, 256), (65537, 13, 128), (65536, 16, 192), (16384, 15, 256)])
+def test_tall_dma_matches_register_ring_kernel(lib, dev, M, N, K):
+    """The LDS-DMA tall kernel adds the same products in the same order as
+    the register-ring tall kernel (forced by TALL_RT=1): bit-identical C for
+    both B layouts, beta 0 and 0.5; A off 16-byte alignment falls back to the
+    register-ring kernel (same bits); a column-bias call through the oneDNN
+    hook (column-major C^T, the tall product with B^T as A) too."""
+    g = torch.Generator(device="cpu").manual_seed(M + N + K)
+    A = torch.rand(M, K, generator=g).to(dev) * 2 - 1
+    B = torch.rand(K, N, generator=g).to(dev) * 2 - 1
+    BT = B.t().contiguous()
+    C0 = torch.rand(M, N, generator=g).to(dev)
+    assert lib.plan_sgemm(M, N, K)["name"] == "dnnopt_tall_dma_f32"
+    for tb, Bx, ldb in ((0, B, N), (1, BT, K)):
+        for beta in (0.0, 0.5):
+            outs = []
+            for rt in (0, 1):
+                C = C0.clone()
+                with lib.tunables(TALL_RT=rt):
+                    want_name = "dnnopt_tall_dma_f32" if rt == 0 else "dnnopt_tall_f32"
+                    assert lib.plan_sgemm(M, N, K, transB=tb)["name"] == want_name
+                    lib.sgemm(M, N, K, 1.25, A, K, Bx, ldb, beta, C, N, transB=tb, stream=stream())
+                outs.append(C)
+            torch.cuda.synchronize()
+            assert torch.equal(outs[0], outs[1]), (M, N, K, tb, beta)
+    exact = (A.double() @ B.double()).cpu().numpy() * 1.25
+    scale = (A.double().abs() @ B.double().abs()).cpu().numpy() * 1.25
+    C = torch.empty(M, N, device=dev)
+    lib.sgemm(M, N, K, 1.25, A, K, B, N, 0.0, C, N, stream=stream())
+    u.assert_fp32_close(host(C), exact, scale, K, f"tall dma {M}x{N}x{K}")
+    # A starting 4 bytes past a 16-byte boundary (rows of K floats stay 16-byte multiples)
+    buf = torch.empty(M * K + 4, device=dev)
+    Am = buf[1:1 + M * K].view(M, K)
+    Am.copy_(A)
+    C = torch.empty(M, N, device=dev)
+    lib.sgemm(M, N, K, 1.25, Am, K, B, N, 0.0, C, N, stream=stream())
+    ref = torch.empty(M, N, device=dev)
+    with lib.tunables(TALL_RT=1):
+        lib.sgemm(M, N, K, 1.25, A, K, B, N, 0.0, ref, N, stream=stream())
+    torch.cuda.synchronize()
+    assert torch.equal(C, ref), (M, N, K, "misaligned A")
+    # column-major hook: C^T (N x M, ldc = N) = B^T A^T with a bias per column of the row-major C
+    bias = torch.rand(N, generator=g).to(dev)
+    outs = []
+    for rt in (0, 1):
+        Ct = C0.clone()
+        with lib.tunables(TALL_RT=rt):
+            lib.ext_sgemm("N", "N", N, M, K, 1.0, B, N, A, K, 0.5, Ct, N, bias=bias, stream=stream())
+        outs.append(Ct)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]), (M, N, K, "hook bias")
 
 
 def test_sgemm_naive_bitwise(lib, orc, dev):
