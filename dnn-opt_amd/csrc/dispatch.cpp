@@ -870,7 +870,13 @@ int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int 
     // vs 33.6, 65536 x 64 x 256 27.4 vs 28.6, 65536 x 48 x 128 14.3 vs 15.1.
     const long long waves = num_cus() * tall_waves();
     int rt = 1;
-    if (ceil_div(M, 32) * 4 < 3 * waves && (K < 256 || ceil_div(M, 16) * 2 < waves)) return DNNOPT_ERR_UNSUPPORTED;
+    // The LDS-DMA kernel (N <= 16, below) needs no such count: its 4-wave
+    // workgroups beat the register tiles from 4K rows (MI355X, us: 4096 x 16
+    // x 256 6.7 -> 4.7, 8192 x 16 x 256 7.9 -> 5.8, 12288 x 16 x 128 4.8 ->
+    // 4.2, 8192 x 8 x 128 4.4 -> 3.7, 24576 x 16 x 64 4.6 -> 4.2).
+    const bool dma = nt == 1 && tall_dma_fits(N, K, lda);
+    if (!dma && ceil_div(M, 32) * 4 < 3 * waves && (K < 256 || ceil_div(M, 16) * 2 < waves))
+        return DNNOPT_ERR_UNSUPPORTED;
     const int forced_rt = tunable(kTuneTallRT);
     if (forced_rt == 1 || forced_rt == 2) rt = forced_rt;
     // N <= 16 with K = 64 .. 256 (a multiple of 64) and 16-byte rows of A:
@@ -880,7 +886,7 @@ int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int 
     // kernel (MI355X, us): 65536 x 16 x 256 16.9 -> 16.8 (B stored N x K
     // 18.3 -> 17.2), 65536 x 13 x 128 11.3 -> 9.9, 16384 x 16 x 256 9.0 ->
     // 7.1, 65536 x 16 x 192 14.7 -> 13.5.
-    if (nt == 1 && forced_rt <= 0 && tall_dma_fits(N, K, lda)) {
+    if (dma && forced_rt <= 0) {
         const size_t dlds = tall_dma_lds_bytes(K);
         const long long per_cu_d = std::max<long long>(1, std::min<long long>(4, 160 * 1024 / (long long)dlds));
         const long long Gd = std::max<long long>(

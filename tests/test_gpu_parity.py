@@ -357,7 +357,9 @@ TALL = [(65536, 64, 256, 0, 0), (65536, 16, 256, 1, 0), (65537, 33, 300, 0, 3), 
         (65536, 16, 256, 0, 0), (65537, 13, 128, 4, 1), (70001, 16, 192, 0, 3), (50000, 15, 256, 8, 0),
         (16384, 16, 256, 0, 0), (131072, 14, 128, 0, 0),
         # ... and N <= 12 or K = 64 on the same kernel
-        (65536, 1, 256, 0, 0), (65536, 8, 256, 4, 0), (262144, 16, 64, 0, 2), (131075, 5, 128, 0, 0)]
+        (65536, 1, 256, 0, 0), (65536, 8, 256, 4, 0), (262144, 16, 64, 0, 2), (131075, 5, 128, 0, 0),
+        # ... and from 4K rows (one tile per wave or fewer)
+        (4096, 16, 256, 0, 0), (8191, 16, 128, 0, 1), (4097, 3, 64, 4, 0)]
 
 
 def _routes_tall(M, N, K, lda=None):
@@ -369,9 +371,11 @@ def _routes_tall(M, N, K, lda=None):
     rows_ok = -(-M // 32) * 4 >= 3 * waves or (K >= 256 and -(-M // 16) * 2 >= waves)
     lda = K if lda is None else lda
     dma = N <= 16 and K % 64 == 0 and 64 <= K <= 256 and lda % 4 == 0
-    if not ((dma or (N > 12 and (N > 16 or K >= 128))) and N <= 64 and rows_ok):
+    if dma:
+        return "dnnopt_tall_dma_f32" if M >= 4096 else None
+    if not (N > 12 and (N > 16 or K >= 128) and N <= 64 and rows_ok):
         return None
-    return "dnnopt_tall_dma_f32" if dma else "dnnopt_tall_f32"
+    return "dnnopt_tall_f32"
 
 
 @pytest.mark.parametrize("M,N,K,pa,pb", TALL)
