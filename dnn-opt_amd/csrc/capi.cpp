@@ -202,7 +202,7 @@ static int sgemm_planned(int transA, int transB, int M, int N, int K, float alph
             // register-ring kernel takes the same grid.
             if ((reinterpret_cast<uintptr_t>(A) & 15u) == 0)
                 return finish_launch(launch_tall_dma_f32(L.mode, L.grid, a, s));
-            return finish_launch(launch_tall_f32(1, L.mode, 1, L.grid, tall_lds_bytes(1, K), a, s));
+            return finish_launch(launch_tall_f32(L.cfg, L.mode, 1, L.grid, tall_lds_bytes(L.cfg, K), a, s));
         }
         return finish_launch(launch_tall_f32(L.cfg, L.mode, L.mr, L.grid, L.lds, a, s));
     }

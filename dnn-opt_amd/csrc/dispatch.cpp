@@ -870,33 +870,35 @@ int plan_tall(int transB, int M, int N, int K, int lda, int ldb, Launch* L, int 
     // vs 33.6, 65536 x 64 x 256 27.4 vs 28.6, 65536 x 48 x 128 14.3 vs 15.1.
     const long long waves = num_cus() * tall_waves();
     int rt = 1;
-    // The LDS-DMA kernel (N <= 16, below) needs no such count: its 4-wave
-    // workgroups beat the register tiles from 4K rows (MI355X, us: 4096 x 16
-    // x 256 6.7 -> 4.7, 8192 x 16 x 256 7.9 -> 5.8, 12288 x 16 x 128 4.8 ->
-    // 4.2, 8192 x 8 x 128 4.4 -> 3.7, 24576 x 16 x 64 4.6 -> 4.2).
-    const bool dma = nt == 1 && tall_dma_fits(N, K, lda);
-    if (!dma && ceil_div(M, 32) * 4 < 3 * waves && (K < 256 || ceil_div(M, 16) * 2 < waves))
+    // K = 64 .. 256 (a multiple of 64) with 16-byte rows of A: A copied
+    // into LDS by the memory unit (dnnopt_tall_dma_f32), except K = 128 with
+    // N > 32, where the register-ring kernel is faster (65536 x 48 / 64 x
+    // 128: 15.0 / 16.4 vs 15.4 / 17.5 us).  For N <= 16 it needs no row
+    // count either: it beats the register tiles from 4K rows (MI355X, us:
+    // 4096 x 16 x 256 6.7 -> 4.7, 8192 x 16 x 256 7.9 -> 5.8, 12288 x 16 x
+    // 128 4.8 -> 4.2, 8192 x 8 x 128 4.4 -> 3.7, 24576 x 16 x 64 4.6 -> 4.2).
+    const bool dma = tall_dma_fits(N, K, lda) && !(K == 128 && N > 32);
+    if (!(dma && nt == 1) && ceil_div(M, 32) * 4 < 3 * waves && (K < 256 || ceil_div(M, 16) * 2 < waves))
         return DNNOPT_ERR_UNSUPPORTED;
     const int forced_rt = tunable(kTuneTallRT);
     if (forced_rt == 1 || forced_rt == 2) rt = forced_rt;
-    // N <= 16 with K = 64 .. 256 (a multiple of 64) and 16-byte rows of A:
-    // A copied into LDS by the memory unit, a whole 16-row tile per wave in
-    // flight (dnnopt_tall_dma_f32); persistent 4-wave workgroups, as many
-    // per CU as their LDS allows (at most 4).  Against the register-ring
-    // kernel (MI355X, us): 65536 x 16 x 256 16.9 -> 16.8 (B stored N x K
-    // 18.3 -> 17.2), 65536 x 13 x 128 11.3 -> 9.9, 16384 x 16 x 256 9.0 ->
-    // 7.1, 65536 x 16 x 192 14.7 -> 13.5.
+    // The LDS-DMA kernel: persistent 8-wave workgroups, as many per CU as
+    // their LDS allows (at most 4).  Against the register-ring kernel
+    // (MI355X, us, 65536 rows): N = 16 x K = 256 16.9 -> 16.2, N = 32 x 192
+    // 17.1 -> 14.7, N = 32 x 256 21.2 -> 19.5, N = 48 x 256 22.9 -> 21.1,
+    // N = 64 x 256 27.4 -> 26.2 (B stored N x K 30.3 -> 28.6), N = 64 x 64
+    // 11.3 -> 11.1, 65536 x 13 x 128 11.3 -> 9.8, 16384 x 16 x 256 9.0 -> 7.1.
     if (dma && forced_rt <= 0) {
-        const size_t dlds = tall_dma_lds_bytes(K);
+        const size_t dlds = tall_dma_lds_bytes(nt, K);
         const long long per_cu_d = std::max<long long>(1, std::min<long long>(4, 160 * 1024 / (long long)dlds));
         const long long Gd = std::max<long long>(
             1, std::min<long long>(num_cus() * per_cu_d, ceil_div(ceil_div(M, 16), tall_dma_waves())));
-        L->cfg = 1;
+        L->cfg = nt;
         L->mr = 0;
         L->lds = dlds;
         L->mode = transB;
         L->grid = dim3((unsigned)Gd, 1, 1);
-        fill_pub(L, DNNOPT_K_TALL_F32, "dnnopt_tall_dma_f32", 16, 16, 1, tall_dma_waves() * 64);
+        fill_pub(L, DNNOPT_K_TALL_F32, "dnnopt_tall_dma_f32", 16, 16 * nt, 1, tall_dma_waves() * 64);
         return DNNOPT_OK;
     }
     const long long tiles = ceil_div(M, 16 * rt);

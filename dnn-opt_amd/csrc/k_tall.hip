@@ -245,65 +245,81 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
 }
 
 // ---------------------------------------------------------------- A by LDS-DMA
-// fp32 tall-skinny GEMM for N <= 16 and K = 64 KQ (KQ = 1..4), A stored
-// M x K with 16-byte aligned rows.  B is staged once into LDS as above; A is
-// copied into LDS by the memory unit (buffer_load ... lds), a 16-row tile
-// (16 K floats) at a time: each copy instruction moves 64 lanes x 16
-// bytes, which are whole rows of A (K = 256: one 1 KiB row per
-// instruction; shorter rows, several per instruction), so HBM sees
-// contiguous row reads where the register-ring kernel reads 16 rows x 64
-// bytes per load, and a wave keeps whole tiles in flight without spending
-// registers on them.  (Copies of 64-k pieces, 256-byte row segments, with
-// more bytes in flight, were slower.)
-//   * every wave owns a private ring of S tile slots: tile i + S - 1 is
-//     copied into the slot tile i - 1 left while tile i's MFMAs run; the
-//     wave waits only for its own copies (vmcnt), no barrier after B's
-//     staging;
+// fp32 tall-skinny GEMM for N <= 16 NT (NT = 1..4) and K = 64 KQ (KQ =
+// 1..4), A stored M x K with 16-byte aligned rows.  B is staged once into
+// LDS as above; A is copied into LDS by the memory unit (buffer_load ...
+// lds) in pieces of 16 rows x PK k, the largest of K, K / 2 and 64 whose
+// two slots per wave fit beside B's image.  Each copy instruction moves 64
+// lanes x 16 bytes of whole row segments (PK = 256: one 1 KiB row per
+// instruction), so HBM sees contiguous row reads where the register-ring
+// kernel reads 16 rows x 64 bytes per load, and a wave keeps a whole piece
+// in flight without spending registers on it.
+//   * 8 waves per workgroup (two per SIMD), each with a private ring of two
+//     piece slots, walking its (16-row tile, piece) pairs as one flat
+//     sequence: piece i + 1 is copied into the slot piece i - 1 left while
+//     piece i's MFMAs run; the wave waits only for its own copies (vmcnt),
+//     no barrier after B's staging;
 //   * within a slot, row r's 16-byte chunk c sits at physical chunk
-//     (c + r) mod (K / 4) of the row (rows are multiples of 256 bytes), so
+//     (c + r) mod (PK / 4) of the row segment (a multiple of 256 bytes), so
 //     the 16 rows a quarter-wave reads at one chunk fall in 16 different
 //     16-byte bank groups;
 //   * MFMA operands as in dnnopt_tall_f32 (lane (r, g) reads k = 16 kc + 4 g
 //     .. + 3 of row r, component c feeding MFMA c), in the same k order, so
 //     both kernels add the same products in the same order.
-#ifndef DNNOPT_TALL_DMA_W
-#define DNNOPT_TALL_DMA_W 4
-#endif
-constexpr int kTallDmaWaves = DNNOPT_TALL_DMA_W;
-// Two tile slots per wave (one tile in flight while the other is read):
-// measured against 3 / 4 slots with 2 / 3 / 4 waves and against 8 waves,
-// this is the fastest at K = 128..256 (K <= 128 then fits two workgroups,
-// 8 waves, per CU).
+// Measured at 65536 rows against 4 waves with two whole-tile slots, 4 waves
+// with 3 / 4 slots, 2 and 3 waves, and 8 waves with one slot: this layout
+// is the fastest at K = 192 / 256 for every N and level elsewhere.
+constexpr int kTallDmaWaves = 8;
 constexpr int kTallDmaSlots = 2;
+constexpr int kTallDmaLds = 163840;  // LDS bytes of one workgroup at most
 
-template <int KQ, int TB, int BETA>
+// k per piece for K = 64 kq and nt column tiles (see above).
+constexpr bool tall_dma_pk_fits(int kq, int nt, int pk) {
+    return kq * 64 * 64 * nt + kTallDmaWaves * kTallDmaSlots * 16 * pk * 4 <= kTallDmaLds;
+}
+constexpr int tall_dma_pk(int kq, int nt) {
+    return tall_dma_pk_fits(kq, nt, kq * 64)                      ? kq * 64
+           : (kq % 2 == 0 && tall_dma_pk_fits(kq, nt, kq * 32)) ? kq * 32
+                                                                  : 64;
+}
+
+template <int KQ, int NT, int TB, int BETA>
 __global__ __launch_bounds__(kTallDmaWaves * 64) void dnnopt_tall_dma_f32(TallArgs p) {
     constexpr int W = kTallDmaWaves;
     constexpr int S = kTallDmaSlots;
     constexpr int K = 64 * KQ;
-    constexpr int CPR = K / 4;        // 16-byte chunks per row of A
-    constexpr int ROWB = K * 4;       // bytes per row of A
-    constexpr int TILEB = 16 * ROWB;  // bytes per 16-row tile
-    constexpr int NI = TILEB / 1024;  // copy instructions per tile
-    constexpr int KC = K / 16;        // 16-k chunks per tile (4 MFMAs each)
-    constexpr int BBYTES = K * 64;    // B image, [K/4][16][4] floats
+    constexpr int NP = 16 * NT;              // columns of B's image
+    constexpr int PK = tall_dma_pk(KQ, NT);  // k per piece
+    constexpr int PPT = K / PK;              // pieces per tile
+    constexpr int CPR = PK / 4;              // 16-byte chunks per row segment
+    constexpr int SEGB = PK * 4;             // bytes per row segment
+    constexpr int PIECEB = 16 * SEGB;        // bytes per piece
+    constexpr int NI = PIECEB / 1024;        // copy instructions per piece
+    constexpr int KCP = PK / 16;             // 16-k chunks per piece (4 MFMAs per column tile each)
+    constexpr int BBYTES = K * NP * 4;       // B image, [K/4][NP][4] floats
+    static_assert(K % PK == 0 && PK % 64 == 0, "pieces of whole 64-k blocks");
     static_assert((S - 1) * NI < 64, "vmcnt range");
-    __shared__ __attribute__((aligned(1024))) char lds[BBYTES + W * S * TILEB];
+    static_assert(BBYTES + W * S * PIECEB <= kTallDmaLds, "LDS");
+    __shared__ __attribute__((aligned(1024))) char lds[BBYTES + W * S * PIECEB];
 
     const int lane = lane_id(), w = wave_id();
     const int r = lane & 15, g = lane >> 4;
     const int tiles = (p.M + 15) / 16;
     const int gw = (int)blockIdx.x * W + w, GW = (int)gridDim.x * W;
     const int my_tiles = gw < tiles ? (tiles - 1 - gw) / GW + 1 : 0;
+    const int total = my_tiles * PPT;  // pieces of this wave
     // The column bias is read with B, before the copies of A.
     const bool has_bias = p.bias != nullptr;
-    const float biasv = (has_bias && r < p.N) ? p.bias[r] : 0.0f;
+    float biasv[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) biasv[nt] = (has_bias && nt * 16 + r < p.N) ? p.bias[nt * 16 + r] : 0.0f;
 
     // A's range ends at the last element of row M - 1: rows >= M of the last
     // tile read zero.
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(p.A, range31(((size_t)(p.M - 1) * p.lda + K) * 4));
-    // Copy instruction j: lane l fills physical chunk q = 64 j + l of the
-    // slot, row q / CPR, with that row's chunk (q mod CPR - row) mod CPR.
+    // Copy instruction j of a piece: lane l fills physical chunk q = 64 j + l
+    // of the slot, row q / CPR, with that row segment's chunk
+    // (q mod CPR - row) mod CPR.
     uint32_t src[NI];
 #pragma unroll
     for (int j = 0; j < NI; ++j) {
@@ -311,28 +327,35 @@ __global__ __launch_bounds__(kTallDmaWaves * 64) void dnnopt_tall_dma_f32(TallAr
         const int lc = (pc - row % CPR + CPR) % CPR;
         src[j] = ((uint32_t)row * (uint32_t)p.lda + (uint32_t)lc * 4u) * 4u;
     }
-    char* ring = lds + BBYTES + w * S * TILEB;
+    char* ring = lds + BBYTES + w * S * PIECEB;
     const uint32_t tile_step = 16u * (uint32_t)GW * (uint32_t)p.lda * 4u;
-    uint32_t t_off = (uint32_t)gw * 16u * (uint32_t)p.lda * 4u;  // next tile this wave copies
-    auto copy_tile = [&](int slot) {
-        char* dst = ring + slot * TILEB;
+    // Copy cursor: byte offset of the next piece's tile and its piece number.
+    uint32_t l_tile = (uint32_t)gw * 16u * (uint32_t)p.lda * 4u;
+    int l_p = 0;
+    auto copy_piece = [&](int slot) {
+        char* dst = ring + slot * PIECEB;
+        const uint32_t base = l_tile + (uint32_t)l_p * (uint32_t)SEGB;
 #pragma unroll
-        for (int j = 0; j < NI; ++j) lds_dma16(ra, dst + j * 1024, src[j] + t_off);
-        t_off += tile_step;
+        for (int j = 0; j < NI; ++j) lds_dma16(ra, dst + j * 1024, src[j] + base);
+        if (++l_p == PPT) {
+            l_p = 0;
+            l_tile += tile_step;
+        }
     };
 
-    // Stage B (as dnnopt_tall_f32 with one column tile): unit u = (k quad
-    // u / 16, column u % 16) is the 16-byte chunk at byte 16 u.
+    // Stage B (as dnnopt_tall_f32): unit u = (k quad u / NP, column u % NP)
+    // is the 16-byte chunk at byte 16 u.
     {
         const __amdgpu_buffer_rsrc_t rb = make_rsrc(
             p.B, range31((TB ? (size_t)(p.N - 1) * p.ldb + K : (size_t)(K - 1) * p.ldb + p.N) * 4));
-        constexpr int SU = (4 * K + W * 64 - 1) / (W * 64);  // units per thread
+        constexpr int UNITS = K / 4 * NP;
+        constexpr int SU = (UNITS + W * 64 - 1) / (W * 64);  // units per thread
         u32x4 v[SU];
 #pragma unroll
         for (int j = 0; j < SU; ++j) {
             const int u = (int)threadIdx.x + j * W * 64;
-            const int k0 = 4 * (u / 16), n = u % 16;
-            const bool ok = u < 4 * K && n < p.N;
+            const int k0 = 4 * (u / NP), n = u % NP;
+            const bool ok = u < UNITS && n < p.N;
             if constexpr (TB) {
                 v[j] = buf_load_x4(rb, ok ? ((uint32_t)n * p.ldb + k0) * 4u : kOobOffset);
             } else {
@@ -344,74 +367,104 @@ __global__ __launch_bounds__(kTallDmaWaves * 64) void dnnopt_tall_dma_f32(TallAr
         // no register the loop uses is still loading when it starts (the
         // compiler would otherwise wait for every copy before the loop).
         // Always S - 1 copies, a fixed sequence the compiler's wait counts
-        // see through: past this wave's last tile they read rows of later
+        // see through: past this wave's last piece they read rows of later
         // tiles or out-of-range zeros into its own slots, never consumed.
-        asm volatile("" ::"v"(biasv));
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) asm volatile("" ::"v"(biasv[nt]));
         wait_vmcnt<0>();
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < S - 1; ++i) copy_tile(i);
+        for (int i = 0; i < S - 1; ++i) copy_piece(i);
 #pragma unroll
         for (int j = 0; j < SU; ++j) {
             const int u = (int)threadIdx.x + j * W * 64;
-            if (u < 4 * K) *reinterpret_cast<u32x4*>(lds + (size_t)u * 16) = v[j];
+            if (u < UNITS) *reinterpret_cast<u32x4*>(lds + (size_t)u * 16) = v[j];
         }
     }
     // B's LDS writes are all the barrier publishes: no wait on the copies of
     // A in flight (each wave waits for its own before reading them).
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
-    if (my_tiles == 0) {
+    if (total == 0) {
         wait_vmcnt<0>();  // the copies land before the wave ends
         return;
     }
 
     const __amdgpu_buffer_rsrc_t rc = make_rsrc(p.C, range31(((size_t)(p.M - 1) * p.ldc + p.N) * 4));
-    const bool col_ok = r < p.N;
     uint32_t lane_c[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) lane_c[e] = col_ok ? ((uint32_t)(4 * g + e) * (uint32_t)p.ldc + (uint32_t)r) * 4u : kOobOffset;
+    for (int e = 0; e < 4; ++e) lane_c[e] = ((uint32_t)(4 * g + e) * (uint32_t)p.ldc + (uint32_t)r) * 4u;
+    bool col_ok[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) col_ok[nt] = nt * 16 + r < p.N;
     const uint32_t c_step = 16u * (uint32_t)GW * (uint32_t)p.ldc * 4u;
     uint32_t c_off = (uint32_t)gw * 16u * (uint32_t)p.ldc * 4u;
-    const char* b_lane = lds + (g * 16 + r) * 16;
+    // This lane's B fragment of 16-k chunk 0, column tile 0; chunk kc adds
+    // kc * NP * 64 bytes, column tile nt adds nt * 256.
+    const char* b_lane = lds + (g * NP + r) * 16;
 
-    for (int i = 0; i < my_tiles; ++i) {
-        float c_old[4] = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (BETA) {
+    f32x4 acc[NT];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) c_old[e] = as_f32(buf_load_x1(rc, c_off + lane_c[e]));
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float c_old[NT][4];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c_old[nt][e] = 0.0f;
+    int c_p = 0;  // piece number within the current tile
+    for (int i = 0; i < total; ++i) {
+        if constexpr (BETA) {
+            if (c_p == 0) {
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        c_old[nt][e] = as_f32(buf_load_x1(rc, col_ok[nt] ? c_off + lane_c[e] + nt * 64u : kOobOffset));
+            }
         }
-        if (i + S - 1 < my_tiles) {
-            // The slot tile i - 1 used is refilled once its reads are done;
-            // then wait for tile i, leaving the S - 1 later tiles' copies in
+        if (i + S - 1 < total) {
+            // The slot piece i - 1 used is refilled once its reads are done;
+            // then wait for piece i, leaving the next piece's copies in
             // flight (vector memory operations complete in order; C loads
             // and stores issued meanwhile only make the wait stricter).
             __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-            copy_tile((i + S - 1) % S);
+            copy_piece((i + S - 1) % S);
             wait_vmcnt<(S - 1) * NI>();
         } else {
             wait_vmcnt<0>();
         }
-        const char* a_row = ring + (i % S) * TILEB + r * ROWB;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const char* a_row = ring + (i % S) * PIECEB + r * SEGB;
+        const char* b_piece = b_lane + c_p * (KCP * NP * 64);
 #pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
+        for (int kc = 0; kc < KCP; ++kc) {
             int pc = 4 * kc + g + r;
             if (pc >= CPR) pc -= CPR;
             const u32x4 av = *reinterpret_cast<const u32x4*>(a_row + pc * 16);
-            const u32x4 bv = *reinterpret_cast<const u32x4*>(b_lane + kc * 1024);
+            u32x4 bv[NT];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(as_f32(av[c]), as_f32(bv[c]), acc, 0, 0, 0);
-        }
+            for (int nt = 0; nt < NT; ++nt) bv[nt] = *reinterpret_cast<const u32x4*>(b_piece + kc * (NP * 64) + nt * 256);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float v;
-            if constexpr (BETA) v = __builtin_fmaf(p.alpha, acc[e], p.beta * c_old[e]);
-            else v = p.alpha * acc[e];
-            if (has_bias) v = add_rn(v, biasv);
-            buf_store_x1(rc, c_off + lane_c[e], as_u32(v));
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(as_f32(av[c]), as_f32(bv[nt][c]), acc[nt], 0, 0, 0);
         }
-        c_off += c_step;
+        if (++c_p == PPT) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt) {
+                    float v;
+                    if constexpr (BETA) v = __builtin_fmaf(p.alpha, acc[nt][e], p.beta * c_old[nt][e]);
+                    else v = p.alpha * acc[nt][e];
+                    if (has_bias) v = add_rn(v, biasv[nt]);
+                    buf_store_x1(rc, col_ok[nt] ? c_off + lane_c[e] + nt * 64u : kOobOffset, as_u32(v));
+                }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            c_p = 0;
+            c_off += c_step;
+        }
     }
 }
 
@@ -459,35 +512,48 @@ hipError_t launch_tall_f32(int nt, int tb, int rt, dim3 grid, size_t lds_bytes, 
     return hipErrorInvalidValue;
 }
 
-bool tall_dma_fits(int N, int K, int lda) { return N >= 1 && N <= 16 && K % 64 == 0 && K >= 64 && K <= 256 && lda % 4 == 0; }
+bool tall_dma_fits(int N, int K, int lda) { return N >= 1 && N <= 64 && K % 64 == 0 && K >= 64 && K <= 256 && lda % 4 == 0; }
 
-size_t tall_dma_lds_bytes(int K) { return (size_t)K * 64 + (size_t)kTallDmaWaves * kTallDmaSlots * 16 * K * 4; }
+size_t tall_dma_lds_bytes(int nt, int K) {
+    return (size_t)K * 64 * nt + (size_t)kTallDmaWaves * kTallDmaSlots * 16 * tall_dma_pk(K / 64, nt) * 4;
+}
 
 int tall_dma_waves() { return kTallDmaWaves; }
 
-template <int KQ>
+template <int KQ, int NT>
 static void launch_tall_dma_kq(int tb, dim3 grid, const TallArgs& a, hipStream_t s) {
     const dim3 blk(kTallDmaWaves * 64);
     if (tb) {
-        if (a.beta == 0.0f) hipLaunchKernelGGL((dnnopt_tall_dma_f32<KQ, 1, 0>), grid, blk, 0, s, a);
-        else hipLaunchKernelGGL((dnnopt_tall_dma_f32<KQ, 1, 1>), grid, blk, 0, s, a);
+        if (a.beta == 0.0f) hipLaunchKernelGGL((dnnopt_tall_dma_f32<KQ, NT, 1, 0>), grid, blk, 0, s, a);
+        else hipLaunchKernelGGL((dnnopt_tall_dma_f32<KQ, NT, 1, 1>), grid, blk, 0, s, a);
     } else {
-        if (a.beta == 0.0f) hipLaunchKernelGGL((dnnopt_tall_dma_f32<KQ, 0, 0>), grid, blk, 0, s, a);
-        else hipLaunchKernelGGL((dnnopt_tall_dma_f32<KQ, 0, 1>), grid, blk, 0, s, a);
+        if (a.beta == 0.0f) hipLaunchKernelGGL((dnnopt_tall_dma_f32<KQ, NT, 0, 0>), grid, blk, 0, s, a);
+        else hipLaunchKernelGGL((dnnopt_tall_dma_f32<KQ, NT, 0, 1>), grid, blk, 0, s, a);
     }
+}
+
+template <int NT>
+static hipError_t launch_tall_dma_nt(int tb, dim3 grid, const TallArgs& a, hipStream_t s) {
+    switch (a.K / 64) {
+        case 1: launch_tall_dma_kq<1, NT>(tb, grid, a, s); break;
+        case 2: launch_tall_dma_kq<2, NT>(tb, grid, a, s); break;
+        case 3: launch_tall_dma_kq<3, NT>(tb, grid, a, s); break;
+        case 4: launch_tall_dma_kq<4, NT>(tb, grid, a, s); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_tall_dma_f32(int tb, dim3 grid, const TallArgs& a, hipStream_t s) {
     // The kernel's LDS-DMA copies need 16-byte aligned rows of A.
     if (!tall_dma_fits(a.N, a.K, a.lda) || (reinterpret_cast<uintptr_t>(a.A) & 15u) != 0) return hipErrorInvalidValue;
-    switch (a.K / 64) {
-        case 1: launch_tall_dma_kq<1>(tb, grid, a, s); break;
-        case 2: launch_tall_dma_kq<2>(tb, grid, a, s); break;
-        case 3: launch_tall_dma_kq<3>(tb, grid, a, s); break;
-        case 4: launch_tall_dma_kq<4>(tb, grid, a, s); break;
+    switch ((a.N + 15) / 16) {
+        case 1: return launch_tall_dma_nt<1>(tb, grid, a, s);
+        case 2: return launch_tall_dma_nt<2>(tb, grid, a, s);
+        case 3: return launch_tall_dma_nt<3>(tb, grid, a, s);
+        case 4: return launch_tall_dma_nt<4>(tb, grid, a, s);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 }  // namespace dnnopt_hip

@@ -113,12 +113,12 @@ inline size_t tall_lds_bytes(int nt, int K) { return (size_t)((K + 15) / 16) * 1
 int tall_waves();  // waves per workgroup of the tall kernel
 // rt: row tiles of 16 a wave takes at a time (1 or 2).
 hipError_t launch_tall_f32(int nt, int tb, int rt, dim3 grid, size_t lds_bytes, const TallArgs& a, hipStream_t s);
-// A copied into LDS by the memory unit (N <= 16, K = 64, 128, 192 or 256,
+// A copied into LDS by the memory unit (N <= 64, K = 64, 128, 192 or 256,
 // lda % 4 == 0, A 16-byte aligned): persistent workgroups of tall_dma_waves()
-// waves, each with a ring of 16-row x 64-k pieces of A, tall_dma_lds_bytes(K)
-// of LDS per workgroup.
+// waves, each with a ring of two 16-row pieces of A, tall_dma_lds_bytes(nt,
+// K) of LDS per workgroup for nt = ceil(N / 16) column tiles.
 bool tall_dma_fits(int N, int K, int lda);
-size_t tall_dma_lds_bytes(int K);
+size_t tall_dma_lds_bytes(int nt, int K);
 int tall_dma_waves();
 hipError_t launch_tall_dma_f32(int tb, dim3 grid, const TallArgs& a, hipStream_t s);
 

@@ -231,11 +231,16 @@ def test_plans_for_tall_skinny(lib):
     assert lib.plan_sgemm(65536, 64, 256)["rows"] == 16
     assert lib.plan_sgemm(65536, 65, 64)["kernel"] == b.K_TILE_F32
     assert lib.plan_sgemm(65536, 16, 256)["kernel"] == b.K_TALL_F32   # N = 16 with K >= 128: B in LDS
-    # N <= 16 with K = 64..256 (a multiple of 64) and rows of A a multiple of
-    # 16 bytes: A copied into LDS by the memory unit, any N down to 1
-    for M, N, K in ((65536, 16, 256), (65536, 16, 64), (65536, 12, 256), (65536, 1, 256), (131072, 8, 128)):
+    # K = 64..256 (a multiple of 64) and rows of A a multiple of 16 bytes: A
+    # copied into LDS by the memory unit, any N down to 1 and up to 64
+    # (except K = 128 with N > 32), 8-wave workgroups
+    for M, N, K in ((65536, 16, 256), (65536, 16, 64), (65536, 12, 256), (65536, 1, 256), (131072, 8, 128),
+                    (65536, 64, 256), (65536, 32, 128), (65536, 40, 192), (65536, 64, 64)):
         p = lib.plan_sgemm(M, N, K)
-        assert (p["kernel"], p["name"], p["block"]) == (b.K_TALL_F32, "dnnopt_tall_dma_f32", 256), (M, N, K, p)
+        assert (p["kernel"], p["name"], p["block"], p["cols"]) == (
+            b.K_TALL_F32, "dnnopt_tall_dma_f32", 512, 16 * -(-N // 16)), (M, N, K, p)
+    assert lib.plan_sgemm(65536, 48, 128)["name"] == "dnnopt_tall_f32"
+    assert lib.plan_sgemm(65536, 64, 256, transA=1)["kernel"] == b.K_TILE_F32
     assert lib.plan_sgemm_ex(65536, 16, 256, 257, 16, 16)["name"] == "dnnopt_tall_f32"  # rows of A off 16 bytes
     assert lib.plan_sgemm(65536, 16, 100)["kernel"] == b.K_TILE_F32   # short K off the 64 grid: register tiles
     assert lib.plan_sgemm(65536, 12, 300)["kernel"] == b.K_TILE_F32   # N <= 12 off the grid: register tiles

@@ -359,7 +359,9 @@ TALL = [(65536, 64, 256, 0, 0), (65536, 16, 256, 1, 0), (65537, 33, 300, 0, 3), 
         # ... and N <= 12 or K = 64 on the same kernel
         (65536, 1, 256, 0, 0), (65536, 8, 256, 4, 0), (262144, 16, 64, 0, 2), (131075, 5, 128, 0, 0),
         # ... and from 4K rows (one tile per wave or fewer)
-        (4096, 16, 256, 0, 0), (8191, 16, 128, 0, 1), (4097, 3, 64, 4, 0)]
+        (4096, 16, 256, 0, 0), (8191, 16, 128, 0, 1), (4097, 3, 64, 4, 0),
+        # ... and 16 < N <= 64 (K = 128 with N > 32 stays on the register-ring kernel)
+        (65536, 64, 192, 0, 2), (65537, 40, 256, 4, 0), (49153, 33, 64, 0, 1), (65536, 48, 128, 0, 0)]
 
 
 def _routes_tall(M, N, K, lda=None):
@@ -370,12 +372,12 @@ def _routes_tall(M, N, K, lda=None):
     waves = 256 * 8
     rows_ok = -(-M // 32) * 4 >= 3 * waves or (K >= 256 and -(-M // 16) * 2 >= waves)
     lda = K if lda is None else lda
-    dma = N <= 16 and K % 64 == 0 and 64 <= K <= 256 and lda % 4 == 0
-    if dma:
+    dma = N <= 64 and K % 64 == 0 and 64 <= K <= 256 and lda % 4 == 0 and not (K == 128 and N > 32)
+    if dma and N <= 16:
         return "dnnopt_tall_dma_f32" if M >= 4096 else None
-    if not (N > 12 and (N > 16 or K >= 128) and N <= 64 and rows_ok):
+    if not (N > 12 and (N > 16 or K >= 128) and N <= 64 and rows_ok and M >= 4096):
         return None
-    return "dnnopt_tall_f32"
+    return "dnnopt_tall_dma_f32" if dma else "dnnopt_tall_f32"
 
 
 @pytest.mark.parametrize("M,N,K,pa,pb", TALL)
@@ -405,7 +407,8 @@ def test_sgemm_tall_skinny(lib, orc, dev, M, N, K, pa, pb, tb):
         u.assert_fp32_close(host(dC), want, scale, K, f"tall {M}x{N}x{K} tb={tb} beta={beta}")
 
 
-@pytest.mark.parametrize("M,N,K", [(65536, 16, 256), (65537, 13, 128), (65536, 16, 192), (16384, 15, 256)])
+@pytest.mark.parametrize("M,N,K", [(65536, 16, 256), (65537, 13, 128), (65536, 16, 192), (16384, 15, 256),
+                                   (65536, 64, 256), (65537, 33, 192), (65536, 48, 64), (65536, 32, 128)])
 def test_tall_dma_matches_register_ring_kernel(lib, dev, M, N, K):
     """The LDS-DMA tall kernel adds the same products in the same order as
     the register-ring tall kernel (forced by TALL_RT=1): bit-identical C for
@@ -1220,6 +1223,8 @@ def _sgemm_sweep_cases():
             M, N, K = int(rng.integers(33, 600)), int(rng.integers(16, 3000)), int(rng.integers(1, 700))
         elif kind == 3:
             M, N, K = int(rng.integers(20000, 70000)), int(rng.integers(17, 65)), 256
+            if (len(cases) // 7) % 2:  # K off the 64-grid: the register-ring tall kernel
+                M, K = M + 30000, 200
         elif kind == 4:
             M, N, K = int(rng.integers(1, 5)), int(rng.integers(1, 9000)), int(rng.integers(1, 2100))
         elif kind == 5:
@@ -1260,7 +1265,8 @@ def test_sgemm_route_sweep(lib, orc, dev, M, N, K, ta, tb, pa, pb, alpha, beta):
 
 def test_sgemm_route_sweep_covers_every_route(lib):
     names = {lib.plan_sgemm(M, N, K, transA=ta, transB=tb)["name"] for M, N, K, ta, tb, *_ in _SGEMM_SWEEP}
-    assert names >= {"dnnopt_skinny", "dnnopt_rowdot", "dnnopt_tile_f32", "dnnopt_tall_f32", "dnnopt_kouter_f32"}, names
+    assert names >= {"dnnopt_skinny", "dnnopt_rowdot", "dnnopt_tile_f32", "dnnopt_tall_f32", "dnnopt_tall_dma_f32",
+                     "dnnopt_kouter_f32"}, names
 
 
 def _s8_sweep_cases():
