@@ -300,8 +300,10 @@ int dnnopt_hip_plan_gemm_int8_f32(int M, int N, int K, dnnopt_plan* out) {
     if (!out || !dims_ok(M, N, K)) return DNNOPT_ERR_INVALID_ARG;
     Launch L;
     if (M <= 8 && plan_skinny(kSkinnyF32, M, N, K, N, &L) == DNNOPT_OK) {
-        // dnnopt_skinny_q8 runs on the fp32 skinny plan's grid and partials.
+        // dnnopt_skinny_q8 runs on the fp32 skinny plan's grid and partials,
+        // summed by its own reduce kernel (no ticket slots).
         *out = L.pub;
+        out->workspace_bytes = L.part_bytes;
         out->kernel = DNNOPT_K_SKINNY_Q8;
         out->block = skinny_q8_waves() * 64;
         snprintf(out->name, sizeof out->name, "%s", "dnnopt_skinny_q8");

@@ -121,7 +121,9 @@ def test_plans_for_the_configs(lib):
         p = lib.plan_int8_f32(M, 4096, 4096)
         assert p["kernel"] == b.K_SKINNY_Q8 and p["name"] == "dnnopt_skinny_q8" and p["rows"] == M, p
         q = lib.plan_sgemm(M, 4096, 4096)
-        assert (p["grid_x"], p["splits"], p["workspace_bytes"]) == (q["grid_x"], q["splits"], q["workspace_bytes"])
+        with lib.tunables(SPLIT_REDUCE=2):  # the fp32 plan with the reduce kernel: partials only
+            r = lib.plan_sgemm(M, 4096, 4096)
+        assert (p["grid_x"], p["splits"], p["workspace_bytes"]) == (q["grid_x"], q["splits"], r["workspace_bytes"])
     # M > 8: int8 tiles that quantize the fp32 B while staging it
     for M in (9, 128):
         p = lib.plan_int8_f32(M, 4096, 4096)
