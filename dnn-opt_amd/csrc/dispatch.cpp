@@ -101,6 +101,7 @@ namespace {
 // Splits beyond this are reduced by a separate kernel rather than by the
 // last-arriving workgroup.
 constexpr int kTicketSplitLimit = 16;
+constexpr int kTileTicketSplits = 8;  // fp32 tiles: last-workgroup split sums up to this many splits
 
 long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
 
@@ -713,8 +714,18 @@ int plan_tile(int mode, int transA, int transB, int M, int N, int K, int lda, in
     const bool dma_ticket = tunable(kTuneTileTicket) == 1;
     const bool dma = (cfg >= kTileFirstDma && cfg < kTileF32Few) || cfg == kTileBF16Dma4w;  // LDS-DMA tiles
     const bool ticket_ok = !lds || (dma_ticket && dma);
+    // Split sums: fp32 tiles (register and LDS-DMA) let the tile's
+    // last-arriving workgroup add up to 8 splits' partials (one kernel; its
+    // threads read the partial block in 16-byte pieces, 8 in flight each),
+    // the reduce kernel beyond (MI355X, 36 split shapes, us, reduce ->
+    // last workgroup: 2-6 splits 1.01-1.11x faster, e.g. 784 x 128 x 1152
+    // 9.35 -> 8.42, 384 x 768 x 768 12.78 -> 11.73; 8 splits level to 1.03x;
+    // 16 splits 0.85-0.96x).  Tunable SPLIT_REDUCE: 0 the last workgroup up
+    // to 16 splits, 2 the reduce kernel.
+    const int srm = tunable(kTuneSplitReduce);
+    const bool want_ticket = srm == 0 || (srm == 1 && s <= kTileTicketSplits);
     L->defer_reduce =
-        (s > 1 && (split_reduce_mode() || s > kTicketSplitLimit || tiles > kMaxTickets || !ticket_ok)) ? 1 : 0;
+        (s > 1 && (!want_ticket || s > kTicketSplitLimit || tiles > kMaxTickets || !ticket_ok)) ? 1 : 0;
     L->part_bytes = s > 1 ? (size_t)s * tiles * bm * bn * sizeof(float) : 0;
     L->tickets = (s > 1 && !L->defer_reduce) ? (int)tiles : 0;
     const int kernel = mode == kTileF32 ? DNNOPT_K_TILE_F32 : DNNOPT_K_TILE_BF16;

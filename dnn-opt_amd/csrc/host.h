@@ -79,7 +79,8 @@ struct Launch {
 // workgroup (ticket) wherever the kernel has one; 1 (default) = the
 // planners' choice: the separate reduce kernel, except skinny launches of at
 // most 3 rows whose last workgroup reads at most kSkinnyTicketBytes of
-// partials; 2 = the reduce kernel everywhere.  split_reduce_mode() is 0 for
+// partials and fp32 tile launches of at most 8 splits; 2 = the reduce kernel
+// everywhere.  split_reduce_mode() is 0 for
 // the ticket, 1 for the reduce kernel (the planners' default).
 constexpr long long kSkinnyTicketBytes = 48 * 1024;
 int split_reduce_mode();

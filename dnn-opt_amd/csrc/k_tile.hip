@@ -130,25 +130,52 @@ __device__ __forceinline__ void tile_finish(const TileArgs& p, f32x4 (&acc)[MT][
         }
         if (p.defer_reduce) return;
         if (!split_ticket(&p.tickets[(size_t)tile_id * kTicketStride], (unsigned)p.splits, last_flag)) return;
-        if (wk != 0) return;
+        // Last workgroup of the tile: every thread sums 16-byte pieces of the
+        // tile's row-major partial block over the splits in ascending split
+        // order (as dnnopt_splitk_reduce, so the same bits), CH splits' loads
+        // in flight at a time, and stores C with the epilogue.  Its own
+        // partial is read back from memory like the others.
+        constexpr int NTH = WM * WN * KW * 64;
+        constexpr int Q4 = S::BM * S::BN / 4;      // 16-byte pieces of the tile
+        constexpr int QT = (Q4 + NTH - 1) / NTH;   // pieces per thread
+        constexpr int CH = QT >= 8 ? 1 : 8 / QT;  // splits per batch of loads (8 pieces in flight)
+        const uint32_t stride = (uint32_t)tiles * (uint32_t)(S::BM * S::BN) * 4u;
+        const uint32_t tbase = (uint32_t)tile_id * (uint32_t)(S::BM * S::BN) * 4u;
+        f32x4 sum[QT];
+        for (int sp0 = 0; sp0 < p.splits; sp0 += CH) {
+            f32x4 v[CH][QT];
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+            for (int u = 0; u < CH; ++u)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int ml = (wm * MT + mt) * 16 + 4 * g + i;
-                    const int nl = tile_col<NT, ILV>(wn, nt, r);
-                    const size_t off0 = (size_t)tile_id * (S::BM * S::BN) + ml * S::BN + nl;
-                    const size_t stride = (size_t)tiles * (S::BM * S::BN);
-                    // Ascending split order; this workgroup's own partial is
-                    // the value in its registers (the same bits it stored).
-                    const float mine = acc[mt][nt][i];
-                    float s = split == 0 ? mine : as_f32(buf_load_x1_coherent(rp, (uint32_t)(off0 * 4)));
-                    for (int sp = 1; sp < p.splits; ++sp)
-                        s += sp == split ? mine : as_f32(buf_load_x1_coherent(rp, (uint32_t)((off0 + sp * stride) * 4)));
-                    acc[mt][nt][i] = s;
+                for (int j = 0; j < QT; ++j) {
+                    const int q = (int)threadIdx.x + j * NTH;
+                    v[u][j] = buf_load_x4_coherent(
+                        rp, sp0 + u < p.splits && q < Q4 ? tbase + (uint32_t)(sp0 + u) * stride + (uint32_t)q * 16u
+                                                         : kOobOffset);
                 }
+#pragma unroll
+            for (int u = 0; u < CH; ++u)
+#pragma unroll
+                for (int j = 0; j < QT; ++j)
+                    if (sp0 + u < p.splits) sum[j] = sp0 + u == 0 ? v[u][j] : sum[j] + v[u][j];
+        }
+        const int m0 = tile_m * S::BM, n0 = tile_n * S::BN;
+#pragma unroll
+        for (int j = 0; j < QT; ++j) {
+            const int q = (int)threadIdx.x + j * NTH;
+            const int m = m0 + (4 * q) / S::BN, n1 = n0 + (4 * q) % S::BN;
+            if (q < Q4 && m < p.M) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int n = n1 + e;
+                    if (n < p.N) {
+                        float* c = p.C + (size_t)m * p.ldc + n;
+                        *c = add_bias(epilogue(sum[j][e], p.alpha, p.beta, c), p.bias, n);
+                    }
+                }
+            }
+        }
+        return;
     } else if (wk != 0) {
         return;
     }

@@ -290,8 +290,10 @@ int dnnopt_hip_device_count(void);    /* 0 when no device is visible        */
 #define DNNOPT_TUNE_SKINNY_NW        4  /* 4, 8 or 16 waves; 0 = by problem size */
 #define DNNOPT_TUNE_SKINNY_WGS_PER_CU 5
 #define DNNOPT_TUNE_MAX_SPLITS       6
-#define DNNOPT_TUNE_SPLIT_REDUCE     7  /* split-k sums: 1 (default) the planners' choice, 2 the
-                                           reduce kernel, 0 the last-arriving workgroup */
+#define DNNOPT_TUNE_SPLIT_REDUCE     7  /* split-k sums: 1 (default) the planners' choice (the
+                                           last-arriving workgroup for small skinny combines and
+                                           fp32 tiles of at most 8 splits), 2 the reduce kernel,
+                                           0 the last-arriving workgroup */
 #define DNNOPT_TUNE_SKINNY_WGS       8
 #define DNNOPT_TUNE_TILE_SPLITS      9  /* force the k-splits of a tile launch */
 #define DNNOPT_TUNE_TILE_CFG        10  /* force a tile configuration (bf16 LDS-staged: 5 and up;

@@ -371,3 +371,28 @@ def test_split_sums_bit_identical_across_modes(lib, dev, M, N, K, dt):
         outs.append(C)
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2]), (M, N, K, dt)
+
+
+@pytest.mark.parametrize("M,N,K,tb,forced", [(128, 3072, 768, 0, 0), (784, 128, 1152, 1, 0), (196, 256, 2304, 0, 0),
+                                             (176, 64, 4608, 1, 0), (49, 512, 4608, 1, 0), (128, 768, 3072, 0, 0),
+                                             (300, 600, 2048, 0, 4), (1000, 1000, 3000, 1, 6)])
+def test_tile_split_sums_bit_identical_across_modes(lib, dev, M, N, K, tb, forced):
+    """fp32 MFMA tiles with k-splits: the tile's last-arriving workgroup
+    (SPLIT_REDUCE=0, and the default up to 8 splits) and the reduce kernel
+    (2) add the partials in the same split order and apply the same
+    epilogue, so C is bit-identical (beta = 1 over a preset C)."""
+    g = torch.Generator(device="cpu").manual_seed(M * 7 + N * 3 + K)
+    A = torch.randn(M, K, generator=g).to(dev)
+    B = (torch.randn(*((N, K) if tb else (K, N)), generator=g) * 0.02).to(dev)
+    C0 = (torch.rand(M, N, generator=g) * 2 - 1).to(dev)
+    outs = []
+    for mode in (0, 1, 2):
+        C = C0.clone()
+        with lib.tunables(SPLIT_REDUCE=mode, TILE_SPLITS=forced):
+            p = lib.plan_sgemm(M, N, K, transB=tb)
+            assert p["name"].startswith("dnnopt_tile_f32") and p["splits"] > 1, p
+            lib.sgemm(M, N, K, 0.75, A, K, B, K if tb else N, 1.0, C, N, transB=tb,
+                      stream=torch.cuda.current_stream().cuda_stream)
+        outs.append(C)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[2]), (M, N, K, tb, forced)
