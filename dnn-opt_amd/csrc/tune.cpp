@@ -9,6 +9,7 @@
 // seeds the table once, at its first use, from DNNOPT_<NAME> environment
 // variables, for sweeps that drive an unmodified program.
 #include <atomic>
+#include <climits>
 #include <mutex>
 #include <stdlib.h>
 
@@ -23,6 +24,7 @@ struct TuneDef {
     const char* env;  // DNNOPT_<NAME> (tuning builds only)
     int dflt;
     bool flag;        // parsed as a switch: "0" turns it off
+    int lo = 1;       // smallest value the environment may set (not for switches)
 };
 
 // Indexed by Tunable (host.h); values are documented there.
@@ -30,10 +32,10 @@ constexpr TuneDef kDefs[kTuneCount] = {
     {"DNNOPT_Q8B", 1, true},           {"DNNOPT_KOUTER", 1, true},
     {"DNNOPT_KOUTER_WGS_PER_CU", 1, false}, {"DNNOPT_WAVES_PER_CU", 8, false},
     {"DNNOPT_SKINNY_NW", 0, false},    {"DNNOPT_SKINNY_WGS_PER_CU", 1, false},
-    {"DNNOPT_MAX_SPLITS", 256, false}, {"DNNOPT_SPLIT_REDUCE", 1, false},
+    {"DNNOPT_MAX_SPLITS", 256, false}, {"DNNOPT_SPLIT_REDUCE", 1, false, 0},
     {"DNNOPT_SKINNY_WGS", 0, false},   {"DNNOPT_TILE_SPLITS", 0, false},
     {"DNNOPT_TILE_CFG", 0, false},     {"DNNOPT_TILE_TICKET", 0, false},
-    {"DNNOPT_S8_CFG", -1, false},      {"DNNOPT_S8_ROWDOT", 1, true},
+    {"DNNOPT_S8_CFG", -1, false, 0},      {"DNNOPT_S8_ROWDOT", 1, true},
     {"DNNOPT_S8_SPLITS", 0, false},    {"DNNOPT_ROWDOT_KW", 0, false},
     {"DNNOPT_TALL_RT", 0, false},      {"DNNOPT_TALL_WGS_PER_CU", 1, false},
     {"DNNOPT_TALL", 1, true},          {"DNNOPT_WIDE", 0, true},
@@ -46,11 +48,13 @@ void init_table() {
     for (int i = 0; i < kTuneCount; ++i) {
         int v = kDefs[i].dflt;
 #if DNNOPT_TUNING
+        // A whole decimal integer only; anything else leaves the default.
         const char* e = getenv(kDefs[i].env);
-        if (e && *e) {
-            const int x = atoi(e);
+        char* end = nullptr;
+        const long x = e && *e ? strtol(e, &end, 10) : 0;
+        if (e && *e && end && *end == '\0' && x >= INT_MIN && x <= INT_MAX) {
             if (kDefs[i].flag) v = x != 0 ? 1 : 0;
-            else if (x > 0) v = x;
+            else if (x >= kDefs[i].lo) v = (int)x;
         }
 #endif
         g_val[i].store(v, std::memory_order_relaxed);

@@ -280,7 +280,8 @@ int dnnopt_hip_device_count(void);    /* 0 when no device is visible        */
  * library starts from built-in defaults and changes one only when a caller
  * sets it here (process-wide, effective from the next planning call).  The
  * default build never reads the environment; a build with -DDNNOPT_TUNING=1
- * seeds the table once from DNNOPT_<NAME> variables.  Switches take 1 / 0;
+ * seeds the table once from DNNOPT_<NAME> variables (whole integers from 1,
+ * from 0 for SPLIT_REDUCE and S8_CFG; others are ignored).  Switches take 1 / 0;
  * forcing keys take 0 (-1 for DNNOPT_TUNE_S8_CFG) to let the planner decide.
  * *previous (if not NULL) receives the old value.                        */
 #define DNNOPT_TUNE_Q8B              0  /* 1: int8 tiles quantize the fp32 B while staging it */

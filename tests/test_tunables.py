@@ -109,3 +109,49 @@ def test_split_reduce_choice():
     assert not ticket(lambda: lib.plan_bf16(4, 11008, 4096))
     with lib.tunables(SPLIT_REDUCE=0):
         assert lib.plan_sgemm(7, 1009, 2048)["workspace_bytes"] > lib.plan_sgemm(1, 1, 1)["workspace_bytes"]
+
+
+def test_tuning_build_seeds_from_environment(tmp_path):
+    """A -DDNNOPT_TUNING=1 build seeds each tunable from DNNOPT_<NAME> once:
+    a whole integer at or above the key's lowest value (0 for SPLIT_REDUCE,
+    whose 0 selects the last-workgroup sums, and for S8_CFG; 1 elsewhere),
+    switches as 0 / 1; anything else leaves the default.  The table's source
+    file is built on its own with the host compiler."""
+    import ctypes
+    import shutil
+
+    import pytest
+
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("no host C++ compiler")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    so = str(tmp_path / "libtune.so")
+    subprocess.run([gxx, "-std=c++17", "-O1", "-shared", "-fPIC", "-DDNNOPT_TUNING=1", "-D__HIP_PLATFORM_AMD__",
+                    "-I" + os.path.join(root, "dnn-opt_amd", "csrc"), "-I" + os.path.join(root, "include"),
+                    "-I/opt/rocm/include", os.path.join(root, "dnn-opt_amd", "csrc", "tune.cpp"), "-o", so],
+                   check=True, capture_output=True)
+    tune = u.binding().TUNE
+    keys = ("SPLIT_REDUCE", "S8_CFG", "MAX_SPLITS", "TALL", "TILE_CFG")
+    child = ("import ctypes, json, sys\n"
+             "L = ctypes.CDLL(sys.argv[1])\n"
+             "out = {}\n"
+             "for k, i in json.loads(sys.argv[2]).items():\n"
+             "    v = ctypes.c_int(-99)\n"
+             "    assert L.dnnopt_hip_get_tunable(i, ctypes.byref(v)) == 0\n"
+             "    out[k] = v.value\n"
+             "print(json.dumps(out))\n")
+
+    def seeded(env):
+        e = {k: v for k, v in os.environ.items() if not k.startswith("DNNOPT_")}
+        e.update({"DNNOPT_" + k: v for k, v in env.items()})
+        r = subprocess.run([sys.executable, "-c", child, so, json.dumps({k: tune[k] for k in keys})], env=e,
+                           check=True, capture_output=True, text=True)
+        return json.loads(r.stdout)
+
+    defaults = {"SPLIT_REDUCE": 1, "S8_CFG": -1, "MAX_SPLITS": 256, "TALL": 1, "TILE_CFG": 0}
+    assert seeded({}) == defaults
+    assert seeded({"SPLIT_REDUCE": "0", "S8_CFG": "0", "MAX_SPLITS": "12", "TALL": "0", "TILE_CFG": "43"}) == {
+        "SPLIT_REDUCE": 0, "S8_CFG": 0, "MAX_SPLITS": 12, "TALL": 0, "TILE_CFG": 43}
+    # Below a key's lowest value, or not a whole integer: the default stays.
+    assert seeded({"SPLIT_REDUCE": "-1", "S8_CFG": "-2", "MAX_SPLITS": "0", "TALL": "x", "TILE_CFG": "4x"}) == defaults
