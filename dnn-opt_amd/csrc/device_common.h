@@ -340,6 +340,18 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t r, char* lds, u
 #endif
 }
 
+// As lds_dma16, for data read once (non-temporal, kAuxNT).
+__device__ __forceinline__ void lds_dma16_stream(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0,
+                                             kAuxNT);
+#else
+    (void)r;
+    (void)lds;
+    (void)voffset;
+#endif
+}
+
 // s_waitcnt vmcnt(n) (n < 64), other counters not waited on.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

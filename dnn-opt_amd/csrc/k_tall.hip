@@ -266,6 +266,11 @@ __global__ __launch_bounds__(kTallWaves * 64) void dnnopt_tall_f32(TallArgs p) {
 //   * MFMA operands as in dnnopt_tall_f32 (lane (r, g) reads k = 16 kc + 4 g
 //     .. + 3 of row r, component c feeding MFMA c), in the same k order, so
 //     both kernels add the same products in the same order.
+//   * with one or two column tiles, where the stream of A bounds the kernel,
+//     its copies carry the non-temporal hint (A is read once): MI355X,
+//     65536 x 16 x 256 15.9 -> 14.7 us, N = 8 / 12 / 24 / 32 4-9% faster;
+//     from three column tiles the MFMAs bound it and the hint measured
+//     1-5% slower (N = 48 / 64), so those copies stay plain.
 // Measured at 65536 rows against 4 waves with two whole-tile slots, 4 waves
 // with 3 / 4 slots, 2 and 3 waves, and 8 waves with one slot: this layout
 // is the fastest at K = 192 / 256 for every N and level elsewhere.
@@ -336,7 +341,10 @@ __global__ __launch_bounds__(kTallDmaWaves * 64) void dnnopt_tall_dma_f32(TallAr
         char* dst = ring + slot * PIECEB;
         const uint32_t base = l_tile + (uint32_t)l_p * (uint32_t)SEGB;
 #pragma unroll
-        for (int j = 0; j < NI; ++j) lds_dma16(ra, dst + j * 1024, src[j] + base);
+        for (int j = 0; j < NI; ++j) {
+            if constexpr (NT <= 2) lds_dma16_stream(ra, dst + j * 1024, src[j] + base);
+            else lds_dma16(ra, dst + j * 1024, src[j] + base);
+        }
         if (++l_p == PPT) {
             l_p = 0;
             l_tile += tile_step;
