@@ -43,8 +43,10 @@ __device__ __forceinline__ i32x4 mask_chunk(i32x4 v, int valid) {
 
 // AL = 1: all rows of A and B start on 4-byte boundaries; AL = 0: rows are
 // read with funnel-shifted loads.
-template <int AL>
+// STREAM: rows read once (B), aligned loads carry the non-temporal hint.
+template <int AL, bool STREAM = false>
 __device__ __forceinline__ i32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    if constexpr (AL && STREAM) return __builtin_bit_cast(i32x4, buf_load_x4_stream(r, off));
     if constexpr (AL) return __builtin_bit_cast(i32x4, buf_load_x4(r, off));
     return __builtin_bit_cast(i32x4, buf_load_x4_unaligned(r, off));
 }
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(WM* WN* KW * 64) void dnnopt_mfma_s8(S8Args p) {
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const uint32_t off = (live && brow[nt] != kOobOffset) ? brow[nt] + kc : kOobOffset;
-                b[nt][j] = load16<AL>(rb, off);
+                b[nt][j] = load16<AL, true>(rb, off);
             }
         }
     };

@@ -93,9 +93,11 @@ __device__ __forceinline__ u32x4 keep_elems(u32x4 v, int valid) {
     return r;
 }
 
-template <int AL>
+// STREAM: rows read once (B), aligned loads carry the non-temporal hint.
+template <int AL, bool STREAM = false>
 __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    if constexpr (AL) return buf_load_x4(r, off);
+    if constexpr (AL && STREAM) return buf_load_x4_stream(r, off);
+    else if constexpr (AL) return buf_load_x4(r, off);
     else return buf_load_x4_unaligned(r, off);
 }
 
@@ -179,7 +181,7 @@ __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
         for (int u = 0; u < kU; ++u) {
             const uint32_t ko = (uint32_t)((j + u) * 64 + lane) * 16u;
 #pragma unroll
-            for (int r = 0; r < R; ++r) bv[u][r] = load16<AL>(rb, b_row[r] + ko);
+            for (int r = 0; r < R; ++r) bv[u][r] = load16<AL, true>(rb, b_row[r] + ko);
 #pragma unroll
             for (int m = 0; m < MR; ++m) av[u][m] = load16<AL>(ra, a_row[m] + ko);
         }
@@ -192,7 +194,7 @@ __global__ __launch_bounds__(kWaves * 64) void dnnopt_rowdot(RowdotArgs p) {
         const int valid = p.K - c * VEC;  // elements of this chunk inside the row
         u32x4 bv[R], av[MR];
 #pragma unroll
-        for (int r = 0; r < R; ++r) bv[r] = load16<AL>(rb, valid > 0 ? b_row[r] + ko : kOobOffset);
+        for (int r = 0; r < R; ++r) bv[r] = load16<AL, true>(rb, valid > 0 ? b_row[r] + ko : kOobOffset);
 #pragma unroll
         for (int m = 0; m < MR; ++m) av[m] = load16<AL>(ra, valid > 0 ? a_row[m] + ko : kOobOffset);
         if (valid < VEC) {
